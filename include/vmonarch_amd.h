@@ -1,0 +1,135 @@
+/*
+ * vmonarch_amd -- C ABI of the MI355X (gfx950) VMonarch attention hot path.
+ *
+ * The reference (EricLina/VMonarch) has no C/C++ API: its device code is Triton JIT kernels
+ * launched from Python.  Each entry point below replaces one launch site of the reference's
+ * Python, keeping the argument meaning; the Python package `vmonarch_amd` (and the alias
+ * package `video_monarch_attention`) binds them with ctypes and keeps the reference's Python
+ * API unchanged.
+ *
+ * Conventions
+ *   - Every call is asynchronous on the given HIP stream (a hipStream_t passed as void*,
+ *     NULL = the default stream) and never allocates device memory: scratch comes from the
+ *     caller's `workspace`.
+ *   - Return 0 (VMO_OK) on success, a VMO_ERR_* code otherwise; vmo_last_error() then holds a
+ *     message for the calling thread.  Argument errors are detected before any launch.
+ *   - Tensors are (batch, heads, tokens, features) views with element strides for the first
+ *     three dims and contiguous features (feature stride 1), 16-byte aligned rows.
+ *   - Element type is bf16 or fp16 (VMO_DTYPE_*); statistics (lse, entropy) are fp32.
+ */
+#ifndef VMONARCH_AMD_H
+#define VMONARCH_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VMO_ABI_VERSION 1
+
+enum {
+  VMO_OK = 0,
+  VMO_ERR_INVALID = 1,     /* bad shape / stride / pointer / alignment */
+  VMO_ERR_UNSUPPORTED = 2, /* valid request this build has no kernel for (e.g. head dim 48) */
+  VMO_ERR_WORKSPACE = 3,   /* workspace missing or too small */
+  VMO_ERR_LAUNCH = 4       /* HIP reported an error at launch */
+};
+
+enum { VMO_DTYPE_BF16 = 0, VMO_DTYPE_F16 = 1 };
+
+/* A strided 4-d view (batch, heads, tokens, features); strides in elements. */
+typedef struct vmo_view {
+  void* data;
+  int64_t stride_b, stride_h, stride_n;
+} vmo_view;
+
+/*
+ * FlashEntropyAttention forward.
+ *
+ * Replaces the `_attn_fwd` launch of _FlashEntropyAttention.forward
+ * (video_monarch_attention/kernel.py:318-358, kernel :104-151, inner loop :32-67).
+ *
+ * Problems: batch * heads * frames independent attentions.  Frame f of (b, h) uses query rows
+ * [f*nq, (f+1)*nq) of q / o / lse / ent and key rows [f*nk, (f+1)*nk) of k / w0 / w1, so
+ * frames = m turns one (B, H, m*b, D) tensor into the reference's R-step batch
+ * (vmonarch.py:25 flattens (B, H, m, b, .) to (B, H*m, b, .)) without a copy.
+ *
+ *   o[:, :, i, 0:dw0]        = sum_j P_ij w0_j
+ *   o[:, :, i, dw0:dw0+dw1]  = sum_j P_ij w1_j          (dw1 = 0: no second value tensor)
+ *   P = softmax_j(sm_scale * q_i . k_j) over the nk keys of the problem (non-causal)
+ *   ent[i] = -sum_j P_ij ln P_ij (nats)    lse[i] = log2(sum_j 2^(sm_scale*log2(e)*q_i.k_j))
+ * Two value tensors replace the reference's torch.cat([k, v], -1) (vmonarch.py:50); when w0
+ * aliases k (same data and strides, dw0 == d) the K tile is staged once and used twice.
+ * ent / lse may be NULL.  num_splits > 1 splits the keys of each problem into num_splits
+ * ranges (split-KV, for problems with few query tiles such as the recompute of
+ * vmonarch.py:66-68); it needs ent == NULL and a workspace of
+ * vmo_fea_fwd_workspace_size() bytes.  Supported: d in {64, 128}; dw0 in {64, 128, 256};
+ * dw1 in {0, 64, 128} (dw1 > 0 only with w0 aliasing k); sm_scale >= 0.
+ */
+typedef struct vmo_fea_fwd_args {
+  int32_t dtype;
+  int32_t batch, heads, frames;
+  int32_t nq, nk;
+  int32_t d, dw0, dw1;
+  vmo_view q, k, w0, w1, o;
+  float* lse;                      /* optional: (batch, heads, frames*nq), token stride 1 */
+  float* ent;                      /* optional: same layout as lse */
+  int64_t stat_stride_b, stat_stride_h;
+  float sm_scale;
+  int32_t num_splits;              /* 1 = no split */
+  void* workspace;
+  size_t workspace_bytes;
+} vmo_fea_fwd_args;
+
+/*
+ * One L-step of the alternating minimisation (vmonarch.py:51-63), fused.
+ *
+ * For every (b, h) and grid column j of the (m, b) token grid (token n = i*block + j):
+ *   logits[i,k] = scale * q[i,j] . out[k,j,0:d]                         (vmonarch.py:51, :55)
+ *   attn[i,:]   = softmax_k(logits[i,k] + ent[k,j])                      (vmonarch.py:56)
+ *   last == 0:  u[k,j]  = scale / max(sum_i attn[i,k], min_col_mass) * sum_i attn[i,k] q[i,j]
+ *                                                                         (vmonarch.py:61-63)
+ *   last == 1:  z[i,j]  = sum_k attn[i,k] out[k,j,d:d+dv]                (vmonarch.py:57-59)
+ * ent is the R-step entropy (the reference subtracts neg_ent = -ent).  `res` receives u
+ * (d features) or z (dv features).  With last == 1, tokens n < skip_tokens are not written
+ * (the recompute of vmonarch.py:66-68 owns them).  Supported: m <= 32, d in {64, 128},
+ * dv in {64, 128}.
+ */
+typedef struct vmo_lstep_args {
+  int32_t dtype;
+  int32_t batch, heads;
+  int32_t num_blocks, block_size;  /* m, b */
+  int32_t d, dv;
+  int32_t last;
+  int32_t skip_tokens;
+  vmo_view q;                      /* (B, H, m*b, d) */
+  vmo_view out;                    /* (B, H, m*b, d + dv*last): R-step output [P k | P v] */
+  const float* ent;                /* (B, H, m*b) with token stride 1 */
+  int64_t ent_stride_b, ent_stride_h;
+  vmo_view res;                    /* u: (B, H, m*b, d)   or   z: (B, H, m*b, dv) */
+  float scale;
+  float min_col_mass;
+} vmo_lstep_args;
+
+/* ABI version of the loaded library (VMO_ABI_VERSION at build time). */
+int vmo_abi_version(void);
+
+/* Message of the calling thread's last failed call ("" if none). */
+const char* vmo_last_error(void);
+
+/* Bytes of workspace vmo_fea_fwd needs for these arguments (0 when num_splits <= 1). */
+size_t vmo_fea_fwd_workspace_size(const vmo_fea_fwd_args* args);
+
+/* FlashEntropyAttention forward; see vmo_fea_fwd_args. */
+int vmo_fea_fwd(const vmo_fea_fwd_args* args, void* stream);
+
+/* Fused L-step; see vmo_lstep_args. */
+int vmo_lstep_fwd(const vmo_lstep_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VMONARCH_AMD_H */

@@ -1,0 +1,102 @@
+"""CPU-side checks of the C ABI: the library loads, exports every symbol include/vmonarch_amd.h
+declares, and rejects bad arguments with an error code before touching the GPU."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "vmonarch_amd.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(vmo_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def L():
+    from vmonarch_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail(f"{_lib.LIB_PATH} not built; run python -m vmonarch_amd.build")
+    return _lib.lib()
+
+
+def test_header_declares_the_entry_points():
+    names = _declared_functions()
+    for n in ("vmo_abi_version", "vmo_last_error", "vmo_fea_fwd", "vmo_fea_fwd_workspace_size", "vmo_lstep_fwd"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol(L):
+    for n in _declared_functions():
+        assert hasattr(L, n), f"{n} declared in the header but not exported"
+
+
+def test_abi_version(L):
+    from vmonarch_amd import _lib
+    assert L.vmo_abi_version() == _lib.ABI_VERSION
+
+
+def test_single_hip_runtime_in_process(L):
+    maps = open("/proc/self/maps").read().splitlines()
+    hip = {ln.split()[-1] for ln in maps if "libamdhip64" in ln}
+    assert len(hip) <= 1, hip
+
+
+def _fwd_args(**kw):
+    from vmonarch_amd import _lib
+    a = _lib.FeaFwdArgs()
+    a.dtype, a.batch, a.heads, a.frames, a.nq, a.nk, a.d, a.dw0, a.dw1 = 0, 1, 1, 1, 128, 128, 128, 128, 0
+    v = _lib.View(4096, 128, 128 * 128, 128)
+    a.q = a.k = a.w0 = a.o = v
+    a.sm_scale = 0.1
+    a.num_splits = 1
+    for k, x in kw.items():
+        setattr(a, k, x)
+    return a
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("dtype", 7, 1), ("d", 48, 2), ("dw0", 96, 2), ("nk", 0, 1), ("sm_scale", -1.0, 1),
+])
+def test_fea_fwd_rejects_bad_arguments_without_launching(L, field, value, code):
+    a = _fwd_args(**{field: value})
+    rc = L.vmo_fea_fwd(ctypes.byref(a), None)
+    assert rc == code
+    assert L.vmo_last_error().decode()
+
+
+def test_fea_fwd_rejects_misaligned_rows(L):
+    from vmonarch_amd import _lib
+    a = _fwd_args()
+    a.q = _lib.View(4096 + 2, 128, 128 * 128, 128)
+    assert L.vmo_fea_fwd(ctypes.byref(a), None) == 1
+    a = _fwd_args()
+    a.k = _lib.View(4096, 128, 128 * 128, 100)
+    assert L.vmo_fea_fwd(ctypes.byref(a), None) == 1
+
+
+def test_fea_fwd_split_needs_workspace(L):
+    a = _fwd_args(num_splits=4, nk=4096)
+    need = L.vmo_fea_fwd_workspace_size(ctypes.byref(a))
+    assert need >= 4 * 128 * 128 * 4
+    assert L.vmo_fea_fwd(ctypes.byref(a), None) == 3
+
+
+def test_fea_fwd_empty_problem_is_a_no_op(L):
+    a = _fwd_args(nq=0)
+    assert L.vmo_fea_fwd(ctypes.byref(a), None) == 0
+
+
+def test_lstep_rejects_too_many_blocks(L):
+    from vmonarch_amd import _lib
+    a = _lib.LstepArgs()
+    a.dtype, a.batch, a.heads, a.num_blocks, a.block_size, a.d, a.dv = 0, 1, 1, 33, 4, 128, 128
+    v = _lib.View(4096, 128, 128, 128)
+    a.q = a.out = a.res = v
+    a.ent = 4096
+    assert L.vmo_lstep_fwd(ctypes.byref(a), None) == 2

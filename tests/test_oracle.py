@@ -1,0 +1,180 @@
+"""Pins the CPU oracle (oracle/) before anything is judged against it.
+
+Each check is chosen so that a plausible slip in the oracle (a dropped term, a wrong sign, a
+transposed operand, a wrong einsum index) fails at least one of them:
+  * brute-force pure-Python loops on tiny inputs (independent restatement of the formulas);
+  * closed forms of the entropy (uniform -> ln n, two keys -> binary entropy, dominant -> 0);
+  * central finite differences for the analytic backward;
+  * golden vectors written by the reference's own code (tests/golden/make_golden.py);
+  * reductions of VMonarch to exact attention (m=1, b=1, rt=N), permutation equivariance
+    within a frame, linearity in v.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from conftest import assert_close_ref, golden_names, load_golden
+from oracle import entropy_attention, entropy_attention_grad, exact_attention, vmonarch_attention
+
+
+def brute_entropy_attention(q, k, v, scale):
+    """Pure-Python loops: o_i = sum_j P_ij v_j, e_i = -sum_j P_ij ln P_ij."""
+    nq, nk = len(q), len(k)
+    o, e = [], []
+    for i in range(nq):
+        s = [scale * sum(q[i][d] * k[j][d] for d in range(len(q[i]))) for j in range(nk)]
+        mx = max(s)
+        w = [math.exp(x - mx) for x in s]
+        tot = sum(w)
+        p = [x / tot for x in w]
+        o.append([sum(p[j] * v[j][c] for j in range(nk)) for c in range(len(v[0]))])
+        e.append(-sum(pj * math.log(pj) for pj in p if pj > 0))
+    return np.array(o), np.array(e)
+
+
+def test_fea_matches_brute_force_loops():
+    rng = np.random.default_rng(0)
+    q, k, v = rng.normal(size=(5, 3)), rng.normal(size=(7, 3)), rng.normal(size=(7, 4))
+    o, e = entropy_attention(q, k, v, 0.7)
+    o_b, e_b = brute_entropy_attention(q.tolist(), k.tolist(), v.tolist(), 0.7)
+    np.testing.assert_allclose(o, o_b, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(e, e_b, rtol=1e-12, atol=1e-12)
+
+
+def test_fea_default_scale_is_inverse_sqrt_d():
+    rng = np.random.default_rng(1)
+    q, k, v = rng.normal(size=(1, 2, 9, 16)), rng.normal(size=(1, 2, 9, 16)), rng.normal(size=(1, 2, 9, 8))
+    o1, e1 = entropy_attention(q, k, v)
+    o2, e2 = entropy_attention(q, k, v, 16 ** -0.5)
+    np.testing.assert_array_equal(o1, o2)
+    np.testing.assert_array_equal(e1, e2)
+
+
+@pytest.mark.parametrize("n", [1, 2, 17, 1560])
+def test_entropy_uniform_is_log_n(n):
+    rng = np.random.default_rng(n)
+    q = rng.normal(size=(3, 8))
+    k = np.tile(rng.normal(size=(1, 8)), (n, 1))          # identical keys -> uniform rows
+    v = rng.normal(size=(n, 5))
+    o, e = entropy_attention(q, k, v, 1.0)
+    np.testing.assert_allclose(e, np.full(3, math.log(n)), atol=1e-12)
+    np.testing.assert_allclose(o, np.tile(v.mean(0), (3, 1)), atol=1e-12)
+    o0, e0 = entropy_attention(np.zeros((2, 8)), rng.normal(size=(n, 8)), v, 1.0)  # q = 0 -> uniform
+    np.testing.assert_allclose(e0, np.full(2, math.log(n)), atol=1e-12)
+
+
+def test_entropy_two_keys_is_binary_entropy():
+    q = np.array([[1.0, 0.0]])
+    for delta in [-3.0, -0.5, 0.0, 0.25, 2.0]:
+        k = np.array([[0.0, 0.0], [delta, 0.0]])
+        _, e = entropy_attention(q, k, np.eye(2), 1.0)
+        p = 1.0 / (1.0 + math.exp(-delta))
+        h = -(p * math.log(p) + (1 - p) * math.log(1 - p))
+        assert abs(e[0] - h) < 1e-12
+
+
+def test_entropy_dominant_logit_goes_to_zero():
+    q = np.array([[1.0]])
+    k = np.array([[0.0], [0.0], [60.0], [0.0]])
+    v = np.arange(8.0).reshape(4, 2)
+    o, e = entropy_attention(q, k, v, 1.0)
+    assert 0.0 <= e[0] < 1e-20
+    np.testing.assert_allclose(o[0], v[2], atol=1e-20)
+
+
+@pytest.mark.parametrize("nq,nk,d,dv", [(4, 6, 3, 2), (3, 3, 5, 4)])
+def test_fea_grad_matches_finite_differences(nq, nk, d, dv):
+    rng = np.random.default_rng(nq * 100 + nk)
+    q, k, v = rng.normal(size=(nq, d)), rng.normal(size=(nk, d)), rng.normal(size=(nk, dv))
+    do, de = rng.normal(size=(nq, dv)), rng.normal(size=(nq,))
+    scale = 0.8
+
+    def loss(q_, k_, v_):
+        o, e = entropy_attention(q_, k_, v_, scale)
+        return (o * do).sum() + (e * de).sum()
+
+    grads = entropy_attention_grad(q, k, v, do, de, scale)
+    eps = 1e-6
+    for x, g in zip((q, k, v), grads):
+        num = np.zeros_like(x)
+        for idx in np.ndindex(x.shape):
+            xp, xm = x.copy(), x.copy()
+            xp[idx] += eps
+            xm[idx] -= eps
+            args_p = [xp if a is x else a for a in (q, k, v)]
+            args_m = [xm if a is x else a for a in (q, k, v)]
+            num[idx] = (loss(*args_p) - loss(*args_m)) / (2 * eps)
+        np.testing.assert_allclose(g, num, rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("name", golden_names("fea_"))
+def test_fea_oracle_matches_reference_golden(name):
+    g = load_golden(name)
+    o, e = entropy_attention(g["q"], g["k"], g["v"], float(g["sm_scale"]))
+    assert_close_ref(o, g["o"], 1e-5)
+    assert_close_ref(e, g["e"], 1e-5)
+    np.testing.assert_allclose(o, g["o"], atol=2e-5, rtol=1e-4)
+    np.testing.assert_allclose(e, g["e"], atol=2e-5, rtol=1e-4)
+
+
+@pytest.mark.parametrize("name", golden_names("vmonarch_"))
+def test_vmonarch_oracle_matches_reference_golden(name):
+    g = load_golden(name)
+    z = vmonarch_attention(g["q"], g["k"], g["v"], int(g["num_blocks"]), int(g["block_size"]),
+                           int(g["num_iters"]), int(g["recompute_tokens"]))
+    assert_close_ref(z, g["z"], 1e-5)
+    np.testing.assert_allclose(z, g["z"], atol=5e-5, rtol=1e-4)
+
+
+def _qkv(seed, B, H, N, D, Dv=None):
+    rng = np.random.default_rng(seed)
+    return rng.normal(size=(B, H, N, D)), rng.normal(size=(B, H, N, D)), rng.normal(size=(B, H, N, Dv or D))
+
+
+@pytest.mark.parametrize("iters", [1, 2, 3])
+def test_vmonarch_single_frame_is_exact_attention(iters):
+    q, k, v = _qkv(3, 1, 2, 24, 8)
+    z = vmonarch_attention(q, k, v, 1, 24, iters)
+    np.testing.assert_allclose(z, exact_attention(q, k, v), atol=1e-12)
+
+
+@pytest.mark.parametrize("iters", [1, 2, 3])
+def test_vmonarch_single_token_frames_is_exact_attention(iters):
+    q, k, v = _qkv(4, 1, 2, 10, 8, 6)
+    z = vmonarch_attention(q, k, v, 10, 1, iters)
+    np.testing.assert_allclose(z, exact_attention(q, k, v), atol=1e-12)
+
+
+def test_vmonarch_full_recompute_is_exact_attention():
+    q, k, v = _qkv(5, 1, 1, 4 * 6, 8)
+    z = vmonarch_attention(q, k, v, 4, 6, 2, recompute_tokens=24)
+    np.testing.assert_allclose(z, exact_attention(q, k, v), atol=1e-12)
+    z2 = vmonarch_attention(q, k, v, 4, 6, 2, recompute_tokens=6)
+    np.testing.assert_allclose(z2[:, :, :6], exact_attention(q[:, :, :6], k, v), atol=1e-12)
+
+
+def test_vmonarch_permutation_equivariant_within_frames():
+    m, b = 3, 7
+    q, k, v = _qkv(6, 1, 1, m * b, 8)
+    perm = np.random.default_rng(9).permutation(b)
+    full = (np.arange(m)[:, None] * b + perm[None, :]).reshape(-1)
+    z = vmonarch_attention(q, k, v, m, b, 2, recompute_tokens=b)
+    zp = vmonarch_attention(q[:, :, full], k[:, :, full], v[:, :, full], m, b, 2, recompute_tokens=b)
+    np.testing.assert_allclose(zp, z[:, :, full], atol=1e-12)
+
+
+def test_vmonarch_linear_in_v():
+    q, k, v = _qkv(7, 1, 1, 4 * 5, 8)
+    v2 = np.random.default_rng(8).normal(size=v.shape)
+    za = vmonarch_attention(q, k, 2.0 * v - 3.0 * v2, 4, 5, 2, recompute_tokens=5)
+    zb = 2.0 * vmonarch_attention(q, k, v, 4, 5, 2, recompute_tokens=5) - 3.0 * vmonarch_attention(q, k, v2, 4, 5, 2, recompute_tokens=5)
+    np.testing.assert_allclose(za, zb, atol=1e-10)
+
+
+def test_vmonarch_rejects_bad_shape_and_zero_iters():
+    q, k, v = _qkv(8, 1, 1, 12, 4)
+    with pytest.raises(AssertionError):
+        vmonarch_attention(q, k, v, 5, 3)
+    with pytest.raises(UnboundLocalError):
+        vmonarch_attention(q, k, v, 4, 3, 0)

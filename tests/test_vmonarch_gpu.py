@@ -1,0 +1,132 @@
+"""GPU parity of VMonarch attention (fused HIP path: R-step flash-entropy kernel, fused L-step,
+split-KV recompute) against the CPU oracle and the reference's own golden outputs.
+
+Mirrors tests/test_vmonarch.py:45-74 of the reference ((m, b) in {(4, 256), (8, 100)}, num_iters in
+{1, 2, 3}, B=1, H=2, D=64, recompute_tokens=b; recompute exactness) plus BASELINE cfg3 and cfg4.
+Tolerance: reference metric max|z - ref| <= 3e-2 * max|ref| (tests/test_vmonarch.py:64) AND
+elementwise |z - ref| <= 2e-2 + 1e-2 |ref|.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close_elementwise, assert_close_ref, golden_names, hip_library_loaded, load_golden, randn_lp
+from oracle import exact_attention, vmonarch_attention as vmonarch_oracle
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _check(z, z_ref, tol=3e-2):
+    z = z.float().cpu().numpy()
+    assert np.isfinite(z).all()
+    assert_close_ref(z, z_ref, tol)
+    assert_close_elementwise(z, z_ref)
+
+
+@pytest.mark.parametrize("name", golden_names("vmonarch_"))
+def test_vmonarch_matches_reference_golden(name):
+    from vmonarch_amd import vmonarch_attention
+    g = load_golden(name)
+    q, k, v = (torch.from_numpy(g[x]).to(torch.bfloat16).to(DEV) for x in "qkv")
+    with torch.no_grad():
+        z = vmonarch_attention(q, k, v, int(g["num_blocks"]), int(g["block_size"]), int(g["num_iters"]),
+                               recompute_tokens=int(g["recompute_tokens"]))
+    _check(z, g["z"])
+    assert hip_library_loaded()
+
+
+@pytest.mark.parametrize("m, b", [(4, 256), (8, 100)])
+@pytest.mark.parametrize("num_iters", [1, 2, 3])
+def test_vmonarch_reference_params(m, b, num_iters):
+    from vmonarch_amd import vmonarch_attention
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (randn_lp(g, 1, 2, m * b, 64) for _ in range(3))
+    z = vmonarch_attention(q.to(DEV), k.to(DEV), v.to(DEV), m, b, num_iters, recompute_tokens=b)
+    z_ref = vmonarch_oracle(q.float().numpy(), k.float().numpy(), v.float().numpy(), m, b, num_iters, b)
+    _check(z, z_ref)
+
+
+def test_vmonarch_cfg3():
+    """BASELINE cfg3: VMonarchAttention(16, 256, 2), rt=256, B=2, H=4, N=4096, D=128, bf16."""
+    from vmonarch_amd import VMonarchAttention
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (randn_lp(g, 2, 4, 4096, 128) for _ in range(3))
+    z = VMonarchAttention(16, 256, 2)(q.to(DEV), k.to(DEV), v.to(DEV), recompute_tokens=256)
+    z_ref = vmonarch_oracle(q.float().numpy(), k.float().numpy(), v.float().numpy(), 16, 256, 2, 256)
+    _check(z, z_ref)
+
+
+def test_vmonarch_cfg4_north_star_head_sample():
+    """BASELINE cfg4 (north star): 21 frames x 1560 tokens, B=1, H=12, D=128, q,k ~ 0.5 N(0,1),
+    v ~ N(0,1), num_iters=2, rt=1560.  The whole problem runs on the GPU; heads 0 and 11 are checked
+    against the oracle (heads are independent end to end)."""
+    from vmonarch_amd import VMonarchAttention
+    g = torch.Generator().manual_seed(0)
+    q = randn_lp(g, 1, 12, 32760, 128, scale=0.5)
+    k = randn_lp(g, 1, 12, 32760, 128, scale=0.5)
+    v = randn_lp(g, 1, 12, 32760, 128)
+    z = VMonarchAttention(21, 1560, 2)(q.to(DEV), k.to(DEV), v.to(DEV), recompute_tokens=1560)
+    assert z.shape == (1, 12, 32760, 128)
+    for h in (0, 11):
+        sl = slice(h, h + 1)
+        z_ref = vmonarch_oracle(q[:, sl].float().numpy(), k[:, sl].float().numpy(), v[:, sl].float().numpy(),
+                                21, 1560, 2, 1560, dtype=np.float32)
+        _check(z[:, sl], z_ref)
+
+
+def test_recompute_tokens_are_exact():
+    """Reference tests/test_vmonarch.py:69-74: the first rows equal exact attention.
+
+    The reference compares torch SDPA with itself; here the recompute is our flash kernel, which
+    rounds P to bf16 before P.V as flash attention does, so the stated tolerance is bf16's default
+    rtol (1.6e-2) with atol 2e-3 (P rounding: 2^-9 relative per weight)."""
+    from vmonarch_amd import vmonarch_attention
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (randn_lp(g, 1, 2, 4 * 128, 64).to(DEV) for _ in range(3))
+    z = vmonarch_attention(q, k, v, 4, 128, recompute_tokens=128)
+    exact = torch.nn.functional.scaled_dot_product_attention(q.float(), k.float(), v.float()).to(q.dtype)
+    torch.testing.assert_close(z[:, :, :128], exact[:, :, :128], atol=2e-3, rtol=1.6e-2)
+    ref = exact_attention(*(t.float().cpu().numpy() for t in (q[:, :, :128], k, v)))
+    assert_close_elementwise(z[:, :, :128].float().cpu().numpy(), ref)
+
+
+def test_vmonarch_single_frame_and_single_token_reduce_to_exact_attention():
+    from vmonarch_amd import vmonarch_attention
+    g = torch.Generator().manual_seed(9)
+    q, k, v = (randn_lp(g, 1, 2, 96, 64) for _ in range(3))
+    ref = exact_attention(q.float().numpy(), k.float().numpy(), v.float().numpy())
+    z = vmonarch_attention(q.to(DEV), k.to(DEV), v.to(DEV), 1, 96, 2)
+    _check(z, ref)
+    q, k, v = (randn_lp(g, 1, 2, 24, 64) for _ in range(3))
+    z = vmonarch_attention(q.to(DEV), k.to(DEV), v.to(DEV), 24, 1, 2)
+    _check(z, exact_attention(q.float().numpy(), k.float().numpy(), v.float().numpy()))
+
+
+def test_vmonarch_fused_matches_composed_path(monkeypatch):
+    """The fused path and the reference-structured composed path (taken when the R-step seam is
+    replaced, as tests/test_vmonarch.py:59 does) agree."""
+    import vmonarch_amd.vmonarch as vm
+    from vmonarch_amd import vmonarch_attention
+    g = torch.Generator().manual_seed(10)
+    q, k, v = (randn_lp(g, 2, 2, 6 * 80, 128).to(DEV) for _ in range(3))
+    z_fused = vmonarch_attention(q, k, v, 6, 80, 3, recompute_tokens=80)
+    orig = vm._row_block_attention
+    monkeypatch.setattr(vm, "_row_block_attention", lambda x, kk, w: orig(x, kk, w))
+    z_comp = vmonarch_attention(q, k, v, 6, 80, 3, recompute_tokens=80)
+    assert_close_ref(z_fused.float().cpu().numpy(), z_comp.float().cpu().numpy(), 3e-2)
+
+
+def test_alias_package_is_the_implementation(monkeypatch):
+    import video_monarch_attention as vma
+    import video_monarch_attention.vmonarch as vm_alias
+    import vmonarch_amd.vmonarch as vm
+    assert vm_alias is vm
+    assert vma.VMonarchAttention is vm.VMonarchAttention
+
+
+def test_vmonarch_rejects_bad_shape():
+    from vmonarch_amd import vmonarch_attention
+    q = torch.zeros(1, 1, 12, 64, device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError):
+        vmonarch_attention(q, q, q, 5, 3)

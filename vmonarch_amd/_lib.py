@@ -1,0 +1,111 @@
+"""ctypes binding of libvmonarch_gfx950.so (the C ABI declared in include/vmonarch_amd.h).
+
+torch is imported before the library is loaded so that the process has one HIP runtime:
+the library asks for libamdhip64.so.7 by soname and the dynamic loader hands it the copy torch
+already mapped.  There is no fallback: if the library is missing or does not load, every call
+raises.
+"""
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libvmonarch_gfx950.so")
+ABI_VERSION = 1
+DTYPES = {torch.bfloat16: 0, torch.float16: 1}
+
+c_int32, c_int64, c_float, c_void_p, c_size_t = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
+
+
+class View(ctypes.Structure):
+    _fields_ = [("data", c_void_p), ("stride_b", c_int64), ("stride_h", c_int64), ("stride_n", c_int64)]
+
+
+class FeaFwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", c_int32), ("batch", c_int32), ("heads", c_int32), ("frames", c_int32),
+        ("nq", c_int32), ("nk", c_int32), ("d", c_int32), ("dw0", c_int32), ("dw1", c_int32),
+        ("q", View), ("k", View), ("w0", View), ("w1", View), ("o", View),
+        ("lse", c_void_p), ("ent", c_void_p), ("stat_stride_b", c_int64), ("stat_stride_h", c_int64),
+        ("sm_scale", c_float), ("num_splits", c_int32), ("workspace", c_void_p), ("workspace_bytes", c_size_t),
+    ]
+
+
+class FeaBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", c_int32), ("batch", c_int32), ("heads", c_int32),
+        ("nq", c_int32), ("nk", c_int32), ("d", c_int32), ("dv", c_int32),
+        ("q", View), ("k", View), ("v", View), ("o", View), ("do", View),
+        ("dq", View), ("dk", View), ("dv_", View),
+        ("lse", c_void_p), ("ent", c_void_p), ("dent", c_void_p),
+        ("stat_stride_b", c_int64), ("stat_stride_h", c_int64),
+        ("dent_stride_b", c_int64), ("dent_stride_h", c_int64),
+        ("sm_scale", c_float), ("workspace", c_void_p), ("workspace_bytes", c_size_t),
+    ]
+
+
+class LstepArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", c_int32), ("batch", c_int32), ("heads", c_int32), ("num_blocks", c_int32),
+        ("block_size", c_int32), ("d", c_int32), ("dv", c_int32), ("last", c_int32), ("skip_tokens", c_int32),
+        ("q", View), ("out", View), ("ent", c_void_p), ("ent_stride_b", c_int64), ("ent_stride_h", c_int64),
+        ("res", View), ("scale", c_float), ("min_col_mass", c_float),
+    ]
+
+
+_lock = threading.Lock()
+_lib = None
+
+
+def lib():
+    """The loaded library (loaded once; raises if it is missing or from another ABI)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"vmonarch_amd: {LIB_PATH} is not built (run `python -m vmonarch_amd.build`)")
+        L = ctypes.CDLL(LIB_PATH)
+        L.vmo_abi_version.restype = ctypes.c_int
+        L.vmo_last_error.restype = ctypes.c_char_p
+        L.vmo_fea_fwd_workspace_size.restype = c_size_t
+        L.vmo_fea_fwd_workspace_size.argtypes = [ctypes.POINTER(FeaFwdArgs)]
+        L.vmo_fea_fwd.restype = ctypes.c_int
+        L.vmo_fea_fwd.argtypes = [ctypes.POINTER(FeaFwdArgs), c_void_p]
+        L.vmo_lstep_fwd.restype = ctypes.c_int
+        L.vmo_lstep_fwd.argtypes = [ctypes.POINTER(LstepArgs), c_void_p]
+        if hasattr(L, "vmo_fea_bwd"):
+            L.vmo_fea_bwd_workspace_size.restype = c_size_t
+            L.vmo_fea_bwd_workspace_size.argtypes = [ctypes.POINTER(FeaBwdArgs)]
+            L.vmo_fea_bwd.restype = ctypes.c_int
+            L.vmo_fea_bwd.argtypes = [ctypes.POINTER(FeaBwdArgs), c_void_p]
+        v = L.vmo_abi_version()
+        if v != ABI_VERSION:
+            raise RuntimeError(f"vmonarch_amd: library ABI {v}, bindings expect {ABI_VERSION}")
+        _lib = L
+        return L
+
+
+def check(rc, what):
+    if rc != 0:
+        msg = lib().vmo_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (code {rc}): {msg}")
+
+
+def view(t):
+    """(B, H, N, F) tensor -> View (element strides, feature dim contiguous)."""
+    assert t.dim() == 4 and t.stride(3) == 1, "feature dimension must be contiguous"
+    return View(t.data_ptr(), t.stride(0), t.stride(1), t.stride(2))
+
+
+def row_aligned(t):
+    """t itself when its rows are 16-byte aligned with a contiguous feature dim, else a contiguous copy."""
+    ok = (t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all(s % 8 == 0 for s in t.stride()[:-1]))
+    return t if ok else t.contiguous()
+
+
+def stream_of(t):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)

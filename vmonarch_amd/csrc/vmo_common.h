@@ -1,0 +1,93 @@
+// Shared gfx950 device helpers for the VMonarch kernels.
+//
+// Register layouts used throughout (v_mfma_f32_32x32x16_{bf16,f16}, wave64, l = lane):
+//   A (32 x 16): lane l holds A[l % 32][8 * (l / 32) + e], e = 0..7
+//   B (16 x 32): lane l holds B[8 * (l / 32) + e][l % 32]
+//   C (32 x 32): lane l holds C[8 * (r / 4) + 4 * (l / 32) + r % 4][l % 32], r = 0..15
+// ds_read_tr16_b64: within each 16-lane group, lane i supplies the address of 4 consecutive
+// 16-bit elements; lanes 4t..4t+3 together cover row t (16 elements).  Lane i receives
+// element i of rows 0..3, i.e. a column of the 4 x 16 block.
+// Both were confirmed on an MI355X by a probe of the builtins' lane layouts.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vmo {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+#define VMO_LDS __attribute__((address_space(3)))
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// Element-type traits: storage type, 8-wide MFMA operand vector and the MFMA itself.
+template <bool F16> struct Elem;
+template <> struct Elem<false> {
+  using T = __bf16;
+  using V8 = bf16x8;
+  using V4 = bf16x4;
+  __device__ static inline f32x16 mfma(V8 a, V8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct Elem<true> {
+  using T = _Float16;
+  using V8 = f16x8;
+  using V4 = f16x4;
+  __device__ static inline f32x16 mfma(V8 a, V8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// 16-byte chunk swizzle of LDS tiles whose rows are >= 8 chunks wide: chunk c of row r is
+// stored at chunk c ^ swz(r).  Eight consecutive rows map one logical chunk to eight distinct
+// bank groups (row-wise ds_read_b128 of an MFMA A operand), and a 4-row x 2-chunk block (one
+// 16-lane group of ds_read_tr16_b64) also lands on eight distinct bank groups.
+__device__ __forceinline__ int swz(int row) { return ((row & 3) << 1) | ((row >> 2) & 1); }
+
+__device__ __forceinline__ float wave_max32(float x) {
+  // combine lane l with lane l ^ 32
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float wave_sum32(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+// 16-byte global -> LDS copy without a register round trip.  The LDS destination of lane l is
+// lds_wave_base + 16 * l (lds_wave_base must be wave-uniform).
+__device__ __forceinline__ void g2l_16(const void* g, VMO_LDS void* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(g, lds_wave_base, 16, 0, 0);
+}
+
+template <class V8>
+__device__ __forceinline__ V8 lds_read8(const VMO_LDS char* p) {
+  return *reinterpret_cast<const VMO_LDS V8*>(p);
+}
+
+// Two transposed 4-element reads concatenated into one 8-element MFMA operand.
+template <class V8>
+__device__ __forceinline__ V8 lds_read_tr8(const VMO_LDS char* p0, const VMO_LDS char* p1) {
+  i16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VMO_LDS i16x4*)p0);
+  i16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VMO_LDS i16x4*)p1);
+  typedef short i16x8 __attribute__((ext_vector_type(8)));
+  i16x8 c = __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(V8, c);
+}
+
+template <class T>
+__device__ __forceinline__ T to_elem(float x) { return static_cast<T>(x); }
+
+}  // namespace vmo

@@ -1,0 +1,171 @@
+"""
+VMonarch attention (drop-in for video_monarch_attention/vmonarch.py of the reference).
+
+The N = m * b tokens are laid out on an (m, b) grid, token n -> (n // b, n % b).  The attention
+map is approximated by a Monarch matrix built from
+  - R: m dense (b x b) blocks, mixing tokens inside each grid row (a batched flash-entropy
+    attention, the R-step);
+  - L: b dense (m x m) blocks, mixing tokens inside each grid column (the L-step);
+fitted by a few steps of alternating minimisation (reference: vmonarch.py:1-11, :29-69).
+
+Two execution paths with identical results (within bf16 tolerance):
+  * fused (default, forward only): every step is a gfx950 HIP kernel -- the R-step reads the
+    (B, H, m*b, D) tensors in place as m frames per head (no flatten copy, no torch.cat of
+    [k | v]), the L-step is one fused kernel per iteration, and the recompute of the first
+    tokens is a split-KV flash kernel writing straight into z;
+  * composed: the reference's structure step by step (R-step through the
+    `_row_block_attention` seam, L-step as torch tensor ops), used when autograd needs the graph
+    or when a caller replaced `_row_block_attention` (tests/test_vmonarch.py:59 does).
+"""
+import torch
+import torch.nn as nn
+
+from . import _lib
+from .kernel import fea_forward, flash_entropy_attention
+
+# number of CUs on an MI355X; the recompute picks its split-KV count to fill them
+_NUM_CUS = 256
+
+
+def _row_block_attention(x, k, w):
+    """Attention inside every grid row (reference vmonarch.py:19-26).
+
+    x, k: (B, H, m, b, D); w: (B, H, m, b, Dw).
+    Returns softmax(x k^T) w and sum_j P_ij log P_ij (= -entropy) for every row of P.
+    """
+    out, ent = flash_entropy_attention(*(t.flatten(1, 2) for t in (x, k, w)), sm_scale=1.0)
+    return out.view(*w.shape[:-1], -1), -ent.view(x.shape[:-1]).detach()
+
+
+_ROW_BLOCK_ATTENTION = _row_block_attention   # the seam as shipped; patched seams use the composed path
+
+
+def _recompute_splits(problems, nq, nk):
+    q_tiles = (nq + 127) // 128
+    base = problems * q_tiles
+    splits = 1
+    while base * splits < 4 * _NUM_CUS and splits < 16 and nk // (splits * 2) >= 512:
+        splits *= 2
+    return splits
+
+
+def _lstep_launch(q, out, ent, res, m, b, scale, last, skip, min_col_mass):
+    L = _lib.lib()
+    B, H, N, D = q.shape
+    a = _lib.LstepArgs()
+    a.dtype = _lib.DTYPES[q.dtype]
+    a.batch, a.heads, a.num_blocks, a.block_size = B, H, m, b
+    a.d = D
+    a.dv = out.shape[-1] - D if last else 0
+    a.last, a.skip_tokens = int(last), int(skip)
+    a.q, a.out, a.res = _lib.view(q), _lib.view(out), _lib.view(res)
+    a.ent = ent.data_ptr()
+    a.ent_stride_b, a.ent_stride_h = ent.stride(0), ent.stride(1)
+    a.scale, a.min_col_mass = float(scale), float(min_col_mass)
+    _lib.check(L.vmo_lstep_fwd(a, _lib.stream_of(q)), "vmo_lstep_fwd")
+
+
+def _fused_supported(q, k, v, num_blocks):
+    D, Dv = q.shape[-1], v.shape[-1]
+    return (q.is_cuda and q.dtype in _lib.DTYPES and k.dtype == q.dtype and v.dtype == q.dtype
+            and D in (64, 128) and Dv in (64, 128) and num_blocks <= 32
+            and k.shape == q.shape and v.shape[:-1] == q.shape[:-1])
+
+
+def _vmonarch_fused(q, k, v, m, b, num_iters, recompute_tokens, min_col_mass):
+    B, H, N, D = q.shape
+    Dv = v.shape[-1]
+    scale = D ** -0.5
+    q, k, v = (_lib.row_aligned(t) for t in (q, k, v))
+    dev, dt = q.device, q.dtype
+    ent = torch.empty((B, H, N), device=dev, dtype=torch.float32)
+    z = torch.empty((B, H, N, Dv), device=dev, dtype=dt)
+    rt = min(int(recompute_tokens), N)
+    u = None
+    for it in range(num_iters):
+        last = it == num_iters - 1
+        # R-step (vmonarch.py:50): iteration 0 folds u = q * scale into the softmax scale
+        x, s = (q, scale) if it == 0 else (u, 1.0)
+        out, _, _ = fea_forward(x, k, k, v if last else None, s, frames=m, ent=ent, want_lse=False)
+        # L-step (vmonarch.py:51-63)
+        if last:
+            _lstep_launch(q, out, ent, z, m, b, scale, True, rt, min_col_mass)
+        else:
+            if u is None:
+                u = torch.empty((B, H, N, D), device=dev, dtype=dt)
+            _lstep_launch(q, out, ent, u, m, b, scale, False, 0, min_col_mass)
+    if rt > 0:   # exact attention for the first rt queries (vmonarch.py:66-68), written into z
+        splits = _recompute_splits(B * H, rt, N)
+        fea_forward(q[:, :, :rt], k, v, None, scale, o=z[:, :, :rt], want_ent=False, want_lse=False,
+                    num_splits=splits)
+    return z
+
+
+def _vmonarch_composed(q, k, v, num_blocks, block_size, num_iters, recompute_tokens, min_col_mass):
+    """Step-by-step restatement of vmonarch.py:41-69 on GPU tensors (autograd-capable)."""
+    B, H, N, D = q.shape
+    scale = D ** -0.5
+    qg, kg, vg = (t.unflatten(2, (num_blocks, block_size)) for t in (q, k, v))
+    u = qg * scale
+    z = None
+    for it in range(num_iters):
+        last = it == num_iters - 1
+        out, neg_ent = _row_block_attention(u, kg, torch.cat([kg, vg], -1) if last else kg)
+        kr = out[..., :D] * scale
+        logits = torch.einsum("bhijd,bhkjd->bhjik", qg, kr).float()
+        attn = (logits - neg_ent.transpose(-1, -2).unsqueeze(-2)).softmax(-1)
+        if last:
+            y = out[..., D:]
+            z = torch.einsum("bhjik,bhkjd->bhijd", attn.to(y.dtype), y)
+        else:
+            col_mass = attn.sum(-2).transpose(-1, -2).clamp_min(min_col_mass)
+            u = torch.einsum("bhjik,bhijd->bhkjd", attn.to(q.dtype), qg)
+            u = u * (scale / col_mass.unsqueeze(-1)).to(q.dtype)
+    z = z.reshape(B, H, N, -1)
+    if recompute_tokens > 0:
+        exact = torch.nn.functional.scaled_dot_product_attention(q[:, :, :recompute_tokens], k, v)
+        z = torch.cat([exact, z[:, :, recompute_tokens:]], dim=2)
+    return z
+
+
+def vmonarch_attention(q, k, v, num_blocks, block_size, num_iters=2, recompute_tokens=0, min_col_mass=0.01):
+    """
+    Args:
+        q, k: (B, H, N, D); v: (B, H, N, Dv), with N == num_blocks * block_size.
+        num_blocks: m, number of grid rows (keep it small).
+        block_size: b, number of tokens per grid row.
+        num_iters: alternating-minimization steps.
+        recompute_tokens: the first `recompute_tokens` queries use exact attention.
+        min_col_mass: lower bound of the column mass of L, for stability.
+    Returns:
+        (B, H, N, Dv)
+    """
+    B, H, N, D = q.shape
+    assert N == num_blocks * block_size, f"N={N} != {num_blocks} * {block_size}"
+    if num_iters < 1:
+        raise UnboundLocalError("local variable 'z' referenced before assignment")  # as the reference (vmonarch.py:65)
+    needs_graph = torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v))
+    if (not needs_graph and _row_block_attention is _ROW_BLOCK_ATTENTION
+            and _fused_supported(q, k, v, num_blocks)):
+        return _vmonarch_fused(q, k, v, num_blocks, block_size, num_iters, recompute_tokens, min_col_mass)
+    if not q.is_cuda:
+        raise RuntimeError("vmonarch_amd: vmonarch_attention needs GPU tensors (no CPU path)")
+    return _vmonarch_composed(q, k, v, num_blocks, block_size, num_iters, recompute_tokens, min_col_mass)
+
+
+class VMonarchAttention(nn.Module):
+    """Module wrapper (reference vmonarch.py:72-85); holds no parameters."""
+
+    def __init__(self, num_blocks, block_size, num_iters=2, min_col_mass=0.01):
+        super().__init__()
+        self.num_blocks = num_blocks
+        self.block_size = block_size
+        self.num_iters = num_iters
+        self.min_col_mass = min_col_mass
+
+    def forward(self, q, k, v, recompute_tokens=0):
+        return vmonarch_attention(q, k, v, self.num_blocks, self.block_size, self.num_iters,
+                                  recompute_tokens, self.min_col_mass)
+
+    def extra_repr(self):
+        return f"num_blocks={self.num_blocks}, block_size={self.block_size}, num_iters={self.num_iters}"
