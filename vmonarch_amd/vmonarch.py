@@ -72,7 +72,10 @@ def _fused_supported(q, k, v, num_blocks):
             and k.shape == q.shape and v.shape[:-1] == q.shape[:-1])
 
 
-def _vmonarch_fused(q, k, v, m, b, num_iters, recompute_tokens, min_col_mass):
+def _vmonarch_fused(q, k, v, m, b, num_iters, recompute_tokens, min_col_mass, stage_hook=None):
+    """All-HIP forward.  `stage_hook(name)`, when given, is called on the host right after each
+    launch ("rstep0", "lstep0", ..., "recompute") -- used by bench.py to bracket every kernel with
+    events on the launch stream."""
     B, H, N, D = q.shape
     Dv = v.shape[-1]
     scale = D ** -0.5
@@ -87,6 +90,8 @@ def _vmonarch_fused(q, k, v, m, b, num_iters, recompute_tokens, min_col_mass):
         # R-step (vmonarch.py:50): iteration 0 folds u = q * scale into the softmax scale
         x, s = (q, scale) if it == 0 else (u, 1.0)
         out, _, _ = fea_forward(x, k, k, v if last else None, s, frames=m, ent=ent, want_lse=False)
+        if stage_hook:
+            stage_hook(f"rstep{it}")
         # L-step (vmonarch.py:51-63)
         if last:
             _lstep_launch(q, out, ent, z, m, b, scale, True, rt, min_col_mass)
@@ -94,10 +99,14 @@ def _vmonarch_fused(q, k, v, m, b, num_iters, recompute_tokens, min_col_mass):
             if u is None:
                 u = torch.empty((B, H, N, D), device=dev, dtype=dt)
             _lstep_launch(q, out, ent, u, m, b, scale, False, 0, min_col_mass)
+        if stage_hook:
+            stage_hook(f"lstep{it}")
     if rt > 0:   # exact attention for the first rt queries (vmonarch.py:66-68), written into z
         splits = _recompute_splits(B * H, rt, N)
         fea_forward(q[:, :, :rt], k, v, None, scale, o=z[:, :, :rt], want_ent=False, want_lse=False,
                     num_splits=splits)
+        if stage_hook:
+            stage_hook("recompute")
     return z
 
 
