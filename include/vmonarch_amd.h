@@ -113,6 +113,35 @@ typedef struct vmo_lstep_args {
   float min_col_mass;
 } vmo_lstep_args;
 
+/*
+ * FlashEntropyAttention backward.
+ *
+ * Replaces the two launches of _FlashEntropyAttention.backward (kernel.py:360-381:
+ * _attn_bwd_preprocess :154-162 and _attn_bwd :251-313).  For the loss L with upstream grads
+ * grad_o = dL/do and grad_ent = dL/dent, writes grad_q, grad_k, grad_v (same dtype as q):
+ *   dS = P (dP - delta) + grad_ent P (-ent - ln P),  dP = grad_o v^T,  delta = rowsum(o * grad_o)
+ *   grad_q = sm_scale dS k,  grad_k = sm_scale dS^T q,  grad_v = P^T grad_o
+ * with P rebuilt from `lse` (log2 units, as written by vmo_fea_fwd).  nq queries attend to nk
+ * keys per (batch, head) (nq != nk allowed).  Supported: d in {64, 128}, dv in {64, 128, 256}.  Needs
+ * vmo_fea_bwd_workspace_size() bytes of workspace.
+ */
+typedef struct vmo_fea_bwd_args {
+  int32_t dtype;
+  int32_t batch, heads;
+  int32_t nq, nk;
+  int32_t d, dv;
+  vmo_view q, k, v, o, grad_o;
+  vmo_view grad_q, grad_k, grad_v;
+  const float* lse;                /* (batch, heads, nq), token stride 1 */
+  const float* ent;                /* same layout as lse */
+  const float* grad_ent;           /* (batch, heads, nq), token stride 1 */
+  int64_t stat_stride_b, stat_stride_h;
+  int64_t grad_ent_stride_b, grad_ent_stride_h;
+  float sm_scale;
+  void* workspace;
+  size_t workspace_bytes;
+} vmo_fea_bwd_args;
+
 /* ABI version of the loaded library (VMO_ABI_VERSION at build time). */
 int vmo_abi_version(void);
 
@@ -124,6 +153,12 @@ size_t vmo_fea_fwd_workspace_size(const vmo_fea_fwd_args* args);
 
 /* FlashEntropyAttention forward; see vmo_fea_fwd_args. */
 int vmo_fea_fwd(const vmo_fea_fwd_args* args, void* stream);
+
+/* Bytes of workspace vmo_fea_bwd needs for these arguments. */
+size_t vmo_fea_bwd_workspace_size(const vmo_fea_bwd_args* args);
+
+/* FlashEntropyAttention backward; see vmo_fea_bwd_args. */
+int vmo_fea_bwd(const vmo_fea_bwd_args* args, void* stream);
 
 /* Fused L-step; see vmo_lstep_args. */
 int vmo_lstep_fwd(const vmo_lstep_args* args, void* stream);

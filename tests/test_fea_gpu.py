@@ -152,3 +152,76 @@ def test_fea_forward_is_deterministic():
     o1, e1 = flash_entropy_attention(q, k, v)
     o2, e2 = flash_entropy_attention(q, k, v)
     assert torch.equal(o1, o2) and torch.equal(e1, e2)
+
+
+# ----------------------------------------------------------------------------------- backward
+def _grads(q, k, v, do, de, sm_scale=None):
+    from vmonarch_amd import flash_entropy_attention
+    qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    o, e = flash_entropy_attention(qd, kd, vd, sm_scale)
+    loss = (o.float() * do.to(DEV)).sum() + (e * de.to(DEV)).sum()   # tests/test_vmonarch.py:35
+    return torch.autograd.grad(loss, (qd, kd, vd))
+
+
+def _check_grads(grads, refs, tol=3e-2):
+    for g, r, name in zip(grads, refs, ("dq", "dk", "dv")):
+        g = g.float().cpu().numpy()
+        assert np.isfinite(g).all(), name
+        assert_close_ref(g, r, tol)
+
+
+@pytest.mark.parametrize("N", [128, 200, 1024])
+@pytest.mark.parametrize("D, Dv", [(64, 64), (128, 128), (64, 128), (128, 256)])
+def test_fea_backward_reference_params(N, D, Dv):
+    """tests/test_vmonarch.py:27-42: loss = sum(o * do) + sum(e * de); grads within 3e-2."""
+    from oracle import entropy_attention_grad
+    g = torch.Generator().manual_seed(0)
+    q, k, v = randn_lp(g, 2, 3, N, D), randn_lp(g, 2, 3, N, D), randn_lp(g, 2, 3, N, Dv)
+    do, de = torch.randn(2, 3, N, Dv, generator=g), torch.randn(2, 3, N, generator=g)
+    grads = _grads(q, k, v, do, de)
+    # the bf16 output o receives do rounded to bf16 (the .float() of the loss casts its grad back)
+    refs = entropy_attention_grad(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                  do.bfloat16().float().numpy(), de.numpy(), D ** -0.5)
+    _check_grads(grads, refs)
+
+
+def test_fea_backward_entropy_term_only():
+    """do = 0: the gradient is the entropy term alone (dS = dE P (-E - ln P))."""
+    from oracle import entropy_attention_grad
+    g = torch.Generator().manual_seed(11)
+    q, k, v = (randn_lp(g, 1, 2, 300, 64) for _ in range(3))
+    do, de = torch.zeros(1, 2, 300, 64), torch.randn(1, 2, 300, generator=g)
+    grads = _grads(q, k, v, do, de)
+    refs = entropy_attention_grad(q.float().numpy(), k.float().numpy(), v.float().numpy(), do.numpy(), de.numpy(), 0.125)
+    _check_grads(grads[:2], refs[:2])
+    assert float(grads[2].abs().max()) == 0.0
+
+
+def test_fea_backward_padding_rows_get_zero_grad():
+    from vmonarch_amd.kernel import _FlashEntropyAttention
+    from oracle import entropy_attention_grad
+    g = torch.Generator().manual_seed(12)
+    q, k, v = (randn_lp(g, 1, 1, 256, 64).to(DEV).requires_grad_() for _ in range(3))
+    o, e = _FlashEntropyAttention.apply(q, k, v, 0.125, 200, True)
+    do, de = torch.randn(1, 1, 256, 64, generator=g), torch.randn(1, 1, 256, generator=g)
+    dq, dk, dv = torch.autograd.grad((o.float() * do.to(DEV)).sum() + (e * de.to(DEV)).sum(), (q, k, v))
+    for t in (dq, dk, dv):
+        assert (t[:, :, 200:] == 0).all()
+    refs = entropy_attention_grad(*(t.detach().float().cpu().numpy()[:, :, :200] for t in (q, k, v)),
+                                  do.bfloat16().float().numpy()[:, :, :200], de.numpy()[:, :, :200], 0.125)
+    _check_grads([t[:, :, :200] for t in (dq, dk, dv)], refs)
+
+
+def test_fea_backward_cfg5_head_sample():
+    """BASELINE cfg5: B=1, H=24, N=16384, D=128 fwd+bwd on the GPU; heads 0 and 23 against the oracle."""
+    from oracle import entropy_attention_grad
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (randn_lp(g, 1, 24, 16384, 128) for _ in range(3))
+    do, de = torch.randn(1, 24, 16384, 128, generator=g), torch.randn(1, 24, 16384, generator=g)
+    grads = _grads(q, k, v, do, de)
+    for h in (0, 23):
+        sl = slice(h, h + 1)
+        refs = entropy_attention_grad(q[:, sl].float().numpy(), k[:, sl].float().numpy(), v[:, sl].float().numpy(),
+                                      do[:, sl].bfloat16().float().numpy(), de[:, sl].numpy(), 128 ** -0.5,
+                                      dtype=np.float32)
+        _check_grads([t[:, sl] for t in grads], refs)

@@ -36,11 +36,11 @@ class FeaBwdArgs(ctypes.Structure):
     _fields_ = [
         ("dtype", c_int32), ("batch", c_int32), ("heads", c_int32),
         ("nq", c_int32), ("nk", c_int32), ("d", c_int32), ("dv", c_int32),
-        ("q", View), ("k", View), ("v", View), ("o", View), ("do", View),
-        ("dq", View), ("dk", View), ("dv_", View),
-        ("lse", c_void_p), ("ent", c_void_p), ("dent", c_void_p),
+        ("q", View), ("k", View), ("v", View), ("o", View), ("grad_o", View),
+        ("grad_q", View), ("grad_k", View), ("grad_v", View),
+        ("lse", c_void_p), ("ent", c_void_p), ("grad_ent", c_void_p),
         ("stat_stride_b", c_int64), ("stat_stride_h", c_int64),
-        ("dent_stride_b", c_int64), ("dent_stride_h", c_int64),
+        ("grad_ent_stride_b", c_int64), ("grad_ent_stride_h", c_int64),
         ("sm_scale", c_float), ("workspace", c_void_p), ("workspace_bytes", c_size_t),
     ]
 
@@ -77,11 +77,10 @@ def lib():
         L.vmo_fea_fwd.argtypes = [ctypes.POINTER(FeaFwdArgs), c_void_p]
         L.vmo_lstep_fwd.restype = ctypes.c_int
         L.vmo_lstep_fwd.argtypes = [ctypes.POINTER(LstepArgs), c_void_p]
-        if hasattr(L, "vmo_fea_bwd"):
-            L.vmo_fea_bwd_workspace_size.restype = c_size_t
-            L.vmo_fea_bwd_workspace_size.argtypes = [ctypes.POINTER(FeaBwdArgs)]
-            L.vmo_fea_bwd.restype = ctypes.c_int
-            L.vmo_fea_bwd.argtypes = [ctypes.POINTER(FeaBwdArgs), c_void_p]
+        L.vmo_fea_bwd_workspace_size.restype = c_size_t
+        L.vmo_fea_bwd_workspace_size.argtypes = [ctypes.POINTER(FeaBwdArgs)]
+        L.vmo_fea_bwd.restype = ctypes.c_int
+        L.vmo_fea_bwd.argtypes = [ctypes.POINTER(FeaBwdArgs), c_void_p]
         v = L.vmo_abi_version()
         if v != ABI_VERSION:
             raise RuntimeError(f"vmonarch_amd: library ABI {v}, bindings expect {ABI_VERSION}")

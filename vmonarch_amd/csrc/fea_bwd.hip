@@ -1,0 +1,451 @@
+// FlashEntropyAttention backward for gfx950.
+//
+// Reference: video_monarch_attention/kernel.py:154-313 (_attn_bwd_preprocess, _attn_bwd_dkdv,
+// _attn_bwd_dq, _attn_bwd) launched from _FlashEntropyAttention.backward (kernel.py:360-381).
+// Gradient of a natural-units logit S_ij = sm_scale q_i . k_j (kernel.py:165-167):
+//   dS = P (dP - delta) + dE P (-E - ln P),  delta_i = sum_d o_id dO_id,  dP = dO V^T
+// rewritten per query row as  dS = P (dP + alpha_i + beta_i x),  x = log2 P = s c - lse,
+//   alpha_i = -delta_i - dE_i E_i,   beta_i = -dE_i ln 2
+// so the inner loops need three per-row scalars (lse, alpha, beta).  Then
+//   dQ = sm_scale dS K,  dK = sm_scale dS^T Q,  dV = P^T dO.
+//
+// Two kernels on the caller's stream:
+//  * fea_bwd_dq: one workgroup = 128 queries (32 per wave), loop over 64-key stages exactly like
+//    the forward (S^T = K Q^T and dP^T = V dO^T with Q / dO held as B operands in registers, one
+//    query per lane); dQ^T += K^T dS^T reads K^T from the same LDS tile by ds_read_tr16_b64.  Its
+//    prologue forms delta from o and dO in registers and writes alpha / beta for the second kernel.
+//  * fea_bwd_dkdv: one workgroup = 128 keys (32 per wave, K / V rows held as B operands), loop over
+//    32-query stages: S = Q K^T and dP = dO V^T (one key per lane), then dV^T += dO^T P and
+//    dK^T += Q^T dS with dO^T / Q^T read transposed from the staged tiles.
+// P and dS enter the MFMAs as bf16 / fp16 (the reference's dK / dQ dots run in fp32 = tf32 on its
+// hardware; gfx950 has no xf32 MFMA -- parity is checked at the stated gradient tolerance).
+#include <type_traits>
+
+#include "vmo_common.h"
+#include "vmo_host.h"
+
+namespace vmo {
+
+constexpr int kBwdWaves = 4;
+constexpr int kDqBM = 128;     // queries per dq workgroup
+constexpr int kDqBN = 64;      // keys per dq stage
+constexpr int kKvBN = 128;     // keys per dkdv workgroup
+constexpr int kKvBM = 32;      // queries per dkdv stage
+
+struct BwdParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* o;
+  const void* dO;
+  void* dq;
+  void* dk;
+  void* dv;
+  const float* lse;
+  const float* ent;
+  const float* dent;
+  float* alpha;     // workspace (problems, nq)
+  float* beta;
+  int64_t q_sb, q_sh, q_sn, k_sb, k_sh, k_sn, v_sb, v_sh, v_sn, o_sb, o_sh, o_sn, do_sb, do_sh, do_sn;
+  int64_t dq_sb, dq_sh, dq_sn, dk_sb, dk_sh, dk_sn, dv_sb, dv_sh, dv_sn;
+  int64_t st_sb, st_sh, de_sb, de_sh;
+  int heads, nq, nk, problems;
+  int dq_tiles, kv_tiles;
+  int dq_total, kv_total;
+  float c;          // sm_scale * log2(e)
+  float sm_scale;
+};
+
+template <class T, int W, int ROWS>
+__device__ __forceinline__ void stage_rows_n(const T* __restrict__ base, int64_t sn, int row0, int nrows,
+                                             VMO_LDS char* dst, int wave, int lane) {
+  constexpr int CH = W / 8;
+  constexpr int RPI = 64 / CH;
+  constexpr int NI = ROWS / RPI;          // wave instructions for the whole tile
+  static_assert(CH >= 8 && NI % kBwdWaves == 0, "tile shape");
+#pragma unroll
+  for (int i = 0; i < NI / kBwdWaves; ++i) {
+    const int inst = i * kBwdWaves + wave;
+    const int r = inst * RPI + lane / CH;
+    const int lc = (lane % CH) ^ swz(r);
+    int gr = row0 + r;
+    gr = gr < nrows ? gr : nrows - 1;
+    g2l_16(base + (int64_t)gr * sn + lc * 8, dst + inst * 1024);
+  }
+}
+
+// Waves per SIMD the register budget is sized for: wide value heads keep more accumulators live.
+template <int D, int DV>
+constexpr int bwd_waves_per_simd() { return D + DV > 256 ? 1 : 2; }
+
+__device__ __forceinline__ int xcd_remap(int nblocks) {
+  const int per_xcd = nblocks >> 3;
+  return (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+}
+
+// ------------------------------------------------------------------------------------------------
+template <bool F16, int D, int DV>
+__global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq_kernel(BwdParams p) {
+  using E = Elem<F16>;
+  using T = typename E::T;
+  using V8 = typename E::V8;
+  using V4 = typename E::V4;
+  constexpr int K_BYTES = kDqBN * D * 2;
+  constexpr int STAGE = kDqBN * (D + DV) * 2;
+  constexpr int NA = D / 32;
+  extern __shared__ __attribute__((aligned(1024))) char smem_raw[];
+  VMO_LDS char* smem = (VMO_LDS char*)smem_raw;
+
+  const int L = xcd_remap(gridDim.x);
+  if (L >= p.dq_total) return;
+  const int qt = L % p.dq_tiles, prob = L / p.dq_tiles;
+  const int hh = prob % p.heads, bb = prob / p.heads;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  const int q0 = qt * kDqBM + wave * 32;
+  const bool wave_live = q0 < p.nq;
+  const int qrow = q0 + l32;
+  const bool qvalid = qrow < p.nq;
+  const int qr = qvalid ? qrow : 0;
+
+  const T* kb = (const T*)p.k + bb * p.k_sb + hh * p.k_sh;
+  const T* vb = (const T*)p.v + bb * p.v_sb + hh * p.v_sh;
+
+  // Q^T and dO^T as B operands (one query per lane); delta = o . dO in fp32
+  V8 qf[D / 16], dof[DV / 16];
+  float delta = 0.f;
+  {
+    const T* qp = (const T*)p.q + bb * p.q_sb + hh * p.q_sh + (int64_t)qr * p.q_sn + hl * 8;
+    const T* dp = (const T*)p.dO + bb * p.do_sb + hh * p.do_sh + (int64_t)qr * p.do_sn + hl * 8;
+    const T* op = (const T*)p.o + bb * p.o_sb + hh * p.o_sh + (int64_t)qr * p.o_sn + hl * 8;
+#pragma unroll
+    for (int ds = 0; ds < D / 16; ++ds) {
+      V8 x = *(const V8*)(qp + ds * 16);
+      qf[ds] = qvalid ? x : V8{};
+    }
+#pragma unroll
+    for (int ds = 0; ds < DV / 16; ++ds) {
+      V8 x = *(const V8*)(dp + ds * 16);
+      V8 y = *(const V8*)(op + ds * 16);
+      dof[ds] = qvalid ? x : V8{};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) delta = fmaf((float)x[e], (float)y[e], delta);
+    }
+  }
+  delta = wave_sum32(delta);
+  const int64_t si = bb * p.st_sb + hh * p.st_sh + qr;
+  const float lse = p.lse[si];
+  const float dE = p.dent[bb * p.de_sb + hh * p.de_sh + qr];
+  const float alpha = -delta - dE * p.ent[si];
+  const float beta = -dE * kLn2;
+  if (qvalid && hl == 0) {
+    p.alpha[(int64_t)prob * p.nq + qrow] = alpha;
+    p.beta[(int64_t)prob * p.nq + qrow] = beta;
+  }
+
+  const int n_tiles = (p.nk + kDqBN - 1) / kDqBN;
+  auto issue = [&](int t) {
+    VMO_LDS char* st = smem + (t & 1) * STAGE;
+    stage_rows_n<T, D, kDqBN>(kb, p.k_sn, t * kDqBN, p.nk, st, wave, lane);
+    stage_rows_n<T, DV, kDqBN>(vb, p.v_sn, t * kDqBN, p.nk, st + K_BYTES, wave, lane);
+  };
+
+  f32x16 acc[NA];
+#pragma unroll
+  for (int a = 0; a < NA; ++a) acc[a] = f32x16{};
+  const float c = p.c;
+  const int srow_sw = swz(l32);
+  const int trow = 4 * hl + ((lane & 15) >> 2);
+  const int tsw = swz(trow);
+  const int tchunk = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+  const int tbyte = (lane & 1) * 8;
+
+  issue(0);
+  for (int t = 0; t < n_tiles; ++t) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t + 1 < n_tiles) issue(t + 1);
+    if (!wave_live) continue;
+    const VMO_LDS char* Ks = smem + (t & 1) * STAGE;
+    const VMO_LDS char* Vs = Ks + K_BYTES;
+    const int nvalid = p.nk - t * kDqBN;
+
+    f32x16 s[2] = {f32x16{}, f32x16{}}, dp[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+    for (int kb2 = 0; kb2 < 2; ++kb2) {
+      const VMO_LDS char* krow = Ks + (32 * kb2 + l32) * (D * 2);
+      const VMO_LDS char* vrow = Vs + (32 * kb2 + l32) * (DV * 2);
+#pragma unroll
+      for (int ds = 0; ds < D / 16; ++ds)
+        s[kb2] = E::mfma(lds_read8<V8>(krow + ((2 * ds + hl) ^ srow_sw) * 16), qf[ds], s[kb2]);
+#pragma unroll
+      for (int ds = 0; ds < DV / 16; ++ds)
+        dp[kb2] = E::mfma(lds_read8<V8>(vrow + ((2 * ds + hl) ^ srow_sw) * 16), dof[ds], dp[kb2]);
+    }
+    V8 G[4];
+#pragma unroll
+    for (int kb2 = 0; kb2 < 2; ++kb2) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float x = fmaf(s[kb2][r], c, -lse);
+        float g = fast_exp2(x) * (dp[kb2][r] + fmaf(beta, x, alpha));
+        if (nvalid < kDqBN && 32 * kb2 + 8 * (r >> 2) + 4 * hl + (r & 3) >= nvalid) g = 0.f;
+        G[2 * kb2 + (r >> 3)][r & 7] = to_elem<T>(g);
+      }
+    }
+#pragma unroll
+    for (int a = 0; a < NA; ++a) {
+      const int coff = ((4 * a + tchunk) ^ tsw) * 16 + tbyte;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const VMO_LDS char* r0 = Ks + (16 * ks + trow) * (D * 2) + coff;
+        acc[a] = E::mfma(lds_read_tr8<V8>(r0, r0 + 8 * D * 2), G[ks], acc[a]);
+      }
+    }
+  }
+  if (!wave_live || !qvalid) return;
+  T* dqr = (T*)p.dq + bb * p.dq_sb + hh * p.dq_sh + (int64_t)qrow * p.dq_sn;
+#pragma unroll
+  for (int a = 0; a < NA; ++a)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      V4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = to_elem<T>(acc[a][4 * j + e] * p.sm_scale);
+      *(V4*)(dqr + 32 * a + 8 * j + 4 * hl) = v;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+template <bool F16, int D, int DV>
+__global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dkdv_kernel(BwdParams p) {
+  using E = Elem<F16>;
+  using T = typename E::T;
+  using V8 = typename E::V8;
+  using V4 = typename E::V4;
+  constexpr int Q_BYTES = kKvBM * D * 2;
+  constexpr int DO_BYTES = kKvBM * DV * 2;
+  constexpr int ST_BYTES = 512;                 // lse[32] | alpha[32] | beta[32] | spare
+  constexpr int STAGE = Q_BYTES + DO_BYTES + ST_BYTES;
+  constexpr int NK = D / 32, NV = DV / 32;
+  extern __shared__ __attribute__((aligned(1024))) char smem_raw[];
+  VMO_LDS char* smem = (VMO_LDS char*)smem_raw;
+
+  const int L = xcd_remap(gridDim.x);
+  if (L >= p.kv_total) return;
+  const int kt = L % p.kv_tiles, prob = L / p.kv_tiles;
+  const int hh = prob % p.heads, bb = prob / p.heads;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  const int k0 = kt * kKvBN + wave * 32;
+  const bool wave_live = k0 < p.nk;
+  const int krow = k0 + l32;
+  const bool kvalid = krow < p.nk;
+  const int kr = kvalid ? krow : p.nk - 1;
+
+  // K^T and V^T as B operands (one key per lane)
+  V8 kf[D / 16], vf[DV / 16];
+  {
+    const T* kp = (const T*)p.k + bb * p.k_sb + hh * p.k_sh + (int64_t)kr * p.k_sn + hl * 8;
+    const T* vp = (const T*)p.v + bb * p.v_sb + hh * p.v_sh + (int64_t)kr * p.v_sn + hl * 8;
+#pragma unroll
+    for (int ds = 0; ds < D / 16; ++ds) kf[ds] = *(const V8*)(kp + ds * 16);
+#pragma unroll
+    for (int ds = 0; ds < DV / 16; ++ds) vf[ds] = *(const V8*)(vp + ds * 16);
+  }
+  const T* qb = (const T*)p.q + bb * p.q_sb + hh * p.q_sh;
+  const T* dob = (const T*)p.dO + bb * p.do_sb + hh * p.do_sh;
+  const float* lseb = p.lse + bb * p.st_sb + hh * p.st_sh;
+  const float* alb = p.alpha + (int64_t)prob * p.nq;
+  const float* beb = p.beta + (int64_t)prob * p.nq;
+
+  const int n_tiles = (p.nq + kKvBM - 1) / kKvBM;
+  auto issue = [&](int t) {
+    VMO_LDS char* st = smem + (t & 1) * STAGE;
+    const int row0 = t * kKvBM;
+    stage_rows_n<T, D, kKvBM>(qb, p.q_sn, row0, p.nq, st, wave, lane);
+    stage_rows_n<T, DV, kKvBM>(dob, p.do_sn, row0, p.nq, st + Q_BYTES, wave, lane);
+    if (wave == 0) {   // per-query scalars: lanes 0-31 lse, 32-63 alpha; then beta
+      int qi = row0 + l32;
+      qi = qi < p.nq ? qi : p.nq - 1;
+      const float* src = hl ? alb + qi : lseb + qi;
+      __builtin_amdgcn_global_load_lds(src, st + Q_BYTES + DO_BYTES, 4, 0, 0);
+      __builtin_amdgcn_global_load_lds(beb + qi, st + Q_BYTES + DO_BYTES + 256, 4, 0, 0);
+    }
+  };
+
+  f32x16 dk[NK], dv[NV];
+#pragma unroll
+  for (int a = 0; a < NK; ++a) dk[a] = f32x16{};
+#pragma unroll
+  for (int a = 0; a < NV; ++a) dv[a] = f32x16{};
+  const float c = p.c;
+  const int srow_sw = swz(l32);
+  const int trow = 4 * hl + ((lane & 15) >> 2);
+  const int tsw = swz(trow);
+  const int tchunk = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+  const int tbyte = (lane & 1) * 8;
+
+  issue(0);
+  for (int t = 0; t < n_tiles; ++t) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t + 1 < n_tiles) issue(t + 1);
+    if (!wave_live) continue;
+    const VMO_LDS char* Qs = smem + (t & 1) * STAGE;
+    const VMO_LDS char* dOs = Qs + Q_BYTES;
+    const VMO_LDS float* sts = (const VMO_LDS float*)(dOs + DO_BYTES);
+    const int nvalid = p.nq - t * kKvBM;
+
+    // S[q][key] = Q K^T and dP[q][key] = dO V^T: lane = key l32, queries 8(r/4) + 4 hl + r%4
+    f32x16 s = f32x16{}, dp = f32x16{};
+    {
+      const VMO_LDS char* qrow = Qs + l32 * (D * 2);
+      const VMO_LDS char* drow = dOs + l32 * (DV * 2);
+#pragma unroll
+      for (int ds = 0; ds < D / 16; ++ds) s = E::mfma(lds_read8<V8>(qrow + ((2 * ds + hl) ^ srow_sw) * 16), kf[ds], s);
+#pragma unroll
+      for (int ds = 0; ds < DV / 16; ++ds) dp = E::mfma(lds_read8<V8>(drow + ((2 * ds + hl) ^ srow_sw) * 16), vf[ds], dp);
+    }
+    V8 P[2], G[2];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 lv = *(const VMO_LDS f32x4*)(sts + 8 * g + 4 * hl);
+      const f32x4 av = *(const VMO_LDS f32x4*)(sts + 32 + 8 * g + 4 * hl);
+      const f32x4 bv = *(const VMO_LDS f32x4*)(sts + 64 + 8 * g + 4 * hl);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = 4 * g + e;
+        const float x = fmaf(s[r], c, -lv[e]);
+        float pv = fast_exp2(x);
+        float gv = pv * (dp[r] + fmaf(bv[e], x, av[e]));
+        if (nvalid < kKvBM && 8 * g + 4 * hl + e >= nvalid) { pv = 0.f; gv = 0.f; }
+        P[r >> 3][r & 7] = to_elem<T>(pv);
+        G[r >> 3][r & 7] = to_elem<T>(gv);
+      }
+    }
+    // dV^T[dv][key] += dO^T P,  dK^T[d][key] += Q^T dS  (transposed reads of the staged tiles)
+#pragma unroll
+    for (int a = 0; a < NV; ++a) {
+      const int coff = ((4 * a + tchunk) ^ tsw) * 16 + tbyte;
+#pragma unroll
+      for (int ss = 0; ss < 2; ++ss) {
+        const VMO_LDS char* r0 = dOs + (16 * ss + trow) * (DV * 2) + coff;
+        dv[a] = E::mfma(lds_read_tr8<V8>(r0, r0 + 8 * DV * 2), P[ss], dv[a]);
+      }
+    }
+#pragma unroll
+    for (int a = 0; a < NK; ++a) {
+      const int coff = ((4 * a + tchunk) ^ tsw) * 16 + tbyte;
+#pragma unroll
+      for (int ss = 0; ss < 2; ++ss) {
+        const VMO_LDS char* r0 = Qs + (16 * ss + trow) * (D * 2) + coff;
+        dk[a] = E::mfma(lds_read_tr8<V8>(r0, r0 + 8 * D * 2), G[ss], dk[a]);
+      }
+    }
+  }
+  if (!wave_live || !kvalid) return;
+  T* dkr = (T*)p.dk + bb * p.dk_sb + hh * p.dk_sh + (int64_t)krow * p.dk_sn;
+  T* dvr = (T*)p.dv + bb * p.dv_sb + hh * p.dv_sh + (int64_t)krow * p.dv_sn;
+#pragma unroll
+  for (int a = 0; a < NK; ++a)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      V4 x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] = to_elem<T>(dk[a][4 * j + e] * p.sm_scale);
+      *(V4*)(dkr + 32 * a + 8 * j + 4 * hl) = x;
+    }
+#pragma unroll
+  for (int a = 0; a < NV; ++a)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      V4 x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] = to_elem<T>(dv[a][4 * j + e]);
+      *(V4*)(dvr + 32 * a + 8 * j + 4 * hl) = x;
+    }
+}
+
+template <bool F16, int D, int DV>
+static int launch_bwd(const BwdParams& p, hipStream_t s) {
+  constexpr int LDS_DQ = 2 * kDqBN * (D + DV) * 2;
+  constexpr int LDS_KV = 2 * (kKvBM * (D + DV) * 2 + 512);
+  static_assert(LDS_DQ <= 160 * 1024 && LDS_KV <= 65536, "bwd LDS");
+  if (LDS_DQ > 65536) {
+    static bool done = false;
+    if (!done) {
+      if (hipFuncSetAttribute((const void*)fea_bwd_dq_kernel<F16, D, DV>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              LDS_DQ) != hipSuccess)
+        return set_error(VMO_ERR_LAUNCH, "fea_bwd_dq: cannot raise the LDS limit to %d bytes", LDS_DQ);
+      done = true;
+    }
+  }
+  hipLaunchKernelGGL((fea_bwd_dq_kernel<F16, D, DV>), dim3(xcd_grid(p.dq_total)), dim3(256), LDS_DQ, s, p);
+  int rc = launch_status("fea_bwd_dq");
+  if (rc != VMO_OK) return rc;
+  hipLaunchKernelGGL((fea_bwd_dkdv_kernel<F16, D, DV>), dim3(xcd_grid(p.kv_total)), dim3(256), LDS_KV, s, p);
+  return launch_status("fea_bwd_dkdv");
+}
+
+template <bool F16>
+static int dispatch_bwd(const BwdParams& p, int d, int dv, hipStream_t s) {
+  if (d == 64 && dv == 64) return launch_bwd<F16, 64, 64>(p, s);
+  if (d == 64 && dv == 128) return launch_bwd<F16, 64, 128>(p, s);
+  if (d == 128 && dv == 64) return launch_bwd<F16, 128, 64>(p, s);
+  if (d == 128 && dv == 128) return launch_bwd<F16, 128, 128>(p, s);
+  if (d == 64 && dv == 256) return launch_bwd<F16, 64, 256>(p, s);
+  if (d == 128 && dv == 256) return launch_bwd<F16, 128, 256>(p, s);
+  return set_error(VMO_ERR_UNSUPPORTED, "fea_bwd: no kernel for d=%d dv=%d", d, dv);
+}
+
+}  // namespace vmo
+
+extern "C" size_t vmo_fea_bwd_workspace_size(const vmo_fea_bwd_args* a) {
+  if (!a) return 0;
+  return (size_t)2 * a->batch * a->heads * (size_t)(a->nq > 0 ? a->nq : 0) * 4 + 256;
+}
+
+extern "C" int vmo_fea_bwd(const vmo_fea_bwd_args* a, void* stream) {
+  using namespace vmo;
+  clear_error();
+  if (!a) return set_error(VMO_ERR_INVALID, "fea_bwd: null args");
+  if (a->dtype != VMO_DTYPE_BF16 && a->dtype != VMO_DTYPE_F16) return set_error(VMO_ERR_INVALID, "fea_bwd: dtype");
+  if (a->batch < 0 || a->heads < 0 || a->nq < 0 || a->nk < 0) return set_error(VMO_ERR_INVALID, "fea_bwd: sizes");
+  if ((int64_t)a->batch * a->heads == 0 || (a->nq == 0 && a->nk == 0)) return VMO_OK;
+  if (a->nq == 0 || a->nk == 0) return set_error(VMO_ERR_INVALID, "fea_bwd: nq and nk must both be > 0");
+  if (!view_ok(a->q) || !view_ok(a->k) || !view_ok(a->v) || !view_ok(a->o) || !view_ok(a->grad_o) ||
+      !view_ok(a->grad_q) || !view_ok(a->grad_k) || !view_ok(a->grad_v))
+    return set_error(VMO_ERR_INVALID, "fea_bwd: tensors need 16-byte aligned rows");
+  if (!a->lse || !a->ent || !a->grad_ent) return set_error(VMO_ERR_INVALID, "fea_bwd: lse / ent / dent required");
+  if (!(a->sm_scale >= 0.f)) return set_error(VMO_ERR_INVALID, "fea_bwd: sm_scale");
+  const size_t ws = vmo_fea_bwd_workspace_size(a);
+  if (!a->workspace || a->workspace_bytes < ws || !aligned16(a->workspace))
+    return set_error(VMO_ERR_WORKSPACE, "fea_bwd: needs %zu workspace bytes", ws);
+  const int64_t problems = (int64_t)a->batch * a->heads;
+  const int64_t dq_tiles = (a->nq + kDqBM - 1) / kDqBM, kv_tiles = (a->nk + kKvBN - 1) / kKvBN;
+  if (problems * dq_tiles > (1ll << 30) || problems * kv_tiles > (1ll << 30))
+    return set_error(VMO_ERR_UNSUPPORTED, "fea_bwd: problem too large");
+  BwdParams p{};
+  p.q = a->q.data; p.k = a->k.data; p.v = a->v.data; p.o = a->o.data; p.dO = a->grad_o.data;
+  p.dq = a->grad_q.data; p.dk = a->grad_k.data; p.dv = a->grad_v.data;
+  p.lse = a->lse; p.ent = a->ent; p.dent = a->grad_ent;
+  p.alpha = (float*)a->workspace;
+  p.beta = p.alpha + problems * a->nq;
+  p.q_sb = a->q.stride_b; p.q_sh = a->q.stride_h; p.q_sn = a->q.stride_n;
+  p.k_sb = a->k.stride_b; p.k_sh = a->k.stride_h; p.k_sn = a->k.stride_n;
+  p.v_sb = a->v.stride_b; p.v_sh = a->v.stride_h; p.v_sn = a->v.stride_n;
+  p.o_sb = a->o.stride_b; p.o_sh = a->o.stride_h; p.o_sn = a->o.stride_n;
+  p.do_sb = a->grad_o.stride_b; p.do_sh = a->grad_o.stride_h; p.do_sn = a->grad_o.stride_n;
+  p.dq_sb = a->grad_q.stride_b; p.dq_sh = a->grad_q.stride_h; p.dq_sn = a->grad_q.stride_n;
+  p.dk_sb = a->grad_k.stride_b; p.dk_sh = a->grad_k.stride_h; p.dk_sn = a->grad_k.stride_n;
+  p.dv_sb = a->grad_v.stride_b; p.dv_sh = a->grad_v.stride_h; p.dv_sn = a->grad_v.stride_n;
+  p.st_sb = a->stat_stride_b; p.st_sh = a->stat_stride_h;
+  p.de_sb = a->grad_ent_stride_b; p.de_sh = a->grad_ent_stride_h;
+  p.heads = a->heads; p.nq = a->nq; p.nk = a->nk; p.problems = (int)problems;
+  p.dq_tiles = (int)dq_tiles; p.kv_tiles = (int)kv_tiles;
+  p.dq_total = (int)(problems * dq_tiles); p.kv_total = (int)(problems * kv_tiles);
+  p.c = a->sm_scale * kLog2e;
+  p.sm_scale = a->sm_scale;
+  hipStream_t s = (hipStream_t)stream;
+  if (a->dtype == VMO_DTYPE_F16) return dispatch_bwd<true>(p, a->d, a->dv, s);
+  return dispatch_bwd<false>(p, a->d, a->dv, s);
+}

@@ -1,0 +1,72 @@
+"""Backward of the flash-entropy attention through the C ABI (vmo_fea_bwd).
+
+Mirrors _FlashEntropyAttention.backward of the reference (kernel.py:360-381): given the saved
+q, k, v, o, lse, ent and the upstream grads (do, de) it returns (dq, dk, dv) in q.dtype.  Rows
+>= n_valid are padding: their gradients are zero.
+"""
+import torch
+
+from . import _lib
+
+
+def _pad_features(t, width):
+    return t if t.shape[-1] == width else torch.nn.functional.pad(t, (0, width - t.shape[-1]))
+
+
+def fea_backward_raw(q, k, v, o, lse, ent, do, de, sm_scale):
+    """q: (B, H, nq, D); k: (B, H, nk, D); v: (B, H, nk, Dv); o, do: (B, H, nq, Dv);
+    lse, ent, de: (B, H, nq) fp32 with unit token stride.  Returns (dq, dk, dv)."""
+    L = _lib.lib()
+    B, H, NQ, D = q.shape
+    NK, Dv = k.shape[2], v.shape[-1]
+    dq = torch.empty((B, H, NQ, D), device=q.device, dtype=q.dtype)
+    dk = torch.empty((B, H, NK, D), device=q.device, dtype=q.dtype)
+    dv = torch.empty((B, H, NK, Dv), device=q.device, dtype=q.dtype)
+    a = _lib.FeaBwdArgs()
+    a.dtype = _lib.DTYPES[q.dtype]
+    a.batch, a.heads, a.nq, a.nk, a.d, a.dv = B, H, NQ, NK, D, Dv
+    a.q, a.k, a.v, a.o, a.grad_o = (_lib.view(t) for t in (q, k, v, o, do))
+    a.grad_q, a.grad_k, a.grad_v = _lib.view(dq), _lib.view(dk), _lib.view(dv)
+    assert lse.stride() == ent.stride() and lse.stride(2) == 1 and de.stride(2) == 1
+    a.lse, a.ent, a.grad_ent = lse.data_ptr(), ent.data_ptr(), de.data_ptr()
+    a.stat_stride_b, a.stat_stride_h = lse.stride(0), lse.stride(1)
+    a.grad_ent_stride_b, a.grad_ent_stride_h = de.stride(0), de.stride(1)
+    a.sm_scale = float(sm_scale)
+    nbytes = L.vmo_fea_bwd_workspace_size(a)
+    ws = torch.empty(nbytes, device=q.device, dtype=torch.uint8)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), nbytes
+    _lib.check(L.vmo_fea_bwd(a, _lib.stream_of(q)), "vmo_fea_bwd")
+    return dq, dk, dv
+
+
+def fea_backward(q, k, v, o, lse, ent, do, de, sm_scale, n_valid):
+    B, H, N, D = q.shape
+    Dv = v.shape[-1]
+    n = int(n_valid)
+    Dk = 64 if D < 64 else D
+    Dvk = 64 if Dv < 64 else Dv
+    if Dk not in (64, 128) or Dvk not in (64, 128, 256):
+        raise NotImplementedError(f"vmonarch_amd: backward for head dims ({D}, {Dv}) is not built")
+    if de is None:
+        de = torch.zeros((B, H, N), device=q.device, dtype=torch.float32)
+    if do is None:
+        do = torch.zeros_like(o)
+    do = do.to(q.dtype)
+    de = de.float()
+    dq = torch.zeros_like(q)
+    dk = torch.zeros_like(k)
+    dv = torch.zeros_like(v)
+    if n == 0:
+        return dq, dk, dv
+    sl = slice(0, n)
+    qx, kx = (_lib.row_aligned(_pad_features(t[:, :, sl], Dk)) for t in (q, k))
+    vx, ox, dox = (_lib.row_aligned(_pad_features(t[:, :, sl], Dvk)) for t in (v, o, do))
+    lse_x, ent_x = lse[:, :, sl], ent[:, :, sl]
+    de_x = de[:, :, sl]
+    if de_x.stride(2) != 1:
+        de_x = de_x.contiguous()
+    gq, gk, gv = fea_backward_raw(qx, kx, vx, ox, lse_x, ent_x, dox, de_x, sm_scale)
+    dq[:, :, sl] = gq[..., :D]
+    dk[:, :, sl] = gk[..., :D]
+    dv[:, :, sl] = gv[..., :Dv]
+    return dq, dk, dv
