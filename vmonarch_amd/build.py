@@ -21,6 +21,8 @@ FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-mcode-object-version=5",
     # no packed-fp32 instructions: ordinary float code only
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # no IEEE-mode NaN quieting: max/min need no canonicalising ops (inputs are finite)
+    "-mno-amdgpu-ieee", "-fno-honor-nans",
     "-I", os.path.join(os.path.dirname(HERE), "include"),
 ]
 

@@ -12,12 +12,14 @@
 //  * O^T += W^T P^T with the P accumulator reused in place as the B operand; the W^T operand is
 //    read from the row-major LDS tile with ds_read_tr16_b64, whose 4-key groups match the
 //    accumulator layout of S^T, so no transposed copy and no key permutation is needed;
-//  * K / W tiles are staged by global_load_lds (no register round trip), double-buffered, with
-//    an XOR swizzle of 16-byte chunks against LDS bank conflicts;
+//  * K / W tiles are staged by global_load_lds (no register round trip) through a 2- or 3-slot
+//    LDS ring, with an XOR swizzle of 16-byte chunks against LDS bank conflicts; the copies are
+//    issued from inline asm and ordered by explicit waits, so the prefetch overlaps the reads of
+//    the current tile;
 //  * when w0 aliases k (the VMonarch R-step values [k | v]) the K tile doubles as W0;
-//  * lazy rescaling: the running max only moves when a stage max exceeds it by > kTau (log2
-//    units), so the O rescale is rare; the entropy identity e = log2 l - h / l holds for any
-//    reference point;
+//  * no rescaling in the loop: the reference point m of p = 2^(s c - m) is the max of the first
+//    32 keys and stays fixed; a row whose sum leaves fp32's safe range sends its workgroup through
+//    an exact two-pass fallback.  The entropy identity e = log2 l - h / l holds for any m;
 //  * tail keys are masked in-kernel (no padding copies, unlike kernel.py:399-400);
 //  * split-KV (num_splits > 1) writes normalised fp32 partials + lse, merged by fea_combine.
 #include <type_traits>
@@ -27,10 +29,11 @@
 
 namespace vmo {
 
-constexpr int kFwdBM = 128;           // queries per workgroup
+constexpr int kFwdQB = 1;             // 32-query MFMA blocks per wave
+constexpr int kFwdWaves = 4;          // waves per workgroup (two workgroups share a CU)
+constexpr int kFwdThreads = 64 * kFwdWaves;
+constexpr int kFwdBM = 32 * kFwdQB * kFwdWaves;   // queries per workgroup
 constexpr int kFwdBN = 64;            // keys per pipeline stage
-constexpr int kFwdWaves = 4;
-constexpr float kTau = 8.0f;          // lazy-rescale threshold, log2 units (p <= 2^8)
 constexpr float kMaskLogit = -1.0e30f;
 
 struct FwdParams {
@@ -55,11 +58,16 @@ struct FwdParams {
   float scale_log2;
 };
 
-// Stage kFwdBN rows of a row-major (token, W) tensor into a swizzled LDS tile.  Rows past the end
-// of the tensor (>= nrows) re-read the last row: they are finite and masked out later.
+// LDS ring slots per workgroup: prefetch two tiles ahead when three slots still let two workgroups
+// share a CU (160 KB), else one ahead.
+constexpr int fwd_slots(int stage_bytes) { return 3 * stage_bytes <= 80 * 1024 ? 3 : 2; }
+
+// Stage kFwdBN rows of a row-major (token, W) tensor into a swizzled LDS tile at LDS byte address
+// dst.  Rows past the end of the tensor (>= nrows) re-read the last row: they are finite and masked
+// out later.  Each wave issues NI copies (vmcnt units).
 template <class T, int W>
 __device__ __forceinline__ void stage_rows(const T* __restrict__ base, int64_t sn, int row0, int nrows,
-                                           VMO_LDS char* dst, int wave, int lane) {
+                                           uint32_t dst, int wave, int lane) {
   constexpr int CH = W / 8;           // 16-byte chunks per row
   constexpr int RPI = 64 / CH;        // rows per wave instruction (1 KB)
   constexpr int NI = kFwdBN / RPI / kFwdWaves;
@@ -71,27 +79,40 @@ __device__ __forceinline__ void stage_rows(const T* __restrict__ base, int64_t s
     const int lc = (lane % CH) ^ swz(r);
     int gr = row0 + r;
     gr = gr < nrows ? gr : nrows - 1;
-    g2l_16(base + (int64_t)gr * sn + lc * 8, dst + inst * 1024);
+    dma16_async(base + (int64_t)gr * sn + lc * 8, dst + inst * 1024);
   }
 }
 
-template <bool F16, int D, int DW0, int DW1, bool W0K, bool ENT, bool SPLIT>
-__global__ __launch_bounds__(256, 2) void fea_fwd_kernel(FwdParams p) {
+// Entropy modes: none; online h = sum p (s c - m) (kernel.py:49-50); or, when the first value
+// block is k itself (the VMonarch R-step), from the P.K accumulator at the end:
+//   e = LSE - sm_scale q . (sum_j p_j k_j) / l   (nats)  -- no per-element work in the loop.
+enum { kEntNone = 0, kEntOnline = 1, kEntFromPK = 2 };
+
+template <bool F16, int D, int DW0, int DW1, bool W0K, int ENT, bool SPLIT>
+__global__ __launch_bounds__(kFwdThreads, 2) void fea_fwd_kernel(FwdParams p) {
   using E = Elem<F16>;
   using T = typename E::T;
   using V8 = typename E::V8;
   using V4 = typename E::V4;
+  using V2 = typename E::V2;
   constexpr int K_BYTES = kFwdBN * D * 2;
   constexpr int W0_BYTES = W0K ? 0 : kFwdBN * DW0 * 2;
   constexpr int W1_BYTES = kFwdBN * DW1 * 2;
   constexpr int STAGE = K_BYTES + W0_BYTES + W1_BYTES;
+  constexpr int NSLOT = fwd_slots(STAGE);
   constexpr int NA0 = DW0 / 32;
   constexpr int NA1 = DW1 / 32;
   constexpr int NA = NA0 + NA1;
+  constexpr int NDS = D / 16;
+  constexpr int QB = kFwdQB;
+  // global_load_lds instructions one tile costs each wave (vmcnt units)
+  constexpr int DMA_PER_TILE = kFwdBN * (D + (W0K ? 0 : DW0) + DW1) * 2 / 1024 / kFwdWaves;
   static_assert(!W0K || DW0 == D, "w0 aliases k");
+  static_assert(ENT != kEntFromPK || W0K, "entropy from P.K needs w0 == k");
 
   extern __shared__ __attribute__((aligned(1024))) char smem_raw[];
   VMO_LDS char* smem = (VMO_LDS char*)smem_raw;
+  const uint32_t smem_u32 = (uint32_t)(uintptr_t)smem;
 
   // XCD-aware block -> tile map: block b runs on XCD b % 8, so give each XCD a contiguous run of
   // logical tiles (all query tiles of a problem then share one L2 for their K / W traffic).
@@ -114,31 +135,39 @@ __global__ __launch_bounds__(256, 2) void fea_fwd_kernel(FwdParams p) {
 
   const int kbeg = split * p.keys_per_split;
   const int kend = min(p.nk, kbeg + p.keys_per_split);
-  const int n_tiles = (kend - kbeg + kFwdBN - 1) / kFwdBN;
+  // uniform by construction; readfirstlane lets the compiler branch on them with scalar compares
+  const int n_tiles = __builtin_amdgcn_readfirstlane((kend - kbeg + kFwdBN - 1) / kFwdBN);
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int hl = lane >> 5;
   const int l32 = lane & 31;
-  const int q0 = qt * kFwdBM + wave * 32;
+  // wave owns QB blocks of 32 queries: rows q0 + 32 j + l32
+  const int q0 = qt * kFwdBM + wave * 32 * QB;
   const bool wave_live = q0 < p.nq;
-  const int qrow = q0 + l32;
-  const bool qvalid = qrow < p.nq;
+  int qrow[QB];
+  bool qvalid[QB];
+#pragma unroll
+  for (int j = 0; j < QB; ++j) {
+    qrow[j] = q0 + 32 * j + l32;
+    qvalid[j] = qrow[j] < p.nq;
+  }
 
   // Q^T as the B operand: lane (query l32, half hl) holds q[query][16 ds + 8 hl + 0..7].
-  V8 qf[D / 16];
-  {
-    const T* qp = qb + (int64_t)(qvalid ? qrow : 0) * p.q_sn + hl * 8;
+  V8 qf[QB][NDS];
 #pragma unroll
-    for (int ds = 0; ds < D / 16; ++ds) {
+  for (int j = 0; j < QB; ++j) {
+    const T* qp = qb + (int64_t)(qvalid[j] ? qrow[j] : 0) * p.q_sn + hl * 8;
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds) {
       V8 v = *(const V8*)(qp + ds * 16);
-      qf[ds] = qvalid ? v : V8{};
+      qf[j][ds] = qvalid[j] ? v : V8{};
     }
   }
 
-  auto issue = [&](int t) {
-    VMO_LDS char* st = smem + (t & 1) * STAGE;
+  auto issue = [&](int t) __attribute__((always_inline)) {
+    const uint32_t st = smem_u32 + (uint32_t)((t % NSLOT) * STAGE);
     const int row0 = kbeg + t * kFwdBN;
     stage_rows<T, D>(kb, p.k_sn, row0, p.nk, st, wave, lane);
     if constexpr (!W0K) stage_rows<T, DW0>(w0b, p.w0_sn, row0, p.nk, st + K_BYTES, wave, lane);
@@ -146,12 +175,14 @@ __global__ __launch_bounds__(256, 2) void fea_fwd_kernel(FwdParams p) {
   };
 
   const float c = p.scale_log2;
-  float m_run = kMaskLogit;
-  float l_run = 0.f;
-  float h_run = 0.f;
-  f32x16 acc[NA];
-#pragma unroll
-  for (int a = 0; a < NA; ++a) acc[a] = f32x16{};
+  // Reference point m of x = s c - m (log2 units): the max of the first 32 keys, then fixed.  p = 2^x
+  // is exact in bf16 / fp32 for any x below ~126, so rows whose logits later rise by up to 64 above
+  // that max need no rescaling at all; a block sum beyond 2^64 flags the row and the workgroup redoes
+  // its tile with the exact row max (two passes) -- only for pathological logit ranges.
+  constexpr float kSumLimit = 1.8446744e19f;   // 2^64
+  float m_run[QB], l_run[QB], h_run[QB];
+  f32x16 acc[QB][NA];
+  bool overflow = false;
 
   // per-lane LDS offsets
   const int srow_sw = swz(l32);                                   // S operand rows 32 kb + l32
@@ -160,169 +191,286 @@ __global__ __launch_bounds__(256, 2) void fea_fwd_kernel(FwdParams p) {
   const int tchunk = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);   // logical chunk within 32 cols
   const int tbyte = (lane & 1) * 8;
 
-  issue(0);
-  for (int t = 0; t < n_tiles; ++t) {
-    __builtin_amdgcn_s_waitcnt(0);    // this wave's part of stage t has landed
-    __syncthreads();                  // ... and everybody else's; stage t-1 is free again
-    if (t + 1 < n_tiles) issue(t + 1);
-    if (!wave_live) continue;
-
-    const VMO_LDS char* Ks = smem + (t & 1) * STAGE;
-    const int nvalid = kend - (kbeg + t * kFwdBN);   // valid keys in this stage (may exceed 64)
-    const bool hi_live = nvalid > 32;
-
-    // ---- S^T = K Q^T : s0 keys 0..31, s1 keys 32..63 of the stage
-    f32x16 s0 = f32x16{}, s1 = f32x16{};
-    {
-      const VMO_LDS char* arow = Ks + l32 * (D * 2);
-      if (hi_live) {
+  // S^T block kb (32 keys) for every query block: K fragments are read once, used QB times.  The
+  // reads run kPre fragments ahead of the MFMAs (pinned by sched_group_barrier) so the LDS latency
+  // hides behind the previous MFMAs instead of stalling each one.
+  constexpr int kPre = 3;
+  auto qk_block = [&](const VMO_LDS char* Ks, int kb2, f32x16 (&x)[QB]) __attribute__((always_inline)) {
+    const VMO_LDS char* arow = Ks + (32 * kb2 + l32) * (D * 2);
+    V8 a[NDS];
 #pragma unroll
-        for (int ds = 0; ds < D / 16; ++ds) {
-          const int off = ((2 * ds + hl) ^ srow_sw) * 16;
-          s0 = E::mfma(lds_read8<V8>(arow + off), qf[ds], s0);
-          s1 = E::mfma(lds_read8<V8>(arow + 32 * D * 2 + off), qf[ds], s1);
-        }
-      } else {
+    for (int ds = 0; ds < NDS; ++ds) a[ds] = lds_read8<V8>(arow + ((2 * ds + hl) ^ srow_sw) * 16);
 #pragma unroll
-        for (int ds = 0; ds < D / 16; ++ds) {
-          const int off = ((2 * ds + hl) ^ srow_sw) * 16;
-          s0 = E::mfma(lds_read8<V8>(arow + off), qf[ds], s0);
+    for (int j = 0; j < QB; ++j) x[j] = f32x16{};
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds)
+#pragma unroll
+      for (int j = 0; j < QB; ++j) x[j] = E::mfma(a[ds], qf[j][ds], x[j]);
+    __builtin_amdgcn_sched_group_barrier(0x100, kPre, 0);
+#pragma unroll
+    for (int ds = 0; ds < NDS - kPre; ++ds) {
+      __builtin_amdgcn_sched_group_barrier(0x008, QB, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, QB * kPre, 0);
+  };
+
+  // masked keys of a block (key index kofs + 8(r/4) + 4 hl + r%4 >= nvalid) get x = kMaskLogit
+  auto mask_block = [&](f32x16& x, int kofs, int nvalid) __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      if (kofs + 8 * (r >> 2) + 4 * hl + (r & 3) >= nvalid) x[r] = kMaskLogit;
+  };
+
+  // x = s c - m; p = 2^x rounded and packed as two B operands; sums over the rounded p
+  auto softmax_block = [&](f32x16 (&x)[QB], V8 (&P)[QB][2], int kofs, int nvalid, auto masked_tag)
+      __attribute__((always_inline)) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
+#pragma unroll
+    for (int j = 0; j < QB; ++j) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x[j][r] = fmaf(x[j][r], c, -m_run[j]);
+      if constexpr (MASKED) mask_block(x[j], kofs, nvalid);
+      float ls0 = 0.f, ls1 = 0.f, hs0 = 0.f, hs1 = 0.f;
+      uint32_t w[8];
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        const float p0 = fast_exp2(x[j][r]), p1 = fast_exp2(x[j][r + 1]);
+        const V2 pk = E::pack2(p0, p1);
+        if (r & 2) ls1 = E::sum2(pk, ls1); else ls0 = E::sum2(pk, ls0);
+        if constexpr (ENT == kEntOnline) {
+          if (r & 2) hs1 = fmaf(p1, x[j][r + 1], fmaf(p0, x[j][r], hs1));
+          else hs0 = fmaf(p1, x[j][r + 1], fmaf(p0, x[j][r], hs0));
         }
+        w[r / 2] = __builtin_bit_cast(uint32_t, pk);
+      }
+      typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+      P[j][0] = __builtin_bit_cast(V8, u32x4{w[0], w[1], w[2], w[3]});
+      P[j][1] = __builtin_bit_cast(V8, u32x4{w[4], w[5], w[6], w[7]});
+      const float ls = ls0 + ls1;
+      overflow |= !(ls <= kSumLimit);   // also catches inf / nan
+      l_run[j] += ls;
+      if constexpr (ENT == kEntOnline) h_run[j] += hs0 + hs1;
+    }
+  };
+
+  // O^T += W^T P^T for the 16-key steps 2 kb, 2 kb + 1 of one value part; W^T fragments are read
+  // once and used for every query block.  Transposed reads (two per operand) run two operands
+  // ahead of the MFMAs.
+  auto pv_part = [&](const VMO_LDS char* W, auto rb_tag, auto na_tag, int a0, int kb2, const V8 (&P)[QB][2])
+      __attribute__((always_inline)) {
+    constexpr int RB = decltype(rb_tag)::value;
+    constexpr int NAP = decltype(na_tag)::value;
+    constexpr int NOP = 2 * NAP;   // operands (MFMA A fragments) of this part
+    V8 wt[NOP];
+#pragma unroll
+    for (int a = 0; a < NAP; ++a) {
+      const int coff = ((4 * a + tchunk) ^ tsw) * 16 + tbyte;
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const VMO_LDS char* r0 = W + (32 * kb2 + 16 * h2 + trow) * RB + coff;
+        wt[2 * a + h2] = lds_read_tr8<V8>(r0, r0 + 8 * RB);
       }
     }
-
-    // ---- row max (raw logits); masked keys can not win while one key is valid
-    const bool masked = nvalid < kFwdBN;
-    if (masked) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = 8 * (r >> 2) + 4 * hl + (r & 3);
-        if (key >= nvalid) s0[r] = kMaskLogit;
-        if (key + 32 >= nvalid) s1[r] = kMaskLogit;
-      }
+    for (int a = 0; a < NAP; ++a)
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+        for (int j = 0; j < QB; ++j) acc[j][a0 + a] = E::mfma(wt[2 * a + h2], P[j][h2], acc[j][a0 + a]);
+    constexpr int kPreOps = 2;
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * kPreOps, 0);
+#pragma unroll
+    for (int o = 0; o < NOP - kPreOps; ++o) {
+      __builtin_amdgcn_sched_group_barrier(0x008, QB, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
-    float mx = s0[0];
-#pragma unroll
-    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s0[r]);
-    if (hi_live) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s1[r]);
-    }
-    mx = wave_max32(mx) * c;
-
-    if (t == 0) {
-      m_run = mx;
-    } else if (__builtin_amdgcn_ballot_w64(mx > m_run + kTau) != 0) {
-      const float m_new = fmaxf(m_run, mx);
-      const float alpha = fast_exp2(m_run - m_new);
-      if constexpr (ENT) h_run = alpha * (h_run + (m_run - m_new) * l_run);
-      l_run *= alpha;
-#pragma unroll
-      for (int a = 0; a < NA; ++a) acc[a] *= alpha;
-      m_run = m_new;
-    }
-
-    // ---- p = 2^(s c - m), per-lane partial sums of p and p * (s c - m); P becomes the
-    // B operand of O^T += W^T P^T.  Masked keys get p = 0 exactly (also when c == 0).
-    float lsum = 0.f, hsum = 0.f;
-    auto softmax_block = [&](f32x16& s, int kofs) {
-      if (masked) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kofs + 8 * (r >> 2) + 4 * hl + (r & 3);
-          float x = fmaf(s[r], c, -m_run);
-          float pv = fast_exp2(x);
-          if (key >= nvalid) { pv = 0.f; x = 0.f; }
-          lsum += pv;
-          if constexpr (ENT) hsum = fmaf(pv, x, hsum);
-          s[r] = pv;
-        }
-      } else {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float x = fmaf(s[r], c, -m_run);
-          const float pv = fast_exp2(x);
-          lsum += pv;
-          if constexpr (ENT) hsum = fmaf(pv, x, hsum);
-          s[r] = pv;
-        }
-      }
-    };
-    softmax_block(s0, 0);
-    if (hi_live) softmax_block(s1, 32);
-    l_run += lsum;
-    if constexpr (ENT) h_run += hsum;
-
-    V8 P[4];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      P[0][e] = to_elem<T>(s0[e]);
-      P[1][e] = to_elem<T>(s0[8 + e]);
-      P[2][e] = to_elem<T>(s1[e]);
-      P[3][e] = to_elem<T>(s1[8 + e]);
-    }
-
-    // ---- O^T += W^T P^T
-    auto pv_part = [&](const VMO_LDS char* W, auto rb_tag, auto na_tag, int a0) {
-      constexpr int RB = decltype(rb_tag)::value;
-      constexpr int NAP = decltype(na_tag)::value;
-#pragma unroll
-      for (int a = 0; a < NAP; ++a) {
-        const int coff = ((4 * a + tchunk) ^ tsw) * 16 + tbyte;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          if (ks >= 2 && !hi_live) break;
-          const VMO_LDS char* r0 = W + (16 * ks + trow) * RB + coff;
-          acc[a0 + a] = E::mfma(lds_read_tr8<V8>(r0, r0 + 8 * RB), P[ks], acc[a0 + a]);
-        }
-      }
-    };
-    pv_part(W0K ? Ks : Ks + K_BYTES, std::integral_constant<int, DW0 * 2>{}, std::integral_constant<int, NA0>{}, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, QB * kPreOps, 0);
+  };
+  auto pv_block = [&](const VMO_LDS char* Ks, int kb2, const V8 (&P)[QB][2]) __attribute__((always_inline)) {
+    pv_part(W0K ? Ks : Ks + K_BYTES, std::integral_constant<int, DW0 * 2>{}, std::integral_constant<int, NA0>{}, 0,
+            kb2, P);
     if constexpr (DW1 > 0)
-      pv_part(Ks + K_BYTES + W0_BYTES, std::integral_constant<int, DW1 * 2>{}, std::integral_constant<int, NA1>{}, NA0);
+      pv_part(Ks + K_BYTES + W0_BYTES, std::integral_constant<int, DW1 * 2>{}, std::integral_constant<int, NA1>{}, NA0,
+              kb2, P);
+  };
+
+  // One 64-key stage, as two 32-key blocks in sequence: S(kb) -> softmax(kb) -> PV(kb).  Only one
+  // block's logits and P are live at a time (the [k | v] variant holds 128 accumulator registers);
+  // the second wave on the SIMD (another workgroup) overlaps its MFMAs with this wave's softmax.
+  auto stage = [&](const VMO_LDS char* Ks, int nvalid, auto masked_tag, auto hi_tag) __attribute__((always_inline)) {
+    constexpr bool HI = decltype(hi_tag)::value;
+#pragma unroll
+    for (int kb2 = 0; kb2 < (HI ? 2 : 1); ++kb2) {
+      f32x16 x[QB];
+      V8 P[QB][2];
+      qk_block(Ks, kb2, x);
+      softmax_block(x, P, 32 * kb2, nvalid, masked_tag);
+      pv_block(Ks, kb2, P);
+    }
+  };
+
+  // max over the valid keys of S^T block kb of a stage (raw logits, whole row after the swap)
+  auto block_max = [&](const VMO_LDS char* Ks, int kb2, int nvalid, float (&mx)[QB]) __attribute__((always_inline)) {
+    f32x16 x[QB];
+    qk_block(Ks, kb2, x);
+#pragma unroll
+    for (int j = 0; j < QB; ++j) {
+      mask_block(x[j], 32 * kb2, nvalid);
+      float v = x[j][0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) v = fmaxf(v, x[j][r]);
+      mx[j] = fmaxf(mx[j], wave_max32(v));
+    }
+  };
+
+  auto reset = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < QB; ++j) {
+      l_run[j] = 0.f;   // per-lane partial sum of the rounded p (the weights P.V uses)
+      h_run[j] = 0.f;   // per-lane partial sum of p x (online entropy mode)
+#pragma unroll
+      for (int a = 0; a < NA; ++a) acc[j][a] = f32x16{};
+    }
+  };
+
+  // Tiles t = 0 .. n_tiles-1 flow through an NSLOT-slot LDS ring; prime() issues tiles 0 ..
+  // NSLOT-2.  At the top of tile t this wave's copies of tile t have landed -- only those of tile
+  // t+1 may still be in flight (three slots) -- and after the barrier every wave's copies have,
+  // and the slot of tile t-1 is free for tile t + NSLOT - 1.  Only the last tile can be partial, so
+  // it is peeled: the steady-state body is one straight path and the accumulators stay in place
+  // across iterations.  Waves without queries still take part in every barrier and tile copy.
+  constexpr int kSteadyPending = NSLOT == 3 ? DMA_PER_TILE : 0;
+  auto slot = [&](int t) __attribute__((always_inline)) { return (const VMO_LDS char*)smem + (t % NSLOT) * STAGE; };
+  auto prime = [&]() __attribute__((always_inline)) {
+    issue(0);
+    if (NSLOT == 3 && n_tiles > 1) issue(1);
+  };
+  auto for_tiles = [&](auto&& steady_body, auto&& last_body) __attribute__((always_inline)) {
+    int t = 0;
+    for (; t < n_tiles - 1; ++t) {
+      tile_sync<kSteadyPending>();
+      if (t + NSLOT - 1 < n_tiles) issue(t + NSLOT - 1);
+      steady_body(t);
+    }
+    tile_sync<0>();
+    last_body(t);
+  };
+  auto key_loop = [&]() __attribute__((always_inline)) {
+    if (wave_live) {
+      for_tiles([&](int t) __attribute__((always_inline)) { stage(slot(t), kFwdBN, std::false_type{}, std::true_type{}); },
+                [&](int t) __attribute__((always_inline)) {
+                  const int nvalid = kend - (kbeg + t * kFwdBN);   // 1 .. 64
+                  if (nvalid == kFwdBN)
+                    stage(slot(t), nvalid, std::false_type{}, std::true_type{});
+                  else if (nvalid > 32)
+                    stage(slot(t), nvalid, std::true_type{}, std::true_type{});
+                  else
+                    stage(slot(t), nvalid, std::true_type{}, std::false_type{});
+                });
+    } else {
+      for_tiles([](int) {}, [](int) {});
+    }
+  };
+
+  // m from the first 32 keys of the range (tile 0 stays in slot 0 for the loop)
+  prime();
+  if constexpr (NSLOT == 3) {
+    if (n_tiles > 1) tile_sync<DMA_PER_TILE>(); else tile_sync<0>();
+  } else {
+    tile_sync<0>();
+  }
+  {
+    float mx[QB];
+#pragma unroll
+    for (int j = 0; j < QB; ++j) mx[j] = kMaskLogit;
+    if (wave_live) block_max(slot(0), 0, kend - kbeg, mx);
+#pragma unroll
+    for (int j = 0; j < QB; ++j) m_run[j] = mx[j] * c;
+  }
+  reset();
+  key_loop();
+
+  if (__syncthreads_or(overflow ? 1 : 0)) {
+    // exact two-pass fallback for this workgroup: the true row max, then the loop again
+    float mx[QB];
+#pragma unroll
+    for (int j = 0; j < QB; ++j) mx[j] = kMaskLogit;
+    auto max_tile = [&](int t) __attribute__((always_inline)) {
+      if (!wave_live) return;
+      const int nvalid = kend - (kbeg + t * kFwdBN);
+      block_max(slot(t), 0, nvalid, mx);
+      if (nvalid > 32) block_max(slot(t), 1, nvalid, mx);
+    };
+    prime();
+    for_tiles(max_tile, max_tile);
+#pragma unroll
+    for (int j = 0; j < QB; ++j) m_run[j] = mx[j] * c;
+    reset();
+    tile_sync<0>();   // every wave is done with the last max-pass tile before the ring is reused
+    prime();
+    key_loop();
   }
 
   if (!wave_live) return;
 
-  // ---- finalise: combine the two half-waves' partial sums
-  const float l_tot = wave_sum32(l_run);
-  const float inv_l = 1.0f / l_tot;
-  const float log2l = fast_log2(l_tot);
-  const float lse = m_run + log2l;
-
-  if constexpr (SPLIT) {
-    if (qvalid) {
-      float* orow = p.part_o + ((int64_t)(split * p.problems + prob) * p.nq + qrow) * (int64_t)(DW0 + DW1);
 #pragma unroll
-      for (int a = 0; a < NA; ++a)
+  for (int j = 0; j < QB; ++j) {
+    // ---- finalise: combine the two half-waves' partial sums
+    const float l_tot = wave_sum32(l_run[j]);
+    const float inv_l = 1.0f / l_tot;
+    const float log2l = fast_log2(l_tot);
+    const float lse = m_run[j] + log2l;
+    const int qr = qrow[j];
+    if constexpr (SPLIT) {
+      if (qvalid[j]) {
+        float* orow = p.part_o + ((int64_t)(split * p.problems + prob) * p.nq + qr) * (int64_t)(DW0 + DW1);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          f32x4 v;
+        for (int a = 0; a < NA; ++a)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = acc[a][4 * j + e] * inv_l;
-          *(f32x4*)(orow + 32 * a + 8 * j + 4 * hl) = v;
-        }
-      if (hl == 0) p.part_lse[(int64_t)(split * p.problems + prob) * p.nq + qrow] = lse;
-    }
-  } else {
-    if (qvalid) {
-      T* orow = (T*)p.o + bb * p.o_sb + hh * p.o_sh + ((int64_t)f * p.nq + qrow) * p.o_sn;
+          for (int g = 0; g < 4; ++g) {
+            f32x4 v;
 #pragma unroll
-      for (int a = 0; a < NA; ++a)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          V4 v;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = to_elem<T>(acc[a][4 * j + e] * inv_l);
-          *(V4*)(orow + 32 * a + 8 * j + 4 * hl) = v;
-        }
-      const int64_t si = bb * p.st_sb + hh * p.st_sh + (int64_t)f * p.nq + qrow;
-      if constexpr (ENT) {
-        // h = sum_j p_j x_j with p_j = 2^x_j, x_j = s_j c - m: entropy (bits) = log2 l - h / l
-        const float h_tot = wave_sum32(h_run);
-        if (hl == 0 && p.ent) p.ent[si] = (log2l - h_tot * inv_l) * kLn2;
+            for (int e = 0; e < 4; ++e) v[e] = acc[j][a][4 * g + e] * inv_l;
+            *(f32x4*)(orow + 32 * a + 8 * g + 4 * hl) = v;
+          }
+        if (hl == 0) p.part_lse[(int64_t)(split * p.problems + prob) * p.nq + qr] = lse;
       }
-      if (hl == 0 && p.lse) p.lse[si] = lse;
+    } else {
+      float ent = 0.f;
+      if constexpr (ENT == kEntOnline) {
+        // h = sum_j p_j x_j with p_j = 2^x_j: entropy (bits) = log2 l - h / l
+        ent = (log2l - wave_sum32(h_run[j]) * inv_l) * kLn2;
+      } else if constexpr (ENT == kEntFromPK) {
+        // sum_j P_j s_j = q . (sum_j p_j k_j) / l, with q re-read in the accumulator's layout
+        const T* qp = qb + (int64_t)(qvalid[j] ? qr : 0) * p.q_sn + 4 * hl;
+        float dot = 0.f;
+#pragma unroll
+        for (int a = 0; a < NA0; ++a)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const V4 qv = *(const V4*)(qp + 32 * a + 8 * g);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dot = fmaf((float)qv[e], acc[j][a][4 * g + e], dot);
+          }
+        dot = wave_sum32(dot);
+        ent = lse * kLn2 - (c * kLn2) * dot * inv_l;
+      }
+      if (qvalid[j]) {
+        T* orow = (T*)p.o + bb * p.o_sb + hh * p.o_sh + ((int64_t)f * p.nq + qr) * p.o_sn;
+#pragma unroll
+        for (int a = 0; a < NA; ++a)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            V4 v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = to_elem<T>(acc[j][a][4 * g + e] * inv_l);
+            *(V4*)(orow + 32 * a + 8 * g + 4 * hl) = v;
+          }
+        const int64_t si = bb * p.st_sb + hh * p.st_sh + (int64_t)f * p.nq + qr;
+        if (ENT != kEntNone && hl == 0 && p.ent) p.ent[si] = ent;
+        if (hl == 0 && p.lse) p.lse[si] = lse;
+      }
     }
   }
 }
@@ -360,10 +508,10 @@ __global__ __launch_bounds__(256) void fea_combine_kernel(FwdParams p) {
   if (c4 == 0 && p.lse) p.lse[bb * p.st_sb + hh * p.st_sh + (int64_t)f * p.nq + qi] = M + fast_log2(wsum);
 }
 
-template <bool F16, int D, int DW0, int DW1, bool W0K, bool ENT, bool SPLIT>
+template <bool F16, int D, int DW0, int DW1, bool W0K, int ENT, bool SPLIT>
 static int launch_fwd(const FwdParams& p, hipStream_t stream) {
   constexpr int STAGE = kFwdBN * (D + (W0K ? 0 : DW0) + DW1) * 2;
-  constexpr int LDS = 2 * STAGE;
+  constexpr int LDS = fwd_slots(STAGE) * STAGE;
   auto kern = fea_fwd_kernel<F16, D, DW0, DW1, W0K, ENT, SPLIT>;
   if (LDS > 65536) {
     static bool done = false;   // attribute is per function; idempotent, so a benign race
@@ -373,7 +521,7 @@ static int launch_fwd(const FwdParams& p, hipStream_t stream) {
       done = true;
     }
   }
-  hipLaunchKernelGGL(kern, dim3(xcd_grid(p.total_wg)), dim3(256), LDS, stream, p);
+  hipLaunchKernelGGL(kern, dim3(xcd_grid(p.total_wg)), dim3(kFwdThreads), LDS, stream, p);
   int rc = launch_status("fea_fwd");
   if (rc != VMO_OK || !SPLIT) return rc;
   constexpr int DWT = DW0 + DW1;
@@ -386,31 +534,31 @@ static int launch_fwd(const FwdParams& p, hipStream_t stream) {
 template <bool F16>
 static int dispatch_fwd(const FwdParams& p, int d, int dw0, int dw1, bool w0k, bool ent, bool split, hipStream_t s) {
 #define VMO_FWD(D_, DW0_, DW1_, W0K_, ENT_, SPLIT_)                                                  \
-  if (d == D_ && dw0 == DW0_ && dw1 == DW1_ && w0k == W0K_ && ent == ENT_ && split == SPLIT_)          \
+  if (d == D_ && dw0 == DW0_ && dw1 == DW1_ && w0k == W0K_ && ent == (ENT_ != kEntNone) && split == SPLIT_) \
     return launch_fwd<F16, D_, DW0_, DW1_, W0K_, ENT_, SPLIT_>(p, s);
-  // standalone flash_entropy_attention (kernel.py:384-402): entropy on
-  VMO_FWD(64, 64, 0, false, true, false)
-  VMO_FWD(64, 128, 0, false, true, false)
-  VMO_FWD(64, 256, 0, false, true, false)
-  VMO_FWD(128, 64, 0, false, true, false)
-  VMO_FWD(128, 128, 0, false, true, false)
-  VMO_FWD(128, 256, 0, false, true, false)
-  // VMonarch R-step (vmonarch.py:50): values k, or [k | v]
-  VMO_FWD(64, 64, 0, true, true, false)
-  VMO_FWD(64, 64, 64, true, true, false)
-  VMO_FWD(64, 64, 128, true, true, false)
-  VMO_FWD(128, 128, 0, true, true, false)
-  VMO_FWD(128, 128, 64, true, true, false)
-  VMO_FWD(128, 128, 128, true, true, false)
+  // standalone flash_entropy_attention (kernel.py:384-402): online entropy
+  VMO_FWD(64, 64, 0, false, kEntOnline, false)
+  VMO_FWD(64, 128, 0, false, kEntOnline, false)
+  VMO_FWD(64, 256, 0, false, kEntOnline, false)
+  VMO_FWD(128, 64, 0, false, kEntOnline, false)
+  VMO_FWD(128, 128, 0, false, kEntOnline, false)
+  VMO_FWD(128, 256, 0, false, kEntOnline, false)
+  // VMonarch R-step (vmonarch.py:50): values k, or [k | v]; entropy from the P.K accumulator
+  VMO_FWD(64, 64, 0, true, kEntFromPK, false)
+  VMO_FWD(64, 64, 64, true, kEntFromPK, false)
+  VMO_FWD(64, 64, 128, true, kEntFromPK, false)
+  VMO_FWD(128, 128, 0, true, kEntFromPK, false)
+  VMO_FWD(128, 128, 64, true, kEntFromPK, false)
+  VMO_FWD(128, 128, 128, true, kEntFromPK, false)
   // exact recompute (vmonarch.py:66-68): no entropy, optionally split-KV
-  VMO_FWD(64, 64, 0, false, false, false)
-  VMO_FWD(64, 128, 0, false, false, false)
-  VMO_FWD(128, 64, 0, false, false, false)
-  VMO_FWD(128, 128, 0, false, false, false)
-  VMO_FWD(64, 64, 0, false, false, true)
-  VMO_FWD(64, 128, 0, false, false, true)
-  VMO_FWD(128, 64, 0, false, false, true)
-  VMO_FWD(128, 128, 0, false, false, true)
+  VMO_FWD(64, 64, 0, false, kEntNone, false)
+  VMO_FWD(64, 128, 0, false, kEntNone, false)
+  VMO_FWD(128, 64, 0, false, kEntNone, false)
+  VMO_FWD(128, 128, 0, false, kEntNone, false)
+  VMO_FWD(64, 64, 0, false, kEntNone, true)
+  VMO_FWD(64, 128, 0, false, kEntNone, true)
+  VMO_FWD(128, 64, 0, false, kEntNone, true)
+  VMO_FWD(128, 128, 0, false, kEntNone, true)
 #undef VMO_FWD
   return set_error(VMO_ERR_UNSUPPORTED, "fea_fwd: no kernel for d=%d dw0=%d dw1=%d w0_is_k=%d entropy=%d split=%d", d,
                    dw0, dw1, (int)w0k, (int)ent, (int)split);

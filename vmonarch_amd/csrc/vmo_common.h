@@ -30,20 +30,35 @@ constexpr float kLn2 = 0.6931471805599453f;
 
 // Element-type traits: storage type, 8-wide MFMA operand vector and the MFMA itself.
 template <bool F16> struct Elem;
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
 template <> struct Elem<false> {
   using T = __bf16;
   using V8 = bf16x8;
   using V4 = bf16x4;
+  using V2 = bf16x2;
   __device__ static inline f32x16 mfma(V8 a, V8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  // round two floats to a packed pair (v_cvt_pk_bf16_f32, round to nearest even)
+  __device__ static inline V2 pack2(float a, float b) { return V2{(T)a, (T)b}; }
+  // acc + a.x + a.y computed on the rounded values (v_dot2c_f32_bf16)
+  __device__ static inline float sum2(V2 a, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(a, V2{(T)1.0f, (T)1.0f}, acc, false);
   }
 };
 template <> struct Elem<true> {
   using T = _Float16;
   using V8 = f16x8;
   using V4 = f16x4;
+  using V2 = f16x2;
   __device__ static inline f32x16 mfma(V8 a, V8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  __device__ static inline V2 pack2(float a, float b) { return V2{(T)a, (T)b}; }
+  __device__ static inline float sum2(V2 a, float acc) {
+    return __builtin_amdgcn_fdot2(a, V2{(T)1.0f, (T)1.0f}, acc, false);
   }
 };
 
@@ -70,6 +85,32 @@ __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_lo
 // lds_wave_base + 16 * l (lds_wave_base must be wave-uniform).
 __device__ __forceinline__ void g2l_16(const void* g, VMO_LDS void* lds_wave_base) {
   __builtin_amdgcn_global_load_lds(g, lds_wave_base, 16, 0, 0);
+}
+
+// The same copy issued from inline asm, for pipelines that order their LDS traffic themselves.
+// The compiler cannot see this store to LDS, so it adds no wait of its own before later LDS reads
+// (with the builtin, every ds_read_tr16_b64 -- whose memory operand has no alias information --
+// waits for the most recent copy, which serialises a prefetch with the reads of the current
+// tile).  The caller must order the copy with tile_sync<>() below.  lds_wave_base is an LDS byte
+// address; it goes through M0, which the asm names as clobbered.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16_async(const void* g, uint32_t lds_wave_base) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_wave_base))
+               : "m0");
+}
+#pragma clang diagnostic pop
+
+// Workgroup barrier for a dma16_async pipeline: this wave's own copies except the newest
+// `PENDING` have landed, its LDS reads have returned, then all waves meet.  After it, every copy
+// older than the newest PENDING of each wave is visible to all waves.  The memory clobber keeps
+// LDS accesses on their side of the barrier.
+template <int PENDING>
+__device__ __forceinline__ void tile_sync() {
+  static_assert(PENDING >= 0 && PENDING < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(PENDING) : "memory");
 }
 
 template <class V8>
