@@ -62,26 +62,58 @@ struct FwdParams {
 // share a CU (160 KB), else one ahead.
 constexpr int fwd_slots(int stage_bytes) { return 3 * stage_bytes <= 80 * 1024 ? 3 : 2; }
 
-// Stage kFwdBN rows of a row-major (token, W) tensor into a swizzled LDS tile at LDS byte address
-// dst.  Rows past the end of the tensor (>= nrows) re-read the last row: they are finite and masked
-// out later.  Each wave issues NI copies (vmcnt units).
+// Copies of kFwdBN-row tiles of a row-major (token, W) tensor into swizzled LDS tiles.  Wave
+// instruction inst (= i * kFwdWaves + wave) covers rows inst * RPI .. inst * RPI + RPI - 1 (1 KB);
+// lane l copies chunk l % CH of row inst * RPI + l / CH to chunk (l % CH) ^ swz_rows(row).  The
+// swizzle depends on the row modulo 16 only, which does not change with i when RPI >= 4 (and
+// alternates with i when RPI = 2), so the lane's byte offset from its instruction's first row
+// takes one or two values: a full tile costs scalar address arithmetic only.  A tile that runs
+// past the end of the tensor (row >= nrows) re-reads the last row instead: finite data, masked out
+// later.  Each wave issues NI copies per tile (vmcnt units).
 template <class T, int W>
-__device__ __forceinline__ void stage_rows(const T* __restrict__ base, int64_t sn, int row0, int nrows,
-                                           uint32_t dst, int wave, int lane) {
-  constexpr int CH = W / 8;           // 16-byte chunks per row
-  constexpr int RPI = 64 / CH;        // rows per wave instruction (1 KB)
-  constexpr int NI = kFwdBN / RPI / kFwdWaves;
-  static_assert(CH >= 8 && NI >= 1, "tile shape");
+struct TileCopy {
+  static constexpr int CH = W / 8;       // 16-byte chunks per row
+  static constexpr int RPI = 64 / CH;    // rows per wave instruction
+  static constexpr int NI = kFwdBN / RPI / kFwdWaves;
+  static constexpr int NV = RPI >= 4 ? 1 : 2;   // distinct lane offsets
+  static_assert(CH >= 8 && NI >= 1 && RPI >= 2, "tile shape");
+  uint64_t ubase;     // base as a scalar byte address
+  uint64_t rbytes;    // bytes per row
+  uint32_t voff[NV];
+  int wave, lane;
+
+  __device__ __forceinline__ TileCopy(const T* b, int64_t s, int w, int l) : wave(w), lane(l) {
+    ubase = uniform64((uint64_t)(uintptr_t)b);
+    rbytes = uniform64((uint64_t)s * 2);
 #pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    const int inst = i * kFwdWaves + wave;
-    const int r = inst * RPI + lane / CH;
-    const int lc = (lane % CH) ^ swz(r);
-    int gr = row0 + r;
-    gr = gr < nrows ? gr : nrows - 1;
-    dma16_async(base + (int64_t)gr * sn + lc * 8, dst + inst * 1024);
+    for (int v = 0; v < NV; ++v) {
+      const int r = (v * kFwdWaves + w) * RPI + l / CH;   // the lane's row in instruction i = v
+      voff[v] = (uint32_t)((int64_t)(l / CH) * s * 2) + (uint32_t)(((l % CH) ^ swz_rows<W * 2>(r)) * 16);
+    }
   }
-}
+  __device__ __forceinline__ void issue(int row0, int nrows, uint32_t dst) const {
+    // The per-instruction addresses are loop invariant up to row0; hoisted out of the key loop
+    // they would pin dozens of scalar registers.  The empty asm hides where ub comes from, so they
+    // are recomputed here (a few scalar adds per copy).
+    uint64_t ub = ubase;
+    asm volatile("" : "+s"(ub));
+    if (row0 + kFwdBN <= nrows) {
+      const uint64_t tb = ub + (uint64_t)(row0 + wave * RPI) * rbytes;
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+        dma16_async_s(tb + (uint64_t)(i * kFwdWaves * RPI) * rbytes, voff[i % NV], dst + (i * kFwdWaves + wave) * 1024);
+    } else {
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int inst = i * kFwdWaves + wave;
+        const int r = inst * RPI + lane / CH;
+        const int gr = min(row0 + r, nrows - 1);
+        dma16_async((const void*)(uintptr_t)(ub + (uint64_t)gr * rbytes + ((lane % CH) ^ swz_rows<W * 2>(r)) * 16),
+                    dst + inst * 1024);
+      }
+    }
+  }
+};
 
 // Entropy modes: none; online h = sum p (s c - m) (kernel.py:49-50); or, when the first value
 // block is k itself (the VMonarch R-step), from the P.K accumulator at the end:
@@ -119,19 +151,29 @@ __global__ __launch_bounds__(kFwdThreads, 2) void fea_fwd_kernel(FwdParams p) {
   const int per_xcd = gridDim.x >> 3;
   const int L = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
   if (L >= p.total_wg) return;
-  const int qt = L % p.q_tiles;
+  // Integer division runs on the vector unit; readfirstlane brings the uniform results back to
+  // scalar registers, so the per-tile address arithmetic stays scalar.  The variants with eight
+  // accumulator blocks are short of registers: for them the extra scalar values cost more (their
+  // spills land in the key loop) than the few vector instructions they save.
+  auto uni = [](int v) __attribute__((always_inline)) { return NA >= 8 ? v : __builtin_amdgcn_readfirstlane(v); };
+  const int qt = uni(L % p.q_tiles);
   const int rest = L / p.q_tiles;
-  const int split = rest % p.splits;
-  const int prob = rest / p.splits;
-  const int f = prob % p.frames;
+  const int split = uni(rest % p.splits);
+  const int prob = uni(rest / p.splits);
+  const int f = uni(prob % p.frames);
   const int bh = prob / p.frames;
-  const int hh = bh % p.heads;
-  const int bb = bh / p.heads;
+  const int hh = uni(bh % p.heads);
+  const int bb = uni(bh / p.heads);
 
   const T* qb = (const T*)p.q + bb * p.q_sb + hh * p.q_sh + (int64_t)f * p.nq * p.q_sn;
   const T* kb = (const T*)p.k + bb * p.k_sb + hh * p.k_sh + (int64_t)f * p.nk * p.k_sn;
   const T* w0b = (const T*)p.w0 + bb * p.w0_sb + hh * p.w0_sh + (int64_t)f * p.nk * p.w0_sn;
   const T* w1b = DW1 ? (const T*)p.w1 + bb * p.w1_sb + hh * p.w1_sh + (int64_t)f * p.nk * p.w1_sn : nullptr;
+  // epilogue bases, formed here so that the raw strides are dead during the key loop
+  T* const ob = (T*)p.o + bb * p.o_sb + hh * p.o_sh + (int64_t)f * p.nq * p.o_sn;
+  const int64_t o_sn = p.o_sn, q_sn = p.q_sn;
+  const int64_t st0 = bb * p.st_sb + hh * p.st_sh + (int64_t)f * p.nq;
+  const int64_t part0 = (int64_t)(split * p.problems + prob) * p.nq;
 
   const int kbeg = split * p.keys_per_split;
   const int kend = min(p.nk, kbeg + p.keys_per_split);
@@ -158,7 +200,7 @@ __global__ __launch_bounds__(kFwdThreads, 2) void fea_fwd_kernel(FwdParams p) {
   V8 qf[QB][NDS];
 #pragma unroll
   for (int j = 0; j < QB; ++j) {
-    const T* qp = qb + (int64_t)(qvalid[j] ? qrow[j] : 0) * p.q_sn + hl * 8;
+    const T* qp = qb + (int64_t)(qvalid[j] ? qrow[j] : 0) * q_sn + hl * 8;
 #pragma unroll
     for (int ds = 0; ds < NDS; ++ds) {
       V8 v = *(const V8*)(qp + ds * 16);
@@ -166,12 +208,17 @@ __global__ __launch_bounds__(kFwdThreads, 2) void fea_fwd_kernel(FwdParams p) {
     }
   }
 
+  const TileCopy<T, D> kcopy(kb, p.k_sn, wave, lane);
+  const TileCopy<T, W0K ? 64 : DW0> w0copy(w0b, p.w0_sn, wave, lane);
+  const TileCopy<T, DW1 ? DW1 : 64> w1copy(w1b, p.w1_sn, wave, lane);
   auto issue = [&](int t) __attribute__((always_inline)) {
-    const uint32_t st = smem_u32 + (uint32_t)((t % NSLOT) * STAGE);
+    uint32_t sb = smem_u32;
+    asm volatile("" : "+s"(sb));   // keep the LDS destinations from being hoisted (see TileCopy)
+    const uint32_t st = sb + (uint32_t)((t % NSLOT) * STAGE);
     const int row0 = kbeg + t * kFwdBN;
-    stage_rows<T, D>(kb, p.k_sn, row0, p.nk, st, wave, lane);
-    if constexpr (!W0K) stage_rows<T, DW0>(w0b, p.w0_sn, row0, p.nk, st + K_BYTES, wave, lane);
-    if constexpr (DW1 > 0) stage_rows<T, DW1>(w1b, p.w1_sn, row0, p.nk, st + K_BYTES + W0_BYTES, wave, lane);
+    kcopy.issue(row0, p.nk, st);
+    if constexpr (!W0K) w0copy.issue(row0, p.nk, st + K_BYTES);
+    if constexpr (DW1 > 0) w1copy.issue(row0, p.nk, st + K_BYTES + W0_BYTES);
   };
 
   const float c = p.scale_log2;
@@ -185,9 +232,8 @@ __global__ __launch_bounds__(kFwdThreads, 2) void fea_fwd_kernel(FwdParams p) {
   bool overflow = false;
 
   // per-lane LDS offsets
-  const int srow_sw = swz(l32);                                   // S operand rows 32 kb + l32
+  const int srow_sw = swz_rows<D * 2>(l32);                       // S operand rows 32 kb + l32
   const int trow = 4 * hl + ((lane & 15) >> 2);                   // W^T rows 16 ks + trow (+8)
-  const int tsw = swz(trow);
   const int tchunk = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);   // logical chunk within 32 cols
   const int tbyte = (lane & 1) * 8;
 
@@ -263,13 +309,16 @@ __global__ __launch_bounds__(kFwdThreads, 2) void fea_fwd_kernel(FwdParams p) {
     constexpr int NAP = decltype(na_tag)::value;
     constexpr int NOP = 2 * NAP;   // operands (MFMA A fragments) of this part
     V8 wt[NOP];
+    // rows 32 kb + 16 h2 + trow and 8 further down: swizzles f and f ^ 2
+    const int tsw = swz_rows<RB>(trow);
 #pragma unroll
     for (int a = 0; a < NAP; ++a) {
-      const int coff = ((4 * a + tchunk) ^ tsw) * 16 + tbyte;
+      // rows 32 kb + 16 h2 + trow and 8 further down: swizzles f and f ^ 2 (chunk bit 1)
+      const int c0 = trow * RB + (((4 * a + tchunk) ^ tsw) * 16 + tbyte);
 #pragma unroll
       for (int h2 = 0; h2 < 2; ++h2) {
-        const VMO_LDS char* r0 = W + (32 * kb2 + 16 * h2 + trow) * RB + coff;
-        wt[2 * a + h2] = lds_read_tr8<V8>(r0, r0 + 8 * RB);
+        const VMO_LDS char* rp = W + (32 * kb2 + 16 * h2) * RB;
+        wt[2 * a + h2] = lds_read_tr8<V8>(rp + c0, rp + 8 * RB + (c0 ^ 32));
       }
     }
 #pragma unroll
@@ -358,16 +407,33 @@ __global__ __launch_bounds__(kFwdThreads, 2) void fea_fwd_kernel(FwdParams p) {
   };
   auto key_loop = [&]() __attribute__((always_inline)) {
     if (wave_live) {
-      for_tiles([&](int t) __attribute__((always_inline)) { stage(slot(t), kFwdBN, std::false_type{}, std::true_type{}); },
-                [&](int t) __attribute__((always_inline)) {
-                  const int nvalid = kend - (kbeg + t * kFwdBN);   // 1 .. 64
-                  if (nvalid == kFwdBN)
-                    stage(slot(t), nvalid, std::false_type{}, std::true_type{});
-                  else if (nvalid > 32)
-                    stage(slot(t), nvalid, std::true_type{}, std::true_type{});
-                  else
-                    stage(slot(t), nvalid, std::true_type{}, std::false_type{});
-                });
+      // Full tiles in groups of NSLOT: tile t + S sits in ring slot S, a compile-time offset that
+      // folds into the LDS reads' immediate field (no per-read address arithmetic in the loop).
+      auto full_tile = [&](int t, auto slot_tag) __attribute__((always_inline)) {
+        constexpr int S = decltype(slot_tag)::value;
+        tile_sync<kSteadyPending>();
+        if (t + NSLOT - 1 < n_tiles) issue(t + NSLOT - 1);
+        stage((const VMO_LDS char*)smem + S * STAGE, kFwdBN, std::false_type{}, std::true_type{});
+      };
+      int t = 0;
+      for (; t + NSLOT < n_tiles; t += NSLOT) {
+        full_tile(t, std::integral_constant<int, 0>{});
+        full_tile(t + 1, std::integral_constant<int, 1>{});
+        if constexpr (NSLOT == 3) full_tile(t + 2, std::integral_constant<int, 2>{});
+      }
+      for (; t < n_tiles - 1; ++t) {   // fewer than NSLOT full tiles left
+        tile_sync<kSteadyPending>();
+        if (t + NSLOT - 1 < n_tiles) issue(t + NSLOT - 1);
+        stage(slot(t), kFwdBN, std::false_type{}, std::true_type{});
+      }
+      tile_sync<0>();
+      const int nvalid = kend - (kbeg + t * kFwdBN);   // 1 .. 64
+      if (nvalid == kFwdBN)
+        stage(slot(t), nvalid, std::false_type{}, std::true_type{});
+      else if (nvalid > 32)
+        stage(slot(t), nvalid, std::true_type{}, std::true_type{});
+      else
+        stage(slot(t), nvalid, std::true_type{}, std::false_type{});
     } else {
       for_tiles([](int) {}, [](int) {});
     }
@@ -424,7 +490,7 @@ __global__ __launch_bounds__(kFwdThreads, 2) void fea_fwd_kernel(FwdParams p) {
     const int qr = qrow[j];
     if constexpr (SPLIT) {
       if (qvalid[j]) {
-        float* orow = p.part_o + ((int64_t)(split * p.problems + prob) * p.nq + qr) * (int64_t)(DW0 + DW1);
+        float* orow = p.part_o + (part0 + qr) * (int64_t)(DW0 + DW1);
 #pragma unroll
         for (int a = 0; a < NA; ++a)
 #pragma unroll
@@ -434,7 +500,7 @@ __global__ __launch_bounds__(kFwdThreads, 2) void fea_fwd_kernel(FwdParams p) {
             for (int e = 0; e < 4; ++e) v[e] = acc[j][a][4 * g + e] * inv_l;
             *(f32x4*)(orow + 32 * a + 8 * g + 4 * hl) = v;
           }
-        if (hl == 0) p.part_lse[(int64_t)(split * p.problems + prob) * p.nq + qr] = lse;
+        if (hl == 0) p.part_lse[part0 + qr] = lse;
       }
     } else {
       float ent = 0.f;
@@ -443,7 +509,7 @@ __global__ __launch_bounds__(kFwdThreads, 2) void fea_fwd_kernel(FwdParams p) {
         ent = (log2l - wave_sum32(h_run[j]) * inv_l) * kLn2;
       } else if constexpr (ENT == kEntFromPK) {
         // sum_j P_j s_j = q . (sum_j p_j k_j) / l, with q re-read in the accumulator's layout
-        const T* qp = qb + (int64_t)(qvalid[j] ? qr : 0) * p.q_sn + 4 * hl;
+        const T* qp = qb + (int64_t)(qvalid[j] ? qr : 0) * q_sn + 4 * hl;
         float dot = 0.f;
 #pragma unroll
         for (int a = 0; a < NA0; ++a)
@@ -457,7 +523,7 @@ __global__ __launch_bounds__(kFwdThreads, 2) void fea_fwd_kernel(FwdParams p) {
         ent = lse * kLn2 - (c * kLn2) * dot * inv_l;
       }
       if (qvalid[j]) {
-        T* orow = (T*)p.o + bb * p.o_sb + hh * p.o_sh + ((int64_t)f * p.nq + qr) * p.o_sn;
+        T* orow = ob + (int64_t)qr * o_sn;
 #pragma unroll
         for (int a = 0; a < NA; ++a)
 #pragma unroll
@@ -467,7 +533,7 @@ __global__ __launch_bounds__(kFwdThreads, 2) void fea_fwd_kernel(FwdParams p) {
             for (int e = 0; e < 4; ++e) v[e] = to_elem<T>(acc[j][a][4 * g + e] * inv_l);
             *(V4*)(orow + 32 * a + 8 * g + 4 * hl) = v;
           }
-        const int64_t si = bb * p.st_sb + hh * p.st_sh + (int64_t)f * p.nq + qr;
+        const int64_t si = st0 + qr;
         if (ENT != kEntNone && hl == 0 && p.ent) p.ent[si] = ent;
         if (hl == 0 && p.lse) p.lse[si] = lse;
       }
@@ -599,6 +665,11 @@ extern "C" int vmo_fea_fwd(const vmo_fea_fwd_args* a, void* stream) {
     return set_error(VMO_ERR_INVALID, "fea_fwd: sm_scale must be finite and >= 0");
   if (!view_ok(a->q) || !view_ok(a->k) || !view_ok(a->w0) || !view_ok(a->o) || (a->dw1 > 0 && !view_ok(a->w1)))
     return set_error(VMO_ERR_INVALID, "fea_fwd: tensors need 16-byte aligned rows (strides multiple of 8 elements)");
+  // tile copies address up to 8 rows from a lane with a 32-bit byte offset
+  const int64_t kMaxRowStride = 1ll << 27;
+  if (a->k.stride_n >= kMaxRowStride || a->w0.stride_n >= kMaxRowStride ||
+      (a->dw1 > 0 && a->w1.stride_n >= kMaxRowStride))
+    return set_error(VMO_ERR_UNSUPPORTED, "fea_fwd: key / value row stride must be below 2^27 elements");
   const bool w0k = a->w0.data == a->k.data && a->w0.stride_b == a->k.stride_b && a->w0.stride_h == a->k.stride_h &&
                    a->w0.stride_n == a->k.stride_n && a->dw0 == a->d;
   if (a->dw1 > 0 && !w0k) return set_error(VMO_ERR_UNSUPPORTED, "fea_fwd: a second value tensor needs w0 == k");

@@ -68,6 +68,21 @@ template <> struct Elem<true> {
 // 16-lane group of ds_read_tr16_b64) also lands on eight distinct bank groups.
 __device__ __forceinline__ int swz(int row) { return ((row & 3) << 1) | ((row >> 2) & 1); }
 
+// Bank-conflict-free chunk swizzle for gfx950's 64-bank LDS (256 bytes per cycle), for tiles with
+// RB-byte rows (RB = 128, 256 or 512): chunk c of row r is stored at chunk c ^ swz_rows<RB>(r).
+//  * ds_read_b128 of 16 consecutive rows at one logical chunk (an MFMA A operand, 16 lanes per
+//    cycle) hits 16 distinct 16-byte bank groups: for RB >= 256 the map r -> f(r) is a bijection
+//    on r mod 16; for RB = 128 (two rows per bank line) it is a bijection on each row parity.
+//  * ds_read_tr16_b64 of 4 aligned rows x 4 aligned chunks (32 lanes per cycle) hits 16 distinct
+//    groups: f(r) >> 2 differs between the rows that share a bank line position.
+// f(r + 8) = f(r) ^ 2 and f(r + 16) = f(r).
+template <int RB>
+__device__ __forceinline__ int swz_rows(int r) {
+  static_assert(RB == 128 || RB == 256 || RB == 512, "row width");
+  if constexpr (RB == 128) return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+  else return ((r & 3) << 2) | ((r >> 2) & 3);
+}
+
 __device__ __forceinline__ float wave_max32(float x) {
   // combine lane l with lane l ^ 32
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -99,6 +114,21 @@ __device__ __forceinline__ void dma16_async(const void* g, uint32_t lds_wave_bas
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
                :
                : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_wave_base))
+               : "m0");
+}
+// A wave-uniform 64-bit value, moved to scalar registers (the compiler may otherwise keep a
+// uniform pointer in VGPRs and do its address arithmetic on the vector unit).
+__device__ __forceinline__ uint64_t uniform64(uint64_t v) {
+  return ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32)) << 32) |
+         (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v);
+}
+
+// As dma16_async, with the source split into a wave-uniform 64-bit base (an SGPR pair) and a
+// per-lane 32-bit byte offset: a copy costs no vector instructions when the offsets are reused.
+__device__ __forceinline__ void dma16_async_s(uint64_t sbase, uint32_t voff, uint32_t lds_wave_base) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"(uniform64(sbase)), "s"(__builtin_amdgcn_readfirstlane(lds_wave_base))
                : "m0");
 }
 #pragma clang diagnostic pop
