@@ -241,7 +241,8 @@ __global__ __launch_bounds__(kFwdThreads, 2) void fea_fwd_kernel(FwdParams p) {
   // reads run kPre fragments ahead of the MFMAs (pinned by sched_group_barrier) so the LDS latency
   // hides behind the previous MFMAs instead of stalling each one.
   constexpr int kPre = 3;
-  auto qk_block = [&](const VMO_LDS char* Ks, int kb2, f32x16 (&x)[QB]) __attribute__((always_inline)) {
+  auto qk_block = [&](const VMO_LDS char* Ks, int kb2, f32x16 (&x)[QB], auto sched_tag)
+      __attribute__((always_inline)) {
     const VMO_LDS char* arow = Ks + (32 * kb2 + l32) * (D * 2);
     V8 a[NDS];
 #pragma unroll
@@ -252,13 +253,15 @@ __global__ __launch_bounds__(kFwdThreads, 2) void fea_fwd_kernel(FwdParams p) {
     for (int ds = 0; ds < NDS; ++ds)
 #pragma unroll
       for (int j = 0; j < QB; ++j) x[j] = E::mfma(a[ds], qf[j][ds], x[j]);
-    __builtin_amdgcn_sched_group_barrier(0x100, kPre, 0);
+    if constexpr (decltype(sched_tag)::value) {
+      __builtin_amdgcn_sched_group_barrier(0x100, kPre, 0);
 #pragma unroll
-    for (int ds = 0; ds < NDS - kPre; ++ds) {
-      __builtin_amdgcn_sched_group_barrier(0x008, QB, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      for (int ds = 0; ds < NDS - kPre; ++ds) {
+        __builtin_amdgcn_sched_group_barrier(0x008, QB, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, QB * kPre, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, QB * kPre, 0);
   };
 
   // masked keys of a block (key index kofs + 8(r/4) + 4 hl + r%4 >= nvalid) get x = kMaskLogit
@@ -303,8 +306,8 @@ __global__ __launch_bounds__(kFwdThreads, 2) void fea_fwd_kernel(FwdParams p) {
   // O^T += W^T P^T for the 16-key steps 2 kb, 2 kb + 1 of one value part; W^T fragments are read
   // once and used for every query block.  Transposed reads (two per operand) run two operands
   // ahead of the MFMAs.
-  auto pv_part = [&](const VMO_LDS char* W, auto rb_tag, auto na_tag, int a0, int kb2, const V8 (&P)[QB][2])
-      __attribute__((always_inline)) {
+  auto pv_part = [&](const VMO_LDS char* W, auto rb_tag, auto na_tag, int a0, int kb2, const V8 (&P)[QB][2],
+                     auto sched_tag) __attribute__((always_inline)) {
     constexpr int RB = decltype(rb_tag)::value;
     constexpr int NAP = decltype(na_tag)::value;
     constexpr int NOP = 2 * NAP;   // operands (MFMA A fragments) of this part
@@ -327,21 +330,24 @@ __global__ __launch_bounds__(kFwdThreads, 2) void fea_fwd_kernel(FwdParams p) {
       for (int h2 = 0; h2 < 2; ++h2)
 #pragma unroll
         for (int j = 0; j < QB; ++j) acc[j][a0 + a] = E::mfma(wt[2 * a + h2], P[j][h2], acc[j][a0 + a]);
-    constexpr int kPreOps = 2;
-    __builtin_amdgcn_sched_group_barrier(0x100, 2 * kPreOps, 0);
+    if constexpr (decltype(sched_tag)::value) {
+      constexpr int kPreOps = 2;
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * kPreOps, 0);
 #pragma unroll
-    for (int o = 0; o < NOP - kPreOps; ++o) {
-      __builtin_amdgcn_sched_group_barrier(0x008, QB, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      for (int o = 0; o < NOP - kPreOps; ++o) {
+        __builtin_amdgcn_sched_group_barrier(0x008, QB, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, QB * kPreOps, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, QB * kPreOps, 0);
   };
-  auto pv_block = [&](const VMO_LDS char* Ks, int kb2, const V8 (&P)[QB][2]) __attribute__((always_inline)) {
+  auto pv_block = [&](const VMO_LDS char* Ks, int kb2, const V8 (&P)[QB][2], auto sched_tag)
+      __attribute__((always_inline)) {
     pv_part(W0K ? Ks : Ks + K_BYTES, std::integral_constant<int, DW0 * 2>{}, std::integral_constant<int, NA0>{}, 0,
-            kb2, P);
+            kb2, P, sched_tag);
     if constexpr (DW1 > 0)
       pv_part(Ks + K_BYTES + W0_BYTES, std::integral_constant<int, DW1 * 2>{}, std::integral_constant<int, NA1>{}, NA0,
-              kb2, P);
+              kb2, P, sched_tag);
   };
 
   // One 64-key stage, as two 32-key blocks in sequence: S(kb) -> softmax(kb) -> PV(kb).  Only one
@@ -353,16 +359,36 @@ __global__ __launch_bounds__(kFwdThreads, 2) void fea_fwd_kernel(FwdParams p) {
     for (int kb2 = 0; kb2 < (HI ? 2 : 1); ++kb2) {
       f32x16 x[QB];
       V8 P[QB][2];
-      qk_block(Ks, kb2, x);
+      qk_block(Ks, kb2, x, std::true_type{});
       softmax_block(x, P, 32 * kb2, nvalid, masked_tag);
-      pv_block(Ks, kb2, P);
+      pv_block(Ks, kb2, P, std::true_type{});
     }
+  };
+
+  // A full 64-key stage with the two 32-key blocks software-pipelined inside the wave: the S MFMAs
+  // of block 1 are independent of the softmax of block 0, and the P.V MFMAs of block 0 of the
+  // softmax of block 1, so the scheduler can interleave each pair (sched_barrier keeps the three
+  // regions apart).  Needs one more S and P block live, so it is used where the accumulators leave
+  // room (at most four accumulator blocks).
+  constexpr bool kPipe = NA <= 4;
+  auto stage_pipe = [&](const VMO_LDS char* Ks) __attribute__((always_inline)) {
+    f32x16 x0[QB], x1[QB];
+    V8 P0[QB][2], P1[QB][2];
+    qk_block(Ks, 0, x0, std::true_type{});
+    __builtin_amdgcn_sched_barrier(0);
+    qk_block(Ks, 1, x1, std::false_type{});
+    softmax_block(x0, P0, 0, kFwdBN, std::false_type{});
+    __builtin_amdgcn_sched_barrier(0);
+    pv_block(Ks, 0, P0, std::false_type{});
+    softmax_block(x1, P1, 32, kFwdBN, std::false_type{});
+    __builtin_amdgcn_sched_barrier(0);
+    pv_block(Ks, 1, P1, std::true_type{});
   };
 
   // max over the valid keys of S^T block kb of a stage (raw logits, whole row after the swap)
   auto block_max = [&](const VMO_LDS char* Ks, int kb2, int nvalid, float (&mx)[QB]) __attribute__((always_inline)) {
     f32x16 x[QB];
-    qk_block(Ks, kb2, x);
+    qk_block(Ks, kb2, x, std::true_type{});
 #pragma unroll
     for (int j = 0; j < QB; ++j) {
       mask_block(x[j], 32 * kb2, nvalid);
@@ -413,7 +439,10 @@ __global__ __launch_bounds__(kFwdThreads, 2) void fea_fwd_kernel(FwdParams p) {
         constexpr int S = decltype(slot_tag)::value;
         tile_sync<kSteadyPending>();
         if (t + NSLOT - 1 < n_tiles) issue(t + NSLOT - 1);
-        stage((const VMO_LDS char*)smem + S * STAGE, kFwdBN, std::false_type{}, std::true_type{});
+        if constexpr (kPipe)
+          stage_pipe((const VMO_LDS char*)smem + S * STAGE);
+        else
+          stage((const VMO_LDS char*)smem + S * STAGE, kFwdBN, std::false_type{}, std::true_type{});
       };
       int t = 0;
       for (; t + NSLOT < n_tiles; t += NSLOT) {
