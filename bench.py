@@ -8,11 +8,16 @@ One step = one full forward (2 R-steps, 2 L-steps, the exact recompute).
 
 Prints ONE JSON line.  `value` is algorithmic TFLOP/s of the whole forward (1107.43 GFLOP / step,
 padding and softmax excluded); `roofline` is the dominant kernel (the flash-entropy R-step launch
-with values [k | v]) timed with HIP events on its launch stream; `kernels` breaks every launch
-down; `cpu_baseline` times the CPU oracle (numpy restatement of the reference) on a bounded sample
+with values [k | v]) timed with HIP events on its launch stream inside the timed region; `kernels` breaks
+every launch down the same way; `cpu_baseline` times the CPU oracle (numpy restatement of the reference) on a bounded sample
 of the same workload on this host.
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--cpu-heads 1 | --no-cpu-baseline]
+    python bench.py --copy-calibration     # a plain 1 GiB device copy, x5 (for HBM counter scaling)
+
+`roofline.traffic` is the HBM traffic of the dominant launch measured with rocprofv3 counters
+(FETCH_SIZE and WRITE_SIZE, each scaled by what the same counter reads for the 1 GiB copy of
+--copy-calibration); the figures live in profiles/traffic_cfg4.json, written from those runs.
 """
 import argparse
 import json
@@ -67,6 +72,31 @@ def cpu_baseline(heads, repeats=3):
                       f"float32, median of {repeats} after a 2-frame warm-up; {t:.2f} s per run"}
 
 
+HERE = os.path.dirname(os.path.abspath(__file__))
+TRAFFIC_FILE = os.path.join(HERE, "profiles", "traffic_cfg4.json")
+
+
+def copy_calibration(reps=5):
+    """A plain device-to-device copy of 1 GiB (reads and writes 2^30 bytes per launch)."""
+    import torch
+    dev = torch.device("cuda:0")
+    a = torch.ones(1 << 30, dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": 1 << 30, "launches": reps}), flush=True)
+
+
+def measured_traffic(kernel_key):
+    """HBM bytes per launch of a kernel from the committed counter summary, or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f)["kernels"][kernel_key]["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -74,7 +104,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-heads", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); the multi-GPU design "
               "(heads shard with no exchange, frames shard with one all-to-all per iteration) is "
@@ -93,29 +127,25 @@ def main():
     mod = VMonarchAttention(M, BS, ITERS)
     stream = torch.cuda.current_stream(dev)
 
+    # One step = VMonarchAttention.forward; without autograd that is exactly _vmonarch_fused, which is
+    # called here with a hook that records an event on the launch stream after each of its five
+    # launch groups, so the timed region itself yields the per-launch durations.
+    names = [f"rstep{i}" for i in range(ITERS)]
+    stages = []
+    for it in range(ITERS):
+        stages += [f"rstep{it}", f"lstep{it}"]
+    stages.append("recompute")
     with torch.no_grad():
         for _ in range(args.warmup):
-            mod(q, k, v, recompute_tokens=RT)
+            z_api = mod(q, k, v, recompute_tokens=RT)
+        z_fused = _vmonarch_fused(q, k, v, M, BS, ITERS, RT, mod.min_col_mass)
         torch.cuda.synchronize()
-        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        t0 = time.perf_counter()
-        ev0.record(stream)
-        for _ in range(args.steps):
-            mod(q, k, v, recompute_tokens=RT)
-        ev1.record(stream)
-        torch.cuda.synchronize()
-        wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-        ms = ev0.elapsed_time(ev1) / args.steps
+        if not torch.equal(z_api, z_fused):
+            raise RuntimeError("bench: the timed path differs from VMonarchAttention.forward")
+        del z_api, z_fused
+        step_events = []
 
-        # per-launch breakdown: the same launches, bracketed by events on the launch stream
-        names = [f"rstep{i}" for i in range(ITERS)]
-        stages = []
-        for it in range(ITERS):
-            stages += [f"rstep{it}", f"lstep{it}"]
-        stages.append("recompute")
-        acc = {s: 0.0 for s in stages}
-        nb = max(5, min(args.steps, 20))
-        for _ in range(nb):
+        def run_step():
             evs = [torch.cuda.Event(enable_timing=True)]
             evs[0].record(stream)
 
@@ -124,10 +154,22 @@ def main():
                 e.record(stream)
                 evs.append(e)
 
-            _vmonarch_fused(q, k, v, M, BS, ITERS, RT, 0.01, stage_hook=hook)
-            torch.cuda.synchronize()
+            _vmonarch_fused(q, k, v, M, BS, ITERS, RT, mod.min_col_mass, stage_hook=hook)
+            step_events.append(evs)
+
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        ev0.record(stream)
+        for _ in range(args.steps):
+            run_step()
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+        ms = ev0.elapsed_time(ev1) / args.steps
+        acc = {s: 0.0 for s in stages}
+        for evs in step_events:
             for i, s in enumerate(stages):
-                acc[s] += evs[i].elapsed_time(evs[i + 1]) / nb
+                acc[s] += evs[i].elapsed_time(evs[i + 1]) / len(step_events)
 
     r_flops, l_flops, l_bytes, rec_flops = algorithmic_work()
     total_flops = sum(r_flops) + ITERS * l_flops + rec_flops
@@ -166,7 +208,7 @@ def main():
                    "batch": B, "heads": H, "seq_len": N, "head_dim": D, "gflop_per_step": round(total_flops / 1e9, 2),
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": measured_traffic("rstep_kv"),
                      "kernel": dom["name"], "gflop_per_launch": dom["gflop"], "ms_per_launch": dom["ms"],
                      "all_rstep_frac": round(sum(r_flops) / fea_ms / 1e9 / PEAK_BF16_TFLOPS, 4)},
         "kernels": kernels,
