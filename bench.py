@@ -7,13 +7,16 @@ B=1, H=12, N=32760, D=128 bf16; q, k ~ 0.5 N(0,1), v ~ N(0,1) from seed 0, resid
 One step = one full forward (2 R-steps, 2 L-steps, the exact recompute).
 
 Prints ONE JSON line.  `value` is algorithmic TFLOP/s of the whole forward (1107.43 GFLOP / step,
-padding and softmax excluded); `roofline` is the dominant kernel (the flash-entropy R-step launch
-with values [k | v]) timed with HIP events on its launch stream inside the timed region; `kernels` breaks
-every launch down the same way; `cpu_baseline` times the CPU oracle (numpy restatement of the reference) on a bounded sample
-of the same workload on this host.
+padding and softmax excluded) in the production launch order, where the exact recompute runs on a
+second stream beside the R/L chain.  `roofline` is the dominant kernel (the flash-entropy R-step
+launch with values [k | v]) and `kernels` every launch, timed with HIP events on the launch stream
+inside a second timed region that runs the same launches serially (each alone on the GPU);
+`ms_per_step_serial` is that region's step time.  `cpu_baseline` times the CPU oracle (numpy
+restatement of the reference) on a bounded sample of the same workload on this host.
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--cpu-heads 1 | --no-cpu-baseline]
     python bench.py --copy-calibration     # a plain 1 GiB device copy, x5 (for HBM counter scaling)
+    python bench.py --serial-only ...      # only the serial-order region (what kernel traces use)
 
 `roofline.traffic` is the HBM traffic of the dominant launch measured with rocprofv3 counters
 (FETCH_SIZE and WRITE_SIZE, each scaled by what the same counter reads for the 1 GiB copy of
@@ -105,6 +108,8 @@ def main():
     ap.add_argument("--cpu-heads", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--serial-only", action="store_true",
+                    help="time only the serial order (every launch alone; for kernel traces)")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration()
@@ -127,14 +132,48 @@ def main():
     mod = VMonarchAttention(M, BS, ITERS)
     stream = torch.cuda.current_stream(dev)
 
-    # One step = VMonarchAttention.forward; without autograd that is exactly _vmonarch_fused, which is
-    # called here with a hook that records an event on the launch stream after each of its five
-    # launch groups, so the timed region itself yields the per-launch durations.
+    # One step = VMonarchAttention.forward; without autograd that is exactly _vmonarch_fused (checked
+    # bit for bit below).  Two timed regions of `steps` steps each:
+    #  * the production order (the exact recompute on a second stream beside the R/L chain): `value`;
+    #  * the serial order (every launch alone on one stream) with an event before and after each
+    #    launch group on its stream: the per-launch breakdown and `roofline` (a launch that shares the
+    #    GPU with another has no meaningful rate of its own).
+    import vmonarch_amd.vmonarch as vm
     names = [f"rstep{i}" for i in range(ITERS)]
     stages = []
     for it in range(ITERS):
         stages += [f"rstep{it}", f"lstep{it}"]
     stages.append("recompute")
+    production_order = vm._RECOMPUTE_OVERLAP
+
+    def timed_region(order, with_events):
+        vm._RECOMPUTE_OVERLAP = order
+        step_events = []
+
+        def hook(name, phase, launch_stream):
+            e = torch.cuda.Event(enable_timing=True)
+            e.record(launch_stream)
+            step_events[-1][(name, phase)] = e
+
+        for _ in range(args.warmup):
+            _vmonarch_fused(q, k, v, M, BS, ITERS, RT, mod.min_col_mass)
+        torch.cuda.synchronize()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        ev0.record(stream)
+        for _ in range(args.steps):
+            step_events.append({})
+            _vmonarch_fused(q, k, v, M, BS, ITERS, RT, mod.min_col_mass, stage_hook=hook if with_events else None)
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) * 1e3 / args.steps
+        per = {s: 0.0 for s in stages}
+        if with_events:
+            for evs in step_events:
+                for s in stages:
+                    per[s] += evs[(s, "begin")].elapsed_time(evs[(s, "end")]) / len(step_events)
+        return ev0.elapsed_time(ev1) / args.steps, wall, per
+
     with torch.no_grad():
         for _ in range(args.warmup):
             z_api = mod(q, k, v, recompute_tokens=RT)
@@ -143,33 +182,15 @@ def main():
         if not torch.equal(z_api, z_fused):
             raise RuntimeError("bench: the timed path differs from VMonarchAttention.forward")
         del z_api, z_fused
-        step_events = []
-
-        def run_step():
-            evs = [torch.cuda.Event(enable_timing=True)]
-            evs[0].record(stream)
-
-            def hook(name, evs=evs):
-                e = torch.cuda.Event(enable_timing=True)
-                e.record(stream)
-                evs.append(e)
-
-            _vmonarch_fused(q, k, v, M, BS, ITERS, RT, mod.min_col_mass, stage_hook=hook)
-            step_events.append(evs)
-
-        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        t0 = time.perf_counter()
-        ev0.record(stream)
-        for _ in range(args.steps):
-            run_step()
-        ev1.record(stream)
-        torch.cuda.synchronize()
-        wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-        ms = ev0.elapsed_time(ev1) / args.steps
-        acc = {s: 0.0 for s in stages}
-        for evs in step_events:
-            for i, s in enumerate(stages):
-                acc[s] += evs[i].elapsed_time(evs[i + 1]) / len(step_events)
+        try:
+            if args.serial_only:
+                ms, wall_ms, acc = timed_region("off", True)
+                ms_serial = ms
+            else:
+                ms, wall_ms, _ = timed_region(production_order, False)
+                ms_serial, _, acc = timed_region("off", True)
+        finally:
+            vm._RECOMPUTE_OVERLAP = production_order
 
     r_flops, l_flops, l_bytes, rec_flops = algorithmic_work()
     total_flops = sum(r_flops) + ITERS * l_flops + rec_flops
@@ -198,6 +219,8 @@ def main():
         "warmup": args.warmup,
         "ms_per_step": round(ms, 4),
         "wall_ms_per_step": round(wall_ms, 4),
+        "ms_per_step_serial": round(ms_serial, 4),
+        "recompute_order": "serial" if args.serial_only else production_order,
         "frac_bf16_peak": round(total_flops / ms / 1e9 / PEAK_BF16_TFLOPS, 4),
         "higher_is_better": True,
         "scaling": "weak",

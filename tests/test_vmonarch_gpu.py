@@ -125,6 +125,24 @@ def test_alias_package_is_the_implementation(monkeypatch):
     assert vma.VMonarchAttention is vm.VMonarchAttention
 
 
+@pytest.mark.parametrize("mode", ["start", "after_r0", "after_r1"])
+def test_recompute_on_side_stream_is_bitwise_serial(monkeypatch, mode):
+    """The recompute runs on a second stream beside the R/L chain; every launch point must give the
+    same z bit for bit as running it after the chain (it writes rows [0, rt) only)."""
+    import vmonarch_amd.vmonarch as vm
+    g = torch.Generator().manual_seed(3)
+    m, b, d = 6, 200, 128
+    q, k, v = (randn_lp(g, 1, 4, m * b, d, scale=0.5).to(DEV) for _ in range(3))
+    with torch.no_grad():
+        monkeypatch.setattr(vm, "_RECOMPUTE_OVERLAP", "off")
+        z_serial = vm._vmonarch_fused(q, k, v, m, b, 2, b, 0.01)
+        monkeypatch.setattr(vm, "_RECOMPUTE_OVERLAP", mode)
+        z = vm._vmonarch_fused(q, k, v, m, b, 2, b, 0.01)
+        torch.cuda.synchronize()
+    assert torch.equal(z, z_serial)
+    assert hip_library_loaded()
+
+
 def test_vmonarch_rejects_bad_shape():
     from vmonarch_amd import vmonarch_attention
     q = torch.zeros(1, 1, 12, 64, device=DEV, dtype=torch.bfloat16)

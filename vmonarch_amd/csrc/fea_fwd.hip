@@ -30,9 +30,11 @@
 namespace vmo {
 
 constexpr int kFwdQB = 1;             // 32-query MFMA blocks per wave
-constexpr int kFwdWaves = 4;          // waves per workgroup (two workgroups share a CU)
-constexpr int kFwdThreads = 64 * kFwdWaves;
-constexpr int kFwdBM = 32 * kFwdQB * kFwdWaves;   // queries per workgroup
+// Waves per workgroup (a template parameter of the kernel): 4 (128 queries, two workgroups per CU)
+// or 8 (256 queries, one workgroup per CU).  Both keep two waves per SIMD; 8 halves the K / W tile
+// traffic per flop, at the price of coarser query tiles.
+constexpr int kFwdWavesSmall = 4;
+constexpr int kFwdWavesLarge = 8;
 constexpr int kFwdBN = 64;            // keys per pipeline stage
 constexpr float kMaskLogit = -1.0e30f;
 
@@ -58,24 +60,26 @@ struct FwdParams {
   float scale_log2;
 };
 
-// LDS ring slots per workgroup: prefetch two tiles ahead when three slots still let two workgroups
-// share a CU (160 KB), else one ahead.
-constexpr int fwd_slots(int stage_bytes) { return 3 * stage_bytes <= 80 * 1024 ? 3 : 2; }
+// LDS ring slots per workgroup: prefetch two tiles ahead when three slots fit the workgroup's share
+// of the CU's 160 KB (two 4-wave workgroups or one 8-wave workgroup per CU), else one ahead.
+constexpr int fwd_slots(int stage_bytes, int waves) {
+  return 3 * stage_bytes <= (waves == kFwdWavesLarge ? 160 : 80) * 1024 ? 3 : 2;
+}
 
 // Copies of kFwdBN-row tiles of a row-major (token, W) tensor into swizzled LDS tiles.  Wave
-// instruction inst (= i * kFwdWaves + wave) covers rows inst * RPI .. inst * RPI + RPI - 1 (1 KB);
+// instruction inst (= i * WAVES + wave) covers rows inst * RPI .. inst * RPI + RPI - 1 (1 KB);
 // lane l copies chunk l % CH of row inst * RPI + l / CH to chunk (l % CH) ^ swz_rows(row).  The
-// swizzle depends on the row modulo 16 only, which does not change with i when RPI >= 4 (and
-// alternates with i when RPI = 2), so the lane's byte offset from its instruction's first row
-// takes one or two values: a full tile costs scalar address arithmetic only.  A tile that runs
+// swizzle depends on the row modulo 16 only, which does not change with i when WAVES * RPI is a
+// multiple of 16 (and alternates with i otherwise), so the lane's byte offset from its instruction's
+// first row takes one or two values: a full tile costs scalar address arithmetic only.  A tile that runs
 // past the end of the tensor (row >= nrows) re-reads the last row instead: finite data, masked out
 // later.  Each wave issues NI copies per tile (vmcnt units).
-template <class T, int W>
+template <class T, int W, int WAVES>
 struct TileCopy {
   static constexpr int CH = W / 8;       // 16-byte chunks per row
   static constexpr int RPI = 64 / CH;    // rows per wave instruction
-  static constexpr int NI = kFwdBN / RPI / kFwdWaves;
-  static constexpr int NV = RPI >= 4 ? 1 : 2;   // distinct lane offsets
+  static constexpr int NI = kFwdBN / RPI / WAVES;
+  static constexpr int NV = (WAVES * RPI) % 16 == 0 ? 1 : 2;   // distinct lane offsets
   static_assert(CH >= 8 && NI >= 1 && RPI >= 2, "tile shape");
   uint64_t ubase;     // base as a scalar byte address
   uint64_t rbytes;    // bytes per row
@@ -87,7 +91,7 @@ struct TileCopy {
     rbytes = uniform64((uint64_t)s * 2);
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
-      const int r = (v * kFwdWaves + w) * RPI + l / CH;   // the lane's row in instruction i = v
+      const int r = (v * WAVES + w) * RPI + l / CH;   // the lane's row in instruction i = v
       voff[v] = (uint32_t)((int64_t)(l / CH) * s * 2) + (uint32_t)(((l % CH) ^ swz_rows<W * 2>(r)) * 16);
     }
   }
@@ -101,11 +105,11 @@ struct TileCopy {
       const uint64_t tb = ub + (uint64_t)(row0 + wave * RPI) * rbytes;
 #pragma unroll
       for (int i = 0; i < NI; ++i)
-        dma16_async_s(tb + (uint64_t)(i * kFwdWaves * RPI) * rbytes, voff[i % NV], dst + (i * kFwdWaves + wave) * 1024);
+        dma16_async_s(tb + (uint64_t)(i * WAVES * RPI) * rbytes, voff[i % NV], dst + (i * WAVES + wave) * 1024);
     } else {
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
-        const int inst = i * kFwdWaves + wave;
+        const int inst = i * WAVES + wave;
         const int r = inst * RPI + lane / CH;
         const int gr = min(row0 + r, nrows - 1);
         dma16_async((const void*)(uintptr_t)(ub + (uint64_t)gr * rbytes + ((lane % CH) ^ swz_rows<W * 2>(r)) * 16),
@@ -120,8 +124,8 @@ struct TileCopy {
 //   e = LSE - sm_scale q . (sum_j p_j k_j) / l   (nats)  -- no per-element work in the loop.
 enum { kEntNone = 0, kEntOnline = 1, kEntFromPK = 2 };
 
-template <bool F16, int D, int DW0, int DW1, bool W0K, int ENT, bool SPLIT>
-__global__ __launch_bounds__(kFwdThreads, 2) void fea_fwd_kernel(FwdParams p) {
+template <bool F16, int D, int DW0, int DW1, bool W0K, int ENT, bool SPLIT, int WAVES>
+__global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void fea_fwd_kernel(FwdParams p) {
   using E = Elem<F16>;
   using T = typename E::T;
   using V8 = typename E::V8;
@@ -131,14 +135,15 @@ __global__ __launch_bounds__(kFwdThreads, 2) void fea_fwd_kernel(FwdParams p) {
   constexpr int W0_BYTES = W0K ? 0 : kFwdBN * DW0 * 2;
   constexpr int W1_BYTES = kFwdBN * DW1 * 2;
   constexpr int STAGE = K_BYTES + W0_BYTES + W1_BYTES;
-  constexpr int NSLOT = fwd_slots(STAGE);
+  constexpr int NSLOT = fwd_slots(STAGE, WAVES);
+  constexpr int kBM = 32 * kFwdQB * WAVES;   // queries per workgroup
   constexpr int NA0 = DW0 / 32;
   constexpr int NA1 = DW1 / 32;
   constexpr int NA = NA0 + NA1;
   constexpr int NDS = D / 16;
   constexpr int QB = kFwdQB;
   // global_load_lds instructions one tile costs each wave (vmcnt units)
-  constexpr int DMA_PER_TILE = kFwdBN * (D + (W0K ? 0 : DW0) + DW1) * 2 / 1024 / kFwdWaves;
+  constexpr int DMA_PER_TILE = kFwdBN * (D + (W0K ? 0 : DW0) + DW1) * 2 / 1024 / WAVES;
   static_assert(!W0K || DW0 == D, "w0 aliases k");
   static_assert(ENT != kEntFromPK || W0K, "entropy from P.K needs w0 == k");
 
@@ -186,7 +191,7 @@ __global__ __launch_bounds__(kFwdThreads, 2) void fea_fwd_kernel(FwdParams p) {
   const int hl = lane >> 5;
   const int l32 = lane & 31;
   // wave owns QB blocks of 32 queries: rows q0 + 32 j + l32
-  const int q0 = qt * kFwdBM + wave * 32 * QB;
+  const int q0 = qt * kBM + wave * 32 * QB;
   const bool wave_live = q0 < p.nq;
   int qrow[QB];
   bool qvalid[QB];
@@ -208,9 +213,9 @@ __global__ __launch_bounds__(kFwdThreads, 2) void fea_fwd_kernel(FwdParams p) {
     }
   }
 
-  const TileCopy<T, D> kcopy(kb, p.k_sn, wave, lane);
-  const TileCopy<T, W0K ? 64 : DW0> w0copy(w0b, p.w0_sn, wave, lane);
-  const TileCopy<T, DW1 ? DW1 : 64> w1copy(w1b, p.w1_sn, wave, lane);
+  const TileCopy<T, D, WAVES> kcopy(kb, p.k_sn, wave, lane);
+  const TileCopy<T, W0K ? 64 : DW0, WAVES> w0copy(w0b, p.w0_sn, wave, lane);
+  const TileCopy<T, DW1 ? DW1 : 64, WAVES> w1copy(w1b, p.w1_sn, wave, lane);
   auto issue = [&](int t) __attribute__((always_inline)) {
     uint32_t sb = smem_u32;
     asm volatile("" : "+s"(sb));   // keep the LDS destinations from being hoisted (see TileCopy)
@@ -603,11 +608,14 @@ __global__ __launch_bounds__(256) void fea_combine_kernel(FwdParams p) {
   if (c4 == 0 && p.lse) p.lse[bb * p.st_sb + hh * p.st_sh + (int64_t)f * p.nq + qi] = M + fast_log2(wsum);
 }
 
-template <bool F16, int D, int DW0, int DW1, bool W0K, int ENT, bool SPLIT>
-static int launch_fwd(const FwdParams& p, hipStream_t stream) {
+template <bool F16, int D, int DW0, int DW1, bool W0K, int ENT, bool SPLIT, int WAVES>
+static int launch_fwd(FwdParams p, hipStream_t stream) {
   constexpr int STAGE = kFwdBN * (D + (W0K ? 0 : DW0) + DW1) * 2;
-  constexpr int LDS = fwd_slots(STAGE) * STAGE;
-  auto kern = fea_fwd_kernel<F16, D, DW0, DW1, W0K, ENT, SPLIT>;
+  constexpr int LDS = fwd_slots(STAGE, WAVES) * STAGE;
+  constexpr int BM = 32 * kFwdQB * WAVES;
+  p.q_tiles = (p.nq + BM - 1) / BM;
+  p.total_wg = p.problems * p.splits * p.q_tiles;
+  auto kern = fea_fwd_kernel<F16, D, DW0, DW1, W0K, ENT, SPLIT, WAVES>;
   if (LDS > 65536) {
     static bool done = false;   // attribute is per function; idempotent, so a benign race
     if (!done) {
@@ -616,7 +624,7 @@ static int launch_fwd(const FwdParams& p, hipStream_t stream) {
       done = true;
     }
   }
-  hipLaunchKernelGGL(kern, dim3(xcd_grid(p.total_wg)), dim3(kFwdThreads), LDS, stream, p);
+  hipLaunchKernelGGL(kern, dim3(xcd_grid(p.total_wg)), dim3(64 * WAVES), LDS, stream, p);
   int rc = launch_status("fea_fwd");
   if (rc != VMO_OK || !SPLIT) return rc;
   constexpr int DWT = DW0 + DW1;
@@ -625,12 +633,16 @@ static int launch_fwd(const FwdParams& p, hipStream_t stream) {
   return launch_status("fea_combine");
 }
 
+// Waves per workgroup for a variant.  Measured at cfg4 (b = 1560 queries per problem), the 8-wave
+// workgroup was slower for every variant (coarser query tiles, one workgroup per CU), so all use 4.
+constexpr int kFwdWavesFor(int, int, int, bool) { return kFwdWavesSmall; }
+
 // Runtime -> template dispatch over the supported shapes.
 template <bool F16>
 static int dispatch_fwd(const FwdParams& p, int d, int dw0, int dw1, bool w0k, bool ent, bool split, hipStream_t s) {
 #define VMO_FWD(D_, DW0_, DW1_, W0K_, ENT_, SPLIT_)                                                  \
   if (d == D_ && dw0 == DW0_ && dw1 == DW1_ && w0k == W0K_ && ent == (ENT_ != kEntNone) && split == SPLIT_) \
-    return launch_fwd<F16, D_, DW0_, DW1_, W0K_, ENT_, SPLIT_>(p, s);
+    return launch_fwd<F16, D_, DW0_, DW1_, W0K_, ENT_, SPLIT_, kFwdWavesFor(D_, DW0_, DW1_, SPLIT_)>(p, s);
   // standalone flash_entropy_attention (kernel.py:384-402): online entropy
   VMO_FWD(64, 64, 0, false, kEntOnline, false)
   VMO_FWD(64, 128, 0, false, kEntOnline, false)
@@ -708,9 +720,9 @@ extern "C" int vmo_fea_fwd(const vmo_fea_fwd_args* a, void* stream) {
   if (splits > 1 && ent) return set_error(VMO_ERR_UNSUPPORTED, "fea_fwd: split-KV with entropy output");
   if (splits > 1 && (a->workspace == nullptr || a->workspace_bytes < (size_t)ws || !aligned16(a->workspace)))
     return set_error(VMO_ERR_WORKSPACE, "fea_fwd: needs %lld workspace bytes", (long long)ws);
-  const int64_t q_tiles = (a->nq + kFwdBM - 1) / kFwdBM;
+  const int64_t q_tiles = (a->nq + 32 * kFwdQB * kFwdWavesSmall - 1) / (32 * kFwdQB * kFwdWavesSmall);
   const int64_t problems = (int64_t)a->batch * a->heads * a->frames;
-  const int64_t total = problems * splits * q_tiles;
+  const int64_t total = problems * splits * q_tiles;   // the most workgroups any variant launches
   if (total > (1ll << 30) || (int64_t)a->frames * a->nq > (1ll << 30) || (int64_t)a->frames * a->nk > (1ll << 30))
     return set_error(VMO_ERR_UNSUPPORTED, "fea_fwd: problem too large");
 

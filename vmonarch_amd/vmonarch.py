@@ -72,41 +72,79 @@ def _fused_supported(q, k, v, num_blocks):
             and k.shape == q.shape and v.shape[:-1] == q.shape[:-1])
 
 
+# Where the exact recompute of the first rt queries starts on its own stream: it reads q, k, v only
+# and writes rows [0, rt) of z, which the L-steps never write, so it can run beside the R/L chain
+# ("start": with R-step 0, "after_r0": beside L-step 0 onwards, "after_r1": beside the last L-step,
+# "off": after the chain on the caller's stream).
+_RECOMPUTE_OVERLAP = "after_r0"
+_side_streams = {}
+
+
+def _side_stream(dev):
+    s = _side_streams.get(dev)
+    if s is None:
+        s = _side_streams[dev] = torch.cuda.Stream(device=dev)   # default priority
+    return s
+
+
 def _vmonarch_fused(q, k, v, m, b, num_iters, recompute_tokens, min_col_mass, stage_hook=None):
-    """All-HIP forward.  `stage_hook(name)`, when given, is called on the host right after each
-    launch ("rstep0", "lstep0", ..., "recompute") -- used by bench.py to bracket every kernel with
-    events on the launch stream."""
+    """All-HIP forward.  `stage_hook(name, phase, stream)`, when given, is called on the host right
+    before ("begin") and after ("end") each launch group ("rstep0", "lstep0", ..., "recompute") with
+    the stream it goes to -- used by bench.py to bracket every kernel with events."""
     B, H, N, D = q.shape
     Dv = v.shape[-1]
     scale = D ** -0.5
     q, k, v = (_lib.row_aligned(t) for t in (q, k, v))
     dev, dt = q.device, q.dtype
+    main = torch.cuda.current_stream(dev)
+    hook = stage_hook or (lambda name, phase, stream: None)
     ent = torch.empty((B, H, N), device=dev, dtype=torch.float32)
     z = torch.empty((B, H, N, Dv), device=dev, dtype=dt)
     rt = min(int(recompute_tokens), N)
+    side = None
+
+    def recompute(stream):
+        # exact attention for the first rt queries (vmonarch.py:66-68), written into z
+        with torch.cuda.stream(stream):
+            hook("recompute", "begin", stream)
+            splits = _recompute_splits(B * H, rt, N)
+            fea_forward(q[:, :, :rt], k, v, None, scale, o=z[:, :, :rt], want_ent=False, want_lse=False,
+                        num_splits=splits)
+            hook("recompute", "end", stream)
+
+    def fork():
+        nonlocal side
+        side = _side_stream(dev)
+        side.wait_stream(main)   # q, k, v and z are ready on the caller's stream
+        recompute(side)
+
+    if rt > 0 and _RECOMPUTE_OVERLAP == "start":
+        fork()
     u = None
     for it in range(num_iters):
         last = it == num_iters - 1
         # R-step (vmonarch.py:50): iteration 0 folds u = q * scale into the softmax scale
         x, s = (q, scale) if it == 0 else (u, 1.0)
+        hook(f"rstep{it}", "begin", main)
         out, _, _ = fea_forward(x, k, k, v if last else None, s, frames=m, ent=ent, want_lse=False)
-        if stage_hook:
-            stage_hook(f"rstep{it}")
+        hook(f"rstep{it}", "end", main)
+        if rt > 0 and side is None and ((_RECOMPUTE_OVERLAP == "after_r0" and it == 0) or
+                                        (_RECOMPUTE_OVERLAP == "after_r1" and last)):
+            fork()
         # L-step (vmonarch.py:51-63)
+        hook(f"lstep{it}", "begin", main)
         if last:
             _lstep_launch(q, out, ent, z, m, b, scale, True, rt, min_col_mass)
         else:
             if u is None:
                 u = torch.empty((B, H, N, D), device=dev, dtype=dt)
             _lstep_launch(q, out, ent, u, m, b, scale, False, 0, min_col_mass)
-        if stage_hook:
-            stage_hook(f"lstep{it}")
-    if rt > 0:   # exact attention for the first rt queries (vmonarch.py:66-68), written into z
-        splits = _recompute_splits(B * H, rt, N)
-        fea_forward(q[:, :, :rt], k, v, None, scale, o=z[:, :, :rt], want_ent=False, want_lse=False,
-                    num_splits=splits)
-        if stage_hook:
-            stage_hook("recompute")
+        hook(f"lstep{it}", "end", main)
+    if rt > 0:
+        if side is None:
+            recompute(main)
+        else:
+            main.wait_stream(side)   # z is complete on the caller's stream
     return z
 
 
