@@ -276,7 +276,9 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void fea_fwd_kernel(FwdParam
       if (kofs + 8 * (r >> 2) + 4 * hl + (r & 3) >= nvalid) x[r] = kMaskLogit;
   };
 
-  // x = s c - m; p = 2^x rounded and packed as two B operands; sums over the rounded p
+  // x = s c - m; p = 2^x, rounded and packed as two B operands.  The row sums add the fp32 p, as
+  // kernel.py:51 does (and with plain adds: v_dot2c_f32_bf16, which would sum the rounded pairs in
+  // one instruction, measured to stall behind a concurrent MFMA of another wave on the SIMD)
   auto softmax_block = [&](f32x16 (&x)[QB], V8 (&P)[QB][2], int kofs, int nvalid, auto masked_tag)
       __attribute__((always_inline)) {
     constexpr bool MASKED = decltype(masked_tag)::value;
@@ -291,7 +293,7 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void fea_fwd_kernel(FwdParam
       for (int r = 0; r < 16; r += 2) {
         const float p0 = fast_exp2(x[j][r]), p1 = fast_exp2(x[j][r + 1]);
         const V2 pk = E::pack2(p0, p1);
-        if (r & 2) ls1 = E::sum2(pk, ls1); else ls0 = E::sum2(pk, ls0);
+        if (r & 2) ls1 += p0 + p1; else ls0 += p0 + p1;
         if constexpr (ENT == kEntOnline) {
           if (r & 2) hs1 = fmaf(p1, x[j][r + 1], fmaf(p0, x[j][r], hs1));
           else hs0 = fmaf(p1, x[j][r + 1], fmaf(p0, x[j][r], hs0));
@@ -407,7 +409,7 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void fea_fwd_kernel(FwdParam
   auto reset = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < QB; ++j) {
-      l_run[j] = 0.f;   // per-lane partial sum of the rounded p (the weights P.V uses)
+      l_run[j] = 0.f;   // per-lane partial sum of p
       h_run[j] = 0.f;   // per-lane partial sum of p x (online entropy mode)
 #pragma unroll
       for (int a = 0; a < NA; ++a) acc[j][a] = f32x16{};

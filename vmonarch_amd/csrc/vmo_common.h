@@ -44,10 +44,6 @@ template <> struct Elem<false> {
   }
   // round two floats to a packed pair (v_cvt_pk_bf16_f32, round to nearest even)
   __device__ static inline V2 pack2(float a, float b) { return V2{(T)a, (T)b}; }
-  // acc + a.x + a.y computed on the rounded values (v_dot2c_f32_bf16)
-  __device__ static inline float sum2(V2 a, float acc) {
-    return __builtin_amdgcn_fdot2_f32_bf16(a, V2{(T)1.0f, (T)1.0f}, acc, false);
-  }
 };
 template <> struct Elem<true> {
   using T = _Float16;
@@ -58,9 +54,6 @@ template <> struct Elem<true> {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
   __device__ static inline V2 pack2(float a, float b) { return V2{(T)a, (T)b}; }
-  __device__ static inline float sum2(V2 a, float acc) {
-    return __builtin_amdgcn_fdot2(a, V2{(T)1.0f, (T)1.0f}, acc, false);
-  }
 };
 
 // 16-byte chunk swizzle of LDS tiles whose rows are >= 8 chunks wide: chunk c of row r is
