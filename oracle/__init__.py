@@ -8,6 +8,8 @@ Contents
   fea.entropy_attention        forward of FlashEntropyAttention (o, e)
   fea.entropy_attention_grad   analytic backward (dq, dk, dv) incl. the entropy term
   vmonarch.vmonarch_attention  alternating-minimisation glue (R-step, L-step, recompute)
+  vmonarch.lstep_grad          backward of one L-step (entropy bias detached)
+  vmonarch.vmonarch_attention_grad  backward of the whole glue (dq, dk, dv)
 
 Every function cites the reference file:line it restates.  Arithmetic is numpy float64 by
 default (float32 for the CPU baseline timing).  How each function is pinned:
@@ -20,6 +22,11 @@ default (float32 for the CPU baseline timing).  How each function is pinned:
                           (video_monarch_attention/vmonarch.py:29-69) with its R-step
                           swapped to the fp32 oracle as in tests/test_vmonarch.py:55-61, plus
                           the m=1 / b=1 / rt=N reductions to exact attention.
+  lstep_grad,             central finite differences (random directions, float64) of
+  vmonarch_attention_grad lstep / vmonarch_attention with the entropy biases frozen at the
+                          base point, as the reference's detach (vmonarch.py:26) makes them;
+                          with and without the col_mass clamp active, 1-3 iterations, rt 0 and b.
 """
 from .fea import entropy_attention, entropy_attention_grad, exact_attention  # noqa: F401
-from .vmonarch import vmonarch_attention, row_block_attention, lstep  # noqa: F401
+from .vmonarch import (vmonarch_attention, row_block_attention, lstep, lstep_grad,  # noqa: F401
+                       vmonarch_attention_grad)

@@ -6,7 +6,7 @@ no bf16 rounding anywhere: this is the fp32 reference the GPU path is judged aga
 """
 import numpy as np
 
-from .fea import entropy_attention, exact_attention
+from .fea import entropy_attention, entropy_attention_grad, exact_attention
 
 
 def row_block_attention(x, k, w, dtype=np.float64):
@@ -44,8 +44,14 @@ def lstep(qg, out, neg_ent, scale, last, min_col_mass=0.01):
 
 
 def vmonarch_attention(q, k, v, num_blocks, block_size, num_iters=2, recompute_tokens=0,
-                       min_col_mass=0.01, dtype=np.float64):
-    """vmonarch.py:29-69.  q, k: (B, H, N, D); v: (B, H, N, Dv); N == num_blocks*block_size."""
+                       min_col_mass=0.01, dtype=np.float64, record=None, frozen_neg_ent=None):
+    """vmonarch.py:29-69.  q, k: (B, H, N, D); v: (B, H, N, Dv); N == num_blocks*block_size.
+
+    ``record``: a list that receives (u, w, out, neg_ent) of every iteration (for the backward).
+    ``frozen_neg_ent``: per-iteration entropy biases used instead of the computed ones -- the
+    reference detaches them (vmonarch.py:26), so a finite-difference check of the gradient holds
+    them at their values at the base point.
+    """
     q, k, v = (np.asarray(t, dtype=dtype) for t in (q, k, v))
     B, H, N, D = q.shape
     if N != num_blocks * block_size:                                     # vmonarch.py:42
@@ -62,6 +68,10 @@ def vmonarch_attention(q, k, v, num_blocks, block_size, num_iters=2, recompute_t
         last = it == num_iters - 1
         w = np.concatenate([kg, vg], -1) if last else kg                 # vmonarch.py:50
         out, neg_ent = row_block_attention(u, kg, w, dtype)
+        if frozen_neg_ent is not None:
+            neg_ent = frozen_neg_ent[it]
+        if record is not None:
+            record.append((u, w, out, neg_ent))
         res = lstep(qg, out, neg_ent, scale, last, min_col_mass)
         if last:
             z = res
@@ -73,3 +83,93 @@ def vmonarch_attention(q, k, v, num_blocks, block_size, num_iters=2, recompute_t
         z = z.copy()
         z[:, :, :rt] = exact_attention(q[:, :, :rt], k, v, None, dtype)
     return z
+
+
+def lstep_grad(qg, out, neg_ent, scale, last, grad, min_col_mass=0.01):
+    """Backward of ``lstep`` (vmonarch.py:51-63) with the entropy bias held constant (vmonarch.py:26
+    detaches it).  ``grad`` is dL/dz (B, H, m, b, Dv) when ``last``, else dL/du (B, H, m, b, D).
+    Returns (dL/dqg, dL/dout).  Derived by hand, step by step backwards through lstep:
+      z = attn y               -> d attn = dz y^T, dy = attn^T dz
+      u = (attn^T q) f, f = scale / max(c, mcm), c = sum_i attn
+                               -> dv = du f, df = du . v, dc = -df scale / cm^2 where c >= mcm,
+                                  d attn = dv q^T + dc, dq = attn dv
+      attn = softmax_k(logits + ent)  -> d logits = attn (d attn - sum_k attn d attn)
+      logits = q kr^T, kr = out[:D] scale  -> dq += d logits kr, d out[:D] = scale d logits^T q
+    """
+    D = qg.shape[-1]
+    kr = out[..., :D] * scale
+    logits = np.einsum("bhijd,bhkjd->bhjik", qg, kr)
+    attn = _softmax(logits - np.swapaxes(neg_ent, -1, -2)[..., None, :])
+    dout = np.zeros_like(out)
+    if last:
+        y = out[..., D:]
+        dattn = np.einsum("bhijd,bhkjd->bhjik", grad, y)
+        dout[..., D:] = np.einsum("bhjik,bhijd->bhkjd", attn, grad)
+        dqg = np.zeros_like(qg)
+    else:
+        c = np.swapaxes(attn.sum(-2), -1, -2)                     # (B, H, k, j)
+        cm = np.maximum(c, min_col_mass)
+        f = scale / cm
+        vsum = np.einsum("bhjik,bhijd->bhkjd", attn, qg)
+        dv = grad * f[..., None]
+        df = (grad * vsum).sum(-1)
+        dc = np.where(c >= min_col_mass, -df * scale / (cm * cm), 0.0)
+        dattn = np.einsum("bhkjd,bhijd->bhjik", dv, qg) + np.swapaxes(dc, -1, -2)[..., None, :]
+        dqg = np.einsum("bhjik,bhkjd->bhijd", attn, dv)
+    dlogits = attn * (dattn - (attn * dattn).sum(-1, keepdims=True))
+    dqg = dqg + np.einsum("bhjik,bhkjd->bhijd", dlogits, kr)
+    dout[..., :D] = scale * np.einsum("bhjik,bhijd->bhkjd", dlogits, qg)
+    return dqg, dout
+
+
+def vmonarch_attention_grad(q, k, v, grad_z, num_blocks, block_size, num_iters=2, recompute_tokens=0,
+                            min_col_mass=0.01, dtype=np.float64):
+    """Gradient of sum(z * grad_z) w.r.t. (q, k, v) for z = vmonarch_attention(...), with the
+    R-step entropies detached as in the reference (vmonarch.py:26).  Reverse pass over the
+    recorded forward: recompute rows through entropy_attention_grad (exact attention,
+    vmonarch.py:66-68; the L-path rows < rt get no gradient, they are overwritten), then each
+    iteration's lstep_grad and R-step entropy_attention_grad (sm_scale 1, values w = k or [k|v]).
+    """
+    q, k, v, grad_z = (np.asarray(t, dtype=dtype) for t in (q, k, v, grad_z))
+    B, H, N, D = q.shape
+    Dv = v.shape[-1]
+    m, b = num_blocks, block_size
+    scale = D ** -0.5
+    rec = []
+    vmonarch_attention(q, k, v, m, b, num_iters, 0, min_col_mass, dtype, record=rec)
+    dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
+    gz = grad_z.copy()
+    rt = recompute_tokens
+    if rt > 0:
+        gq, gk, gv = entropy_attention_grad(q[:, :, :rt], k, v, grad_z[:, :, :rt],
+                                            np.zeros(grad_z.shape[:2] + (rt,)), None, dtype)
+        dq[:, :, :rt] += gq
+        dk += gk
+        dv += gv
+        gz[:, :, :rt] = 0.0
+    qg = q.reshape(B, H, m, b, D)
+    dqg = np.zeros_like(qg)
+    dkg = np.zeros((B, H, m, b, D), dtype)
+    dvg = np.zeros((B, H, m, b, Dv), dtype)
+    kg = k.reshape(B, H, m, b, D)
+    g = gz.reshape(B, H, m, b, Dv)
+    for it in reversed(range(num_iters)):
+        last = it == num_iters - 1
+        u, w, out, neg_ent = rec[it]
+        dq_l, dout = lstep_grad(qg, out, neg_ent, scale, last, g, min_col_mass)
+        dqg += dq_l
+        du, dk_key, dw = entropy_attention_grad(u, kg, w, dout, np.zeros(u.shape[:-1]), 1.0, dtype)
+        dkg += dk_key
+        if last:
+            dkg += dw[..., :D]
+            dvg += dw[..., D:]
+        else:
+            dkg += dw
+        if it > 0:
+            g = du
+        else:
+            dqg += du * scale
+    dq += dqg.reshape(B, H, N, D)
+    dk += dkg.reshape(B, H, N, D)
+    dv += dvg.reshape(B, H, N, Dv)
+    return dq, dk, dv

@@ -15,7 +15,8 @@ import numpy as np
 import pytest
 
 from conftest import assert_close_ref, golden_names, load_golden
-from oracle import entropy_attention, entropy_attention_grad, exact_attention, vmonarch_attention
+from oracle import (entropy_attention, entropy_attention_grad, exact_attention, lstep, lstep_grad,
+                    vmonarch_attention, vmonarch_attention_grad)
 
 
 def brute_entropy_attention(q, k, v, scale):
@@ -106,6 +107,68 @@ def test_fea_grad_matches_finite_differences(nq, nk, d, dv):
             args_m = [xm if a is x else a for a in (q, k, v)]
             num[idx] = (loss(*args_p) - loss(*args_m)) / (2 * eps)
         np.testing.assert_allclose(g, num, rtol=1e-6, atol=1e-7)
+
+
+def _numeric_grads(loss, xs, eps=1e-6):
+    """Central differences of the scalar loss(*xs) with respect to every element of every x."""
+    out = []
+    for n, x in enumerate(xs):
+        num = np.zeros_like(x)
+        for idx in np.ndindex(x.shape):
+            xp, xm = x.copy(), x.copy()
+            xp[idx] += eps
+            xm[idx] -= eps
+            num[idx] = (loss(*xs[:n], xp, *xs[n + 1:]) - loss(*xs[:n], xm, *xs[n + 1:])) / (2 * eps)
+        out.append(num)
+    return out
+
+
+@pytest.mark.parametrize("last", [False, True])
+@pytest.mark.parametrize("min_col_mass", [0.01, 0.7])
+def test_lstep_grad_matches_finite_differences(last, min_col_mass):
+    # m = 4 frames: with min_col_mass 0.7 some columns of attn sum below it (clamp active), some above
+    rng = np.random.default_rng(7 + last)
+    B, H, m, b, D, Dv = 1, 2, 4, 3, 3, 2
+    qg = rng.normal(size=(B, H, m, b, D))
+    out = rng.normal(size=(B, H, m, b, D + (Dv if last else 0)))
+    neg_ent = rng.normal(size=(B, H, m, b))
+    grad = rng.normal(size=(B, H, m, b, Dv if last else D))
+    scale = 0.7
+    if not last and min_col_mass > 0.5:
+        attn_sums = []
+        kr = out[..., :D] * scale
+        logits = np.einsum("bhijd,bhkjd->bhjik", qg, kr) - np.swapaxes(neg_ent, -1, -2)[..., None, :]
+        a = np.exp(logits - logits.max(-1, keepdims=True))
+        a /= a.sum(-1, keepdims=True)
+        attn_sums = a.sum(-2)
+        assert (attn_sums < min_col_mass).any() and (attn_sums > min_col_mass).any()
+
+    def loss(qg_, out_):
+        return (lstep(qg_, out_, neg_ent, scale, last, min_col_mass) * grad).sum()
+
+    dq, dout = lstep_grad(qg, out, neg_ent, scale, last, grad, min_col_mass)
+    nq, nout = _numeric_grads(loss, [qg, out])
+    np.testing.assert_allclose(dq, nq, rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(dout, nout, rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("iters,rt,min_col_mass", [(1, 0, 0.01), (2, 4, 0.01), (3, 0, 0.6), (2, 0, 0.6)])
+def test_vmonarch_grad_matches_finite_differences(iters, rt, min_col_mass):
+    rng = np.random.default_rng(iters * 10 + rt)
+    B, H, m, b, D, Dv = 1, 1, 3, 4, 3, 2
+    q, k = rng.normal(size=(B, H, m * b, D)), rng.normal(size=(B, H, m * b, D))
+    v, gz = rng.normal(size=(B, H, m * b, Dv)), rng.normal(size=(B, H, m * b, Dv))
+    rec = []
+    vmonarch_attention(q, k, v, m, b, iters, rt, min_col_mass, record=rec)
+    frozen = [r[3] for r in rec]   # the reference detaches the entropy bias (vmonarch.py:26)
+
+    def loss(q_, k_, v_):
+        z = vmonarch_attention(q_, k_, v_, m, b, iters, rt, min_col_mass, frozen_neg_ent=frozen)
+        return (z * gz).sum()
+
+    grads = vmonarch_attention_grad(q, k, v, gz, m, b, iters, rt, min_col_mass)
+    for g, n in zip(grads, _numeric_grads(loss, [q, k, v])):
+        np.testing.assert_allclose(g, n, rtol=1e-5, atol=1e-7)
 
 
 @pytest.mark.parametrize("name", golden_names("fea_"))
