@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define VMO_ABI_VERSION 1
+#define VMO_ABI_VERSION 2
 
 enum {
   VMO_OK = 0,
@@ -142,6 +142,41 @@ typedef struct vmo_fea_bwd_args {
   size_t workspace_bytes;
 } vmo_fea_bwd_args;
 
+/*
+ * Backward of one L-step (the gradient autograd takes through vmonarch.py:51-63, with the entropy
+ * bias detached as vmonarch.py:26 does), fused per grid column j.  With attn as in
+ * vmo_lstep_args, y = out[..., d:] and g = grad_res (dL/dz when last, dL/du otherwise):
+ *   last == 1:  d attn[i,k] = g[i,j] . y[k,j];  grad_out[k,j,d:] = sum_i attn[i,k] g[i,j]
+ *               (tokens n < skip_tokens carry no gradient: the recompute overwrote them)
+ *   last == 0:  c_k = sum_i attn[i,k], cm_k = max(c_k, min_col_mass), f_k = scale / cm_k,
+ *               v_k = sum_i attn[i,k] q[i,j];  dv_k = f_k g[k,j];
+ *               d attn[i,k] = dv_k . q[i,j] - [c_k >= min_col_mass] (g[k,j] . v_k) f_k / cm_k;
+ *               grad_q[i,j] += sum_k attn[i,k] dv_k
+ *   both:       dlogit = attn (d attn - sum_k attn d attn);
+ *               grad_q[i,j] += scale sum_k dlogit[i,k] out[k,j,:d];
+ *               grad_out[k,j,:d] = scale sum_i dlogit[i,k] q[i,j]
+ * grad_q is float32 and accumulated into (+=); grad_out (the dtype of q) is written.  Replaces
+ * the autograd graph of the reference's L-step (batched einsum/softmax/clamp backward); there is
+ * no launch site of its own in the reference.  Supported: m <= 32, d in {64, 128}, dv in {64, 128}.
+ */
+typedef struct vmo_lstep_bwd_args {
+  int32_t dtype;
+  int32_t batch, heads;
+  int32_t num_blocks, block_size;  /* m, b */
+  int32_t d, dv;
+  int32_t last;
+  int32_t skip_tokens;
+  vmo_view q;                      /* (B, H, m*b, d) */
+  vmo_view out;                    /* (B, H, m*b, d + dv*last): R-step output */
+  const float* ent;                /* (B, H, m*b) with token stride 1 */
+  int64_t ent_stride_b, ent_stride_h;
+  vmo_view grad_res;               /* dL/dz (B, H, m*b, dv)   or   dL/du (B, H, m*b, d) */
+  vmo_view grad_q;                 /* float32 (B, H, m*b, d), accumulated into */
+  vmo_view grad_out;               /* (B, H, m*b, d + dv*last), written */
+  float scale;
+  float min_col_mass;
+} vmo_lstep_bwd_args;
+
 /* ABI version of the loaded library (VMO_ABI_VERSION at build time). */
 int vmo_abi_version(void);
 
@@ -162,6 +197,9 @@ int vmo_fea_bwd(const vmo_fea_bwd_args* args, void* stream);
 
 /* Fused L-step; see vmo_lstep_args. */
 int vmo_lstep_fwd(const vmo_lstep_args* args, void* stream);
+
+/* Backward of the fused L-step; see vmo_lstep_bwd_args. */
+int vmo_lstep_bwd(const vmo_lstep_bwd_args* args, void* stream);
 
 #ifdef __cplusplus
 }

@@ -27,7 +27,8 @@ def L():
 
 def test_header_declares_the_entry_points():
     names = _declared_functions()
-    for n in ("vmo_abi_version", "vmo_last_error", "vmo_fea_fwd", "vmo_fea_fwd_workspace_size", "vmo_lstep_fwd"):
+    for n in ("vmo_abi_version", "vmo_last_error", "vmo_fea_fwd", "vmo_fea_fwd_workspace_size", "vmo_lstep_fwd",
+              "vmo_fea_bwd", "vmo_fea_bwd_workspace_size", "vmo_lstep_bwd"):
         assert n in names
 
 
@@ -100,3 +101,15 @@ def test_lstep_rejects_too_many_blocks(L):
     a.q = a.out = a.res = v
     a.ent = 4096
     assert L.vmo_lstep_fwd(ctypes.byref(a), None) == 2
+
+
+def test_lstep_bwd_rejects_too_many_blocks_and_null_args(L):
+    from vmonarch_amd import _lib
+    a = _lib.LstepBwdArgs()
+    a.dtype, a.batch, a.heads, a.num_blocks, a.block_size, a.d, a.dv = 0, 1, 1, 33, 4, 128, 128
+    v = _lib.View(4096, 128, 128, 128)
+    a.q = a.out = a.grad_res = a.grad_q = a.grad_out = v
+    a.ent = 4096
+    assert L.vmo_lstep_bwd(ctypes.byref(a), None) == 2
+    assert b"num_blocks" in L.vmo_last_error()
+    assert L.vmo_lstep_bwd(None, None) != 0

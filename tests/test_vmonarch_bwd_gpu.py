@@ -1,0 +1,113 @@
+"""VMonarch backward on the GPU: the fused L-step backward (vmo_lstep_bwd) and the whole
+gradient of vmonarch_attention (the autograd Function over the HIP forward / backward), against
+the CPU oracle's reverse pass (oracle/vmonarch.py lstep_grad, vmonarch_attention_grad), which is
+pinned by finite differences in tests/test_oracle.py.
+
+Tolerances use the reference's metric (tests/test_vmonarch.py:22-24, max|x - ref| <= tol *
+max|ref|) with the reference's own gradient tolerance, 5e-2 (tests/test_vmonarch.py:66), for
+the whole VMonarch gradient; the L-step backward alone is held to 2e-2.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close_ref, hip_library_loaded, randn_lp
+from oracle import lstep_grad, vmonarch_attention_grad
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.mark.parametrize("d,dv,last", [(64, 64, False), (128, 128, False), (64, 64, True), (128, 128, True),
+                                       (64, 128, True), (128, 64, True)])
+@pytest.mark.parametrize("m,mcm", [(4, 0.6), (21, 0.01), (32, 0.3)])
+def test_lstep_bwd_matches_oracle(d, dv, last, m, mcm):
+    from vmonarch_amd.vmonarch import _lstep_bwd_launch
+    g = torch.Generator().manual_seed(1000 * m + d + dv + last)
+    B, H, b = 1, 2, 40
+    N = m * b
+    wout = d + (dv if last else 0)
+    q = randn_lp(g, B, H, N, d)
+    out = randn_lp(g, B, H, N, wout)
+    ent = torch.rand(B, H, N, generator=g) * 3.0
+    grad = randn_lp(g, B, H, N, dv if last else d)
+    skip = b if last else 0      # as the recompute of the first block leaves it
+    dq0 = torch.randn(B, H, N, d, generator=g)   # grad_q is accumulated into
+    dq = dq0.to(DEV)
+    dout = torch.empty((B, H, N, wout), device=DEV, dtype=q.dtype)
+    print(f"lstep_bwd d={d} dv={dv} last={last} m={m} mcm={mcm}", flush=True)
+    _lstep_bwd_launch(q.to(DEV), out.to(DEV), ent.to(DEV), grad.to(DEV), dq, dout, m, b, d ** -0.5, last, skip, mcm)
+    torch.cuda.synchronize()
+    assert hip_library_loaded()
+
+    r5 = lambda t: t.float().numpy().reshape(B, H, m, b, -1)
+    gg = r5(grad)
+    if last:
+        gg[:, :, 0] = 0.0        # tokens n = 0*b + j < skip carry no gradient
+    dq_ref, dout_ref = lstep_grad(r5(q), r5(out), -ent.numpy().reshape(B, H, m, b), d ** -0.5, last, gg, mcm)
+    assert_close_ref((dq.cpu() - dq0).numpy(), dq_ref.reshape(B, H, N, d), 2e-2)
+    assert_close_ref(dout.float().cpu().numpy(), dout_ref.reshape(B, H, N, wout), 2e-2)
+
+
+def _grads(q, k, v, do, m, b, iters, rt):
+    from vmonarch_amd import vmonarch_attention
+    qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    z = vmonarch_attention(qd, kd, vd, m, b, iters, recompute_tokens=rt)
+    assert type(z.grad_fn).__name__ == "_VMonarchFunctionBackward"
+    grads = torch.autograd.grad((z.float() * do.to(DEV)).sum(), (qd, kd, vd))
+    return z, grads
+
+
+@pytest.mark.parametrize("m, b", [(4, 256), (8, 100)])
+@pytest.mark.parametrize("num_iters", [1, 2, 3])
+def test_vmonarch_grad_reference_params(m, b, num_iters):
+    # the reference's gradient test (tests/test_vmonarch.py:45-66): (1, 2, m*b, 64), rt = b
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (randn_lp(g, 1, 2, m * b, 64) for _ in range(3))
+    do = torch.randn(1, 2, m * b, 64, generator=g)
+    print(f"vmonarch grad m={m} b={b} iters={num_iters}", flush=True)
+    _, grads = _grads(q, k, v, do, m, b, num_iters, b)
+    ref = vmonarch_attention_grad(*(t.float().numpy() for t in (q, k, v)), do.numpy(), m, b, num_iters, b)
+    for gd, gr in zip(grads, ref):
+        assert_close_ref(gd.float().cpu().numpy(), gr, 5e-2)
+    assert hip_library_loaded()
+
+
+def test_vmonarch_grad_d128_cfg3_shape_sample():
+    # cfg3 geometry (m=16, b=256, rt=256) at D = 128, one head
+    g = torch.Generator().manual_seed(3)
+    m, b = 16, 256
+    q, k = (randn_lp(g, 1, 1, m * b, 128, scale=0.5) for _ in range(2))
+    v = randn_lp(g, 1, 1, m * b, 128)
+    do = torch.randn(1, 1, m * b, 128, generator=g)
+    print("vmonarch grad cfg3 sample", flush=True)
+    _, grads = _grads(q, k, v, do, m, b, 2, b)
+    ref = vmonarch_attention_grad(*(t.float().numpy() for t in (q, k, v)), do.numpy(), m, b, 2, b)
+    for gd, gr in zip(grads, ref):
+        assert_close_ref(gd.float().cpu().numpy(), gr, 5e-2)
+
+
+def test_vmonarch_grad_forward_matches_inference_path():
+    # the autograd Function's forward is the same HIP pipeline as the no-grad path: equal z
+    from vmonarch_amd import vmonarch_attention
+    g = torch.Generator().manual_seed(5)
+    m, b = 8, 100
+    q, k, v = (randn_lp(g, 1, 2, m * b, 64).to(DEV) for _ in range(3))
+    with torch.no_grad():
+        z0 = vmonarch_attention(q, k, v, m, b, 2, recompute_tokens=b)
+    z1 = vmonarch_attention(q.requires_grad_(), k, v, m, b, 2, recompute_tokens=b)
+    assert torch.equal(z0, z1.detach())
+
+
+def test_vmonarch_grad_accumulates_into_leaf_grads():
+    from vmonarch_amd import VMonarchAttention
+    g = torch.Generator().manual_seed(6)
+    m, b = 4, 64
+    q, k, v = (randn_lp(g, 1, 1, m * b, 64).to(DEV).requires_grad_() for _ in range(3))
+    mod = VMonarchAttention(m, b, 2)
+    mod(q, k, v, recompute_tokens=b).float().square().sum().backward()
+    grads1 = [t.grad.clone() for t in (q, k, v)]
+    mod(q, k, v, recompute_tokens=b).float().square().sum().backward()
+    for t, g1 in zip((q, k, v), grads1):
+        assert torch.isfinite(t.grad.float()).all()
+        torch.testing.assert_close(t.grad.float(), 2 * g1.float(), rtol=1e-2, atol=1e-2)

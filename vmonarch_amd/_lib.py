@@ -12,7 +12,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libvmonarch_gfx950.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 DTYPES = {torch.bfloat16: 0, torch.float16: 1}
 
 c_int32, c_int64, c_float, c_void_p, c_size_t = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
@@ -54,6 +54,15 @@ class LstepArgs(ctypes.Structure):
     ]
 
 
+class LstepBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", c_int32), ("batch", c_int32), ("heads", c_int32), ("num_blocks", c_int32),
+        ("block_size", c_int32), ("d", c_int32), ("dv", c_int32), ("last", c_int32), ("skip_tokens", c_int32),
+        ("q", View), ("out", View), ("ent", c_void_p), ("ent_stride_b", c_int64), ("ent_stride_h", c_int64),
+        ("grad_res", View), ("grad_q", View), ("grad_out", View), ("scale", c_float), ("min_col_mass", c_float),
+    ]
+
+
 _lock = threading.Lock()
 _lib = None
 
@@ -77,6 +86,8 @@ def lib():
         L.vmo_fea_fwd.argtypes = [ctypes.POINTER(FeaFwdArgs), c_void_p]
         L.vmo_lstep_fwd.restype = ctypes.c_int
         L.vmo_lstep_fwd.argtypes = [ctypes.POINTER(LstepArgs), c_void_p]
+        L.vmo_lstep_bwd.restype = ctypes.c_int
+        L.vmo_lstep_bwd.argtypes = [ctypes.POINTER(LstepBwdArgs), c_void_p]
         L.vmo_fea_bwd_workspace_size.restype = c_size_t
         L.vmo_fea_bwd_workspace_size.argtypes = [ctypes.POINTER(FeaBwdArgs)]
         L.vmo_fea_bwd.restype = ctypes.c_int

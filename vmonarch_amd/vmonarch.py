@@ -22,6 +22,7 @@ import torch.nn as nn
 
 from . import _lib
 from .kernel import fea_forward, flash_entropy_attention
+from .kernel_bwd import fea_backward_raw
 
 # number of CUs on an MI355X; the recompute picks its split-KV count to fill them
 _NUM_CUS = 256
@@ -63,6 +64,24 @@ def _lstep_launch(q, out, ent, res, m, b, scale, last, skip, min_col_mass):
     a.ent_stride_b, a.ent_stride_h = ent.stride(0), ent.stride(1)
     a.scale, a.min_col_mass = float(scale), float(min_col_mass)
     _lib.check(L.vmo_lstep_fwd(a, _lib.stream_of(q)), "vmo_lstep_fwd")
+
+
+def _lstep_bwd_launch(q, out, ent, grad_res, grad_q, grad_out, m, b, scale, last, skip, min_col_mass):
+    """Backward of one L-step (vmo_lstep_bwd): grad_q (fp32) += dL/dq, grad_out = dL/d out."""
+    L = _lib.lib()
+    B, H, N, D = q.shape
+    a = _lib.LstepBwdArgs()
+    a.dtype = _lib.DTYPES[q.dtype]
+    a.batch, a.heads, a.num_blocks, a.block_size = B, H, m, b
+    a.d = D
+    a.dv = out.shape[-1] - D if last else 0
+    a.last, a.skip_tokens = int(last), int(skip)
+    a.q, a.out, a.grad_res = _lib.view(q), _lib.view(out), _lib.view(grad_res)
+    a.grad_q, a.grad_out = _lib.view(grad_q), _lib.view(grad_out)
+    a.ent = ent.data_ptr()
+    a.ent_stride_b, a.ent_stride_h = ent.stride(0), ent.stride(1)
+    a.scale, a.min_col_mass = float(scale), float(min_col_mass)
+    _lib.check(L.vmo_lstep_bwd(a, _lib.stream_of(q)), "vmo_lstep_bwd")
 
 
 def _fused_supported(q, k, v, num_blocks):
@@ -148,6 +167,96 @@ def _vmonarch_fused(q, k, v, m, b, num_iters, recompute_tokens, min_col_mass, st
     return z
 
 
+def _hip_backward_supported(q, k, v, num_blocks):
+    # the last R-step's backward takes [k | v] as one value tensor: widths 128 or 256
+    return _fused_supported(q, k, v, num_blocks) and q.shape[-1] == v.shape[-1]
+
+
+class _VMonarchFunction(torch.autograd.Function):
+    """VMonarch attention with a HIP backward (the gradient autograd takes through vmonarch.py:41-69).
+
+    The forward is the all-HIP pipeline of _vmonarch_fused, keeping what the backward needs: every
+    R-step's input u, output, LSE and entropy, and the recompute's LSE.  The backward walks it in
+    reverse: the recompute rows through vmo_fea_bwd (rt queries against all N keys), then per
+    iteration the fused L-step backward (vmo_lstep_bwd) and the R-step's flash-entropy backward
+    (vmo_fea_bwd on the m frames of each head, values k or [k | v]; the entropy enters the L-step
+    detached, vmonarch.py:26, so its gradient is zero).  Gradients of q, k, v accumulate in fp32.
+    """
+
+    @staticmethod
+    def forward(ctx, q, k, v, m, b, num_iters, recompute_tokens, min_col_mass):
+        B, H, N, D = q.shape
+        Dv = v.shape[-1]
+        scale = D ** -0.5
+        q, k, v = (t.contiguous() for t in (q, k, v))
+        dev, dt = q.device, q.dtype
+        z = torch.empty((B, H, N, Dv), device=dev, dtype=dt)
+        rt = min(int(recompute_tokens), N)
+        saved = []
+        u = None
+        for it in range(num_iters):
+            last = it == num_iters - 1
+            x, s = (q, scale) if it == 0 else (u, 1.0)
+            out, lse, ent = fea_forward(x, k, k, v if last else None, s, frames=m)
+            if last:
+                _lstep_launch(q, out, ent, z, m, b, scale, True, rt, min_col_mass)
+            else:
+                u = torch.empty((B, H, N, D), device=dev, dtype=dt)
+                _lstep_launch(q, out, ent, u, m, b, scale, False, 0, min_col_mass)
+            saved += [x, out, lse, ent]
+        lse_rt = None
+        if rt > 0:
+            _, lse_rt, _ = fea_forward(q[:, :, :rt], k, v, None, scale, o=z[:, :, :rt], want_ent=False,
+                                       num_splits=_recompute_splits(B * H, rt, N))
+        ctx.dims = (m, b, num_iters, rt, float(min_col_mass))
+        ctx.save_for_backward(q, k, v, z, lse_rt if lse_rt is not None else z.new_empty(0), *saved)
+        return z
+
+    @staticmethod
+    def backward(ctx, dz):
+        m, b, num_iters, rt, min_col_mass = ctx.dims
+        q, k, v, z, lse_rt, *saved = ctx.saved_tensors
+        B, H, N, D = q.shape
+        Dv = v.shape[-1]
+        scale = D ** -0.5
+        dev, dt = q.device, q.dtype
+        dz = _lib.row_aligned(dz.to(dt))
+        dq = torch.zeros((B, H, N, D), device=dev, dtype=torch.float32)
+        dk = torch.zeros((B, H, N, D), device=dev, dtype=torch.float32)
+        dv = torch.zeros((B, H, N, Dv), device=dev, dtype=torch.float32)
+        if rt > 0:
+            # exact attention of the first rt queries (vmonarch.py:66-68)
+            zeros = torch.zeros((B, H, rt), device=dev, dtype=torch.float32)
+            gq, gk, gv = fea_backward_raw(q[:, :, :rt], k, v, z[:, :, :rt], lse_rt, zeros,
+                                          _lib.row_aligned(dz[:, :, :rt]), zeros, scale)
+            dq[:, :, :rt] += gq
+            dk += gk
+            dv += gv
+        frames = lambda t: t.reshape(B, H * m, b, *t.shape[3:])   # the R-step's m frames per head
+        de = torch.zeros((B, H * m, b), device=dev, dtype=torch.float32)
+        g = dz
+        for it in reversed(range(num_iters)):
+            last = it == num_iters - 1
+            x, out, lse, ent = saved[4 * it: 4 * it + 4]
+            dout = torch.empty_like(out)
+            _lstep_bwd_launch(q, out, ent, g, dq, dout, m, b, scale, last, rt if last else 0, min_col_mass)
+            w = torch.cat([k, v], -1) if last else k
+            gx, gk, gw = fea_backward_raw(frames(x), frames(k), frames(w), frames(out), frames(lse),
+                                          frames(ent), frames(dout), de, scale if it == 0 else 1.0)
+            dk += gk.view(B, H, N, D)
+            gw = gw.view(B, H, N, -1)
+            if last:
+                dk += gw[..., :D]
+                dv += gw[..., D:]
+            else:
+                dk += gw
+            if it == 0:
+                dq += gx.view(B, H, N, D)   # R-step 0 read q with the softmax scale folded in
+            else:
+                g = gx.view(B, H, N, D)     # dL/du of the previous L-step's output
+        return dq.to(dt), dk.to(dt), dv.to(dt), None, None, None, None, None
+
+
 def _vmonarch_composed(q, k, v, num_blocks, block_size, num_iters, recompute_tokens, min_col_mass):
     """Step-by-step restatement of vmonarch.py:41-69 on GPU tensors (autograd-capable)."""
     B, H, N, D = q.shape
@@ -192,9 +301,12 @@ def vmonarch_attention(q, k, v, num_blocks, block_size, num_iters=2, recompute_t
     if num_iters < 1:
         raise UnboundLocalError("local variable 'z' referenced before assignment")  # as the reference (vmonarch.py:65)
     needs_graph = torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v))
-    if (not needs_graph and _row_block_attention is _ROW_BLOCK_ATTENTION
-            and _fused_supported(q, k, v, num_blocks)):
-        return _vmonarch_fused(q, k, v, num_blocks, block_size, num_iters, recompute_tokens, min_col_mass)
+    if _row_block_attention is _ROW_BLOCK_ATTENTION:
+        if not needs_graph and _fused_supported(q, k, v, num_blocks):
+            return _vmonarch_fused(q, k, v, num_blocks, block_size, num_iters, recompute_tokens, min_col_mass)
+        if needs_graph and _hip_backward_supported(q, k, v, num_blocks):
+            return _VMonarchFunction.apply(q, k, v, num_blocks, block_size, num_iters, recompute_tokens,
+                                           min_col_mass)
     if not q.is_cuda:
         raise RuntimeError("vmonarch_amd: vmonarch_attention needs GPU tensors (no CPU path)")
     return _vmonarch_composed(q, k, v, num_blocks, block_size, num_iters, recompute_tokens, min_col_mass)
