@@ -100,6 +100,59 @@ def measured_traffic(kernel_key):
         return None
 
 
+def backward_timings(steps):
+    """Training-side timings (not `value`): the cfg4 VMonarch step with autograd (HIP forward that
+    keeps its activations, then the HIP backward: fused L-step backward + flash-entropy backward)
+    and the cfg5 flash-entropy forward + backward, (1, 24, 16384, 128) bf16.  Events on the
+    current stream around each half, `steps` timed steps after one warm-up."""
+    import torch
+    from vmonarch_amd import flash_entropy_attention, vmonarch_attention
+
+    dev = torch.device("cuda:0")
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+
+    def timed(fwd, grads_of):
+        out = fwd()
+        torch.autograd.grad(*grads_of(out))
+        torch.cuda.synchronize()
+        tf = tb = 0.0
+        for _ in range(steps):
+            ev[0].record()
+            out = fwd()
+            ev[1].record()
+            torch.autograd.grad(*grads_of(out))
+            ev[2].record()
+            torch.cuda.synchronize()
+            tf += ev[0].elapsed_time(ev[1])
+            tb += ev[1].elapsed_time(ev[2])
+        return tf / steps, tb / steps
+
+    g = torch.Generator().manual_seed(0)
+    q = (torch.randn(B, H, N, D, generator=g) * 0.5).bfloat16().to(dev).requires_grad_()
+    k = (torch.randn(B, H, N, D, generator=g) * 0.5).bfloat16().to(dev).requires_grad_()
+    v = torch.randn(B, H, N, DV, generator=g).bfloat16().to(dev).requires_grad_()
+    dz = torch.randn(B, H, N, DV, generator=g).bfloat16().to(dev)
+    f4, b4 = timed(lambda: vmonarch_attention(q, k, v, M, BS, ITERS, recompute_tokens=RT),
+                   lambda z: (z, (q, k, v), dz))
+    del q, k, v, dz
+    # cfg5: FEA (1, 24, 16384, 128), loss = sum(o * dO) + sum(e * dE) as tests/test_vmonarch.py:35
+    B5, H5, N5, D5 = 1, 24, 16384, 128
+    g = torch.Generator().manual_seed(0)
+    q5, k5, v5 = (torch.randn(B5, H5, N5, D5, generator=g).bfloat16().to(dev).requires_grad_() for _ in range(3))
+    do5 = torch.randn(B5, H5, N5, D5, generator=g).bfloat16().to(dev)
+    de5 = torch.randn(B5, H5, N5, generator=g).to(dev)
+    f5, b5 = timed(lambda: flash_entropy_attention(q5, k5, v5), lambda oe: (oe, (q5, k5, v5), (do5, de5)))
+    fwd_flop = 4.0 * B5 * H5 * N5 * N5 * D5
+    bwd_flop = 2.5 * fwd_flop   # algorithmic (S, dP, dV, dK, dQ); the kernels recompute S and dP twice
+    return {
+        "vmonarch_cfg4": {"fwd_with_activations_ms": round(f4, 4), "bwd_ms": round(b4, 4)},
+        "fea_cfg5": {"shape": [B5, H5, N5, D5], "fwd_ms": round(f5, 4), "bwd_ms": round(b5, 4),
+                     "fwd_tflops": round(fwd_flop / f5 / 1e9, 1), "bwd_tflops": round(bwd_flop / b5 / 1e9, 1),
+                     "bwd_frac_mfma_peak": round(bwd_flop / b5 / 1e9 / PEAK_BF16_TFLOPS, 4)},
+        "steps": steps,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -108,6 +161,8 @@ def main():
     ap.add_argument("--cpu-heads", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--no-backward", action="store_true",
+                    help="skip the backward measurements (cfg4 VMonarch fwd+bwd, cfg5 FEA fwd+bwd)")
     ap.add_argument("--serial-only", action="store_true",
                     help="time only the serial order (every launch alone; for kernel traces)")
     args = ap.parse_args()
@@ -236,6 +291,9 @@ def main():
                      "all_rstep_frac": round(sum(r_flops) / fea_ms / 1e9 / PEAK_BF16_TFLOPS, 4)},
         "kernels": kernels,
     }
+    if not args.no_backward:
+        del q, k, v
+        result["backward"] = backward_timings(max(3, args.steps // 5))
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_heads)
     print(json.dumps(result), flush=True)

@@ -56,9 +56,12 @@ struct BwdParams {
   float sm_scale;
 };
 
+// Copy rows row0 .. row0 + ROWS - 1 (clamped to nrows - 1) of a row-major (token, W) tensor into an
+// LDS tile with the 64-bank chunk swizzle swz_rows<2 W>, by the 4 waves together.  The copies are
+// asynchronous (dma16_async); the caller orders them with tile_sync<>.
 template <class T, int W, int ROWS>
 __device__ __forceinline__ void stage_rows_n(const T* __restrict__ base, int64_t sn, int row0, int nrows,
-                                             VMO_LDS char* dst, int wave, int lane) {
+                                             uint32_t dst, int wave, int lane) {
   constexpr int CH = W / 8;
   constexpr int RPI = 64 / CH;
   constexpr int NI = ROWS / RPI;          // wave instructions for the whole tile
@@ -67,16 +70,36 @@ __device__ __forceinline__ void stage_rows_n(const T* __restrict__ base, int64_t
   for (int i = 0; i < NI / kBwdWaves; ++i) {
     const int inst = i * kBwdWaves + wave;
     const int r = inst * RPI + lane / CH;
-    const int lc = (lane % CH) ^ swz(r);
+    const int lc = (lane % CH) ^ swz_rows<W * 2>(r);
     int gr = row0 + r;
     gr = gr < nrows ? gr : nrows - 1;
-    g2l_16(base + (int64_t)gr * sn + lc * 8, dst + inst * 1024);
+    dma16_async(base + (int64_t)gr * sn + lc * 8, dst + inst * 1024);
   }
+}
+
+// Byte offset, within a 32-row block of a row-major LDS tile with RB-byte rows, of this lane's
+// first ds_read_tr16_b64 for accumulator block a (rows trow and trow + 4 of the 4-row groups); the
+// second read of the pair is 8 rows down at (offset ^ 32), since swz_rows(r + 8) = swz_rows(r) ^ 2.
+template <int RB>
+__device__ __forceinline__ int tr_offset(int trow, int tchunk, int tbyte, int a) {
+  return trow * RB + (((4 * a + tchunk) ^ swz_rows<RB>(trow)) * 16 + tbyte);
+}
+template <class V8, int RB>
+__device__ __forceinline__ V8 tr_pair(const VMO_LDS char* block16, int c0) {
+  return lds_read_tr8<V8>(block16 + c0, block16 + 8 * RB + (c0 ^ 32));
 }
 
 // Waves per SIMD the register budget is sized for: wide value heads keep more accumulators live.
 template <int D, int DV>
 constexpr int bwd_waves_per_simd() { return D + DV > 256 ? 1 : 2; }
+// dkdv variants that read the V operand of dP = dO V^T from an LDS copy of the workgroup's 128 V rows
+// instead of holding it in registers (128 / 128 and the 256-wide value variants would otherwise spill).
+template <int D, int DV>
+constexpr bool dkdv_v_in_lds() { return D + DV >= 256; }
+template <int D, int DV>
+constexpr int dkdv_lds_bytes() {
+  return 2 * (kKvBM * (D + DV) * 2 + 512) + (dkdv_v_in_lds<D, DV>() ? kKvBN * DV * 2 : 0);
+}
 
 __device__ __forceinline__ int xcd_remap(int nblocks) {
   const int per_xcd = nblocks >> 3;
@@ -143,8 +166,9 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
   }
 
   const int n_tiles = (p.nk + kDqBN - 1) / kDqBN;
+  const uint32_t smem_u32 = (uint32_t)(uintptr_t)smem;
   auto issue = [&](int t) {
-    VMO_LDS char* st = smem + (t & 1) * STAGE;
+    const uint32_t st = smem_u32 + (uint32_t)((t & 1) * STAGE);
     stage_rows_n<T, D, kDqBN>(kb, p.k_sn, t * kDqBN, p.nk, st, wave, lane);
     stage_rows_n<T, DV, kDqBN>(vb, p.v_sn, t * kDqBN, p.nk, st + K_BYTES, wave, lane);
   };
@@ -153,16 +177,14 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
 #pragma unroll
   for (int a = 0; a < NA; ++a) acc[a] = f32x16{};
   const float c = p.c;
-  const int srow_sw = swz(l32);
+  const int ksw = swz_rows<D * 2>(l32), vsw = swz_rows<DV * 2>(l32);
   const int trow = 4 * hl + ((lane & 15) >> 2);
-  const int tsw = swz(trow);
   const int tchunk = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
   const int tbyte = (lane & 1) * 8;
 
   issue(0);
   for (int t = 0; t < n_tiles; ++t) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    tile_sync<0>();   // stage t has landed for every wave, and stage t - 1's slot is free
     if (t + 1 < n_tiles) issue(t + 1);
     if (!wave_live) continue;
     const VMO_LDS char* Ks = smem + (t & 1) * STAGE;
@@ -176,10 +198,10 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
       const VMO_LDS char* vrow = Vs + (32 * kb2 + l32) * (DV * 2);
 #pragma unroll
       for (int ds = 0; ds < D / 16; ++ds)
-        s[kb2] = E::mfma(lds_read8<V8>(krow + ((2 * ds + hl) ^ srow_sw) * 16), qf[ds], s[kb2]);
+        s[kb2] = E::mfma(lds_read8<V8>(krow + ((2 * ds + hl) ^ ksw) * 16), qf[ds], s[kb2]);
 #pragma unroll
       for (int ds = 0; ds < DV / 16; ++ds)
-        dp[kb2] = E::mfma(lds_read8<V8>(vrow + ((2 * ds + hl) ^ srow_sw) * 16), dof[ds], dp[kb2]);
+        dp[kb2] = E::mfma(lds_read8<V8>(vrow + ((2 * ds + hl) ^ vsw) * 16), dof[ds], dp[kb2]);
     }
     V8 G[4];
 #pragma unroll
@@ -194,12 +216,10 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
     }
 #pragma unroll
     for (int a = 0; a < NA; ++a) {
-      const int coff = ((4 * a + tchunk) ^ tsw) * 16 + tbyte;
+      const int c0 = tr_offset<D * 2>(trow, tchunk, tbyte, a);
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const VMO_LDS char* r0 = Ks + (16 * ks + trow) * (D * 2) + coff;
-        acc[a] = E::mfma(lds_read_tr8<V8>(r0, r0 + 8 * D * 2), G[ks], acc[a]);
-      }
+      for (int ks = 0; ks < 4; ++ks)
+        acc[a] = E::mfma(tr_pair<V8, D * 2>(Ks + 16 * ks * (D * 2), c0), G[ks], acc[a]);
     }
   }
   if (!wave_live || !qvalid) return;
@@ -227,6 +247,7 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dk
   constexpr int ST_BYTES = 512;                 // lse[32] | alpha[32] | beta[32] | spare
   constexpr int STAGE = Q_BYTES + DO_BYTES + ST_BYTES;
   constexpr int NK = D / 32, NV = DV / 32;
+  constexpr bool V_LDS = dkdv_v_in_lds<D, DV>();
   extern __shared__ __attribute__((aligned(1024))) char smem_raw[];
   VMO_LDS char* smem = (VMO_LDS char*)smem_raw;
 
@@ -241,15 +262,25 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dk
   const bool kvalid = krow < p.nk;
   const int kr = kvalid ? krow : p.nk - 1;
 
-  // K^T and V^T as B operands (one key per lane)
-  V8 kf[D / 16], vf[DV / 16];
+  // K^T and V^T as B operands (one key per lane); V^T from LDS in the V_LDS variants
+  V8 kf[D / 16], vf[V_LDS ? 1 : DV / 16];
   {
     const T* kp = (const T*)p.k + bb * p.k_sb + hh * p.k_sh + (int64_t)kr * p.k_sn + hl * 8;
     const T* vp = (const T*)p.v + bb * p.v_sb + hh * p.v_sh + (int64_t)kr * p.v_sn + hl * 8;
 #pragma unroll
-    for (int ds = 0; ds < D / 16; ++ds) kf[ds] = *(const V8*)(kp + ds * 16);
+    for (int ds = 0; ds < D / 16; ++ds) {
+      kf[ds] = *(const V8*)(kp + ds * 16);
+      // opaque to the optimiser: otherwise it re-loads K inside the loop under register pressure,
+      // and those loads' waits would also wait for the tile copies in flight
+      asm volatile("" : "+v"(kf[ds]));
+    }
+    if constexpr (!V_LDS) {
 #pragma unroll
-    for (int ds = 0; ds < DV / 16; ++ds) vf[ds] = *(const V8*)(vp + ds * 16);
+      for (int ds = 0; ds < DV / 16; ++ds) {
+        vf[ds] = *(const V8*)(vp + ds * 16);
+        asm volatile("" : "+v"(vf[ds]));   // as kf: waited for here, not inside the loop
+      }
+    }
   }
   const T* qb = (const T*)p.q + bb * p.q_sb + hh * p.q_sh;
   const T* dob = (const T*)p.dO + bb * p.do_sb + hh * p.do_sh;
@@ -258,8 +289,9 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dk
   const float* beb = p.beta + (int64_t)prob * p.nq;
 
   const int n_tiles = (p.nq + kKvBM - 1) / kKvBM;
+  const uint32_t smem_u32 = (uint32_t)(uintptr_t)smem;
   auto issue = [&](int t) {
-    VMO_LDS char* st = smem + (t & 1) * STAGE;
+    const uint32_t st = smem_u32 + (uint32_t)((t & 1) * STAGE);
     const int row0 = t * kKvBM;
     stage_rows_n<T, D, kKvBM>(qb, p.q_sn, row0, p.nq, st, wave, lane);
     stage_rows_n<T, DV, kKvBM>(dob, p.do_sn, row0, p.nq, st + Q_BYTES, wave, lane);
@@ -267,8 +299,8 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dk
       int qi = row0 + l32;
       qi = qi < p.nq ? qi : p.nq - 1;
       const float* src = hl ? alb + qi : lseb + qi;
-      __builtin_amdgcn_global_load_lds(src, st + Q_BYTES + DO_BYTES, 4, 0, 0);
-      __builtin_amdgcn_global_load_lds(beb + qi, st + Q_BYTES + DO_BYTES + 256, 4, 0, 0);
+      dma4_async(src, st + Q_BYTES + DO_BYTES);
+      dma4_async(beb + qi, st + Q_BYTES + DO_BYTES + 256);
     }
   };
 
@@ -278,16 +310,18 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dk
 #pragma unroll
   for (int a = 0; a < NV; ++a) dv[a] = f32x16{};
   const float c = p.c;
-  const int srow_sw = swz(l32);
+  const int qsw = swz_rows<D * 2>(l32), dsw = swz_rows<DV * 2>(l32);
   const int trow = 4 * hl + ((lane & 15) >> 2);
-  const int tsw = swz(trow);
   const int tchunk = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
   const int tbyte = (lane & 1) * 8;
 
+  const VMO_LDS char* vt_row = smem + 2 * STAGE + (wave * 32 + l32) * (DV * 2);
+  if constexpr (V_LDS)   // this workgroup's 128 V rows, once (landed by the first tile_sync)
+    stage_rows_n<T, DV, kKvBN>((const T*)p.v + bb * p.v_sb + hh * p.v_sh, p.v_sn, kt * kKvBN, p.nk,
+                               smem_u32 + 2 * STAGE, wave, lane);
   issue(0);
   for (int t = 0; t < n_tiles; ++t) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    tile_sync<0>();   // stage t has landed for every wave, and stage t - 1's slot is free
     if (t + 1 < n_tiles) issue(t + 1);
     if (!wave_live) continue;
     const VMO_LDS char* Qs = smem + (t & 1) * STAGE;
@@ -301,9 +335,13 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dk
       const VMO_LDS char* qrow = Qs + l32 * (D * 2);
       const VMO_LDS char* drow = dOs + l32 * (DV * 2);
 #pragma unroll
-      for (int ds = 0; ds < D / 16; ++ds) s = E::mfma(lds_read8<V8>(qrow + ((2 * ds + hl) ^ srow_sw) * 16), kf[ds], s);
+      for (int ds = 0; ds < D / 16; ++ds) s = E::mfma(lds_read8<V8>(qrow + ((2 * ds + hl) ^ qsw) * 16), kf[ds], s);
 #pragma unroll
-      for (int ds = 0; ds < DV / 16; ++ds) dp = E::mfma(lds_read8<V8>(drow + ((2 * ds + hl) ^ srow_sw) * 16), vf[ds], dp);
+      for (int ds = 0; ds < DV / 16; ++ds) {
+        const int off = ((2 * ds + hl) ^ dsw) * 16;
+        const V8 vop = V_LDS ? lds_read8<V8>(vt_row + off) : vf[V_LDS ? 0 : ds];
+        dp = E::mfma(lds_read8<V8>(drow + off), vop, dp);
+      }
     }
     V8 P[2], G[2];
 #pragma unroll
@@ -325,21 +363,15 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dk
     // dV^T[dv][key] += dO^T P,  dK^T[d][key] += Q^T dS  (transposed reads of the staged tiles)
 #pragma unroll
     for (int a = 0; a < NV; ++a) {
-      const int coff = ((4 * a + tchunk) ^ tsw) * 16 + tbyte;
+      const int c0 = tr_offset<DV * 2>(trow, tchunk, tbyte, a);
 #pragma unroll
-      for (int ss = 0; ss < 2; ++ss) {
-        const VMO_LDS char* r0 = dOs + (16 * ss + trow) * (DV * 2) + coff;
-        dv[a] = E::mfma(lds_read_tr8<V8>(r0, r0 + 8 * DV * 2), P[ss], dv[a]);
-      }
+      for (int ss = 0; ss < 2; ++ss) dv[a] = E::mfma(tr_pair<V8, DV * 2>(dOs + 16 * ss * (DV * 2), c0), P[ss], dv[a]);
     }
 #pragma unroll
     for (int a = 0; a < NK; ++a) {
-      const int coff = ((4 * a + tchunk) ^ tsw) * 16 + tbyte;
+      const int c0 = tr_offset<D * 2>(trow, tchunk, tbyte, a);
 #pragma unroll
-      for (int ss = 0; ss < 2; ++ss) {
-        const VMO_LDS char* r0 = Qs + (16 * ss + trow) * (D * 2) + coff;
-        dk[a] = E::mfma(lds_read_tr8<V8>(r0, r0 + 8 * D * 2), G[ss], dk[a]);
-      }
+      for (int ss = 0; ss < 2; ++ss) dk[a] = E::mfma(tr_pair<V8, D * 2>(Qs + 16 * ss * (D * 2), c0), G[ss], dk[a]);
     }
   }
   if (!wave_live || !kvalid) return;
@@ -368,8 +400,8 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dk
 template <bool F16, int D, int DV>
 static int launch_bwd(const BwdParams& p, hipStream_t s) {
   constexpr int LDS_DQ = 2 * kDqBN * (D + DV) * 2;
-  constexpr int LDS_KV = 2 * (kKvBM * (D + DV) * 2 + 512);
-  static_assert(LDS_DQ <= 160 * 1024 && LDS_KV <= 65536, "bwd LDS");
+  constexpr int LDS_KV = dkdv_lds_bytes<D, DV>();
+  static_assert(LDS_DQ <= 160 * 1024 && LDS_KV <= 160 * 1024, "bwd LDS");
   if (LDS_DQ > 65536) {
     static bool done = false;
     if (!done) {
@@ -382,6 +414,15 @@ static int launch_bwd(const BwdParams& p, hipStream_t s) {
   hipLaunchKernelGGL((fea_bwd_dq_kernel<F16, D, DV>), dim3(xcd_grid(p.dq_total)), dim3(256), LDS_DQ, s, p);
   int rc = launch_status("fea_bwd_dq");
   if (rc != VMO_OK) return rc;
+  if (LDS_KV > 65536) {
+    static bool done = false;
+    if (!done) {
+      if (hipFuncSetAttribute((const void*)fea_bwd_dkdv_kernel<F16, D, DV>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, LDS_KV) != hipSuccess)
+        return set_error(VMO_ERR_LAUNCH, "fea_bwd_dkdv: cannot raise the LDS limit to %d bytes", LDS_KV);
+      done = true;
+    }
+  }
   hipLaunchKernelGGL((fea_bwd_dkdv_kernel<F16, D, DV>), dim3(xcd_grid(p.kv_total)), dim3(256), LDS_KV, s, p);
   return launch_status("fea_bwd_dkdv");
 }

@@ -110,6 +110,13 @@ __device__ __forceinline__ void dma16_async(const void* g, uint32_t lds_wave_bas
                : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_wave_base))
                : "m0");
 }
+// 4-byte variant of dma16_async: lane l copies one dword to lds_wave_base + 4 * l.
+__device__ __forceinline__ void dma4_async(const void* g, uint32_t lds_wave_base) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off"
+               :
+               : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_wave_base))
+               : "m0");
+}
 // A wave-uniform 64-bit value, moved to scalar registers (the compiler may otherwise keep a
 // uniform pointer in VGPRs and do its address arithmetic on the vector unit).
 __device__ __forceinline__ uint64_t uniform64(uint64_t v) {
