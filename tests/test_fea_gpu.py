@@ -171,7 +171,7 @@ def _check_grads(grads, refs, tol=3e-2):
 
 
 @pytest.mark.parametrize("N", [128, 200, 1024])
-@pytest.mark.parametrize("D, Dv", [(64, 64), (128, 128), (64, 128), (128, 256)])
+@pytest.mark.parametrize("D, Dv", [(64, 64), (128, 128), (64, 128), (128, 64), (128, 256), (64, 256)])
 def test_fea_backward_reference_params(N, D, Dv):
     """tests/test_vmonarch.py:27-42: loss = sum(o * do) + sum(e * de); grads within 3e-2."""
     from oracle import entropy_attention_grad

@@ -91,14 +91,31 @@ __device__ __forceinline__ V8 tr_pair(const VMO_LDS char* block16, int c0) {
 
 // Waves per SIMD the register budget is sized for: wide value heads keep more accumulators live.
 template <int D, int DV>
-constexpr int bwd_waves_per_simd() { return D + DV > 256 ? 1 : 2; }
+constexpr int bwd_waves_per_simd() { return D + DV > 320 ? 1 : 2; }
+
+// The dkdv kernel for 256-wide values runs as two launches (PART 1: dK and dV[:, :128], with dP over
+// all 256 value columns; PART 2: dV[:, 128:] from P alone): one launch holding dK and the whole dV
+// needs ~290 accumulator and operand registers, and the compiler then moves every accumulator
+// between AGPRs and VGPRs around each MFMA.  PART 0 is the single launch of the narrower variants.
+template <int DV>
+constexpr int dkdv_parts() { return DV > 128 ? 2 : 1; }
+template <int DV, int PART>
+constexpr int dkdv_do_width() { return PART == 2 ? DV / 2 : DV; }   // dO columns staged per stage
+template <int DV, int PART>
+constexpr int dkdv_dv_width() { return PART == 0 ? DV : DV / 2; }   // dV columns accumulated
 // dkdv variants that read the V operand of dP = dO V^T from an LDS copy of the workgroup's 128 V rows
 // instead of holding it in registers (128 / 128 and the 256-wide value variants would otherwise spill).
-template <int D, int DV>
-constexpr bool dkdv_v_in_lds() { return D + DV >= 256; }
-template <int D, int DV>
+template <int D, int DV, int PART>
+constexpr bool dkdv_v_in_lds() { return PART != 2 && D + DV >= 256; }
+// ... and of K for S = Q K^T, in the first part of the 128 / 256 variant
+template <int D, int DV, int PART>
+constexpr bool dkdv_k_in_lds() { return PART == 1 && D + DV > 320; }
+template <int D, int DV, int PART>
+constexpr int dkdv_waves_per_simd() { return PART != 0 ? 2 : bwd_waves_per_simd<D, DV>(); }
+template <int D, int DV, int PART>
 constexpr int dkdv_lds_bytes() {
-  return 2 * (kKvBM * (D + DV) * 2 + 512) + (dkdv_v_in_lds<D, DV>() ? kKvBN * DV * 2 : 0);
+  return 2 * (kKvBM * (D + dkdv_do_width<DV, PART>()) * 2 + 512) +
+         (dkdv_v_in_lds<D, DV, PART>() ? kKvBN * DV * 2 : 0) + (dkdv_k_in_lds<D, DV, PART>() ? kKvBN * D * 2 : 0);
 }
 
 __device__ __forceinline__ int xcd_remap(int nblocks) {
@@ -236,18 +253,23 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
 }
 
 // ------------------------------------------------------------------------------------------------
-template <bool F16, int D, int DV>
-__global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dkdv_kernel(BwdParams p) {
+template <bool F16, int D, int DV, int PART>
+__global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea_bwd_dkdv_kernel(BwdParams p) {
   using E = Elem<F16>;
   using T = typename E::T;
   using V8 = typename E::V8;
   using V4 = typename E::V4;
+  constexpr int DOW = dkdv_do_width<DV, PART>();
+  constexpr int VOFF = PART == 2 ? DV / 2 : 0;  // first dV (and staged dO) column of this launch
+  constexpr bool WANT_DK = PART != 2;           // dK, and with it dP and dS
   constexpr int Q_BYTES = kKvBM * D * 2;
-  constexpr int DO_BYTES = kKvBM * DV * 2;
+  constexpr int DO_BYTES = kKvBM * DOW * 2;
   constexpr int ST_BYTES = 512;                 // lse[32] | alpha[32] | beta[32] | spare
   constexpr int STAGE = Q_BYTES + DO_BYTES + ST_BYTES;
-  constexpr int NK = D / 32, NV = DV / 32;
-  constexpr bool V_LDS = dkdv_v_in_lds<D, DV>();
+  constexpr int NK = D / 32, NV = dkdv_dv_width<DV, PART>() / 32;
+  constexpr bool V_LDS = dkdv_v_in_lds<D, DV, PART>();
+  constexpr bool K_LDS = dkdv_k_in_lds<D, DV, PART>();
+  constexpr int V_TILE = V_LDS ? kKvBN * DV * 2 : 0;
   extern __shared__ __attribute__((aligned(1024))) char smem_raw[];
   VMO_LDS char* smem = (VMO_LDS char*)smem_raw;
 
@@ -263,18 +285,18 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dk
   const int kr = kvalid ? krow : p.nk - 1;
 
   // K^T and V^T as B operands (one key per lane); V^T from LDS in the V_LDS variants
-  V8 kf[D / 16], vf[V_LDS ? 1 : DV / 16];
+  V8 kf[K_LDS ? 1 : D / 16], vf[(V_LDS || !WANT_DK) ? 1 : DV / 16];
   {
     const T* kp = (const T*)p.k + bb * p.k_sb + hh * p.k_sh + (int64_t)kr * p.k_sn + hl * 8;
     const T* vp = (const T*)p.v + bb * p.v_sb + hh * p.v_sh + (int64_t)kr * p.v_sn + hl * 8;
 #pragma unroll
-    for (int ds = 0; ds < D / 16; ++ds) {
+    for (int ds = 0; ds < (K_LDS ? 0 : D / 16); ++ds) {
       kf[ds] = *(const V8*)(kp + ds * 16);
       // opaque to the optimiser: otherwise it re-loads K inside the loop under register pressure,
       // and those loads' waits would also wait for the tile copies in flight
       asm volatile("" : "+v"(kf[ds]));
     }
-    if constexpr (!V_LDS) {
+    if constexpr (!V_LDS && WANT_DK) {
 #pragma unroll
       for (int ds = 0; ds < DV / 16; ++ds) {
         vf[ds] = *(const V8*)(vp + ds * 16);
@@ -294,7 +316,7 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dk
     const uint32_t st = smem_u32 + (uint32_t)((t & 1) * STAGE);
     const int row0 = t * kKvBM;
     stage_rows_n<T, D, kKvBM>(qb, p.q_sn, row0, p.nq, st, wave, lane);
-    stage_rows_n<T, DV, kKvBM>(dob, p.do_sn, row0, p.nq, st + Q_BYTES, wave, lane);
+    stage_rows_n<T, DOW, kKvBM>(dob + VOFF, p.do_sn, row0, p.nq, st + Q_BYTES, wave, lane);
     if (wave == 0) {   // per-query scalars: lanes 0-31 lse, 32-63 alpha; then beta
       int qi = row0 + l32;
       qi = qi < p.nq ? qi : p.nq - 1;
@@ -310,15 +332,19 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dk
 #pragma unroll
   for (int a = 0; a < NV; ++a) dv[a] = f32x16{};
   const float c = p.c;
-  const int qsw = swz_rows<D * 2>(l32), dsw = swz_rows<DV * 2>(l32);
+  const int qsw = swz_rows<D * 2>(l32), dsw = swz_rows<DOW * 2>(l32);
   const int trow = 4 * hl + ((lane & 15) >> 2);
   const int tchunk = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
   const int tbyte = (lane & 1) * 8;
 
   const VMO_LDS char* vt_row = smem + 2 * STAGE + (wave * 32 + l32) * (DV * 2);
+  const VMO_LDS char* kt_row = smem + 2 * STAGE + V_TILE + (wave * 32 + l32) * (D * 2);
   if constexpr (V_LDS)   // this workgroup's 128 V rows, once (landed by the first tile_sync)
     stage_rows_n<T, DV, kKvBN>((const T*)p.v + bb * p.v_sb + hh * p.v_sh, p.v_sn, kt * kKvBN, p.nk,
                                smem_u32 + 2 * STAGE, wave, lane);
+  if constexpr (K_LDS)   // and its 128 K rows
+    stage_rows_n<T, D, kKvBN>((const T*)p.k + bb * p.k_sb + hh * p.k_sh, p.k_sn, kt * kKvBN, p.nk,
+                              smem_u32 + 2 * STAGE + V_TILE, wave, lane);
   issue(0);
   for (int t = 0; t < n_tiles; ++t) {
     tile_sync<0>();   // stage t has landed for every wave, and stage t - 1's slot is free
@@ -333,14 +359,20 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dk
     f32x16 s = f32x16{}, dp = f32x16{};
     {
       const VMO_LDS char* qrow = Qs + l32 * (D * 2);
-      const VMO_LDS char* drow = dOs + l32 * (DV * 2);
 #pragma unroll
-      for (int ds = 0; ds < D / 16; ++ds) s = E::mfma(lds_read8<V8>(qrow + ((2 * ds + hl) ^ qsw) * 16), kf[ds], s);
+      for (int ds = 0; ds < D / 16; ++ds) {
+        const int off = ((2 * ds + hl) ^ qsw) * 16;
+        const V8 kop = K_LDS ? lds_read8<V8>(kt_row + off) : kf[K_LDS ? 0 : ds];
+        s = E::mfma(lds_read8<V8>(qrow + off), kop, s);
+      }
+      if constexpr (WANT_DK) {
+        const VMO_LDS char* drow = dOs + l32 * (DOW * 2);
 #pragma unroll
-      for (int ds = 0; ds < DV / 16; ++ds) {
-        const int off = ((2 * ds + hl) ^ dsw) * 16;
-        const V8 vop = V_LDS ? lds_read8<V8>(vt_row + off) : vf[V_LDS ? 0 : ds];
-        dp = E::mfma(lds_read8<V8>(drow + off), vop, dp);
+        for (int ds = 0; ds < DV / 16; ++ds) {
+          const int off = ((2 * ds + hl) ^ dsw) * 16;
+          const V8 vop = V_LDS ? lds_read8<V8>(vt_row + off) : vf[V_LDS ? 0 : ds];
+          dp = E::mfma(lds_read8<V8>(drow + off), vop, dp);
+        }
       }
     }
     V8 P[2], G[2];
@@ -354,7 +386,7 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dk
         const int r = 4 * g + e;
         const float x = fmaf(s[r], c, -lv[e]);
         float pv = fast_exp2(x);
-        float gv = pv * (dp[r] + fmaf(bv[e], x, av[e]));
+        float gv = WANT_DK ? pv * (dp[r] + fmaf(bv[e], x, av[e])) : 0.f;
         if (nvalid < kKvBM && 8 * g + 4 * hl + e >= nvalid) { pv = 0.f; gv = 0.f; }
         P[r >> 3][r & 7] = to_elem<T>(pv);
         G[r >> 3][r & 7] = to_elem<T>(gv);
@@ -363,22 +395,24 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dk
     // dV^T[dv][key] += dO^T P,  dK^T[d][key] += Q^T dS  (transposed reads of the staged tiles)
 #pragma unroll
     for (int a = 0; a < NV; ++a) {
-      const int c0 = tr_offset<DV * 2>(trow, tchunk, tbyte, a);
+      const int c0 = tr_offset<DOW * 2>(trow, tchunk, tbyte, a);
 #pragma unroll
-      for (int ss = 0; ss < 2; ++ss) dv[a] = E::mfma(tr_pair<V8, DV * 2>(dOs + 16 * ss * (DV * 2), c0), P[ss], dv[a]);
+      for (int ss = 0; ss < 2; ++ss) dv[a] = E::mfma(tr_pair<V8, DOW * 2>(dOs + 16 * ss * (DOW * 2), c0), P[ss], dv[a]);
     }
+    if constexpr (WANT_DK) {
 #pragma unroll
-    for (int a = 0; a < NK; ++a) {
-      const int c0 = tr_offset<D * 2>(trow, tchunk, tbyte, a);
+      for (int a = 0; a < NK; ++a) {
+        const int c0 = tr_offset<D * 2>(trow, tchunk, tbyte, a);
 #pragma unroll
-      for (int ss = 0; ss < 2; ++ss) dk[a] = E::mfma(tr_pair<V8, D * 2>(Qs + 16 * ss * (D * 2), c0), G[ss], dk[a]);
+        for (int ss = 0; ss < 2; ++ss) dk[a] = E::mfma(tr_pair<V8, D * 2>(Qs + 16 * ss * (D * 2), c0), G[ss], dk[a]);
+      }
     }
   }
   if (!wave_live || !kvalid) return;
   T* dkr = (T*)p.dk + bb * p.dk_sb + hh * p.dk_sh + (int64_t)krow * p.dk_sn;
-  T* dvr = (T*)p.dv + bb * p.dv_sb + hh * p.dv_sh + (int64_t)krow * p.dv_sn;
+  T* dvr = (T*)p.dv + bb * p.dv_sb + hh * p.dv_sh + (int64_t)krow * p.dv_sn + VOFF;
 #pragma unroll
-  for (int a = 0; a < NK; ++a)
+  for (int a = 0; a < (WANT_DK ? NK : 0); ++a)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       V4 x;
@@ -397,11 +431,27 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dk
     }
 }
 
+template <bool F16, int D, int DV, int PART>
+static int launch_dkdv(const BwdParams& p, hipStream_t s) {
+  constexpr int LDS_KV = dkdv_lds_bytes<D, DV, PART>();
+  static_assert(LDS_KV <= 160 * 1024, "dkdv LDS");
+  auto kern = fea_bwd_dkdv_kernel<F16, D, DV, PART>;
+  if (LDS_KV > 65536) {
+    static bool done = false;
+    if (!done) {
+      if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_KV) != hipSuccess)
+        return set_error(VMO_ERR_LAUNCH, "fea_bwd_dkdv: cannot raise the LDS limit to %d bytes", LDS_KV);
+      done = true;
+    }
+  }
+  hipLaunchKernelGGL(kern, dim3(xcd_grid(p.kv_total)), dim3(256), LDS_KV, s, p);
+  return launch_status("fea_bwd_dkdv");
+}
+
 template <bool F16, int D, int DV>
 static int launch_bwd(const BwdParams& p, hipStream_t s) {
   constexpr int LDS_DQ = 2 * kDqBN * (D + DV) * 2;
-  constexpr int LDS_KV = dkdv_lds_bytes<D, DV>();
-  static_assert(LDS_DQ <= 160 * 1024 && LDS_KV <= 160 * 1024, "bwd LDS");
+  static_assert(LDS_DQ <= 160 * 1024, "bwd LDS");
   if (LDS_DQ > 65536) {
     static bool done = false;
     if (!done) {
@@ -414,17 +464,13 @@ static int launch_bwd(const BwdParams& p, hipStream_t s) {
   hipLaunchKernelGGL((fea_bwd_dq_kernel<F16, D, DV>), dim3(xcd_grid(p.dq_total)), dim3(256), LDS_DQ, s, p);
   int rc = launch_status("fea_bwd_dq");
   if (rc != VMO_OK) return rc;
-  if (LDS_KV > 65536) {
-    static bool done = false;
-    if (!done) {
-      if (hipFuncSetAttribute((const void*)fea_bwd_dkdv_kernel<F16, D, DV>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, LDS_KV) != hipSuccess)
-        return set_error(VMO_ERR_LAUNCH, "fea_bwd_dkdv: cannot raise the LDS limit to %d bytes", LDS_KV);
-      done = true;
-    }
+  if constexpr (dkdv_parts<DV>() == 1) {
+    return launch_dkdv<F16, D, DV, 0>(p, s);
+  } else {
+    rc = launch_dkdv<F16, D, DV, 1>(p, s);
+    if (rc != VMO_OK) return rc;
+    return launch_dkdv<F16, D, DV, 2>(p, s);
   }
-  hipLaunchKernelGGL((fea_bwd_dkdv_kernel<F16, D, DV>), dim3(xcd_grid(p.kv_total)), dim3(256), LDS_KV, s, p);
-  return launch_status("fea_bwd_dkdv");
 }
 
 template <bool F16>
