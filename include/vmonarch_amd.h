@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define VMO_ABI_VERSION 2
+#define VMO_ABI_VERSION 3
 
 enum {
   VMO_OK = 0,
@@ -125,6 +125,9 @@ typedef struct vmo_lstep_args {
  * keys per (batch, head) (nq != nk allowed).  Supported: d in {64, 128}, dv in {64, 128, 256}.  Needs
  * vmo_fea_bwd_workspace_size() bytes of workspace.
  */
+/* vmo_fea_bwd_args.flags: the marked gradient is float32 and the kernels add into it (+=) */
+enum { VMO_BWD_ACCUM_Q = 1, VMO_BWD_ACCUM_K = 2, VMO_BWD_ACCUM_V = 4 };
+
 typedef struct vmo_fea_bwd_args {
   int32_t dtype;
   int32_t batch, heads;
@@ -140,6 +143,7 @@ typedef struct vmo_fea_bwd_args {
   float sm_scale;
   void* workspace;
   size_t workspace_bytes;
+  int32_t flags;                   /* VMO_BWD_ACCUM_* */
 } vmo_fea_bwd_args;
 
 /*

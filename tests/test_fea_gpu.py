@@ -225,3 +225,48 @@ def test_fea_backward_cfg5_head_sample():
                                       do[:, sl].bfloat16().float().numpy(), de[:, sl].numpy(), 128 ** -0.5,
                                       dtype=np.float32)
         _check_grads([t[:, sl] for t in grads], refs)
+
+
+@pytest.mark.parametrize("nq, nk, D, Dv", [(200, 8192, 64, 64), (130, 16000, 128, 128), (64, 4096, 128, 256)])
+def test_fea_backward_few_queries_many_keys(nq, nk, D, Dv):
+    """nq != nk with few query tiles (the shape of VMonarch's recompute backward): the dq kernel
+    splits the keys and sums fp32 partials; dE = 0 and ent = 0 as that caller passes them."""
+    from oracle import entropy_attention_grad
+    from vmonarch_amd.kernel import fea_forward
+    from vmonarch_amd.kernel_bwd import fea_backward_raw
+    g = torch.Generator().manual_seed(nq + nk)
+    q, k = randn_lp(g, 1, 2, nq, D, scale=0.5), randn_lp(g, 1, 2, nk, D, scale=0.5)
+    v, do = randn_lp(g, 1, 2, nk, Dv), randn_lp(g, 1, 2, nq, Dv)
+    qd, kd, vd, dod = (t.to(DEV) for t in (q, k, v, do))
+    o, lse, _ = fea_forward(qd, kd, vd, None, D ** -0.5)
+    zeros = torch.zeros(1, 2, nq, device=DEV)
+    print(f"fea_bwd nq={nq} nk={nk} D={D} Dv={Dv}", flush=True)
+    grads = fea_backward_raw(qd, kd, vd, o, lse, zeros, dod, zeros, D ** -0.5)
+    refs = entropy_attention_grad(q.float().numpy(), k.float().numpy(), v.float().numpy(), do.float().numpy(),
+                                  np.zeros((1, 2, nq)), D ** -0.5)
+    _check_grads(grads, refs)
+
+
+def test_fea_backward_accumulates_into_fp32_gradients():
+    """With float32 gradient views passed in, the kernels add into them (VMO_BWD_ACCUM_*): result =
+    prefill + the gradients the plain call returns, for a split-KV dq and strided column slices."""
+    from vmonarch_amd.kernel import fea_forward
+    from vmonarch_amd.kernel_bwd import fea_backward_raw
+    g = torch.Generator().manual_seed(11)
+    nq, nk, D, Dv = 96, 8192, 128, 128
+    q, k = randn_lp(g, 1, 2, nq, D, scale=0.5).to(DEV), randn_lp(g, 1, 2, nk, D, scale=0.5).to(DEV)
+    v, do = randn_lp(g, 1, 2, nk, Dv).to(DEV), randn_lp(g, 1, 2, nq, Dv).to(DEV)
+    de = torch.randn(1, 2, nq, generator=g).to(DEV)
+    o, lse, ent = fea_forward(q, k, v, None, D ** -0.5)
+    plain = fea_backward_raw(q, k, v, o, lse, ent, do, de, D ** -0.5)
+    dq0 = torch.randn(1, 2, nq, D, generator=g).to(DEV)
+    kv0 = torch.randn(1, 2, nk, D + Dv + 32, generator=g).to(DEV)   # dk | dv | spare columns
+    dq, kv = dq0.clone(), kv0.clone()
+    fea_backward_raw(q, k, v, o, lse, ent, do, de, D ** -0.5, dq=dq, dk=kv[..., :D], dv=kv[..., D:D + Dv])
+    torch.cuda.synchronize()
+    torch.testing.assert_close(dq - dq0, plain[0].float(), rtol=2e-2, atol=2e-2 * plain[0].float().abs().max().item())
+    torch.testing.assert_close(kv[..., :D] - kv0[..., :D], plain[1].float(), rtol=2e-2,
+                               atol=2e-2 * plain[1].float().abs().max().item())
+    torch.testing.assert_close(kv[..., D:D + Dv] - kv0[..., D:D + Dv], plain[2].float(), rtol=2e-2,
+                               atol=2e-2 * plain[2].float().abs().max().item())
+    assert torch.equal(kv[..., D + Dv:], kv0[..., D + Dv:])

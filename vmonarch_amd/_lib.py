@@ -12,7 +12,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libvmonarch_gfx950.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 DTYPES = {torch.bfloat16: 0, torch.float16: 1}
 
 c_int32, c_int64, c_float, c_void_p, c_size_t = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
@@ -41,8 +41,11 @@ class FeaBwdArgs(ctypes.Structure):
         ("lse", c_void_p), ("ent", c_void_p), ("grad_ent", c_void_p),
         ("stat_stride_b", c_int64), ("stat_stride_h", c_int64),
         ("grad_ent_stride_b", c_int64), ("grad_ent_stride_h", c_int64),
-        ("sm_scale", c_float), ("workspace", c_void_p), ("workspace_bytes", c_size_t),
+        ("sm_scale", c_float), ("workspace", c_void_p), ("workspace_bytes", c_size_t), ("flags", c_int32),
     ]
+
+
+BWD_ACCUM_Q, BWD_ACCUM_K, BWD_ACCUM_V = 1, 2, 4
 
 
 class LstepArgs(ctypes.Structure):

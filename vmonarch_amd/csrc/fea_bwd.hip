@@ -46,12 +46,15 @@ struct BwdParams {
   const float* dent;
   float* alpha;     // workspace (problems, nq)
   float* beta;
+  float* dq_part;   // workspace (dq_splits, problems, nq, D): split-KV partial dQ, when dq_splits > 1
   int64_t q_sb, q_sh, q_sn, k_sb, k_sh, k_sn, v_sb, v_sh, v_sn, o_sb, o_sh, o_sn, do_sb, do_sh, do_sn;
   int64_t dq_sb, dq_sh, dq_sn, dk_sb, dk_sh, dk_sn, dv_sb, dv_sh, dv_sn;
   int64_t st_sb, st_sh, de_sb, de_sh;
   int heads, nq, nk, problems;
   int dq_tiles, kv_tiles;
   int dq_total, kv_total;
+  int dq_splits, keys_per_split;   // dq workgroups per query tile, each over one key range
+  int accum;                       // VMO_BWD_ACCUM_* bits: that gradient is fp32 and accumulated into
   float c;          // sm_scale * log2(e)
   float sm_scale;
 };
@@ -138,7 +141,9 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
 
   const int L = xcd_remap(gridDim.x);
   if (L >= p.dq_total) return;
-  const int qt = L % p.dq_tiles, prob = L / p.dq_tiles;
+  const int qt = L % p.dq_tiles, split = (L / p.dq_tiles) % p.dq_splits, prob = L / p.dq_tiles / p.dq_splits;
+  const int kbeg = split * p.keys_per_split;
+  const int kend = min(p.nk, kbeg + p.keys_per_split);
   const int hh = prob % p.heads, bb = prob / p.heads;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int q0 = qt * kDqBM + wave * 32;
@@ -177,17 +182,17 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
   const float dE = p.dent[bb * p.de_sb + hh * p.de_sh + qr];
   const float alpha = -delta - dE * p.ent[si];
   const float beta = -dE * kLn2;
-  if (qvalid && hl == 0) {
+  if (qvalid && hl == 0 && split == 0) {
     p.alpha[(int64_t)prob * p.nq + qrow] = alpha;
     p.beta[(int64_t)prob * p.nq + qrow] = beta;
   }
 
-  const int n_tiles = (p.nk + kDqBN - 1) / kDqBN;
+  const int n_tiles = (kend - kbeg + kDqBN - 1) / kDqBN;
   const uint32_t smem_u32 = (uint32_t)(uintptr_t)smem;
   auto issue = [&](int t) {
     const uint32_t st = smem_u32 + (uint32_t)((t & 1) * STAGE);
-    stage_rows_n<T, D, kDqBN>(kb, p.k_sn, t * kDqBN, p.nk, st, wave, lane);
-    stage_rows_n<T, DV, kDqBN>(vb, p.v_sn, t * kDqBN, p.nk, st + K_BYTES, wave, lane);
+    stage_rows_n<T, D, kDqBN>(kb, p.k_sn, kbeg + t * kDqBN, kend, st, wave, lane);
+    stage_rows_n<T, DV, kDqBN>(vb, p.v_sn, kbeg + t * kDqBN, kend, st + K_BYTES, wave, lane);
   };
 
   f32x16 acc[NA];
@@ -206,7 +211,7 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
     if (!wave_live) continue;
     const VMO_LDS char* Ks = smem + (t & 1) * STAGE;
     const VMO_LDS char* Vs = Ks + K_BYTES;
-    const int nvalid = p.nk - t * kDqBN;
+    const int nvalid = kend - kbeg - t * kDqBN;
 
     f32x16 s[2] = {f32x16{}, f32x16{}}, dp[2] = {f32x16{}, f32x16{}};
 #pragma unroll
@@ -240,16 +245,68 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
     }
   }
   if (!wave_live || !qvalid) return;
-  T* dqr = (T*)p.dq + bb * p.dq_sb + hh * p.dq_sh + (int64_t)qrow * p.dq_sn;
+  if (p.dq_splits > 1) {   // fp32 partial of this key range; fea_bwd_dq_reduce sums the splits
+    float* pr = p.dq_part + (((int64_t)split * p.problems + prob) * p.nq + qrow) * D;
 #pragma unroll
-  for (int a = 0; a < NA; ++a)
+    for (int a = 0; a < NA; ++a)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      V4 v;
+      for (int j = 0; j < 4; ++j) {
+        f32x4 v;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = to_elem<T>(acc[a][4 * j + e] * p.sm_scale);
-      *(V4*)(dqr + 32 * a + 8 * j + 4 * hl) = v;
-    }
+        for (int e = 0; e < 4; ++e) v[e] = acc[a][4 * j + e] * p.sm_scale;
+        *(f32x4*)(pr + 32 * a + 8 * j + 4 * hl) = v;
+      }
+  } else if (p.accum & VMO_BWD_ACCUM_Q) {
+    float* dqr = (float*)p.dq + bb * p.dq_sb + hh * p.dq_sh + (int64_t)qrow * p.dq_sn;
+#pragma unroll
+    for (int a = 0; a < NA; ++a)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        f32x4* ptr = (f32x4*)(dqr + 32 * a + 8 * j + 4 * hl);
+        f32x4 v = *ptr;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += acc[a][4 * j + e] * p.sm_scale;
+        *ptr = v;
+      }
+  } else {
+    T* dqr = (T*)p.dq + bb * p.dq_sb + hh * p.dq_sh + (int64_t)qrow * p.dq_sn;
+#pragma unroll
+    for (int a = 0; a < NA; ++a)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        V4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = to_elem<T>(acc[a][4 * j + e] * p.sm_scale);
+        *(V4*)(dqr + 32 * a + 8 * j + 4 * hl) = v;
+      }
+  }
+}
+
+// Sum the split-KV partials of dQ (fixed split order, so the result does not depend on timing) and
+// write grad_q, or add them into an fp32 grad_q.
+template <bool F16, int D>
+__global__ __launch_bounds__(256) void fea_bwd_dq_reduce(BwdParams p) {
+  using T = typename Elem<F16>::T;
+  using V4 = typename Elem<F16>::V4;
+  constexpr int TPR = D / 4;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t row = gid / TPR;
+  const int c4 = (int)(gid % TPR);
+  if (row >= (int64_t)p.problems * p.nq) return;
+  const int prob = (int)(row / p.nq), qi = (int)(row % p.nq);
+  f32x4 acc = f32x4{};
+  for (int sp = 0; sp < p.dq_splits; ++sp)
+    acc += *(const f32x4*)(p.dq_part + (((int64_t)sp * p.problems + prob) * p.nq + qi) * D + 4 * c4);
+  const int hh = prob % p.heads, bb = prob / p.heads;
+  if (p.accum & VMO_BWD_ACCUM_Q) {
+    f32x4* ptr = (f32x4*)((float*)p.dq + bb * p.dq_sb + hh * p.dq_sh + (int64_t)qi * p.dq_sn + 4 * c4);
+    *ptr = *ptr + acc;
+  } else {
+    V4 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = to_elem<T>(acc[e]);
+    *(V4*)((T*)p.dq + bb * p.dq_sb + hh * p.dq_sh + (int64_t)qi * p.dq_sn + 4 * c4) = v;
+  }
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -409,26 +466,34 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
     }
   }
   if (!wave_live || !kvalid) return;
-  T* dkr = (T*)p.dk + bb * p.dk_sb + hh * p.dk_sh + (int64_t)krow * p.dk_sn;
-  T* dvr = (T*)p.dv + bb * p.dv_sb + hh * p.dv_sh + (int64_t)krow * p.dv_sn + VOFF;
+  // store (or, for an fp32 gradient with its accumulate bit, add) NACC accumulator blocks times f
+  auto put = [&](void* base, int64_t sb, int64_t sh, int64_t sn, int col0, const f32x16* acc, int nacc, float f,
+                 bool add) __attribute__((always_inline)) {
+    if (add) {
+      float* r = (float*)base + bb * sb + hh * sh + (int64_t)krow * sn + col0;
+      for (int a = 0; a < nacc; ++a)
 #pragma unroll
-  for (int a = 0; a < (WANT_DK ? NK : 0); ++a)
+        for (int j = 0; j < 4; ++j) {
+          f32x4* ptr = (f32x4*)(r + 32 * a + 8 * j + 4 * hl);
+          f32x4 v = *ptr;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      V4 x;
+          for (int e = 0; e < 4; ++e) v[e] += acc[a][4 * j + e] * f;
+          *ptr = v;
+        }
+    } else {
+      T* r = (T*)base + bb * sb + hh * sh + (int64_t)krow * sn + col0;
+      for (int a = 0; a < nacc; ++a)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) x[e] = to_elem<T>(dk[a][4 * j + e] * p.sm_scale);
-      *(V4*)(dkr + 32 * a + 8 * j + 4 * hl) = x;
+        for (int j = 0; j < 4; ++j) {
+          V4 x;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) x[e] = to_elem<T>(acc[a][4 * j + e] * f);
+          *(V4*)(r + 32 * a + 8 * j + 4 * hl) = x;
+        }
     }
-#pragma unroll
-  for (int a = 0; a < NV; ++a)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      V4 x;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) x[e] = to_elem<T>(dv[a][4 * j + e]);
-      *(V4*)(dvr + 32 * a + 8 * j + 4 * hl) = x;
-    }
+  };
+  if constexpr (WANT_DK) put(p.dk, p.dk_sb, p.dk_sh, p.dk_sn, 0, dk, NK, p.sm_scale, (p.accum & VMO_BWD_ACCUM_K) != 0);
+  put(p.dv, p.dv_sb, p.dv_sh, p.dv_sn, VOFF, dv, NV, 1.0f, (p.accum & VMO_BWD_ACCUM_V) != 0);
 }
 
 template <bool F16, int D, int DV, int PART>
@@ -464,6 +529,12 @@ static int launch_bwd(const BwdParams& p, hipStream_t s) {
   hipLaunchKernelGGL((fea_bwd_dq_kernel<F16, D, DV>), dim3(xcd_grid(p.dq_total)), dim3(256), LDS_DQ, s, p);
   int rc = launch_status("fea_bwd_dq");
   if (rc != VMO_OK) return rc;
+  if (p.dq_splits > 1) {
+    const int64_t threads = (int64_t)p.problems * p.nq * (D / 4);
+    hipLaunchKernelGGL((fea_bwd_dq_reduce<F16, D>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, p);
+    rc = launch_status("fea_bwd_dq_reduce");
+    if (rc != VMO_OK) return rc;
+  }
   if constexpr (dkdv_parts<DV>() == 1) {
     return launch_dkdv<F16, D, DV, 0>(p, s);
   } else {
@@ -486,9 +557,29 @@ static int dispatch_bwd(const BwdParams& p, int d, int dv, hipStream_t s) {
 
 }  // namespace vmo
 
+namespace vmo {
+// Key splits of the dq kernel: a problem with few query tiles and many keys (the exact recompute of
+// VMonarch: 13 query tiles per head against 32760 keys) would otherwise leave most CUs idle.
+static int bwd_dq_splits(int64_t problems, int nq, int nk) {
+  const int64_t wgs = problems * ((nq + kDqBM - 1) / kDqBM);
+  int splits = 1;
+  while (wgs * splits < 1024 && splits < 16 && nk / (splits * 2) >= 1024) splits *= 2;
+  return splits;
+}
+static int bwd_keys_per_split(int nk, int splits) {
+  return ((nk + splits - 1) / splits + kDqBN - 1) / kDqBN * kDqBN;
+}
+static size_t bwd_stats_bytes(int64_t problems, int nq) { return ((size_t)2 * problems * nq * 4 + 255) / 256 * 256; }
+}  // namespace vmo
+
 extern "C" size_t vmo_fea_bwd_workspace_size(const vmo_fea_bwd_args* a) {
-  if (!a) return 0;
-  return (size_t)2 * a->batch * a->heads * (size_t)(a->nq > 0 ? a->nq : 0) * 4 + 256;
+  using namespace vmo;
+  if (!a || a->batch <= 0 || a->heads <= 0 || a->nq <= 0 || a->nk <= 0) return 256;
+  const int64_t problems = (int64_t)a->batch * a->heads;
+  const int splits = bwd_dq_splits(problems, a->nq, a->nk);
+  size_t bytes = bwd_stats_bytes(problems, a->nq) + 256;
+  if (splits > 1) bytes += (size_t)splits * problems * a->nq * (a->d > 0 ? a->d : 0) * 4;
+  return bytes;
 }
 
 extern "C" int vmo_fea_bwd(const vmo_fea_bwd_args* a, void* stream) {
@@ -503,6 +594,8 @@ extern "C" int vmo_fea_bwd(const vmo_fea_bwd_args* a, void* stream) {
       !view_ok(a->grad_q) || !view_ok(a->grad_k) || !view_ok(a->grad_v))
     return set_error(VMO_ERR_INVALID, "fea_bwd: tensors need 16-byte aligned rows");
   if (!a->lse || !a->ent || !a->grad_ent) return set_error(VMO_ERR_INVALID, "fea_bwd: lse / ent / dent required");
+  if (a->flags & ~(VMO_BWD_ACCUM_Q | VMO_BWD_ACCUM_K | VMO_BWD_ACCUM_V))
+    return set_error(VMO_ERR_INVALID, "fea_bwd: unknown flags 0x%x", (unsigned)a->flags);
   if (!(a->sm_scale >= 0.f)) return set_error(VMO_ERR_INVALID, "fea_bwd: sm_scale");
   const size_t ws = vmo_fea_bwd_workspace_size(a);
   if (!a->workspace || a->workspace_bytes < ws || !aligned16(a->workspace))
@@ -517,6 +610,10 @@ extern "C" int vmo_fea_bwd(const vmo_fea_bwd_args* a, void* stream) {
   p.lse = a->lse; p.ent = a->ent; p.dent = a->grad_ent;
   p.alpha = (float*)a->workspace;
   p.beta = p.alpha + problems * a->nq;
+  p.dq_splits = bwd_dq_splits(problems, a->nq, a->nk);
+  p.keys_per_split = bwd_keys_per_split(a->nk, p.dq_splits);
+  p.dq_part = (float*)((char*)a->workspace + bwd_stats_bytes(problems, a->nq));
+  p.accum = a->flags;
   p.q_sb = a->q.stride_b; p.q_sh = a->q.stride_h; p.q_sn = a->q.stride_n;
   p.k_sb = a->k.stride_b; p.k_sh = a->k.stride_h; p.k_sn = a->k.stride_n;
   p.v_sb = a->v.stride_b; p.v_sh = a->v.stride_h; p.v_sn = a->v.stride_n;
@@ -529,7 +626,7 @@ extern "C" int vmo_fea_bwd(const vmo_fea_bwd_args* a, void* stream) {
   p.de_sb = a->grad_ent_stride_b; p.de_sh = a->grad_ent_stride_h;
   p.heads = a->heads; p.nq = a->nq; p.nk = a->nk; p.problems = (int)problems;
   p.dq_tiles = (int)dq_tiles; p.kv_tiles = (int)kv_tiles;
-  p.dq_total = (int)(problems * dq_tiles); p.kv_total = (int)(problems * kv_tiles);
+  p.dq_total = (int)(problems * dq_tiles * p.dq_splits); p.kv_total = (int)(problems * kv_tiles);
   p.c = a->sm_scale * kLog2e;
   p.sm_scale = a->sm_scale;
   hipStream_t s = (hipStream_t)stream;

@@ -13,16 +13,28 @@ def _pad_features(t, width):
     return t if t.shape[-1] == width else torch.nn.functional.pad(t, (0, width - t.shape[-1]))
 
 
-def fea_backward_raw(q, k, v, o, lse, ent, do, de, sm_scale):
+def fea_backward_raw(q, k, v, o, lse, ent, do, de, sm_scale, dq=None, dk=None, dv=None):
     """q: (B, H, nq, D); k: (B, H, nk, D); v: (B, H, nk, Dv); o, do: (B, H, nq, Dv);
-    lse, ent, de: (B, H, nq) fp32 with unit token stride.  Returns (dq, dk, dv)."""
+    lse, ent, de: (B, H, nq) fp32 with unit token stride.  Returns (dq, dk, dv).
+
+    A gradient passed in as a float32 view is accumulated into (+= in the kernels); otherwise it is
+    returned as a new tensor of q's dtype."""
     L = _lib.lib()
     B, H, NQ, D = q.shape
     NK, Dv = k.shape[2], v.shape[-1]
-    dq = torch.empty((B, H, NQ, D), device=q.device, dtype=q.dtype)
-    dk = torch.empty((B, H, NK, D), device=q.device, dtype=q.dtype)
-    dv = torch.empty((B, H, NK, Dv), device=q.device, dtype=q.dtype)
+    flags = 0
+    for t, bit in ((dq, _lib.BWD_ACCUM_Q), (dk, _lib.BWD_ACCUM_K), (dv, _lib.BWD_ACCUM_V)):
+        if t is not None:
+            assert t.dtype == torch.float32, "an accumulated gradient must be float32"
+            flags |= bit
+    if dq is None:
+        dq = torch.empty((B, H, NQ, D), device=q.device, dtype=q.dtype)
+    if dk is None:
+        dk = torch.empty((B, H, NK, D), device=q.device, dtype=q.dtype)
+    if dv is None:
+        dv = torch.empty((B, H, NK, Dv), device=q.device, dtype=q.dtype)
     a = _lib.FeaBwdArgs()
+    a.flags = flags
     a.dtype = _lib.DTYPES[q.dtype]
     a.batch, a.heads, a.nq, a.nk, a.d, a.dv = B, H, NQ, NK, D, Dv
     a.q, a.k, a.v, a.o, a.grad_o = (_lib.view(t) for t in (q, k, v, o, do))

@@ -221,19 +221,19 @@ class _VMonarchFunction(torch.autograd.Function):
         scale = D ** -0.5
         dev, dt = q.device, q.dtype
         dz = _lib.row_aligned(dz.to(dt))
-        dq = torch.zeros((B, H, N, D), device=dev, dtype=torch.float32)
-        dk = torch.zeros((B, H, N, D), device=dev, dtype=torch.float32)
-        dv = torch.zeros((B, H, N, Dv), device=dev, dtype=torch.float32)
+        f32 = torch.float32
+        # fp32 accumulators the kernels add into: dq, and one (.., 2D + Dv) buffer holding dk from
+        # the key role | dk from the value role (w starts with k) | dv
+        dq = torch.zeros((B, H, N, D), device=dev, dtype=f32)
+        g_kv = torch.zeros((B, H, N, 2 * D + Dv), device=dev, dtype=f32)
         if rt > 0:
             # exact attention of the first rt queries (vmonarch.py:66-68)
-            zeros = torch.zeros((B, H, rt), device=dev, dtype=torch.float32)
-            gq, gk, gv = fea_backward_raw(q[:, :, :rt], k, v, z[:, :, :rt], lse_rt, zeros,
-                                          _lib.row_aligned(dz[:, :, :rt]), zeros, scale)
-            dq[:, :, :rt] += gq
-            dk += gk
-            dv += gv
+            zeros = torch.zeros((B, H, rt), device=dev, dtype=f32)
+            fea_backward_raw(q[:, :, :rt], k, v, z[:, :, :rt], lse_rt, zeros, _lib.row_aligned(dz[:, :, :rt]), zeros,
+                             scale, dq=dq[:, :, :rt], dk=g_kv[..., :D], dv=g_kv[..., 2 * D:])
         frames = lambda t: t.reshape(B, H * m, b, *t.shape[3:])   # the R-step's m frames per head
-        de = torch.zeros((B, H * m, b), device=dev, dtype=torch.float32)
+        de = torch.zeros((B, H * m, b), device=dev, dtype=f32)
+        g_fr = frames(g_kv)
         g = dz
         for it in reversed(range(num_iters)):
             last = it == num_iters - 1
@@ -241,20 +241,14 @@ class _VMonarchFunction(torch.autograd.Function):
             dout = torch.empty_like(out)
             _lstep_bwd_launch(q, out, ent, g, dq, dout, m, b, scale, last, rt if last else 0, min_col_mass)
             w = torch.cat([k, v], -1) if last else k
-            gx, gk, gw = fea_backward_raw(frames(x), frames(k), frames(w), frames(out), frames(lse),
-                                          frames(ent), frames(dout), de, scale if it == 0 else 1.0)
-            dk += gk.view(B, H, N, D)
-            gw = gw.view(B, H, N, -1)
-            if last:
-                dk += gw[..., :D]
-                dv += gw[..., D:]
-            else:
-                dk += gw
-            if it == 0:
-                dq += gx.view(B, H, N, D)   # R-step 0 read q with the softmax scale folded in
-            else:
+            gx, _, _ = fea_backward_raw(frames(x), frames(k), frames(w), frames(out), frames(lse), frames(ent),
+                                        frames(dout), de, scale if it == 0 else 1.0,
+                                        dq=frames(dq) if it == 0 else None,   # R-step 0 read q directly
+                                        dk=g_fr[..., :D], dv=g_fr[..., D:] if last else g_fr[..., D:2 * D])
+            if it > 0:
                 g = gx.view(B, H, N, D)     # dL/du of the previous L-step's output
-        return dq.to(dt), dk.to(dt), dv.to(dt), None, None, None, None, None
+        dk = (g_kv[..., :D] + g_kv[..., D:2 * D]).to(dt)
+        return dq.to(dt), dk, g_kv[..., 2 * D:].to(dt), None, None, None, None, None
 
 
 def _vmonarch_composed(q, k, v, num_blocks, block_size, num_iters, recompute_tokens, min_col_mass):
