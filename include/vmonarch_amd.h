@@ -65,7 +65,8 @@ typedef struct vmo_view {
  * ent / lse may be NULL.  num_splits > 1 splits the keys of each problem into num_splits
  * ranges (split-KV, for problems with few query tiles such as the recompute of
  * vmonarch.py:66-68); it needs ent == NULL and a workspace of
- * vmo_fea_fwd_workspace_size() bytes.  Supported: d in {64, 128}; dw0 in {64, 128, 256};
+ * vmo_fea_fwd_workspace_size() bytes.  Supported: d in {64, 128} with dw0 in {64, 128, 256}, and d = dw0 = 256
+ * (entropy output, no split);
  * dw1 in {0, 64, 128} (dw1 > 0 only with w0 aliasing k); sm_scale >= 0.
  */
 typedef struct vmo_fea_fwd_args {

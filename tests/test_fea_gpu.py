@@ -118,6 +118,27 @@ def test_fea_narrow_head_dims(D, Dv):
     _check(o, e, o_ref, e_ref)
 
 
+@pytest.mark.parametrize("N", [77, 256, 1000])
+def test_fea_head_dim_256(N):
+    """D = Dv = 256, the widest head the reference accepts (kernel.py:324, Dv a multiple of D)."""
+    from vmonarch_amd import flash_entropy_attention
+    g = torch.Generator().manual_seed(N)
+    q, k, v = (randn_lp(g, 1, 2, N, 256) for _ in range(3))
+    print(f"fea D=256 N={N}", flush=True)
+    o, e = flash_entropy_attention(q.to(DEV), k.to(DEV), v.to(DEV))
+    o_ref, e_ref = entropy_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), 256 ** -0.5)
+    _check(o, e, o_ref, e_ref)
+
+
+def test_fea_head_dim_256_backward_is_not_built():
+    from vmonarch_amd import flash_entropy_attention
+    g = torch.Generator().manual_seed(3)
+    q, k, v = (randn_lp(g, 1, 1, 64, 256).to(DEV).requires_grad_() for _ in range(3))
+    o, e = flash_entropy_attention(q, k, v)
+    with pytest.raises(NotImplementedError):
+        o.float().sum().backward()
+
+
 @pytest.mark.parametrize("splits", [1, 2, 4, 7])
 def test_fea_split_kv_cross_attention(splits):
     """Nq != Nk with split-KV (the recompute path): o and lse against the oracle."""

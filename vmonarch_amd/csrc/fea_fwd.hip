@@ -124,8 +124,14 @@ struct TileCopy {
 //   e = LSE - sm_scale q . (sum_j p_j k_j) / l   (nats)  -- no per-element work in the loop.
 enum { kEntNone = 0, kEntOnline = 1, kEntFromPK = 2 };
 
+// Workgroups per CU the register budget is sized for: a 256-wide value tensor (its accumulators alone are
+// 128 registers) or 256-wide q/k heads run one 4-wave workgroup per CU; at two the compiler spilled
+// hundreds of registers in the key loop.
+template <int D, int DW0, int WAVES>
+constexpr int fwd_min_blocks() { return (D >= 256 || DW0 >= 256) ? 1 : 8 / WAVES; }
+
 template <bool F16, int D, int DW0, int DW1, bool W0K, int ENT, bool SPLIT, int WAVES>
-__global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void fea_fwd_kernel(FwdParams p) {
+__global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, WAVES>())) void fea_fwd_kernel(FwdParams p) {
   using E = Elem<F16>;
   using T = typename E::T;
   using V8 = typename E::V8;
@@ -652,6 +658,7 @@ static int dispatch_fwd(const FwdParams& p, int d, int dw0, int dw1, bool w0k, b
   VMO_FWD(128, 64, 0, false, kEntOnline, false)
   VMO_FWD(128, 128, 0, false, kEntOnline, false)
   VMO_FWD(128, 256, 0, false, kEntOnline, false)
+  VMO_FWD(256, 256, 0, false, kEntOnline, false)
   // VMonarch R-step (vmonarch.py:50): values k, or [k | v]; entropy from the P.K accumulator
   VMO_FWD(64, 64, 0, true, kEntFromPK, false)
   VMO_FWD(64, 64, 64, true, kEntFromPK, false)

@@ -89,8 +89,8 @@ class _FlashEntropyAttention(torch.autograd.Function):
         assert q.dtype in _lib.DTYPES, f"unsupported dtype {q.dtype}"
         assert k.shape == q.shape and v.shape[:-1] == q.shape[:-1]
         assert D in _HEAD_DIMS and Dv in _HEAD_DIMS
-        if D == 256:
-            raise NotImplementedError("vmonarch_amd: head dim 256 for q/k is not built yet")
+        if D == 256 and Dv != 256:
+            raise NotImplementedError("vmonarch_amd: head dim 256 for q/k is built with 256-wide values only")
         if not q.is_cuda:
             raise RuntimeError("vmonarch_amd: flash_entropy_attention needs GPU tensors (no CPU path)")
         n = int(n_valid)
