@@ -125,13 +125,16 @@ struct TileCopy {
 enum { kEntNone = 0, kEntOnline = 1, kEntFromPK = 2 };
 
 // Workgroups per CU the register budget is sized for: a 256-wide value tensor (its accumulators alone are
-// 128 registers) or 256-wide q/k heads run one 4-wave workgroup per CU; at two the compiler spilled
-// hundreds of registers in the key loop.
-template <int D, int DW0, int WAVES>
-constexpr int fwd_min_blocks() { return (D >= 256 || DW0 >= 256) ? 1 : 8 / WAVES; }
+// 128 registers), 256-wide q/k heads, and two narrower shapes that spilled inside the key loop at two
+// workgroups per CU (64-wide q/k with 128-wide values and the online entropy; [k | v] with v narrower
+// than k) run one 4-wave workgroup per CU.
+template <int D, int DW0, int DW1, int ENT, int WAVES>
+constexpr int fwd_min_blocks() {
+  return (D >= 256 || DW0 >= 256 || (ENT == kEntOnline && D < DW0) || (DW1 > 0 && DW1 < D)) ? 1 : 8 / WAVES;
+}
 
 template <bool F16, int D, int DW0, int DW1, bool W0K, int ENT, bool SPLIT, int WAVES>
-__global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, WAVES>())) void fea_fwd_kernel(FwdParams p) {
+__global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES>())) void fea_fwd_kernel(FwdParams p) {
   using E = Elem<F16>;
   using T = typename E::T;
   using V8 = typename E::V8;
