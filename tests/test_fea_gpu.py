@@ -105,6 +105,8 @@ def test_fea_strided_inputs():
     o, e = flash_entropy_attention(q, k, v)
     o_ref, e_ref = entropy_attention(*(t.float().cpu().numpy() for t in (q, k, v)), 128 ** -0.5)
     _check(o, e, o_ref, e_ref)
+    # o comes back in the caller's layout: a (B, N, H, Dv) buffer viewed as (B, H, N, Dv)
+    assert o.shape == (2, 3, 300, 128) and o.stride() == (300 * 3 * 128, 128, 3 * 128, 1)
 
 
 @pytest.mark.parametrize("D, Dv", [(16, 16), (32, 64), (64, 32)])

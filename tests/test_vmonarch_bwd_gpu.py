@@ -111,3 +111,24 @@ def test_vmonarch_grad_accumulates_into_leaf_grads():
     for t, g1 in zip((q, k, v), grads1):
         assert torch.isfinite(t.grad.float()).all()
         torch.testing.assert_close(t.grad.float(), 2 * g1.float(), rtol=1e-2, atol=1e-2)
+
+
+def test_vmonarch_grad_dit_layout():
+    """(B, N, H, D)-buffer inputs: gradients come back in that layout and equal the contiguous run's."""
+    from vmonarch_amd import vmonarch_attention
+    g = torch.Generator().manual_seed(22)
+    m, b, H = 4, 64, 2
+    base = [randn_lp(g, 1, m * b, H, 64).to(DEV) for _ in range(3)]
+    dz = torch.randn(1, H, m * b, 64, generator=g).to(DEV)
+
+    def run(make):
+        leaves = [make(t).requires_grad_() for t in base]
+        z = vmonarch_attention(*leaves, m, b, 2, recompute_tokens=b)
+        return z, torch.autograd.grad(z, leaves, dz)
+
+    z_d, g_d = run(lambda t: t.transpose(1, 2).detach())
+    z_c, g_c = run(lambda t: t.transpose(1, 2).contiguous())
+    assert torch.equal(z_d, z_c)
+    for gd, gc in zip(g_d, g_c):
+        assert gd.stride() == (m * b * H * 64, 64, H * 64, 1)
+        assert torch.equal(gd, gc)

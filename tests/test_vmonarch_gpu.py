@@ -148,3 +148,18 @@ def test_vmonarch_rejects_bad_shape():
     q = torch.zeros(1, 1, 12, 64, device=DEV, dtype=torch.bfloat16)
     with pytest.raises(AssertionError):
         vmonarch_attention(q, q, q, 5, 3)
+
+
+def test_vmonarch_dit_layout_in_place_and_out():
+    """q, k, v as (B, N, H, D) buffers viewed as (B, H, N, D) (a DiT block's layout): read in place,
+    z written in the same layout, values bitwise equal to the contiguous-input result."""
+    from vmonarch_amd import vmonarch_attention
+    g = torch.Generator().manual_seed(21)
+    m, b, H = 8, 100, 3
+    qs, ks, vs = (randn_lp(g, 1, m * b, H, 128, scale=0.5).to(DEV) for _ in range(3))
+    q, k, v = (t.transpose(1, 2) for t in (qs, ks, vs))
+    with torch.no_grad():
+        z = vmonarch_attention(q, k, v, m, b, 2, recompute_tokens=b)
+        z_c = vmonarch_attention(q.contiguous(), k.contiguous(), v.contiguous(), m, b, 2, recompute_tokens=b)
+    assert z.stride() == (m * b * H * 128, 128, H * 128, 1)
+    assert torch.equal(z, z_c)

@@ -120,5 +120,24 @@ def row_aligned(t):
     return t if ok else t.contiguous()
 
 
+def layout_order(t):
+    """Order of t's (B, H, N) dims in memory, outermost first (by stride)."""
+    return tuple(sorted(range(3), key=lambda d: (-t.stride(d), d)))
+
+
+def empty_in_order(order, shape3, feat, dtype, device):
+    """An uninitialised (B, H, N, feat) tensor whose (B, H, N) dims lie in memory in `order`, feature dim
+    innermost."""
+    buf = torch.empty([shape3[d] for d in order] + [feat], device=device, dtype=dtype)
+    return buf.permute(*[order.index(d) for d in range(3)], 3)
+
+
+def empty_in_layout(ref, feat, dtype):
+    """An uninitialised (B, H, N, feat) tensor laid out like ref: for q given as a (B, N, H, D) buffer
+    viewed as (B, H, N, D) (a DiT block's layout) the result is a (B, N, H, feat) buffer viewed the same
+    way, so the caller needs no permute copy afterwards."""
+    return empty_in_order(layout_order(ref), ref.shape[:3], feat, dtype, ref.device)
+
+
 def stream_of(t):
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)

@@ -99,7 +99,7 @@ class _FlashEntropyAttention(torch.autograd.Function):
         ent = torch.empty((B, H, N), device=q.device, dtype=torch.float32)
         lse = torch.empty((B, H, N), device=q.device, dtype=torch.float32)
         if Dvk == Dv:
-            o = torch.empty((B, H, N, Dv), device=q.device, dtype=q.dtype)
+            o = _lib.empty_in_layout(q, Dv, q.dtype)   # o in the caller's layout (e.g. (B, N, H, Dv))
             if n > 0:
                 fea_forward(qx, kx, vx, None, sm_scale, o=o[:, :, :n], lse=lse[:, :, :n], ent=ent[:, :, :n])
         else:

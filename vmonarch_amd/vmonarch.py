@@ -118,7 +118,7 @@ def _vmonarch_fused(q, k, v, m, b, num_iters, recompute_tokens, min_col_mass, st
     main = torch.cuda.current_stream(dev)
     hook = stage_hook or (lambda name, phase, stream: None)
     ent = torch.empty((B, H, N), device=dev, dtype=torch.float32)
-    z = torch.empty((B, H, N, Dv), device=dev, dtype=dt)
+    z = _lib.empty_in_layout(q, Dv, dt)   # z in the caller's layout (a DiT block's (B, N, H, Dv))
     rt = min(int(recompute_tokens), N)
     side = None
 
@@ -188,9 +188,11 @@ class _VMonarchFunction(torch.autograd.Function):
         B, H, N, D = q.shape
         Dv = v.shape[-1]
         scale = D ** -0.5
+        z = _lib.empty_in_layout(q, Dv, q.dtype)
+        ctx.orders = tuple(_lib.layout_order(t) for t in (q, k, v))
+        # the backward views every head's m frames as one (B, H * m, b) problem set: contiguous copies
         q, k, v = (t.contiguous() for t in (q, k, v))
         dev, dt = q.device, q.dtype
-        z = torch.empty((B, H, N, Dv), device=dev, dtype=dt)
         rt = min(int(recompute_tokens), N)
         saved = []
         u = None
@@ -247,8 +249,12 @@ class _VMonarchFunction(torch.autograd.Function):
                                         dk=g_fr[..., :D], dv=g_fr[..., D:] if last else g_fr[..., D:2 * D])
             if it > 0:
                 g = gx.view(B, H, N, D)     # dL/du of the previous L-step's output
-        dk = (g_kv[..., :D] + g_kv[..., D:2 * D]).to(dt)
-        return dq.to(dt), dk, g_kv[..., 2 * D:].to(dt), None, None, None, None, None
+        # gradients in the memory order the caller's q, k, v had (the fp32 -> dtype copy places them)
+        gq, gk, gv = (_lib.empty_in_order(o, (B, H, N), f, dt, dev) for o, f in zip(ctx.orders, (D, D, Dv)))
+        gq.copy_(dq)
+        gk.copy_(g_kv[..., :D] + g_kv[..., D:2 * D])
+        gv.copy_(g_kv[..., 2 * D:])
+        return gq, gk, gv, None, None, None, None, None
 
 
 def _vmonarch_composed(q, k, v, num_blocks, block_size, num_iters, recompute_tokens, min_col_mass):
