@@ -293,3 +293,18 @@ def test_fea_backward_accumulates_into_fp32_gradients():
     torch.testing.assert_close(kv[..., D:D + Dv] - kv0[..., D:D + Dv], plain[2].float(), rtol=2e-2,
                                atol=2e-2 * plain[2].float().abs().max().item())
     assert torch.equal(kv[..., D + Dv:], kv0[..., D + Dv:])
+
+
+@pytest.mark.parametrize("D, Dv", [(64, 64), (128, 128), (128, 256)])
+def test_fea_backward_fp16(D, Dv):
+    """fp16 inputs (kernel.py:13 accepts float16): gradients within the reference's 3e-2."""
+    from oracle import entropy_attention_grad
+    g = torch.Generator().manual_seed(D + Dv)
+    q, k = randn_lp(g, 1, 2, 300, D, dtype=torch.float16), randn_lp(g, 1, 2, 300, D, dtype=torch.float16)
+    v = randn_lp(g, 1, 2, 300, Dv, dtype=torch.float16)
+    do, de = torch.randn(1, 2, 300, Dv, generator=g), torch.randn(1, 2, 300, generator=g)
+    grads = _grads(q, k, v, do, de)
+    assert all(t.dtype == torch.float16 for t in grads)
+    refs = entropy_attention_grad(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                  do.half().float().numpy(), de.numpy(), D ** -0.5)
+    _check_grads(grads, refs)

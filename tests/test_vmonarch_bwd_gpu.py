@@ -132,3 +132,23 @@ def test_vmonarch_grad_dit_layout():
     for gd, gc in zip(g_d, g_c):
         assert gd.stride() == (m * b * H * 64, 64, H * 64, 1)
         assert torch.equal(gd, gc)
+
+
+def test_vmonarch_fp16_forward_and_grad():
+    """float16 through the fused forward and the HIP backward."""
+    from vmonarch_amd import vmonarch_attention
+    g = torch.Generator().manual_seed(23)
+    m, b = 8, 100
+    q, k, v = (randn_lp(g, 1, 2, m * b, 64, dtype=torch.float16) for _ in range(3))
+    do = torch.randn(1, 2, m * b, 64, generator=g)
+    qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    z = vmonarch_attention(qd, kd, vd, m, b, 2, recompute_tokens=b)
+    assert z.dtype == torch.float16 and type(z.grad_fn).__name__ == "_VMonarchFunctionBackward"
+    grads = torch.autograd.grad((z.float() * do.to(DEV)).sum(), (qd, kd, vd))
+    from oracle import vmonarch_attention as vm_oracle
+    z_ref = vm_oracle(*(t.float().numpy() for t in (q, k, v)), m, b, 2, b)
+    assert_close_ref(z.detach().float().cpu().numpy(), z_ref, 3e-2)
+    ref = vmonarch_attention_grad(*(t.float().numpy() for t in (q, k, v)), do.numpy(), m, b, 2, b)
+    for gd, gr in zip(grads, ref):
+        assert gd.dtype == torch.float16
+        assert_close_ref(gd.float().cpu().numpy(), gr, 5e-2)
