@@ -166,12 +166,14 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
     for (int ds = 0; ds < D / 16; ++ds) {
       V8 x = *(const V8*)(qp + ds * 16);
       qf[ds] = qvalid ? x : V8{};
+      asm volatile("" : "+v"(qf[ds]));   // loaded and waited for here, never re-loaded in the loop
     }
 #pragma unroll
     for (int ds = 0; ds < DV / 16; ++ds) {
       V8 x = *(const V8*)(dp + ds * 16);
       V8 y = *(const V8*)(op + ds * 16);
       dof[ds] = qvalid ? x : V8{};
+      asm volatile("" : "+v"(dof[ds]));
 #pragma unroll
       for (int e = 0; e < 8; ++e) delta = fmaf((float)x[e], (float)y[e], delta);
     }
@@ -180,8 +182,11 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
   const int64_t si = bb * p.st_sb + hh * p.st_sh + qr;
   const float lse = p.lse[si];
   const float dE = p.dent[bb * p.de_sb + hh * p.de_sh + qr];
-  const float alpha = -delta - dE * p.ent[si];
-  const float beta = -dE * kLn2;
+  float alpha = -delta - dE * p.ent[si];
+  float beta = -dE * kLn2;
+  float lse_r = lse;
+  // the per-row scalars are waited for here: a wait inside the key loop would also wait for the copies
+  asm volatile("" : "+v"(alpha), "+v"(beta), "+v"(lse_r));
   if (qvalid && hl == 0 && split == 0) {
     p.alpha[(int64_t)prob * p.nq + qrow] = alpha;
     p.beta[(int64_t)prob * p.nq + qrow] = beta;
@@ -204,15 +209,15 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
   const int tchunk = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
   const int tbyte = (lane & 1) * 8;
 
-  issue(0);
-  for (int t = 0; t < n_tiles; ++t) {
+  // one 64-key stage; only a partial last stage masks its keys, and it is peeled out of the loop
+  auto iteration = [&](int t, auto masked_tag) __attribute__((always_inline)) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
     tile_sync<0>();   // stage t has landed for every wave, and stage t - 1's slot is free
     if (t + 1 < n_tiles) issue(t + 1);
-    if (!wave_live) continue;
+    if (!wave_live) return;
     const VMO_LDS char* Ks = smem + (t & 1) * STAGE;
     const VMO_LDS char* Vs = Ks + K_BYTES;
     const int nvalid = kend - kbeg - t * kDqBN;
-
     f32x16 s[2] = {f32x16{}, f32x16{}}, dp[2] = {f32x16{}, f32x16{}};
 #pragma unroll
     for (int kb2 = 0; kb2 < 2; ++kb2) {
@@ -230,9 +235,9 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
     for (int kb2 = 0; kb2 < 2; ++kb2) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float x = fmaf(s[kb2][r], c, -lse);
+        const float x = fmaf(s[kb2][r], c, -lse_r);
         float g = fast_exp2(x) * (dp[kb2][r] + fmaf(beta, x, alpha));
-        if (nvalid < kDqBN && 32 * kb2 + 8 * (r >> 2) + 4 * hl + (r & 3) >= nvalid) g = 0.f;
+        if (MASKED && 32 * kb2 + 8 * (r >> 2) + 4 * hl + (r & 3) >= nvalid) g = 0.f;
         G[2 * kb2 + (r >> 3)][r & 7] = to_elem<T>(g);
       }
     }
@@ -243,7 +248,11 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
       for (int ks = 0; ks < 4; ++ks)
         acc[a] = E::mfma(tr_pair<V8, D * 2>(Ks + 16 * ks * (D * 2), c0), G[ks], acc[a]);
     }
-  }
+  };
+  issue(0);
+  const int n_full = (kend - kbeg) / kDqBN;   // stages with 64 valid keys
+  for (int t = 0; t < n_full; ++t) iteration(t, std::false_type{});
+  if (n_full < n_tiles) iteration(n_full, std::true_type{});
   if (!wave_live || !qvalid) return;
   if (p.dq_splits > 1) {   // fp32 partial of this key range; fea_bwd_dq_reduce sums the splits
     float* pr = p.dq_part + (((int64_t)split * p.problems + prob) * p.nq + qrow) * D;
@@ -402,11 +411,13 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
   if constexpr (K_LDS)   // and its 128 K rows
     stage_rows_n<T, D, kKvBN>((const T*)p.k + bb * p.k_sb + hh * p.k_sh, p.k_sn, kt * kKvBN, p.nk,
                               smem_u32 + 2 * STAGE + V_TILE, wave, lane);
-  issue(0);
-  for (int t = 0; t < n_tiles; ++t) {
+  // one 32-query stage; only a partial last stage masks its queries, and it is peeled out of the loop
+  // (both versions inside one loop body made the compiler spill the accumulators)
+  auto iteration = [&](int t, auto masked_tag) __attribute__((always_inline)) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
     tile_sync<0>();   // stage t has landed for every wave, and stage t - 1's slot is free
     if (t + 1 < n_tiles) issue(t + 1);
-    if (!wave_live) continue;
+    if (!wave_live) return;
     const VMO_LDS char* Qs = smem + (t & 1) * STAGE;
     const VMO_LDS char* dOs = Qs + Q_BYTES;
     const VMO_LDS float* sts = (const VMO_LDS float*)(dOs + DO_BYTES);
@@ -444,7 +455,7 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
         const float x = fmaf(s[r], c, -lv[e]);
         float pv = fast_exp2(x);
         float gv = WANT_DK ? pv * (dp[r] + fmaf(bv[e], x, av[e])) : 0.f;
-        if (nvalid < kKvBM && 8 * g + 4 * hl + e >= nvalid) { pv = 0.f; gv = 0.f; }
+        if (MASKED && 8 * g + 4 * hl + e >= nvalid) { pv = 0.f; gv = 0.f; }
         P[r >> 3][r & 7] = to_elem<T>(pv);
         G[r >> 3][r & 7] = to_elem<T>(gv);
       }
@@ -464,7 +475,11 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
         for (int ss = 0; ss < 2; ++ss) dk[a] = E::mfma(tr_pair<V8, D * 2>(Qs + 16 * ss * (D * 2), c0), G[ss], dk[a]);
       }
     }
-  }
+  };
+  issue(0);
+  const int n_full = p.nq / kKvBM;   // stages with 32 valid queries
+  for (int t = 0; t < n_full; ++t) iteration(t, std::false_type{});
+  if (n_full < n_tiles) iteration(n_full, std::true_type{});
   if (!wave_live || !kvalid) return;
   // store (or, for an fp32 gradient with its accumulate bit, add) NACC accumulator blocks times f
   auto put = [&](void* base, int64_t sb, int64_t sh, int64_t sn, int col0, const f32x16* acc, int nacc, float f,
