@@ -80,6 +80,51 @@ __device__ __forceinline__ void stage_rows_n(const T* __restrict__ base, int64_t
   }
 }
 
+// The same copy for the tiles staged inside the key / query loops: per-lane byte offsets computed
+// once, a scalar row base per tile (a full tile costs scalar adds only; the clamped per-lane path is
+// taken by a tile that runs past the end).  Row strides must stay below 2^27 elements (32-bit lane
+// offsets over up to 7 rows).
+template <class T, int W, int ROWS>
+struct BwdTileCopy {
+  static constexpr int CH = W / 8;
+  static constexpr int RPI = 64 / CH;
+  static constexpr int NI = ROWS / RPI / kBwdWaves;
+  static constexpr int NV = (kBwdWaves * RPI) % 16 == 0 ? 1 : 2;   // distinct lane offsets (swizzle period 16)
+  static_assert(CH >= 8 && NI >= 1 && RPI >= 2, "tile shape");
+  uint64_t ubase, rbytes;
+  uint32_t voff[NV];
+  int wave, lane;
+
+  __device__ __forceinline__ BwdTileCopy(const T* b, int64_t sn, int w, int l) : wave(w), lane(l) {
+    ubase = uniform64((uint64_t)(uintptr_t)b);
+    rbytes = uniform64((uint64_t)sn * 2);
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int r = (v * kBwdWaves + w) * RPI + l / CH;
+      voff[v] = (uint32_t)((int64_t)(l / CH) * sn * 2) + (uint32_t)(((l % CH) ^ swz_rows<W * 2>(r)) * 16);
+    }
+  }
+  __device__ __forceinline__ void issue(int row0, int nrows, uint32_t dst) const {
+    uint64_t ub = ubase;
+    asm volatile("" : "+s"(ub));   // recomputed per call: hoisted, the addresses would pin scalar registers
+    if (row0 + ROWS <= nrows) {
+      const uint64_t tb = ub + (uint64_t)(row0 + wave * RPI) * rbytes;
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+        dma16_async_s(tb + (uint64_t)(i * kBwdWaves * RPI) * rbytes, voff[i % NV], dst + (i * kBwdWaves + wave) * 1024);
+    } else {
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int inst = i * kBwdWaves + wave;
+        const int r = inst * RPI + lane / CH;
+        const int gr = min(row0 + r, nrows - 1);
+        dma16_async((const void*)(uintptr_t)(ub + (uint64_t)gr * rbytes + ((lane % CH) ^ swz_rows<W * 2>(r)) * 16),
+                    dst + inst * 1024);
+      }
+    }
+  }
+};
+
 // Byte offset, within a 32-row block of a row-major LDS tile with RB-byte rows, of this lane's
 // first ds_read_tr16_b64 for accumulator block a (rows trow and trow + 4 of the 4-row groups); the
 // second read of the pair is 8 rows down at (offset ^ 32), since swz_rows(r + 8) = swz_rows(r) ^ 2.
@@ -141,11 +186,14 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
 
   const int L = xcd_remap(gridDim.x);
   if (L >= p.dq_total) return;
-  const int qt = L % p.dq_tiles, split = (L / p.dq_tiles) % p.dq_splits, prob = L / p.dq_tiles / p.dq_splits;
+  // workgroup-uniform indices, moved to scalar registers (integer division runs on the vector unit)
+  auto uni = [](int x) __attribute__((always_inline)) { return __builtin_amdgcn_readfirstlane(x); };
+  const int qt = uni(L % p.dq_tiles), split = uni((L / p.dq_tiles) % p.dq_splits);
+  const int prob = uni(L / p.dq_tiles / p.dq_splits);
   const int kbeg = split * p.keys_per_split;
   const int kend = min(p.nk, kbeg + p.keys_per_split);
   const int hh = prob % p.heads, bb = prob / p.heads;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  const int tid = threadIdx.x, wave = uni(tid >> 6), lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int q0 = qt * kDqBM + wave * 32;
   const bool wave_live = q0 < p.nq;
   const int qrow = q0 + l32;
@@ -194,10 +242,12 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
 
   const int n_tiles = (kend - kbeg + kDqBN - 1) / kDqBN;
   const uint32_t smem_u32 = (uint32_t)(uintptr_t)smem;
+  const BwdTileCopy<T, D, kDqBN> kcopy(kb, p.k_sn, wave, lane);
+  const BwdTileCopy<T, DV, kDqBN> vcopy(vb, p.v_sn, wave, lane);
   auto issue = [&](int t) {
     const uint32_t st = smem_u32 + (uint32_t)((t & 1) * STAGE);
-    stage_rows_n<T, D, kDqBN>(kb, p.k_sn, kbeg + t * kDqBN, kend, st, wave, lane);
-    stage_rows_n<T, DV, kDqBN>(vb, p.v_sn, kbeg + t * kDqBN, kend, st + K_BYTES, wave, lane);
+    kcopy.issue(kbeg + t * kDqBN, kend, st);
+    vcopy.issue(kbeg + t * kDqBN, kend, st + K_BYTES);
   };
 
   f32x16 acc[NA];
@@ -341,9 +391,10 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
 
   const int L = xcd_remap(gridDim.x);
   if (L >= p.kv_total) return;
-  const int kt = L % p.kv_tiles, prob = L / p.kv_tiles;
+  auto uni = [](int x) __attribute__((always_inline)) { return __builtin_amdgcn_readfirstlane(x); };
+  const int kt = uni(L % p.kv_tiles), prob = uni(L / p.kv_tiles);
   const int hh = prob % p.heads, bb = prob / p.heads;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  const int tid = threadIdx.x, wave = uni(tid >> 6), lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int k0 = kt * kKvBN + wave * 32;
   const bool wave_live = k0 < p.nk;
   const int krow = k0 + l32;
@@ -378,11 +429,13 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
 
   const int n_tiles = (p.nq + kKvBM - 1) / kKvBM;
   const uint32_t smem_u32 = (uint32_t)(uintptr_t)smem;
+  const BwdTileCopy<T, D, kKvBM> qcopy(qb, p.q_sn, wave, lane);
+  const BwdTileCopy<T, DOW, kKvBM> docopy(dob + VOFF, p.do_sn, wave, lane);
   auto issue = [&](int t) {
     const uint32_t st = smem_u32 + (uint32_t)((t & 1) * STAGE);
     const int row0 = t * kKvBM;
-    stage_rows_n<T, D, kKvBM>(qb, p.q_sn, row0, p.nq, st, wave, lane);
-    stage_rows_n<T, DOW, kKvBM>(dob + VOFF, p.do_sn, row0, p.nq, st + Q_BYTES, wave, lane);
+    qcopy.issue(row0, p.nq, st);
+    docopy.issue(row0, p.nq, st + Q_BYTES);
     if (wave == 0) {   // per-query scalars: lanes 0-31 lse, 32-63 alpha; then beta
       int qi = row0 + l32;
       qi = qi < p.nq ? qi : p.nq - 1;
@@ -612,6 +665,11 @@ extern "C" int vmo_fea_bwd(const vmo_fea_bwd_args* a, void* stream) {
   if (a->flags & ~(VMO_BWD_ACCUM_Q | VMO_BWD_ACCUM_K | VMO_BWD_ACCUM_V))
     return set_error(VMO_ERR_INVALID, "fea_bwd: unknown flags 0x%x", (unsigned)a->flags);
   if (!(a->sm_scale >= 0.f)) return set_error(VMO_ERR_INVALID, "fea_bwd: sm_scale");
+  // the tile copies address up to 7 rows from a lane with a 32-bit byte offset
+  const int64_t kMaxRowStride = 1ll << 27;
+  if (a->q.stride_n >= kMaxRowStride || a->k.stride_n >= kMaxRowStride || a->v.stride_n >= kMaxRowStride ||
+      a->grad_o.stride_n >= kMaxRowStride)
+    return set_error(VMO_ERR_UNSUPPORTED, "fea_bwd: q / k / v / grad_o row stride must be below 2^27 elements");
   const size_t ws = vmo_fea_bwd_workspace_size(a);
   if (!a->workspace || a->workspace_bytes < ws || !aligned16(a->workspace))
     return set_error(VMO_ERR_WORKSPACE, "fea_bwd: needs %zu workspace bytes", ws);
