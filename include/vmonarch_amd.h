@@ -123,8 +123,8 @@ typedef struct vmo_lstep_args {
  *   dS = P (dP - delta) + grad_ent P (-ent - ln P),  dP = grad_o v^T,  delta = rowsum(o * grad_o)
  *   grad_q = sm_scale dS k,  grad_k = sm_scale dS^T q,  grad_v = P^T grad_o
  * with P rebuilt from `lse` (log2 units, as written by vmo_fea_fwd).  nq queries attend to nk
- * keys per (batch, head) (nq != nk allowed).  Supported: d in {64, 128}, dv in {64, 128, 256}.  Needs
- * vmo_fea_bwd_workspace_size() bytes of workspace.
+ * keys per (batch, head) (nq != nk allowed).  Supported: d in {64, 128} with dv in {64, 128, 256},
+ * and d = dv = 256.  Needs vmo_fea_bwd_workspace_size() bytes of workspace.
  */
 /* vmo_fea_bwd_args.flags: the marked gradient is float32 and the kernels add into it (+=) */
 enum { VMO_BWD_ACCUM_Q = 1, VMO_BWD_ACCUM_K = 2, VMO_BWD_ACCUM_V = 4 };

@@ -132,13 +132,25 @@ def test_fea_head_dim_256(N):
     _check(o, e, o_ref, e_ref)
 
 
-def test_fea_head_dim_256_backward_is_not_built():
+@pytest.mark.parametrize("N", [77, 300])
+def test_fea_head_dim_256_backward(N):
+    """D = Dv = 256 gradients (q, k, v) against the oracle, tests/test_vmonarch.py:27-42's loss."""
+    from oracle import entropy_attention_grad
+    g = torch.Generator().manual_seed(30 + N)
+    q, k, v = (randn_lp(g, 1, 2, N, 256) for _ in range(3))
+    do, de = torch.randn(1, 2, N, 256, generator=g), torch.randn(1, 2, N, generator=g)
+    print(f"fea bwd D=256 N={N}", flush=True)
+    grads = _grads(q, k, v, do, de)
+    refs = entropy_attention_grad(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                  do.bfloat16().float().numpy(), de.numpy(), 256 ** -0.5)
+    _check_grads(grads, refs)
+
+
+def test_fea_head_dim_256_with_narrower_values_is_not_built():
     from vmonarch_amd import flash_entropy_attention
-    g = torch.Generator().manual_seed(3)
-    q, k, v = (randn_lp(g, 1, 1, 64, 256).to(DEV).requires_grad_() for _ in range(3))
-    o, e = flash_entropy_attention(q, k, v)
+    q = torch.zeros(1, 1, 64, 256, device=DEV, dtype=torch.bfloat16)
     with pytest.raises(NotImplementedError):
-        o.float().sum().backward()
+        flash_entropy_attention(q, q, q[..., :128])
 
 
 @pytest.mark.parametrize("splits", [1, 2, 4, 7])
@@ -250,7 +262,8 @@ def test_fea_backward_cfg5_head_sample():
         _check_grads([t[:, sl] for t in grads], refs)
 
 
-@pytest.mark.parametrize("nq, nk, D, Dv", [(200, 8192, 64, 64), (130, 16000, 128, 128), (64, 4096, 128, 256)])
+@pytest.mark.parametrize("nq, nk, D, Dv", [(200, 8192, 64, 64), (130, 16000, 128, 128), (64, 4096, 128, 256),
+                                          (40, 4096, 256, 256)])
 def test_fea_backward_few_queries_many_keys(nq, nk, D, Dv):
     """nq != nk with few query tiles (the shape of VMonarch's recompute backward): the dq kernel
     splits the keys and sums fp32 partials; dE = 0 and ent = 0 as that caller passes them."""
@@ -295,7 +308,7 @@ def test_fea_backward_accumulates_into_fp32_gradients():
     assert torch.equal(kv[..., D + Dv:], kv0[..., D + Dv:])
 
 
-@pytest.mark.parametrize("D, Dv", [(64, 64), (128, 128), (128, 256)])
+@pytest.mark.parametrize("D, Dv", [(64, 64), (128, 128), (128, 256), (256, 256)])
 def test_fea_backward_fp16(D, Dv):
     """fp16 inputs (kernel.py:13 accepts float16): gradients within the reference's 3e-2."""
     from oracle import entropy_attention_grad

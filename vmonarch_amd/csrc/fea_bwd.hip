@@ -31,6 +31,10 @@ constexpr int kDqBM = 128;     // queries per dq workgroup
 constexpr int kDqBN = 64;      // keys per dq stage
 constexpr int kKvBN = 128;     // keys per dkdv workgroup
 constexpr int kKvBM = 32;      // queries per dkdv stage
+constexpr int kBwdPrefetch = 2;   // LDS operand reads kept in flight ahead of the MFMA that uses them
+// ... in the dq kernel: none for 64 / 64, which then fits three waves per SIMD (168 registers)
+template <int D, int DV>
+constexpr int dq_prefetch() { return D + DV <= 128 ? 0 : kBwdPrefetch; }
 
 struct BwdParams {
   const void* q;
@@ -157,9 +161,10 @@ template <int D, int DV, int PART>
 constexpr bool dkdv_v_in_lds() { return PART != 2 && D + DV >= 256; }
 // ... and of K for S = Q K^T, in the first part of the 128 / 256 variant
 template <int D, int DV, int PART>
-constexpr bool dkdv_k_in_lds() { return PART == 1 && D + DV > 320; }
+constexpr bool dkdv_k_in_lds() { return PART == 1 && D == 128 && DV == 256; }
+// 256-wide q/k heads (K alone is 64 registers, dK 128) run one wave per SIMD in both parts
 template <int D, int DV, int PART>
-constexpr int dkdv_waves_per_simd() { return PART != 0 ? 2 : bwd_waves_per_simd<D, DV>(); }
+constexpr int dkdv_waves_per_simd() { return D >= 256 ? 1 : PART != 0 ? 2 : bwd_waves_per_simd<D, DV>(); }
 template <int D, int DV, int PART>
 constexpr int dkdv_lds_bytes() {
   return 2 * (kKvBM * (D + dkdv_do_width<DV, PART>()) * 2 + 512) +
@@ -269,17 +274,19 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
     const VMO_LDS char* Vs = Ks + K_BYTES;
     const int nvalid = kend - kbeg - t * kDqBN;
     f32x16 s[2] = {f32x16{}, f32x16{}}, dp[2] = {f32x16{}, f32x16{}};
-#pragma unroll
-    for (int kb2 = 0; kb2 < 2; ++kb2) {
-      const VMO_LDS char* krow = Ks + (32 * kb2 + l32) * (D * 2);
-      const VMO_LDS char* vrow = Vs + (32 * kb2 + l32) * (DV * 2);
-#pragma unroll
-      for (int ds = 0; ds < D / 16; ++ds)
-        s[kb2] = E::mfma(lds_read8<V8>(krow + ((2 * ds + hl) ^ ksw) * 16), qf[ds], s[kb2]);
-#pragma unroll
-      for (int ds = 0; ds < DV / 16; ++ds)
-        dp[kb2] = E::mfma(lds_read8<V8>(vrow + ((2 * ds + hl) ^ vsw) * 16), dof[ds], dp[kb2]);
-    }
+    // S = K Q^T and dP = V dO^T for two 32-key blocks
+    constexpr int NSQ = D / 16, NSD = D / 16 + DV / 16;
+    prefetched_chain<2 * NSD, dq_prefetch<D, DV>()>(
+        [&](int i) __attribute__((always_inline)) {
+          const int kb2 = i / NSD, j = i % NSD;
+          return j < NSQ ? lds_read8<V8>(Ks + (32 * kb2 + l32) * (D * 2) + ((2 * j + hl) ^ ksw) * 16)
+                         : lds_read8<V8>(Vs + (32 * kb2 + l32) * (DV * 2) + ((2 * (j - NSQ) + hl) ^ vsw) * 16);
+        },
+        [&](int i, const V8& x) __attribute__((always_inline)) {
+          const int kb2 = i / NSD, j = i % NSD;
+          if (j < NSQ) s[kb2] = E::mfma(x, qf[j], s[kb2]);
+          else dp[kb2] = E::mfma(x, dof[j - NSQ], dp[kb2]);
+        });
     V8 G[4];
 #pragma unroll
     for (int kb2 = 0; kb2 < 2; ++kb2) {
@@ -291,13 +298,12 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
         G[2 * kb2 + (r >> 3)][r & 7] = to_elem<T>(g);
       }
     }
-#pragma unroll
-    for (int a = 0; a < NA; ++a) {
-      const int c0 = tr_offset<D * 2>(trow, tchunk, tbyte, a);
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        acc[a] = E::mfma(tr_pair<V8, D * 2>(Ks + 16 * ks * (D * 2), c0), G[ks], acc[a]);
-    }
+    // dQ^T[d][q] += K^T dS^T (transposed reads of the staged K tile)
+    prefetched_chain<4 * NA, dq_prefetch<D, DV>()>(
+        [&](int i) __attribute__((always_inline)) {
+          return tr_pair<V8, D * 2>(Ks + 16 * (i % 4) * (D * 2), tr_offset<D * 2>(trow, tchunk, tbyte, i / 4));
+        },
+        [&](int i, const V8& x) __attribute__((always_inline)) { acc[i / 4] = E::mfma(x, G[i % 4], acc[i / 4]); });
   };
   issue(0);
   const int n_full = (kend - kbeg) / kDqBN;   // stages with 64 valid keys
@@ -480,21 +486,27 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
     f32x16 s = f32x16{}, dp = f32x16{};
     {
       const VMO_LDS char* qrow = Qs + l32 * (D * 2);
-#pragma unroll
-      for (int ds = 0; ds < D / 16; ++ds) {
-        const int off = ((2 * ds + hl) ^ qsw) * 16;
-        const V8 kop = K_LDS ? lds_read8<V8>(kt_row + off) : kf[K_LDS ? 0 : ds];
-        s = E::mfma(lds_read8<V8>(qrow + off), kop, s);
-      }
-      if constexpr (WANT_DK) {
-        const VMO_LDS char* drow = dOs + l32 * (DOW * 2);
-#pragma unroll
-        for (int ds = 0; ds < DV / 16; ++ds) {
-          const int off = ((2 * ds + hl) ^ dsw) * 16;
-          const V8 vop = V_LDS ? lds_read8<V8>(vt_row + off) : vf[V_LDS ? 0 : ds];
-          dp = E::mfma(lds_read8<V8>(drow + off), vop, dp);
-        }
-      }
+      const VMO_LDS char* drow = dOs + l32 * (DOW * 2);
+      struct Ops { V8 a, b; };
+      constexpr int NS = D / 16, NOP = NS + (WANT_DK ? DV / 16 : 0);
+      prefetched_chain<NOP, kBwdPrefetch>(
+          [&](int i) __attribute__((always_inline)) {
+            Ops o;
+            if (i < NS) {
+              const int off = ((2 * i + hl) ^ qsw) * 16;
+              o.a = lds_read8<V8>(qrow + off);
+              o.b = K_LDS ? lds_read8<V8>(kt_row + off) : kf[K_LDS ? 0 : i];
+            } else {
+              const int off = ((2 * (i - NS) + hl) ^ dsw) * 16;
+              o.a = lds_read8<V8>(drow + off);
+              o.b = V_LDS ? lds_read8<V8>(vt_row + off) : vf[V_LDS ? 0 : i - NS];
+            }
+            return o;
+          },
+          [&](int i, const Ops& o) __attribute__((always_inline)) {
+            if (i < NS) s = E::mfma(o.a, o.b, s);
+            else dp = E::mfma(o.a, o.b, dp);
+          });
     }
     V8 P[2], G[2];
 #pragma unroll
@@ -514,20 +526,22 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
       }
     }
     // dV^T[dv][key] += dO^T P,  dK^T[d][key] += Q^T dS  (transposed reads of the staged tiles)
-#pragma unroll
-    for (int a = 0; a < NV; ++a) {
-      const int c0 = tr_offset<DOW * 2>(trow, tchunk, tbyte, a);
-#pragma unroll
-      for (int ss = 0; ss < 2; ++ss) dv[a] = E::mfma(tr_pair<V8, DOW * 2>(dOs + 16 * ss * (DOW * 2), c0), P[ss], dv[a]);
-    }
-    if constexpr (WANT_DK) {
-#pragma unroll
-      for (int a = 0; a < NK; ++a) {
-        const int c0 = tr_offset<D * 2>(trow, tchunk, tbyte, a);
-#pragma unroll
-        for (int ss = 0; ss < 2; ++ss) dk[a] = E::mfma(tr_pair<V8, D * 2>(Qs + 16 * ss * (D * 2), c0), G[ss], dk[a]);
-      }
-    }
+    constexpr int NT = 2 * NV + (WANT_DK ? 2 * NK : 0);
+    prefetched_chain<NT, kBwdPrefetch>(
+        [&](int i) __attribute__((always_inline)) {
+          if (i < 2 * NV)
+            return tr_pair<V8, DOW * 2>(dOs + 16 * (i % 2) * (DOW * 2), tr_offset<DOW * 2>(trow, tchunk, tbyte, i / 2));
+          const int j = i - 2 * NV;
+          return tr_pair<V8, D * 2>(Qs + 16 * (j % 2) * (D * 2), tr_offset<D * 2>(trow, tchunk, tbyte, j / 2));
+        },
+        [&](int i, const V8& x) __attribute__((always_inline)) {
+          if (i < 2 * NV) {
+            dv[i / 2] = E::mfma(x, P[i % 2], dv[i / 2]);
+          } else if constexpr (WANT_DK) {
+            const int j = i - 2 * NV;
+            dk[j / 2] = E::mfma(x, G[j % 2], dk[j / 2]);
+          }
+        });
   };
   issue(0);
   const int n_full = p.nq / kKvBM;   // stages with 32 valid queries
@@ -620,6 +634,7 @@ static int dispatch_bwd(const BwdParams& p, int d, int dv, hipStream_t s) {
   if (d == 128 && dv == 128) return launch_bwd<F16, 128, 128>(p, s);
   if (d == 64 && dv == 256) return launch_bwd<F16, 64, 256>(p, s);
   if (d == 128 && dv == 256) return launch_bwd<F16, 128, 256>(p, s);
+  if (d == 256 && dv == 256) return launch_bwd<F16, 256, 256>(p, s);
   return set_error(VMO_ERR_UNSUPPORTED, "fea_bwd: no kernel for d=%d dv=%d", d, dv);
 }
 

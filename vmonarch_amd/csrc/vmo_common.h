@@ -162,4 +162,30 @@ __device__ __forceinline__ V8 lds_read_tr8(const VMO_LDS char* p0, const VMO_LDS
 template <class T>
 __device__ __forceinline__ T to_elem(float x) { return static_cast<T>(x); }
 
+// Runs step(i, operand(i)) for i = 0 .. N-1 with operand(i + PF) read before step(i), so that the
+// LDS reads of the next PF products are in flight behind each MFMA (at one or two waves per SIMD no
+// other wave hides a read's latency, and the scheduler otherwise issues each read just before its
+// product).  operand(i) and step(i, .) must be inlinable with compile-time i after unrolling.
+// PF = 0 reads each operand just before its product (the scheduler's choice).
+template <int N, int PF, class Operand, class Step>
+__device__ __forceinline__ void prefetched_chain(Operand operand, Step step) {
+  static_assert(N >= 1 && PF >= 0, "chain");
+  if constexpr (PF == 0) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) step(i, operand(i));
+  } else {
+    using V = decltype(operand(0));
+    V ring[PF];
+#pragma unroll
+    for (int i = 0; i < PF; ++i)
+      if (i < N) ring[i] = operand(i);
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const V cur = ring[i % PF];
+      if (i + PF < N) ring[i % PF] = operand(i + PF);
+      step(i, cur);
+    }
+  }
+}
+
 }  // namespace vmo

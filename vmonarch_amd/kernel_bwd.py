@@ -57,7 +57,7 @@ def fea_backward(q, k, v, o, lse, ent, do, de, sm_scale, n_valid):
     n = int(n_valid)
     Dk = 64 if D < 64 else D
     Dvk = 64 if Dv < 64 else Dv
-    if Dk not in (64, 128) or Dvk not in (64, 128, 256):
+    if not ((Dk in (64, 128) and Dvk in (64, 128, 256)) or (Dk == 256 and Dvk == 256)):
         raise NotImplementedError(f"vmonarch_amd: backward for head dims ({D}, {Dv}) is not built")
     if de is None:
         de = torch.zeros((B, H, N), device=q.device, dtype=torch.float32)
