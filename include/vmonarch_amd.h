@@ -126,8 +126,13 @@ typedef struct vmo_lstep_args {
  * keys per (batch, head) (nq != nk allowed).  Supported: d in {64, 128} with dv in {64, 128, 256},
  * and d = dv = 256.  Needs vmo_fea_bwd_workspace_size() bytes of workspace.
  */
-/* vmo_fea_bwd_args.flags: the marked gradient is float32 and the kernels add into it (+=) */
-enum { VMO_BWD_ACCUM_Q = 1, VMO_BWD_ACCUM_K = 2, VMO_BWD_ACCUM_V = 4 };
+/* vmo_fea_bwd_args.flags: the marked gradient is float32 and the kernels add into it (+=, ACCUM) or
+ * overwrite it (=, F32); without either bit it has the inputs' dtype.  ACCUM and F32 of the same
+ * gradient together are rejected. */
+enum {
+  VMO_BWD_ACCUM_Q = 1, VMO_BWD_ACCUM_K = 2, VMO_BWD_ACCUM_V = 4,
+  VMO_BWD_F32_Q = 8, VMO_BWD_F32_K = 16, VMO_BWD_F32_V = 32
+};
 
 typedef struct vmo_fea_bwd_args {
   int32_t dtype;
@@ -144,7 +149,7 @@ typedef struct vmo_fea_bwd_args {
   float sm_scale;
   void* workspace;
   size_t workspace_bytes;
-  int32_t flags;                   /* VMO_BWD_ACCUM_* */
+  int32_t flags;                   /* VMO_BWD_ACCUM_* | VMO_BWD_F32_* */
 } vmo_fea_bwd_args;
 
 /*

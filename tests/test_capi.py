@@ -113,3 +113,17 @@ def test_lstep_bwd_rejects_too_many_blocks_and_null_args(L):
     assert L.vmo_lstep_bwd(ctypes.byref(a), None) == 2
     assert b"num_blocks" in L.vmo_last_error()
     assert L.vmo_lstep_bwd(None, None) != 0
+
+
+def test_fea_bwd_rejects_unknown_and_conflicting_flags(L):
+    from vmonarch_amd import _lib
+    a = _lib.FeaBwdArgs()
+    a.dtype, a.batch, a.heads, a.nq, a.nk, a.d, a.dv = 0, 1, 1, 128, 128, 128, 128
+    v = _lib.View(4096, 128, 128 * 128, 128)
+    a.q = a.k = a.v = a.o = a.grad_o = a.grad_q = a.grad_k = a.grad_v = v
+    a.lse = a.ent = a.grad_ent = 4096
+    a.sm_scale = 0.1
+    for flags in (_lib.BWD_ACCUM_K | _lib.BWD_F32_K, _lib.BWD_ACCUM_Q | _lib.BWD_F32_Q, 64):
+        a.flags = flags
+        assert L.vmo_fea_bwd(ctypes.byref(a), None) == 1
+        assert b"flags" in L.vmo_last_error()

@@ -285,7 +285,8 @@ def test_fea_backward_few_queries_many_keys(nq, nk, D, Dv):
 
 def test_fea_backward_accumulates_into_fp32_gradients():
     """With float32 gradient views passed in, the kernels add into them (VMO_BWD_ACCUM_*): result =
-    prefill + the gradients the plain call returns, for a split-KV dq and strided column slices."""
+    prefill + the gradients the plain call returns, for a split-KV dq and strided column slices; or
+    overwrite them (VMO_BWD_F32_*)."""
     from vmonarch_amd.kernel import fea_forward
     from vmonarch_amd.kernel_bwd import fea_backward_raw
     g = torch.Generator().manual_seed(11)
@@ -305,6 +306,14 @@ def test_fea_backward_accumulates_into_fp32_gradients():
                                atol=2e-2 * plain[1].float().abs().max().item())
     torch.testing.assert_close(kv[..., D:D + Dv] - kv0[..., D:D + Dv], plain[2].float(), rtol=2e-2,
                                atol=2e-2 * plain[2].float().abs().max().item())
+    assert torch.equal(kv[..., D + Dv:], kv0[..., D + Dv:])
+    # overwrite mode (VMO_BWD_F32_*): the prefill is replaced, the spare columns stay untouched
+    dq, kv = dq0.clone(), kv0.clone()
+    fea_backward_raw(q, k, v, o, lse, ent, do, de, D ** -0.5, dq=dq, dk=kv[..., :D], dv=kv[..., D:D + Dv],
+                     overwrite="qkv")
+    torch.cuda.synchronize()
+    for got, want in ((dq, plain[0]), (kv[..., :D], plain[1]), (kv[..., D:D + Dv], plain[2])):
+        torch.testing.assert_close(got, want.float(), rtol=2e-2, atol=2e-2 * want.float().abs().max().item())
     assert torch.equal(kv[..., D + Dv:], kv0[..., D + Dv:])
 
 

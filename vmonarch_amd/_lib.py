@@ -46,6 +46,7 @@ class FeaBwdArgs(ctypes.Structure):
 
 
 BWD_ACCUM_Q, BWD_ACCUM_K, BWD_ACCUM_V = 1, 2, 4
+BWD_F32_Q, BWD_F32_K, BWD_F32_V = 8, 16, 32
 
 
 class LstepArgs(ctypes.Structure):

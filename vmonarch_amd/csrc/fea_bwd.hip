@@ -58,7 +58,7 @@ struct BwdParams {
   int dq_tiles, kv_tiles;
   int dq_total, kv_total;
   int dq_splits, keys_per_split;   // dq workgroups per query tile, each over one key range
-  int accum;                       // VMO_BWD_ACCUM_* bits: that gradient is fp32 and accumulated into
+  int accum;                       // VMO_BWD_ACCUM_* / VMO_BWD_F32_* bits: that gradient is fp32, added to / stored
   float c;          // sm_scale * log2(e)
   float sm_scale;
 };
@@ -174,6 +174,12 @@ constexpr int dkdv_lds_bytes() {
 __device__ __forceinline__ int xcd_remap(int nblocks) {
   const int per_xcd = nblocks >> 3;
   return (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+}
+
+// How a gradient is written: in the inputs' type, or into an fp32 buffer (added to or overwritten).
+enum { kGradStore = 0, kGradAddF32 = 1, kGradStoreF32 = 2 };
+__device__ __forceinline__ int grad_mode(int flags, int accum_bit, int f32_bit) {
+  return (flags & accum_bit) ? kGradAddF32 : (flags & f32_bit) ? kGradStoreF32 : kGradStore;
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -321,14 +327,14 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
         for (int e = 0; e < 4; ++e) v[e] = acc[a][4 * j + e] * p.sm_scale;
         *(f32x4*)(pr + 32 * a + 8 * j + 4 * hl) = v;
       }
-  } else if (p.accum & VMO_BWD_ACCUM_Q) {
+  } else if (const int mode = grad_mode(p.accum, VMO_BWD_ACCUM_Q, VMO_BWD_F32_Q); mode != kGradStore) {
     float* dqr = (float*)p.dq + bb * p.dq_sb + hh * p.dq_sh + (int64_t)qrow * p.dq_sn;
 #pragma unroll
     for (int a = 0; a < NA; ++a)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         f32x4* ptr = (f32x4*)(dqr + 32 * a + 8 * j + 4 * hl);
-        f32x4 v = *ptr;
+        f32x4 v = mode == kGradAddF32 ? *ptr : f32x4{};
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] += acc[a][4 * j + e] * p.sm_scale;
         *ptr = v;
@@ -348,7 +354,7 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
 }
 
 // Sum the split-KV partials of dQ (fixed split order, so the result does not depend on timing) and
-// write grad_q, or add them into an fp32 grad_q.
+// write grad_q, or store / add them into an fp32 grad_q.
 template <bool F16, int D>
 __global__ __launch_bounds__(256) void fea_bwd_dq_reduce(BwdParams p) {
   using T = typename Elem<F16>::T;
@@ -363,9 +369,9 @@ __global__ __launch_bounds__(256) void fea_bwd_dq_reduce(BwdParams p) {
   for (int sp = 0; sp < p.dq_splits; ++sp)
     acc += *(const f32x4*)(p.dq_part + (((int64_t)sp * p.problems + prob) * p.nq + qi) * D + 4 * c4);
   const int hh = prob % p.heads, bb = prob / p.heads;
-  if (p.accum & VMO_BWD_ACCUM_Q) {
+  if (const int mode = grad_mode(p.accum, VMO_BWD_ACCUM_Q, VMO_BWD_F32_Q); mode != kGradStore) {
     f32x4* ptr = (f32x4*)((float*)p.dq + bb * p.dq_sb + hh * p.dq_sh + (int64_t)qi * p.dq_sn + 4 * c4);
-    *ptr = *ptr + acc;
+    *ptr = mode == kGradAddF32 ? *ptr + acc : acc;
   } else {
     V4 v;
 #pragma unroll
@@ -548,16 +554,16 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
   for (int t = 0; t < n_full; ++t) iteration(t, std::false_type{});
   if (n_full < n_tiles) iteration(n_full, std::true_type{});
   if (!wave_live || !kvalid) return;
-  // store (or, for an fp32 gradient with its accumulate bit, add) NACC accumulator blocks times f
+  // write NACC accumulator blocks times f: stored in T, or added to / stored into an fp32 gradient
   auto put = [&](void* base, int64_t sb, int64_t sh, int64_t sn, int col0, const f32x16* acc, int nacc, float f,
-                 bool add) __attribute__((always_inline)) {
-    if (add) {
+                 int mode) __attribute__((always_inline)) {
+    if (mode != kGradStore) {
       float* r = (float*)base + bb * sb + hh * sh + (int64_t)krow * sn + col0;
       for (int a = 0; a < nacc; ++a)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           f32x4* ptr = (f32x4*)(r + 32 * a + 8 * j + 4 * hl);
-          f32x4 v = *ptr;
+          f32x4 v = mode == kGradAddF32 ? *ptr : f32x4{};
 #pragma unroll
           for (int e = 0; e < 4; ++e) v[e] += acc[a][4 * j + e] * f;
           *ptr = v;
@@ -574,8 +580,9 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
         }
     }
   };
-  if constexpr (WANT_DK) put(p.dk, p.dk_sb, p.dk_sh, p.dk_sn, 0, dk, NK, p.sm_scale, (p.accum & VMO_BWD_ACCUM_K) != 0);
-  put(p.dv, p.dv_sb, p.dv_sh, p.dv_sn, VOFF, dv, NV, 1.0f, (p.accum & VMO_BWD_ACCUM_V) != 0);
+  if constexpr (WANT_DK)
+    put(p.dk, p.dk_sb, p.dk_sh, p.dk_sn, 0, dk, NK, p.sm_scale, grad_mode(p.accum, VMO_BWD_ACCUM_K, VMO_BWD_F32_K));
+  put(p.dv, p.dv_sb, p.dv_sh, p.dv_sn, VOFF, dv, NV, 1.0f, grad_mode(p.accum, VMO_BWD_ACCUM_V, VMO_BWD_F32_V));
 }
 
 template <bool F16, int D, int DV, int PART>
@@ -677,8 +684,9 @@ extern "C" int vmo_fea_bwd(const vmo_fea_bwd_args* a, void* stream) {
       !view_ok(a->grad_q) || !view_ok(a->grad_k) || !view_ok(a->grad_v))
     return set_error(VMO_ERR_INVALID, "fea_bwd: tensors need 16-byte aligned rows");
   if (!a->lse || !a->ent || !a->grad_ent) return set_error(VMO_ERR_INVALID, "fea_bwd: lse / ent / dent required");
-  if (a->flags & ~(VMO_BWD_ACCUM_Q | VMO_BWD_ACCUM_K | VMO_BWD_ACCUM_V))
-    return set_error(VMO_ERR_INVALID, "fea_bwd: unknown flags 0x%x", (unsigned)a->flags);
+  constexpr int kFlags = VMO_BWD_ACCUM_Q | VMO_BWD_ACCUM_K | VMO_BWD_ACCUM_V | VMO_BWD_F32_Q | VMO_BWD_F32_K | VMO_BWD_F32_V;
+  if ((a->flags & ~kFlags) || ((a->flags >> 3) & a->flags & 7))
+    return set_error(VMO_ERR_INVALID, "fea_bwd: unknown or conflicting flags 0x%x", (unsigned)a->flags);
   if (!(a->sm_scale >= 0.f)) return set_error(VMO_ERR_INVALID, "fea_bwd: sm_scale");
   // the tile copies address up to 7 rows from a lane with a 32-bit byte offset
   const int64_t kMaxRowStride = 1ll << 27;

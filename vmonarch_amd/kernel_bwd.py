@@ -13,20 +13,22 @@ def _pad_features(t, width):
     return t if t.shape[-1] == width else torch.nn.functional.pad(t, (0, width - t.shape[-1]))
 
 
-def fea_backward_raw(q, k, v, o, lse, ent, do, de, sm_scale, dq=None, dk=None, dv=None):
+def fea_backward_raw(q, k, v, o, lse, ent, do, de, sm_scale, dq=None, dk=None, dv=None, overwrite=""):
     """q: (B, H, nq, D); k: (B, H, nk, D); v: (B, H, nk, Dv); o, do: (B, H, nq, Dv);
     lse, ent, de: (B, H, nq) fp32 with unit token stride.  Returns (dq, dk, dv).
 
-    A gradient passed in as a float32 view is accumulated into (+= in the kernels); otherwise it is
-    returned as a new tensor of q's dtype."""
+    A gradient passed in as a float32 view is accumulated into (+= in the kernels), or overwritten
+    when its letter ("q", "k", "v") is in `overwrite`; otherwise it is returned as a new tensor of
+    q's dtype."""
     L = _lib.lib()
     B, H, NQ, D = q.shape
     NK, Dv = k.shape[2], v.shape[-1]
     flags = 0
-    for t, bit in ((dq, _lib.BWD_ACCUM_Q), (dk, _lib.BWD_ACCUM_K), (dv, _lib.BWD_ACCUM_V)):
+    for t, name, acc_bit, f32_bit in ((dq, "q", _lib.BWD_ACCUM_Q, _lib.BWD_F32_Q), (dk, "k", _lib.BWD_ACCUM_K, _lib.BWD_F32_K),
+                                      (dv, "v", _lib.BWD_ACCUM_V, _lib.BWD_F32_V)):
         if t is not None:
-            assert t.dtype == torch.float32, "an accumulated gradient must be float32"
-            flags |= bit
+            assert t.dtype == torch.float32, "a gradient passed in must be float32"
+            flags |= f32_bit if name in overwrite else acc_bit
     if dq is None:
         dq = torch.empty((B, H, NQ, D), device=q.device, dtype=q.dtype)
     if dk is None:

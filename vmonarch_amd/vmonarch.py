@@ -176,11 +176,12 @@ class _VMonarchFunction(torch.autograd.Function):
     """VMonarch attention with a HIP backward (the gradient autograd takes through vmonarch.py:41-69).
 
     The forward is the all-HIP pipeline of _vmonarch_fused, keeping what the backward needs: every
-    R-step's input u, output, LSE and entropy, and the recompute's LSE.  The backward walks it in
-    reverse: the recompute rows through vmo_fea_bwd (rt queries against all N keys), then per
-    iteration the fused L-step backward (vmo_lstep_bwd) and the R-step's flash-entropy backward
-    (vmo_fea_bwd on the m frames of each head, values k or [k | v]; the entropy enters the L-step
-    detached, vmonarch.py:26, so its gradient is zero).  Gradients of q, k, v accumulate in fp32.
+    R-step's input u, output, LSE and entropy, and the recompute's LSE.  The backward walks the
+    iterations in reverse, each as the fused L-step backward (vmo_lstep_bwd) and the R-step's
+    flash-entropy backward (vmo_fea_bwd on the m frames of each head, values k or [k | v]; the
+    entropy enters the L-step detached, vmonarch.py:26, so its gradient is zero), then the
+    recompute rows through vmo_fea_bwd (rt queries against all N keys).  Gradients of q, k, v
+    collect in fp32.
     """
 
     @staticmethod
@@ -224,15 +225,12 @@ class _VMonarchFunction(torch.autograd.Function):
         dev, dt = q.device, q.dtype
         dz = _lib.row_aligned(dz.to(dt))
         f32 = torch.float32
-        # fp32 accumulators the kernels add into: dq, and one (.., 2D + Dv) buffer holding dk from
-        # the key role | dk from the value role (w starts with k) | dv
+        # fp32 gradient buffers: dq (the L-step backward adds into it, so it starts at zero), and one
+        # (.., 2D + Dv) buffer holding dk from the key role | dk from the value role (w starts with
+        # k) | dv, which the last R-step's backward (the first one run, covering every token)
+        # overwrites and every later backward adds into
         dq = torch.zeros((B, H, N, D), device=dev, dtype=f32)
-        g_kv = torch.zeros((B, H, N, 2 * D + Dv), device=dev, dtype=f32)
-        if rt > 0:
-            # exact attention of the first rt queries (vmonarch.py:66-68)
-            zeros = torch.zeros((B, H, rt), device=dev, dtype=f32)
-            fea_backward_raw(q[:, :, :rt], k, v, z[:, :, :rt], lse_rt, zeros, _lib.row_aligned(dz[:, :, :rt]), zeros,
-                             scale, dq=dq[:, :, :rt], dk=g_kv[..., :D], dv=g_kv[..., 2 * D:])
+        g_kv = torch.empty((B, H, N, 2 * D + Dv), device=dev, dtype=f32)
         frames = lambda t: t.reshape(B, H * m, b, *t.shape[3:])   # the R-step's m frames per head
         de = torch.zeros((B, H * m, b), device=dev, dtype=f32)
         g_fr = frames(g_kv)
@@ -246,13 +244,19 @@ class _VMonarchFunction(torch.autograd.Function):
             gx, _, _ = fea_backward_raw(frames(x), frames(k), frames(w), frames(out), frames(lse), frames(ent),
                                         frames(dout), de, scale if it == 0 else 1.0,
                                         dq=frames(dq) if it == 0 else None,   # R-step 0 read q directly
-                                        dk=g_fr[..., :D], dv=g_fr[..., D:] if last else g_fr[..., D:2 * D])
+                                        dk=g_fr[..., :D], dv=g_fr[..., D:] if last else g_fr[..., D:2 * D],
+                                        overwrite="kv" if last else "")
             if it > 0:
                 g = gx.view(B, H, N, D)     # dL/du of the previous L-step's output
-        # gradients in the memory order the caller's q, k, v had (the fp32 -> dtype copy places them)
+        if rt > 0:
+            # exact attention of the first rt queries (vmonarch.py:66-68)
+            zeros = torch.zeros((B, H, rt), device=dev, dtype=f32)
+            fea_backward_raw(q[:, :, :rt], k, v, z[:, :, :rt], lse_rt, zeros, _lib.row_aligned(dz[:, :, :rt]), zeros,
+                             scale, dq=dq[:, :, :rt], dk=g_kv[..., :D], dv=g_kv[..., 2 * D:])
+        # gradients in the memory order the caller's q, k, v had (the fp32 -> dtype writes place them)
         gq, gk, gv = (_lib.empty_in_order(o, (B, H, N), f, dt, dev) for o, f in zip(ctx.orders, (D, D, Dv)))
         gq.copy_(dq)
-        gk.copy_(g_kv[..., :D] + g_kv[..., D:2 * D])
+        torch.add(g_kv[..., :D], g_kv[..., D:2 * D], out=gk)
         gv.copy_(g_kv[..., 2 * D:])
         return gq, gk, gv, None, None, None, None, None
 
