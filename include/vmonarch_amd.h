@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define VMO_ABI_VERSION 3
+#define VMO_ABI_VERSION 4
 
 enum {
   VMO_OK = 0,
@@ -150,6 +150,12 @@ typedef struct vmo_fea_bwd_args {
   void* workspace;
   size_t workspace_bytes;
   int32_t flags;                   /* VMO_BWD_ACCUM_* | VMO_BWD_F32_* */
+  /* Values given in two parts: with dv1 > 0 the value tensor is [v | v1], v holding columns
+   * [0, dv - dv1) and v1 (same strides as v) the last dv1 (VMonarch's last R-step, values [k | v],
+   * vmonarch.py:50, without the concatenated copy).  Built for dv1 = dv / 2 with (d, dv) = (64, 128)
+   * and (128, 256).  grad_v stays one (.., dv) tensor. */
+  vmo_view v1;
+  int32_t dv1;
 } vmo_fea_bwd_args;
 
 /*

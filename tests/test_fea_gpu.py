@@ -330,3 +330,23 @@ def test_fea_backward_fp16(D, Dv):
     refs = entropy_attention_grad(q.float().numpy(), k.float().numpy(), v.float().numpy(),
                                   do.half().float().numpy(), de.numpy(), D ** -0.5)
     _check_grads(grads, refs)
+
+
+@pytest.mark.parametrize("nq, nk, D", [(300, 300, 64), (300, 300, 128), (40, 4096, 128), (200, 1000, 64)])
+def test_fea_backward_values_in_two_parts(nq, nk, D):
+    """Values given as [v0 | v1] (vmo_fea_bwd_args.v1, VMonarch's last R-step [k | v]) read in place
+    give the gradients of the concatenated tensor bit for bit."""
+    from vmonarch_amd.kernel import fea_forward
+    from vmonarch_amd.kernel_bwd import fea_backward_raw
+    g = torch.Generator().manual_seed(nq + nk + D)
+    q, k = randn_lp(g, 1, 2, nq, D).to(DEV), randn_lp(g, 1, 2, nk, D).to(DEV)
+    v0, v1 = randn_lp(g, 1, 2, nk, D).to(DEV), randn_lp(g, 1, 2, nk, D).to(DEV)
+    w = torch.cat([v0, v1], -1)
+    do = randn_lp(g, 1, 2, nq, 2 * D).to(DEV)
+    de = torch.randn(1, 2, nq, generator=g).to(DEV)
+    o, lse, ent = fea_forward(q, k, w, None, D ** -0.5)
+    print(f"fea_bwd two-part values nq={nq} nk={nk} D={D}", flush=True)
+    ref = fea_backward_raw(q, k, w, o, lse, ent, do, de, D ** -0.5)
+    got = fea_backward_raw(q, k, v0, o, lse, ent, do, de, D ** -0.5, v1=v1)
+    for a, b, name in zip(got, ref, ("dq", "dk", "dv")):
+        assert torch.equal(a, b), name

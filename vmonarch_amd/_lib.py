@@ -12,7 +12,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libvmonarch_gfx950.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 DTYPES = {torch.bfloat16: 0, torch.float16: 1}
 
 c_int32, c_int64, c_float, c_void_p, c_size_t = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
@@ -42,6 +42,7 @@ class FeaBwdArgs(ctypes.Structure):
         ("stat_stride_b", c_int64), ("stat_stride_h", c_int64),
         ("grad_ent_stride_b", c_int64), ("grad_ent_stride_h", c_int64),
         ("sm_scale", c_float), ("workspace", c_void_p), ("workspace_bytes", c_size_t), ("flags", c_int32),
+        ("v1", View), ("dv1", c_int32),
     ]
 
 

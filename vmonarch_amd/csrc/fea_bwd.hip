@@ -40,6 +40,7 @@ struct BwdParams {
   const void* q;
   const void* k;
   const void* v;
+  const void* v1;   // second value part ([v | v1], same strides as v), or null
   const void* o;
   const void* dO;
   void* dq;
@@ -84,6 +85,28 @@ __device__ __forceinline__ void stage_rows_n(const T* __restrict__ base, int64_t
   }
 }
 
+// The same copy of a tile whose rows are [a | b]: columns [0, W/2) from a, [W/2, W) from b (same
+// strides).  swz_rows only flips a chunk index within its 16-chunk group, so for W >= 256 each lane's
+// source stays in the half of its destination; for W = 128 the half follows the swizzled chunk.
+template <class T, int W, int ROWS>
+__device__ __forceinline__ void stage_rows_n2(const T* __restrict__ a, const T* __restrict__ b, int64_t sn, int row0,
+                                              int nrows, uint32_t dst, int wave, int lane) {
+  constexpr int CH = W / 8;
+  constexpr int RPI = 64 / CH;
+  constexpr int NI = ROWS / RPI;
+  static_assert(CH >= 8 && NI % kBwdWaves == 0, "tile shape");
+#pragma unroll
+  for (int i = 0; i < NI / kBwdWaves; ++i) {
+    const int inst = i * kBwdWaves + wave;
+    const int r = inst * RPI + lane / CH;
+    const int lc = (lane % CH) ^ swz_rows<W * 2>(r);
+    int gr = row0 + r;
+    gr = gr < nrows ? gr : nrows - 1;
+    const T* src = lc < CH / 2 ? a : b;
+    dma16_async(src + (int64_t)gr * sn + (lc % (CH / 2)) * 8, dst + inst * 1024);
+  }
+}
+
 // The same copy for the tiles staged inside the key / query loops: per-lane byte offsets computed
 // once, a scalar row base per tile (a full tile costs scalar adds only; the clamped per-lane path is
 // taken by a tile that runs past the end).  Row strides must stay below 2^27 elements (32-bit lane
@@ -124,6 +147,52 @@ struct BwdTileCopy {
         const int gr = min(row0 + r, nrows - 1);
         dma16_async((const void*)(uintptr_t)(ub + (uint64_t)gr * rbytes + ((lane % CH) ^ swz_rows<W * 2>(r)) * 16),
                     dst + inst * 1024);
+      }
+    }
+  }
+};
+
+// BwdTileCopy for a tile whose rows are [a | b] (as stage_rows_n2): each lane keeps the 64-bit
+// address of its chunk in its instruction's first row, so a full tile costs one 64-bit add per copy.
+template <class T, int W, int ROWS>
+struct BwdTileCopy2 {
+  static constexpr int CH = W / 8;
+  static constexpr int RPI = 64 / CH;
+  static constexpr int NI = ROWS / RPI / kBwdWaves;
+  static constexpr int NV = (kBwdWaves * RPI) % 16 == 0 ? 1 : 2;
+  static_assert(CH >= 8 && NI >= 1 && RPI >= 2, "tile shape");
+  const T* a;
+  const T* b;
+  int64_t sn;
+  uint64_t rbytes;
+  uint64_t lbase[NV];
+  int wave, lane;
+
+  __device__ __forceinline__ BwdTileCopy2(const T* a_, const T* b_, int64_t sn_, int w, int l)
+      : a(a_), b(b_), sn(sn_), wave(w), lane(l) {
+    rbytes = uniform64((uint64_t)sn_ * 2);
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int r = (v * kBwdWaves + w) * RPI + l / CH;
+      const int lc = (l % CH) ^ swz_rows<W * 2>(r);
+      lbase[v] = (uint64_t)(uintptr_t)((lc < CH / 2 ? a_ : b_) + (int64_t)(l / CH) * sn_ + (lc % (CH / 2)) * 8);
+    }
+  }
+  __device__ __forceinline__ void issue(int row0, int nrows, uint32_t dst) const {
+    if (row0 + ROWS <= nrows) {
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const uint64_t roff = (uint64_t)(row0 + (i * kBwdWaves + wave) * RPI) * rbytes;
+        dma16_async((const void*)(uintptr_t)(lbase[i % NV] + roff), dst + (i * kBwdWaves + wave) * 1024);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int inst = i * kBwdWaves + wave;
+        const int r = inst * RPI + lane / CH;
+        const int lc = (lane % CH) ^ swz_rows<W * 2>(r);
+        const int gr = min(row0 + r, nrows - 1);
+        dma16_async((lc < CH / 2 ? a : b) + (int64_t)gr * sn + (lc % (CH / 2)) * 8, dst + inst * 1024);
       }
     }
   }
@@ -183,7 +252,7 @@ __device__ __forceinline__ int grad_mode(int flags, int accum_bit, int f32_bit) 
 }
 
 // ------------------------------------------------------------------------------------------------
-template <bool F16, int D, int DV>
+template <bool F16, int D, int DV, bool V2>
 __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq_kernel(BwdParams p) {
   using E = Elem<F16>;
   using T = typename E::T;
@@ -254,7 +323,12 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
   const int n_tiles = (kend - kbeg + kDqBN - 1) / kDqBN;
   const uint32_t smem_u32 = (uint32_t)(uintptr_t)smem;
   const BwdTileCopy<T, D, kDqBN> kcopy(kb, p.k_sn, wave, lane);
-  const BwdTileCopy<T, DV, kDqBN> vcopy(vb, p.v_sn, wave, lane);
+  const auto vcopy = [&]() __attribute__((always_inline)) {
+    if constexpr (V2)
+      return BwdTileCopy2<T, DV, kDqBN>(vb, (const T*)p.v1 + bb * p.v_sb + hh * p.v_sh, p.v_sn, wave, lane);
+    else
+      return BwdTileCopy<T, DV, kDqBN>(vb, p.v_sn, wave, lane);
+  }();
   auto issue = [&](int t) {
     const uint32_t st = smem_u32 + (uint32_t)((t & 1) * STAGE);
     kcopy.issue(kbeg + t * kDqBN, kend, st);
@@ -418,6 +492,7 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
   {
     const T* kp = (const T*)p.k + bb * p.k_sb + hh * p.k_sh + (int64_t)kr * p.k_sn + hl * 8;
     const T* vp = (const T*)p.v + bb * p.v_sb + hh * p.v_sh + (int64_t)kr * p.v_sn + hl * 8;
+    const T* vp1 = p.v1 ? (const T*)p.v1 + bb * p.v_sb + hh * p.v_sh + (int64_t)kr * p.v_sn + hl * 8 : vp;
 #pragma unroll
     for (int ds = 0; ds < (K_LDS ? 0 : D / 16); ++ds) {
       kf[ds] = *(const V8*)(kp + ds * 16);
@@ -428,7 +503,8 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
     if constexpr (!V_LDS && WANT_DK) {
 #pragma unroll
       for (int ds = 0; ds < DV / 16; ++ds) {
-        vf[ds] = *(const V8*)(vp + ds * 16);
+        // columns 16 ds + 8 hl + 0..7: from the second value part when there is one and ds >= DV / 32
+        vf[ds] = p.v1 && ds >= DV / 32 ? *(const V8*)(vp1 + (ds - DV / 32) * 16) : *(const V8*)(vp + ds * 16);
         asm volatile("" : "+v"(vf[ds]));   // as kf: waited for here, not inside the loop
       }
     }
@@ -470,9 +546,14 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
 
   const VMO_LDS char* vt_row = smem + 2 * STAGE + (wave * 32 + l32) * (DV * 2);
   const VMO_LDS char* kt_row = smem + 2 * STAGE + V_TILE + (wave * 32 + l32) * (D * 2);
-  if constexpr (V_LDS)   // this workgroup's 128 V rows, once (landed by the first tile_sync)
-    stage_rows_n<T, DV, kKvBN>((const T*)p.v + bb * p.v_sb + hh * p.v_sh, p.v_sn, kt * kKvBN, p.nk,
-                               smem_u32 + 2 * STAGE, wave, lane);
+  if constexpr (V_LDS) {   // this workgroup's 128 V rows, once (landed by the first tile_sync)
+    const T* vb0 = (const T*)p.v + bb * p.v_sb + hh * p.v_sh;
+    if (p.v1)
+      stage_rows_n2<T, DV, kKvBN>(vb0, (const T*)p.v1 + bb * p.v_sb + hh * p.v_sh, p.v_sn, kt * kKvBN, p.nk,
+                                  smem_u32 + 2 * STAGE, wave, lane);
+    else
+      stage_rows_n<T, DV, kKvBN>(vb0, p.v_sn, kt * kKvBN, p.nk, smem_u32 + 2 * STAGE, wave, lane);
+  }
   if constexpr (K_LDS)   // and its 128 K rows
     stage_rows_n<T, D, kKvBN>((const T*)p.k + bb * p.k_sb + hh * p.k_sh, p.k_sn, kt * kKvBN, p.nk,
                               smem_u32 + 2 * STAGE + V_TILE, wave, lane);
@@ -602,20 +683,20 @@ static int launch_dkdv(const BwdParams& p, hipStream_t s) {
   return launch_status("fea_bwd_dkdv");
 }
 
-template <bool F16, int D, int DV>
+template <bool F16, int D, int DV, bool V2 = false>
 static int launch_bwd(const BwdParams& p, hipStream_t s) {
   constexpr int LDS_DQ = 2 * kDqBN * (D + DV) * 2;
   static_assert(LDS_DQ <= 160 * 1024, "bwd LDS");
   if (LDS_DQ > 65536) {
     static bool done = false;
     if (!done) {
-      if (hipFuncSetAttribute((const void*)fea_bwd_dq_kernel<F16, D, DV>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              LDS_DQ) != hipSuccess)
+      if (hipFuncSetAttribute((const void*)fea_bwd_dq_kernel<F16, D, DV, V2>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, LDS_DQ) != hipSuccess)
         return set_error(VMO_ERR_LAUNCH, "fea_bwd_dq: cannot raise the LDS limit to %d bytes", LDS_DQ);
       done = true;
     }
   }
-  hipLaunchKernelGGL((fea_bwd_dq_kernel<F16, D, DV>), dim3(xcd_grid(p.dq_total)), dim3(256), LDS_DQ, s, p);
+  hipLaunchKernelGGL((fea_bwd_dq_kernel<F16, D, DV, V2>), dim3(xcd_grid(p.dq_total)), dim3(256), LDS_DQ, s, p);
   int rc = launch_status("fea_bwd_dq");
   if (rc != VMO_OK) return rc;
   if (p.dq_splits > 1) {
@@ -635,6 +716,11 @@ static int launch_bwd(const BwdParams& p, hipStream_t s) {
 
 template <bool F16>
 static int dispatch_bwd(const BwdParams& p, int d, int dv, hipStream_t s) {
+  if (p.v1) {   // values in two halves (the caller checked dv1 = dv / 2)
+    if (d == 64 && dv == 128) return launch_bwd<F16, 64, 128, true>(p, s);
+    if (d == 128 && dv == 256) return launch_bwd<F16, 128, 256, true>(p, s);
+    return set_error(VMO_ERR_UNSUPPORTED, "fea_bwd: no kernel for d=%d with values in two parts of %d", d, dv / 2);
+  }
   if (d == 64 && dv == 64) return launch_bwd<F16, 64, 64>(p, s);
   if (d == 64 && dv == 128) return launch_bwd<F16, 64, 128>(p, s);
   if (d == 128 && dv == 64) return launch_bwd<F16, 128, 64>(p, s);
@@ -684,6 +770,13 @@ extern "C" int vmo_fea_bwd(const vmo_fea_bwd_args* a, void* stream) {
       !view_ok(a->grad_q) || !view_ok(a->grad_k) || !view_ok(a->grad_v))
     return set_error(VMO_ERR_INVALID, "fea_bwd: tensors need 16-byte aligned rows");
   if (!a->lse || !a->ent || !a->grad_ent) return set_error(VMO_ERR_INVALID, "fea_bwd: lse / ent / dent required");
+  if (a->dv1 < 0 || a->dv1 >= a->dv) return set_error(VMO_ERR_INVALID, "fea_bwd: dv1 = %d with dv = %d", a->dv1, a->dv);
+  if (a->dv1 > 0) {
+    if (a->dv1 * 2 != a->dv) return set_error(VMO_ERR_UNSUPPORTED, "fea_bwd: value parts must be dv / 2 wide");
+    if (!view_ok(a->v1) || a->v1.stride_b != a->v.stride_b || a->v1.stride_h != a->v.stride_h ||
+        a->v1.stride_n != a->v.stride_n)
+      return set_error(VMO_ERR_INVALID, "fea_bwd: v1 needs 16-byte aligned rows and the strides of v");
+  }
   constexpr int kFlags = VMO_BWD_ACCUM_Q | VMO_BWD_ACCUM_K | VMO_BWD_ACCUM_V | VMO_BWD_F32_Q | VMO_BWD_F32_K | VMO_BWD_F32_V;
   if ((a->flags & ~kFlags) || ((a->flags >> 3) & a->flags & 7))
     return set_error(VMO_ERR_INVALID, "fea_bwd: unknown or conflicting flags 0x%x", (unsigned)a->flags);
@@ -702,6 +795,7 @@ extern "C" int vmo_fea_bwd(const vmo_fea_bwd_args* a, void* stream) {
     return set_error(VMO_ERR_UNSUPPORTED, "fea_bwd: problem too large");
   BwdParams p{};
   p.q = a->q.data; p.k = a->k.data; p.v = a->v.data; p.o = a->o.data; p.dO = a->grad_o.data;
+  p.v1 = a->dv1 > 0 ? a->v1.data : nullptr;
   p.dq = a->grad_q.data; p.dk = a->grad_k.data; p.dv = a->grad_v.data;
   p.lse = a->lse; p.ent = a->ent; p.dent = a->grad_ent;
   p.alpha = (float*)a->workspace;

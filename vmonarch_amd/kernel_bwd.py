@@ -13,16 +13,18 @@ def _pad_features(t, width):
     return t if t.shape[-1] == width else torch.nn.functional.pad(t, (0, width - t.shape[-1]))
 
 
-def fea_backward_raw(q, k, v, o, lse, ent, do, de, sm_scale, dq=None, dk=None, dv=None, overwrite=""):
+def fea_backward_raw(q, k, v, o, lse, ent, do, de, sm_scale, dq=None, dk=None, dv=None, overwrite="", v1=None):
     """q: (B, H, nq, D); k: (B, H, nk, D); v: (B, H, nk, Dv); o, do: (B, H, nq, Dv);
     lse, ent, de: (B, H, nq) fp32 with unit token stride.  Returns (dq, dk, dv).
+
+    With `v1` (same shape and strides as v) the values are [v | v1], 2 Dv wide, read in place.
 
     A gradient passed in as a float32 view is accumulated into (+= in the kernels), or overwritten
     when its letter ("q", "k", "v") is in `overwrite`; otherwise it is returned as a new tensor of
     q's dtype."""
     L = _lib.lib()
     B, H, NQ, D = q.shape
-    NK, Dv = k.shape[2], v.shape[-1]
+    NK, Dv = k.shape[2], v.shape[-1] * (2 if v1 is not None else 1)
     flags = 0
     for t, name, acc_bit, f32_bit in ((dq, "q", _lib.BWD_ACCUM_Q, _lib.BWD_F32_Q), (dk, "k", _lib.BWD_ACCUM_K, _lib.BWD_F32_K),
                                       (dv, "v", _lib.BWD_ACCUM_V, _lib.BWD_F32_V)):
@@ -46,6 +48,9 @@ def fea_backward_raw(q, k, v, o, lse, ent, do, de, sm_scale, dq=None, dk=None, d
     a.stat_stride_b, a.stat_stride_h = lse.stride(0), lse.stride(1)
     a.grad_ent_stride_b, a.grad_ent_stride_h = de.stride(0), de.stride(1)
     a.sm_scale = float(sm_scale)
+    if v1 is not None:
+        assert v1.shape == v.shape and v1.stride() == v.stride() and v1.dtype == v.dtype
+        a.v1, a.dv1 = _lib.view(v1), v1.shape[-1]
     nbytes = L.vmo_fea_bwd_workspace_size(a)
     ws = torch.empty(nbytes, device=q.device, dtype=torch.uint8)
     a.workspace, a.workspace_bytes = ws.data_ptr(), nbytes

@@ -168,7 +168,7 @@ def _vmonarch_fused(q, k, v, m, b, num_iters, recompute_tokens, min_col_mass, st
 
 
 def _hip_backward_supported(q, k, v, num_blocks):
-    # the last R-step's backward takes [k | v] as one value tensor: widths 128 or 256
+    # the last R-step's backward takes the values [k | v] as two equal halves of 64 or 128
     return _fused_supported(q, k, v, num_blocks) and q.shape[-1] == v.shape[-1]
 
 
@@ -240,12 +240,12 @@ class _VMonarchFunction(torch.autograd.Function):
             x, out, lse, ent = saved[4 * it: 4 * it + 4]
             dout = torch.empty_like(out)
             _lstep_bwd_launch(q, out, ent, g, dq, dout, m, b, scale, last, rt if last else 0, min_col_mass)
-            w = torch.cat([k, v], -1) if last else k
-            gx, _, _ = fea_backward_raw(frames(x), frames(k), frames(w), frames(out), frames(lse), frames(ent),
+            # values k, or [k | v] read from the two tensors in place (vmonarch.py:50)
+            gx, _, _ = fea_backward_raw(frames(x), frames(k), frames(k), frames(out), frames(lse), frames(ent),
                                         frames(dout), de, scale if it == 0 else 1.0,
                                         dq=frames(dq) if it == 0 else None,   # R-step 0 read q directly
                                         dk=g_fr[..., :D], dv=g_fr[..., D:] if last else g_fr[..., D:2 * D],
-                                        overwrite="kv" if last else "")
+                                        overwrite="kv" if last else "", v1=frames(v) if last else None)
             if it > 0:
                 g = gx.view(B, H, N, D)     # dL/du of the previous L-step's output
         if rt > 0:
