@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define VMO_ABI_VERSION 4
+#define VMO_ABI_VERSION 5
 
 enum {
   VMO_OK = 0,
@@ -187,11 +187,13 @@ typedef struct vmo_lstep_bwd_args {
   const float* ent;                /* (B, H, m*b) with token stride 1 */
   int64_t ent_stride_b, ent_stride_h;
   vmo_view grad_res;               /* dL/dz (B, H, m*b, dv)   or   dL/du (B, H, m*b, d) */
-  vmo_view grad_q;                 /* float32 (B, H, m*b, d), accumulated into */
+  vmo_view grad_q;                 /* float32 (B, H, m*b, d), accumulated into (or overwritten) */
   vmo_view grad_out;               /* (B, H, m*b, d + dv*last), written */
   float scale;
   float min_col_mass;
+  int32_t flags;                   /* VMO_LSTEP_BWD_OVERWRITE_Q: grad_q = dL/dq instead of += */
 } vmo_lstep_bwd_args;
+enum { VMO_LSTEP_BWD_OVERWRITE_Q = 1 };
 
 /* ABI version of the loaded library (VMO_ABI_VERSION at build time). */
 int vmo_abi_version(void);

@@ -127,3 +127,15 @@ def test_fea_bwd_rejects_unknown_and_conflicting_flags(L):
         a.flags = flags
         assert L.vmo_fea_bwd(ctypes.byref(a), None) == 1
         assert b"flags" in L.vmo_last_error()
+
+
+def test_lstep_bwd_rejects_unknown_flags(L):
+    from vmonarch_amd import _lib
+    a = _lib.LstepBwdArgs()
+    a.dtype, a.batch, a.heads, a.num_blocks, a.block_size, a.d, a.dv = 0, 1, 1, 4, 4, 128, 128
+    v = _lib.View(4096, 128, 128, 128)
+    a.q = a.out = a.grad_res = a.grad_q = a.grad_out = v
+    a.ent = 4096
+    a.flags = 2
+    assert L.vmo_lstep_bwd(ctypes.byref(a), None) == 1
+    assert b"flags" in L.vmo_last_error()

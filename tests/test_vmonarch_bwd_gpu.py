@@ -47,6 +47,14 @@ def test_lstep_bwd_matches_oracle(d, dv, last, m, mcm):
     dq_ref, dout_ref = lstep_grad(r5(q), r5(out), -ent.numpy().reshape(B, H, m, b), d ** -0.5, last, gg, mcm)
     assert_close_ref((dq.cpu() - dq0).numpy(), dq_ref.reshape(B, H, N, d), 2e-2)
     assert_close_ref(dout.float().cpu().numpy(), dout_ref.reshape(B, H, N, wout), 2e-2)
+    # VMO_LSTEP_BWD_OVERWRITE_Q: the prefill is replaced by the same increment, bit for bit
+    dq_ow = dq0.to(DEV)
+    _lstep_bwd_launch(q.to(DEV), out.to(DEV), ent.to(DEV), grad.to(DEV), dq_ow, dout, m, b, d ** -0.5, last, skip, mcm,
+                      overwrite_q=True)
+    dq_inc = torch.zeros_like(dq_ow)
+    _lstep_bwd_launch(q.to(DEV), out.to(DEV), ent.to(DEV), grad.to(DEV), dq_inc, dout, m, b, d ** -0.5, last, skip, mcm)
+    torch.cuda.synchronize()
+    assert torch.equal(dq_ow, dq_inc)
 
 
 def _grads(q, k, v, do, m, b, iters, rt):

@@ -12,7 +12,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libvmonarch_gfx950.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 DTYPES = {torch.bfloat16: 0, torch.float16: 1}
 
 c_int32, c_int64, c_float, c_void_p, c_size_t = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
@@ -48,6 +48,7 @@ class FeaBwdArgs(ctypes.Structure):
 
 BWD_ACCUM_Q, BWD_ACCUM_K, BWD_ACCUM_V = 1, 2, 4
 BWD_F32_Q, BWD_F32_K, BWD_F32_V = 8, 16, 32
+LSTEP_BWD_OVERWRITE_Q = 1
 
 
 class LstepArgs(ctypes.Structure):
@@ -65,6 +66,7 @@ class LstepBwdArgs(ctypes.Structure):
         ("block_size", c_int32), ("d", c_int32), ("dv", c_int32), ("last", c_int32), ("skip_tokens", c_int32),
         ("q", View), ("out", View), ("ent", c_void_p), ("ent_stride_b", c_int64), ("ent_stride_h", c_int64),
         ("grad_res", View), ("grad_q", View), ("grad_out", View), ("scale", c_float), ("min_col_mass", c_float),
+        ("flags", c_int32),
     ]
 
 

@@ -289,6 +289,7 @@ struct LBParams {
   const float* ent;
   const void* g;
   float* dq;
+  int dq_overwrite;   // dq = dL/dq instead of +=
   void* dout;
   int64_t q_sb, q_sh, q_sn;
   int64_t out_sb, out_sh, out_sn;
@@ -559,7 +560,7 @@ __global__ __launch_bounds__(64 * kLBWaves) void lstep_bwd_kernel(LBParams p) {
 #pragma unroll
   for (int r = 0; r < 16; ++r) dl[r] = ivalid ? p.scale * s[r] * (da[r] - rs) : 0.f;
 
-  // ---- dq_i += sum_k dL[i,k] kr_k (+ sum_k a[i,k] dv_k): fp32 read-modify-write
+  // ---- dq_i += sum_k dL[i,k] kr_k (+ sum_k a[i,k] dv_k): fp32 read-modify-write (or store)
   {
     f32x16 accq[ND];
 #pragma unroll
@@ -573,7 +574,7 @@ __global__ __launch_bounds__(64 * kLBWaves) void lstep_bwd_kernel(LBParams p) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           f32x4* ptr = (f32x4*)(dqr + 32 * a + 8 * g + 4 * hl);
-          f32x4 v = *ptr;
+          f32x4 v = p.dq_overwrite ? f32x4{} : *ptr;
 #pragma unroll
           for (int e = 0; e < 4; ++e) v[e] += accq[a][4 * g + e];
           *ptr = v;
@@ -678,7 +679,9 @@ extern "C" int vmo_lstep_bwd(const vmo_lstep_bwd_args* a, void* stream) {
   const int64_t cols = (int64_t)a->batch * a->heads * a->block_size;
   if (cols > (1ll << 30) || (int64_t)a->num_blocks * a->block_size > (1ll << 30))
     return set_error(VMO_ERR_UNSUPPORTED, "lstep_bwd: problem too large");
+  if (a->flags & ~VMO_LSTEP_BWD_OVERWRITE_Q) return set_error(VMO_ERR_INVALID, "lstep_bwd: unknown flags 0x%x", (unsigned)a->flags);
   LBParams p{};
+  p.dq_overwrite = (a->flags & VMO_LSTEP_BWD_OVERWRITE_Q) != 0;
   p.q = a->q.data; p.out = a->out.data; p.ent = a->ent; p.g = a->grad_res.data;
   p.dq = (float*)a->grad_q.data; p.dout = a->grad_out.data;
   p.q_sb = a->q.stride_b; p.q_sh = a->q.stride_h; p.q_sn = a->q.stride_n;

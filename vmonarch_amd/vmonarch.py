@@ -66,8 +66,10 @@ def _lstep_launch(q, out, ent, res, m, b, scale, last, skip, min_col_mass):
     _lib.check(L.vmo_lstep_fwd(a, _lib.stream_of(q)), "vmo_lstep_fwd")
 
 
-def _lstep_bwd_launch(q, out, ent, grad_res, grad_q, grad_out, m, b, scale, last, skip, min_col_mass):
-    """Backward of one L-step (vmo_lstep_bwd): grad_q (fp32) += dL/dq, grad_out = dL/d out."""
+def _lstep_bwd_launch(q, out, ent, grad_res, grad_q, grad_out, m, b, scale, last, skip, min_col_mass,
+                      overwrite_q=False):
+    """Backward of one L-step (vmo_lstep_bwd): grad_q (fp32) += dL/dq (= with overwrite_q),
+    grad_out = dL/d out."""
     L = _lib.lib()
     B, H, N, D = q.shape
     a = _lib.LstepBwdArgs()
@@ -81,6 +83,7 @@ def _lstep_bwd_launch(q, out, ent, grad_res, grad_q, grad_out, m, b, scale, last
     a.ent = ent.data_ptr()
     a.ent_stride_b, a.ent_stride_h = ent.stride(0), ent.stride(1)
     a.scale, a.min_col_mass = float(scale), float(min_col_mass)
+    a.flags = _lib.LSTEP_BWD_OVERWRITE_Q if overwrite_q else 0
     _lib.check(L.vmo_lstep_bwd(a, _lib.stream_of(q)), "vmo_lstep_bwd")
 
 
@@ -225,11 +228,11 @@ class _VMonarchFunction(torch.autograd.Function):
         dev, dt = q.device, q.dtype
         dz = _lib.row_aligned(dz.to(dt))
         f32 = torch.float32
-        # fp32 gradient buffers: dq (the L-step backward adds into it, so it starts at zero), and one
+        # fp32 gradient buffers, overwritten by the first backward that writes them (the last
+        # iteration's, which covers every token) and added into by every later one: dq, and one
         # (.., 2D + Dv) buffer holding dk from the key role | dk from the value role (w starts with
-        # k) | dv, which the last R-step's backward (the first one run, covering every token)
-        # overwrites and every later backward adds into
-        dq = torch.zeros((B, H, N, D), device=dev, dtype=f32)
+        # k) | dv
+        dq = torch.empty((B, H, N, D), device=dev, dtype=f32)
         g_kv = torch.empty((B, H, N, 2 * D + Dv), device=dev, dtype=f32)
         frames = lambda t: t.reshape(B, H * m, b, *t.shape[3:])   # the R-step's m frames per head
         de = torch.zeros((B, H * m, b), device=dev, dtype=f32)
@@ -239,7 +242,8 @@ class _VMonarchFunction(torch.autograd.Function):
             last = it == num_iters - 1
             x, out, lse, ent = saved[4 * it: 4 * it + 4]
             dout = torch.empty_like(out)
-            _lstep_bwd_launch(q, out, ent, g, dq, dout, m, b, scale, last, rt if last else 0, min_col_mass)
+            _lstep_bwd_launch(q, out, ent, g, dq, dout, m, b, scale, last, rt if last else 0, min_col_mass,
+                              overwrite_q=last)
             # values k, or [k | v] read from the two tensors in place (vmonarch.py:50)
             gx, _, _ = fea_backward_raw(frames(x), frames(k), frames(k), frames(out), frames(lse), frames(ent),
                                         frames(dout), de, scale if it == 0 else 1.0,
