@@ -350,3 +350,11 @@ def test_fea_backward_values_in_two_parts(nq, nk, D):
     got = fea_backward_raw(q, k, v0, o, lse, ent, do, de, D ** -0.5, v1=v1)
     for a, b, name in zip(got, ref, ("dq", "dk", "dv")):
         assert torch.equal(a, b), name
+    # values [k | v1] with the first part k itself: the kernels reuse the K operands for dP's k half,
+    # accumulating in the same order, so again bit for bit
+    w = torch.cat([k, v1], -1)
+    o, lse, ent = fea_forward(q, k, w, None, D ** -0.5)
+    ref = fea_backward_raw(q, k, w, o, lse, ent, do, de, D ** -0.5)
+    got = fea_backward_raw(q, k, k, o, lse, ent, do, de, D ** -0.5, v1=v1)
+    for a, b, name in zip(got, ref, ("dq", "dk", "dv")):
+        assert torch.equal(a, b), "k-first " + name

@@ -41,6 +41,7 @@ struct BwdParams {
   const void* k;
   const void* v;
   const void* v1;   // second value part ([v | v1], same strides as v), or null
+  int v0_is_k;      // with v1: the first value part is k itself (same address and strides)
   const void* o;
   const void* dO;
   void* dq;
@@ -234,10 +235,15 @@ constexpr bool dkdv_k_in_lds() { return PART == 1 && D == 128 && DV == 256; }
 // 256-wide q/k heads (K alone is 64 registers, dK 128) run one wave per SIMD in both parts
 template <int D, int DV, int PART>
 constexpr int dkdv_waves_per_simd() { return D >= 256 ? 1 : PART != 0 ? 2 : bwd_waves_per_simd<D, DV>(); }
-template <int D, int DV, int PART>
+// V columns the dkdv kernel holds per key: all DV, or with the values [k | v1] (W0K) the v1 half only --
+// dP's k half then takes the K operand that S = Q K^T reads anyway
+template <int D, int DV, bool W0K>
+constexpr int dkdv_v_width() { return W0K ? DV - D : DV; }
+template <int D, int DV, int PART, bool W0K>
 constexpr int dkdv_lds_bytes() {
   return 2 * (kKvBM * (D + dkdv_do_width<DV, PART>()) * 2 + 512) +
-         (dkdv_v_in_lds<D, DV, PART>() ? kKvBN * DV * 2 : 0) + (dkdv_k_in_lds<D, DV, PART>() ? kKvBN * D * 2 : 0);
+         (dkdv_v_in_lds<D, DV, PART>() ? kKvBN * dkdv_v_width<D, DV, W0K>() * 2 : 0) +
+         (dkdv_k_in_lds<D, DV, PART>() ? kKvBN * D * 2 : 0);
 }
 
 __device__ __forceinline__ int xcd_remap(int nblocks) {
@@ -252,14 +258,21 @@ __device__ __forceinline__ int grad_mode(int flags, int accum_bit, int f32_bit) 
 }
 
 // ------------------------------------------------------------------------------------------------
-template <bool F16, int D, int DV, bool V2>
+// Value columns the dq kernel stages per key: all DV, or with the values [k | v1] (W0K) only the v1
+// half -- the k half of dP = dO V^T reuses the K fragments that S = K Q^T reads anyway.
+template <int D, int DV, bool W0K>
+constexpr int dq_staged_dv() { return W0K ? DV - D : DV; }
+
+template <bool F16, int D, int DV, bool V2, bool W0K>
 __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq_kernel(BwdParams p) {
   using E = Elem<F16>;
   using T = typename E::T;
   using V8 = typename E::V8;
   using V4 = typename E::V4;
+  static_assert(!W0K || (V2 && DV == 2 * D), "values [k | v1]");
+  constexpr int DVL = dq_staged_dv<D, DV, W0K>();
   constexpr int K_BYTES = kDqBN * D * 2;
-  constexpr int STAGE = kDqBN * (D + DV) * 2;
+  constexpr int STAGE = kDqBN * (D + DVL) * 2;
   constexpr int NA = D / 32;
   extern __shared__ __attribute__((aligned(1024))) char smem_raw[];
   VMO_LDS char* smem = (VMO_LDS char*)smem_raw;
@@ -324,7 +337,9 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
   const uint32_t smem_u32 = (uint32_t)(uintptr_t)smem;
   const BwdTileCopy<T, D, kDqBN> kcopy(kb, p.k_sn, wave, lane);
   const auto vcopy = [&]() __attribute__((always_inline)) {
-    if constexpr (V2)
+    if constexpr (W0K)
+      return BwdTileCopy<T, DVL, kDqBN>((const T*)p.v1 + bb * p.v_sb + hh * p.v_sh, p.v_sn, wave, lane);
+    else if constexpr (V2)
       return BwdTileCopy2<T, DV, kDqBN>(vb, (const T*)p.v1 + bb * p.v_sb + hh * p.v_sh, p.v_sn, wave, lane);
     else
       return BwdTileCopy<T, DV, kDqBN>(vb, p.v_sn, wave, lane);
@@ -339,7 +354,7 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
 #pragma unroll
   for (int a = 0; a < NA; ++a) acc[a] = f32x16{};
   const float c = p.c;
-  const int ksw = swz_rows<D * 2>(l32), vsw = swz_rows<DV * 2>(l32);
+  const int ksw = swz_rows<D * 2>(l32), vsw = swz_rows<DVL * 2>(l32);
   const int trow = 4 * hl + ((lane & 15) >> 2);
   const int tchunk = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
   const int tbyte = (lane & 1) * 8;
@@ -354,18 +369,22 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
     const VMO_LDS char* Vs = Ks + K_BYTES;
     const int nvalid = kend - kbeg - t * kDqBN;
     f32x16 s[2] = {f32x16{}, f32x16{}}, dp[2] = {f32x16{}, f32x16{}};
-    // S = K Q^T and dP = V dO^T for two 32-key blocks
-    constexpr int NSQ = D / 16, NSD = D / 16 + DV / 16;
+    // S = K Q^T and dP = V dO^T for two 32-key blocks (with W0K the K fragments also give dP's k half)
+    constexpr int NSQ = D / 16, NSD = D / 16 + DVL / 16, DO0 = (DV - DVL) / 16;
     prefetched_chain<2 * NSD, dq_prefetch<D, DV>()>(
         [&](int i) __attribute__((always_inline)) {
           const int kb2 = i / NSD, j = i % NSD;
           return j < NSQ ? lds_read8<V8>(Ks + (32 * kb2 + l32) * (D * 2) + ((2 * j + hl) ^ ksw) * 16)
-                         : lds_read8<V8>(Vs + (32 * kb2 + l32) * (DV * 2) + ((2 * (j - NSQ) + hl) ^ vsw) * 16);
+                         : lds_read8<V8>(Vs + (32 * kb2 + l32) * (DVL * 2) + ((2 * (j - NSQ) + hl) ^ vsw) * 16);
         },
         [&](int i, const V8& x) __attribute__((always_inline)) {
           const int kb2 = i / NSD, j = i % NSD;
-          if (j < NSQ) s[kb2] = E::mfma(x, qf[j], s[kb2]);
-          else dp[kb2] = E::mfma(x, dof[j - NSQ], dp[kb2]);
+          if (j < NSQ) {
+            s[kb2] = E::mfma(x, qf[j], s[kb2]);
+            if constexpr (W0K) dp[kb2] = E::mfma(x, dof[j], dp[kb2]);
+          } else {
+            dp[kb2] = E::mfma(x, dof[DO0 + j - NSQ], dp[kb2]);
+          }
         });
     V8 G[4];
 #pragma unroll
@@ -455,7 +474,7 @@ __global__ __launch_bounds__(256) void fea_bwd_dq_reduce(BwdParams p) {
 }
 
 // ------------------------------------------------------------------------------------------------
-template <bool F16, int D, int DV, int PART>
+template <bool F16, int D, int DV, int PART, bool W0K>
 __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea_bwd_dkdv_kernel(BwdParams p) {
   using E = Elem<F16>;
   using T = typename E::T;
@@ -471,7 +490,9 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
   constexpr int NK = D / 32, NV = dkdv_dv_width<DV, PART>() / 32;
   constexpr bool V_LDS = dkdv_v_in_lds<D, DV, PART>();
   constexpr bool K_LDS = dkdv_k_in_lds<D, DV, PART>();
-  constexpr int V_TILE = V_LDS ? kKvBN * DV * 2 : 0;
+  constexpr int VW = dkdv_v_width<D, DV, W0K>();   // V columns held (LDS tile or registers)
+  constexpr int V_TILE = V_LDS ? kKvBN * VW * 2 : 0;
+  static_assert(!W0K || DV == 2 * D, "values [k | v1]");
   extern __shared__ __attribute__((aligned(1024))) char smem_raw[];
   VMO_LDS char* smem = (VMO_LDS char*)smem_raw;
 
@@ -488,7 +509,7 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
   const int kr = kvalid ? krow : p.nk - 1;
 
   // K^T and V^T as B operands (one key per lane); V^T from LDS in the V_LDS variants
-  V8 kf[K_LDS ? 1 : D / 16], vf[(V_LDS || !WANT_DK) ? 1 : DV / 16];
+  V8 kf[K_LDS ? 1 : D / 16], vf[(V_LDS || !WANT_DK) ? 1 : VW / 16];
   {
     const T* kp = (const T*)p.k + bb * p.k_sb + hh * p.k_sh + (int64_t)kr * p.k_sn + hl * 8;
     const T* vp = (const T*)p.v + bb * p.v_sb + hh * p.v_sh + (int64_t)kr * p.v_sn + hl * 8;
@@ -502,9 +523,13 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
     }
     if constexpr (!V_LDS && WANT_DK) {
 #pragma unroll
-      for (int ds = 0; ds < DV / 16; ++ds) {
-        // columns 16 ds + 8 hl + 0..7: from the second value part when there is one and ds >= DV / 32
-        vf[ds] = p.v1 && ds >= DV / 32 ? *(const V8*)(vp1 + (ds - DV / 32) * 16) : *(const V8*)(vp + ds * 16);
+      for (int ds = 0; ds < VW / 16; ++ds) {
+        // columns 16 ds + 8 hl + 0..7 (of the v1 half with W0K): from the second value part when
+        // there is one and ds >= DV / 32
+        if constexpr (W0K)
+          vf[ds] = *(const V8*)(vp1 + ds * 16);
+        else
+          vf[ds] = p.v1 && ds >= DV / 32 ? *(const V8*)(vp1 + (ds - DV / 32) * 16) : *(const V8*)(vp + ds * 16);
         asm volatile("" : "+v"(vf[ds]));   // as kf: waited for here, not inside the loop
       }
     }
@@ -539,16 +564,19 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
 #pragma unroll
   for (int a = 0; a < NV; ++a) dv[a] = f32x16{};
   const float c = p.c;
-  const int qsw = swz_rows<D * 2>(l32), dsw = swz_rows<DOW * 2>(l32);
+  const int qsw = swz_rows<D * 2>(l32), dsw = swz_rows<DOW * 2>(l32), vsw = swz_rows<VW * 2>(l32);
   const int trow = 4 * hl + ((lane & 15) >> 2);
   const int tchunk = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
   const int tbyte = (lane & 1) * 8;
 
-  const VMO_LDS char* vt_row = smem + 2 * STAGE + (wave * 32 + l32) * (DV * 2);
+  const VMO_LDS char* vt_row = smem + 2 * STAGE + (wave * 32 + l32) * (VW * 2);
   const VMO_LDS char* kt_row = smem + 2 * STAGE + V_TILE + (wave * 32 + l32) * (D * 2);
   if constexpr (V_LDS) {   // this workgroup's 128 V rows, once (landed by the first tile_sync)
     const T* vb0 = (const T*)p.v + bb * p.v_sb + hh * p.v_sh;
-    if (p.v1)
+    if constexpr (W0K)
+      stage_rows_n<T, VW, kKvBN>((const T*)p.v1 + bb * p.v_sb + hh * p.v_sh, p.v_sn, kt * kKvBN, p.nk,
+                                 smem_u32 + 2 * STAGE, wave, lane);
+    else if (p.v1)
       stage_rows_n2<T, DV, kKvBN>(vb0, (const T*)p.v1 + bb * p.v_sb + hh * p.v_sh, p.v_sn, kt * kKvBN, p.nk,
                                   smem_u32 + 2 * STAGE, wave, lane);
     else
@@ -574,8 +602,11 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
     {
       const VMO_LDS char* qrow = Qs + l32 * (D * 2);
       const VMO_LDS char* drow = dOs + l32 * (DOW * 2);
-      struct Ops { V8 a, b; };
-      constexpr int NS = D / 16, NOP = NS + (WANT_DK ? DV / 16 : 0);
+      // with W0K the K operand of S also multiplies dO's first D columns (dP's k half), in the
+      // same column order as a concatenated [k | v1] would
+      constexpr bool KDP = W0K && WANT_DK;
+      struct Ops { V8 a, b, c; };
+      constexpr int NS = D / 16, NOP = NS + (WANT_DK ? VW / 16 : 0), DO0 = KDP ? NS : 0;
       prefetched_chain<NOP, kBwdPrefetch>(
           [&](int i) __attribute__((always_inline)) {
             Ops o;
@@ -583,16 +614,21 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
               const int off = ((2 * i + hl) ^ qsw) * 16;
               o.a = lds_read8<V8>(qrow + off);
               o.b = K_LDS ? lds_read8<V8>(kt_row + off) : kf[K_LDS ? 0 : i];
+              if constexpr (KDP) o.c = lds_read8<V8>(drow + ((2 * i + hl) ^ dsw) * 16);
             } else {
-              const int off = ((2 * (i - NS) + hl) ^ dsw) * 16;
-              o.a = lds_read8<V8>(drow + off);
-              o.b = V_LDS ? lds_read8<V8>(vt_row + off) : vf[V_LDS ? 0 : i - NS];
+              const int j = i - NS;
+              o.a = lds_read8<V8>(drow + ((2 * (DO0 + j) + hl) ^ dsw) * 16);
+              o.b = V_LDS ? lds_read8<V8>(vt_row + ((2 * j + hl) ^ vsw) * 16) : vf[V_LDS ? 0 : j];
             }
             return o;
           },
           [&](int i, const Ops& o) __attribute__((always_inline)) {
-            if (i < NS) s = E::mfma(o.a, o.b, s);
-            else dp = E::mfma(o.a, o.b, dp);
+            if (i < NS) {
+              s = E::mfma(o.a, o.b, s);
+              if constexpr (KDP) dp = E::mfma(o.c, o.b, dp);
+            } else {
+              dp = E::mfma(o.a, o.b, dp);
+            }
           });
     }
     V8 P[2], G[2];
@@ -666,11 +702,11 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
   put(p.dv, p.dv_sb, p.dv_sh, p.dv_sn, VOFF, dv, NV, 1.0f, grad_mode(p.accum, VMO_BWD_ACCUM_V, VMO_BWD_F32_V));
 }
 
-template <bool F16, int D, int DV, int PART>
+template <bool F16, int D, int DV, int PART, bool W0K>
 static int launch_dkdv(const BwdParams& p, hipStream_t s) {
-  constexpr int LDS_KV = dkdv_lds_bytes<D, DV, PART>();
+  constexpr int LDS_KV = dkdv_lds_bytes<D, DV, PART, W0K>();
   static_assert(LDS_KV <= 160 * 1024, "dkdv LDS");
-  auto kern = fea_bwd_dkdv_kernel<F16, D, DV, PART>;
+  auto kern = fea_bwd_dkdv_kernel<F16, D, DV, PART, W0K>;
   if (LDS_KV > 65536) {
     static bool done = false;
     if (!done) {
@@ -683,20 +719,20 @@ static int launch_dkdv(const BwdParams& p, hipStream_t s) {
   return launch_status("fea_bwd_dkdv");
 }
 
-template <bool F16, int D, int DV, bool V2 = false>
+template <bool F16, int D, int DV, bool V2 = false, bool W0K = false>
 static int launch_bwd(const BwdParams& p, hipStream_t s) {
-  constexpr int LDS_DQ = 2 * kDqBN * (D + DV) * 2;
+  constexpr int LDS_DQ = 2 * kDqBN * (D + dq_staged_dv<D, DV, W0K>()) * 2;
   static_assert(LDS_DQ <= 160 * 1024, "bwd LDS");
   if (LDS_DQ > 65536) {
     static bool done = false;
     if (!done) {
-      if (hipFuncSetAttribute((const void*)fea_bwd_dq_kernel<F16, D, DV, V2>,
+      if (hipFuncSetAttribute((const void*)fea_bwd_dq_kernel<F16, D, DV, V2, W0K>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, LDS_DQ) != hipSuccess)
         return set_error(VMO_ERR_LAUNCH, "fea_bwd_dq: cannot raise the LDS limit to %d bytes", LDS_DQ);
       done = true;
     }
   }
-  hipLaunchKernelGGL((fea_bwd_dq_kernel<F16, D, DV, V2>), dim3(xcd_grid(p.dq_total)), dim3(256), LDS_DQ, s, p);
+  hipLaunchKernelGGL((fea_bwd_dq_kernel<F16, D, DV, V2, W0K>), dim3(xcd_grid(p.dq_total)), dim3(256), LDS_DQ, s, p);
   int rc = launch_status("fea_bwd_dq");
   if (rc != VMO_OK) return rc;
   if (p.dq_splits > 1) {
@@ -706,17 +742,20 @@ static int launch_bwd(const BwdParams& p, hipStream_t s) {
     if (rc != VMO_OK) return rc;
   }
   if constexpr (dkdv_parts<DV>() == 1) {
-    return launch_dkdv<F16, D, DV, 0>(p, s);
+    return launch_dkdv<F16, D, DV, 0, W0K>(p, s);
   } else {
-    rc = launch_dkdv<F16, D, DV, 1>(p, s);
+    rc = launch_dkdv<F16, D, DV, 1, W0K>(p, s);
     if (rc != VMO_OK) return rc;
-    return launch_dkdv<F16, D, DV, 2>(p, s);
+    return launch_dkdv<F16, D, DV, 2, false>(p, s);   // dV's second half from P alone: no V read
   }
 }
 
 template <bool F16>
 static int dispatch_bwd(const BwdParams& p, int d, int dv, hipStream_t s) {
-  if (p.v1) {   // values in two halves (the caller checked dv1 = dv / 2)
+  if (p.v1 && p.v0_is_k) {   // values [k | v1]
+    if (d == 64 && dv == 128) return launch_bwd<F16, 64, 128, true, true>(p, s);
+    if (d == 128 && dv == 256) return launch_bwd<F16, 128, 256, true, true>(p, s);
+  } else if (p.v1) {   // values in two halves (the caller checked dv1 = dv / 2)
     if (d == 64 && dv == 128) return launch_bwd<F16, 64, 128, true>(p, s);
     if (d == 128 && dv == 256) return launch_bwd<F16, 128, 256, true>(p, s);
     return set_error(VMO_ERR_UNSUPPORTED, "fea_bwd: no kernel for d=%d with values in two parts of %d", d, dv / 2);
@@ -796,6 +835,8 @@ extern "C" int vmo_fea_bwd(const vmo_fea_bwd_args* a, void* stream) {
   BwdParams p{};
   p.q = a->q.data; p.k = a->k.data; p.v = a->v.data; p.o = a->o.data; p.dO = a->grad_o.data;
   p.v1 = a->dv1 > 0 ? a->v1.data : nullptr;
+  p.v0_is_k = a->dv1 > 0 && a->v.data == a->k.data && a->v.stride_b == a->k.stride_b &&
+              a->v.stride_h == a->k.stride_h && a->v.stride_n == a->k.stride_n && a->dv - a->dv1 == a->d;
   p.dq = a->grad_q.data; p.dk = a->grad_k.data; p.dv = a->grad_v.data;
   p.lse = a->lse; p.ent = a->ent; p.dent = a->grad_ent;
   p.alpha = (float*)a->workspace;
