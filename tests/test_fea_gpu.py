@@ -358,3 +358,21 @@ def test_fea_backward_values_in_two_parts(nq, nk, D):
     got = fea_backward_raw(q, k, k, o, lse, ent, do, de, D ** -0.5, v1=v1)
     for a, b, name in zip(got, ref, ("dq", "dk", "dv")):
         assert torch.equal(a, b), "k-first " + name
+
+
+@pytest.mark.parametrize("nq, nk, D", [(300, 300, 64), (300, 300, 128), (40, 4096, 128)])
+def test_fea_backward_values_are_keys(nq, nk, D):
+    """Values that are k itself (VMonarch's R-steps before the last, vmonarch.py:50): the kernels
+    take dP's operand from the K fragments they already read, bit for bit the result for a copy of k."""
+    from vmonarch_amd.kernel import fea_forward
+    from vmonarch_amd.kernel_bwd import fea_backward_raw
+    g = torch.Generator().manual_seed(7 * nq + nk + D)
+    q, k = randn_lp(g, 1, 2, nq, D).to(DEV), randn_lp(g, 1, 2, nk, D).to(DEV)
+    do = randn_lp(g, 1, 2, nq, D).to(DEV)
+    de = torch.randn(1, 2, nq, generator=g).to(DEV)
+    o, lse, ent = fea_forward(q, k, k, None, D ** -0.5)
+    print(f"fea_bwd values = keys nq={nq} nk={nk} D={D}", flush=True)
+    ref = fea_backward_raw(q, k, k.clone(), o, lse, ent, do, de, D ** -0.5)
+    got = fea_backward_raw(q, k, k, o, lse, ent, do, de, D ** -0.5)
+    for a, b, name in zip(got, ref, ("dq", "dk", "dv")):
+        assert torch.equal(a, b), name

@@ -41,7 +41,7 @@ struct BwdParams {
   const void* k;
   const void* v;
   const void* v1;   // second value part ([v | v1], same strides as v), or null
-  int v0_is_k;      // with v1: the first value part is k itself (same address and strides)
+  int v0_is_k;      // the values are k itself, or with v1 start with it (same address and strides)
   const void* o;
   const void* dO;
   void* dq;
@@ -235,8 +235,8 @@ constexpr bool dkdv_k_in_lds() { return PART == 1 && D == 128 && DV == 256; }
 // 256-wide q/k heads (K alone is 64 registers, dK 128) run one wave per SIMD in both parts
 template <int D, int DV, int PART>
 constexpr int dkdv_waves_per_simd() { return D >= 256 ? 1 : PART != 0 ? 2 : bwd_waves_per_simd<D, DV>(); }
-// V columns the dkdv kernel holds per key: all DV, or with the values [k | v1] (W0K) the v1 half only --
-// dP's k half then takes the K operand that S = Q K^T reads anyway
+// V columns the dkdv kernel holds per key: all DV, or when the values start with k itself (W0K) only
+// the columns after k (none for values k) -- dP's k part takes the K operand that S = Q K^T reads anyway
 template <int D, int DV, bool W0K>
 constexpr int dkdv_v_width() { return W0K ? DV - D : DV; }
 template <int D, int DV, int PART, bool W0K>
@@ -258,8 +258,9 @@ __device__ __forceinline__ int grad_mode(int flags, int accum_bit, int f32_bit) 
 }
 
 // ------------------------------------------------------------------------------------------------
-// Value columns the dq kernel stages per key: all DV, or with the values [k | v1] (W0K) only the v1
-// half -- the k half of dP = dO V^T reuses the K fragments that S = K Q^T reads anyway.
+// Value columns the dq kernel stages per key: all DV, or when the values start with k itself (W0K:
+// values k, or [k | v1]) only the columns after k -- dP's k part reuses the K fragments that
+// S = K Q^T reads anyway (values k alone stage no V tile at all).
 template <int D, int DV, bool W0K>
 constexpr int dq_staged_dv() { return W0K ? DV - D : DV; }
 
@@ -269,7 +270,7 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
   using T = typename E::T;
   using V8 = typename E::V8;
   using V4 = typename E::V4;
-  static_assert(!W0K || (V2 && DV == 2 * D), "values [k | v1]");
+  static_assert(!W0K || (V2 ? DV == 2 * D : DV == D), "values k or [k | v1]");
   constexpr int DVL = dq_staged_dv<D, DV, W0K>();
   constexpr int K_BYTES = kDqBN * D * 2;
   constexpr int STAGE = kDqBN * (D + DVL) * 2;
@@ -337,7 +338,9 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
   const uint32_t smem_u32 = (uint32_t)(uintptr_t)smem;
   const BwdTileCopy<T, D, kDqBN> kcopy(kb, p.k_sn, wave, lane);
   const auto vcopy = [&]() __attribute__((always_inline)) {
-    if constexpr (W0K)
+    if constexpr (W0K && DVL == 0)
+      return 0;   // values k: nothing beyond the K tile
+    else if constexpr (W0K)
       return BwdTileCopy<T, DVL, kDqBN>((const T*)p.v1 + bb * p.v_sb + hh * p.v_sh, p.v_sn, wave, lane);
     else if constexpr (V2)
       return BwdTileCopy2<T, DV, kDqBN>(vb, (const T*)p.v1 + bb * p.v_sb + hh * p.v_sh, p.v_sn, wave, lane);
@@ -347,14 +350,14 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
   auto issue = [&](int t) {
     const uint32_t st = smem_u32 + (uint32_t)((t & 1) * STAGE);
     kcopy.issue(kbeg + t * kDqBN, kend, st);
-    vcopy.issue(kbeg + t * kDqBN, kend, st + K_BYTES);
+    if constexpr (DVL > 0) vcopy.issue(kbeg + t * kDqBN, kend, st + K_BYTES);
   };
 
   f32x16 acc[NA];
 #pragma unroll
   for (int a = 0; a < NA; ++a) acc[a] = f32x16{};
   const float c = p.c;
-  const int ksw = swz_rows<D * 2>(l32), vsw = swz_rows<DVL * 2>(l32);
+  const int ksw = swz_rows<D * 2>(l32), vsw = swz_rows<(DVL > 0 ? DVL : D) * 2>(l32);
   const int trow = 4 * hl + ((lane & 15) >> 2);
   const int tchunk = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
   const int tbyte = (lane & 1) * 8;
@@ -492,7 +495,7 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
   constexpr bool K_LDS = dkdv_k_in_lds<D, DV, PART>();
   constexpr int VW = dkdv_v_width<D, DV, W0K>();   // V columns held (LDS tile or registers)
   constexpr int V_TILE = V_LDS ? kKvBN * VW * 2 : 0;
-  static_assert(!W0K || DV == 2 * D, "values [k | v1]");
+  static_assert(!W0K || DV == 2 * D || DV == D, "values k or [k | v1]");
   extern __shared__ __attribute__((aligned(1024))) char smem_raw[];
   VMO_LDS char* smem = (VMO_LDS char*)smem_raw;
 
@@ -509,7 +512,7 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
   const int kr = kvalid ? krow : p.nk - 1;
 
   // K^T and V^T as B operands (one key per lane); V^T from LDS in the V_LDS variants
-  V8 kf[K_LDS ? 1 : D / 16], vf[(V_LDS || !WANT_DK) ? 1 : VW / 16];
+  V8 kf[K_LDS ? 1 : D / 16], vf[(V_LDS || !WANT_DK || VW == 0) ? 1 : VW / 16];
   {
     const T* kp = (const T*)p.k + bb * p.k_sb + hh * p.k_sh + (int64_t)kr * p.k_sn + hl * 8;
     const T* vp = (const T*)p.v + bb * p.v_sb + hh * p.v_sh + (int64_t)kr * p.v_sn + hl * 8;
@@ -564,14 +567,14 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
 #pragma unroll
   for (int a = 0; a < NV; ++a) dv[a] = f32x16{};
   const float c = p.c;
-  const int qsw = swz_rows<D * 2>(l32), dsw = swz_rows<DOW * 2>(l32), vsw = swz_rows<VW * 2>(l32);
+  const int qsw = swz_rows<D * 2>(l32), dsw = swz_rows<DOW * 2>(l32), vsw = swz_rows<(VW > 0 ? VW : D) * 2>(l32);
   const int trow = 4 * hl + ((lane & 15) >> 2);
   const int tchunk = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
   const int tbyte = (lane & 1) * 8;
 
   const VMO_LDS char* vt_row = smem + 2 * STAGE + (wave * 32 + l32) * (VW * 2);
   const VMO_LDS char* kt_row = smem + 2 * STAGE + V_TILE + (wave * 32 + l32) * (D * 2);
-  if constexpr (V_LDS) {   // this workgroup's 128 V rows, once (landed by the first tile_sync)
+  if constexpr (V_LDS && VW > 0) {   // this workgroup's 128 V rows, once (landed by the first tile_sync)
     const T* vb0 = (const T*)p.v + bb * p.v_sb + hh * p.v_sh;
     if constexpr (W0K)
       stage_rows_n<T, VW, kKvBN>((const T*)p.v1 + bb * p.v_sb + hh * p.v_sh, p.v_sn, kt * kKvBN, p.nk,
@@ -755,6 +758,9 @@ static int dispatch_bwd(const BwdParams& p, int d, int dv, hipStream_t s) {
   if (p.v1 && p.v0_is_k) {   // values [k | v1]
     if (d == 64 && dv == 128) return launch_bwd<F16, 64, 128, true, true>(p, s);
     if (d == 128 && dv == 256) return launch_bwd<F16, 128, 256, true, true>(p, s);
+  } else if (p.v0_is_k) {   // values k (VMonarch's R-steps before the last, vmonarch.py:50)
+    if (d == 64 && dv == 64) return launch_bwd<F16, 64, 64, false, true>(p, s);
+    if (d == 128 && dv == 128) return launch_bwd<F16, 128, 128, false, true>(p, s);
   } else if (p.v1) {   // values in two halves (the caller checked dv1 = dv / 2)
     if (d == 64 && dv == 128) return launch_bwd<F16, 64, 128, true>(p, s);
     if (d == 128 && dv == 256) return launch_bwd<F16, 128, 256, true>(p, s);
@@ -835,8 +841,8 @@ extern "C" int vmo_fea_bwd(const vmo_fea_bwd_args* a, void* stream) {
   BwdParams p{};
   p.q = a->q.data; p.k = a->k.data; p.v = a->v.data; p.o = a->o.data; p.dO = a->grad_o.data;
   p.v1 = a->dv1 > 0 ? a->v1.data : nullptr;
-  p.v0_is_k = a->dv1 > 0 && a->v.data == a->k.data && a->v.stride_b == a->k.stride_b &&
-              a->v.stride_h == a->k.stride_h && a->v.stride_n == a->k.stride_n && a->dv - a->dv1 == a->d;
+  p.v0_is_k = a->v.data == a->k.data && a->v.stride_b == a->k.stride_b && a->v.stride_h == a->k.stride_h &&
+              a->v.stride_n == a->k.stride_n && a->dv - a->dv1 == a->d;
   p.dq = a->grad_q.data; p.dk = a->grad_k.data; p.dv = a->grad_v.data;
   p.lse = a->lse; p.ent = a->ent; p.dent = a->grad_ent;
   p.alpha = (float*)a->workspace;
