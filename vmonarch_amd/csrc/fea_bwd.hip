@@ -218,9 +218,11 @@ constexpr int bwd_waves_per_simd() { return D + DV > 320 ? 1 : 2; }
 // The dkdv kernel for 256-wide values runs as two launches (PART 1: dK and dV[:, :128], with dP over
 // all 256 value columns; PART 2: dV[:, 128:] from P alone): one launch holding dK and the whole dV
 // needs ~290 accumulator and operand registers, and the compiler then moves every accumulator
-// between AGPRs and VGPRs around each MFMA.  PART 0 is the single launch of the narrower variants.
-template <int DV>
-constexpr int dkdv_parts() { return DV > 128 ? 2 : 1; }
+// between AGPRs and VGPRs around each MFMA.  PART 0 is the single launch of the narrower variants,
+// and of values [k | v1] at 128 / 256, whose V operand registers the K operand replaces (it then fits
+// one wave per SIMD without moving accumulators).
+template <int D, int DV, bool W0K>
+constexpr int dkdv_parts() { return DV > 128 && !(W0K && D == 128 && DV == 256) ? 2 : 1; }
 template <int DV, int PART>
 constexpr int dkdv_do_width() { return PART == 2 ? DV / 2 : DV; }   // dO columns staged per stage
 template <int DV, int PART>
@@ -744,7 +746,7 @@ static int launch_bwd(const BwdParams& p, hipStream_t s) {
     rc = launch_status("fea_bwd_dq_reduce");
     if (rc != VMO_OK) return rc;
   }
-  if constexpr (dkdv_parts<DV>() == 1) {
+  if constexpr (dkdv_parts<D, DV, W0K>() == 1) {
     return launch_dkdv<F16, D, DV, 0, W0K>(p, s);
   } else {
     rc = launch_dkdv<F16, D, DV, 1, W0K>(p, s);
