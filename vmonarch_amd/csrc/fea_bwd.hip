@@ -248,11 +248,6 @@ constexpr int dkdv_lds_bytes() {
          (dkdv_k_in_lds<D, DV, PART>() ? kKvBN * D * 2 : 0);
 }
 
-__device__ __forceinline__ int xcd_remap(int nblocks) {
-  const int per_xcd = nblocks >> 3;
-  return (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-}
-
 // How a gradient is written: in the inputs' type, or into an fp32 buffer (added to or overwritten).
 enum { kGradStore = 0, kGradAddF32 = 1, kGradStoreF32 = 2 };
 __device__ __forceinline__ int grad_mode(int flags, int accum_bit, int f32_bit) {

@@ -281,7 +281,9 @@ static int dispatch_lstep(const LParams& p, int d, int dv, bool last, hipStream_
 // transposed in the accumulator layout (one query row i per lane), and goes through an LDS tile
 // [k][i] wherever a product needs one lane per k.  dq is accumulated (read-modify-write) into an
 // fp32 buffer, since every L-step and the R-step chain add to it; d out is written.
-constexpr int kLBWaves = 2;   // columns per workgroup
+// Columns (waves) per workgroup: one, so that the LDS a wave needs (29 KB at 128 / 128) is the whole
+// allocation unit and five waves share a CU (two per workgroup fitted four).
+constexpr int kLBWaves = 1;
 
 struct LBParams {
   const void* q;
@@ -308,13 +310,12 @@ template <int D, int DV, bool LAST>
 struct LBLds {
   static constexpr int QT = 32 * D * 2;               // q rows i
   static constexpr int KT = 32 * D * 2;               // kr rows k
-  static constexpr int YT = LAST ? 32 * DV * 2 : 0;   // y rows k
   static constexpr int GT = LAST ? 32 * DV * 2 : 0;   // dz rows i
   static constexpr int VT = LAST ? 0 : 32 * D * 2;    // dv rows k
   static constexpr int AT = 32 * kAttStride * 4;      // an m x m matrix as [k][i]
   static constexpr int ET = 32 * 4;
   static constexpr int CT = 32 * 4;
-  static constexpr int PER_WAVE = QT + KT + YT + GT + VT + AT + ET + CT;
+  static constexpr int PER_WAVE = QT + KT + GT + VT + AT + ET + CT;   // y is read into registers
 };
 
 template <bool F16, int D, int DV, bool LAST>
@@ -333,8 +334,7 @@ __global__ __launch_bounds__(64 * kLBWaves) void lstep_bwd_kernel(LBParams p) {
   const int col = live ? blockIdx.x * kLBWaves + wave : p.cols_total - 1;
   VMO_LDS char* q_t = (VMO_LDS char*)smem_raw + wave * LL::PER_WAVE;
   VMO_LDS char* k_t = q_t + LL::QT;
-  VMO_LDS char* y_t = k_t + LL::KT;
-  VMO_LDS char* g_t = y_t + LL::YT;
+  VMO_LDS char* g_t = k_t + LL::KT;
   VMO_LDS char* v_t = g_t + LL::GT;
   VMO_LDS float* att = (VMO_LDS float*)(v_t + LL::VT);
   VMO_LDS float* e_t = att + 32 * kAttStride;
@@ -353,15 +353,18 @@ __global__ __launch_bounds__(64 * kLBWaves) void lstep_bwd_kernel(LBParams p) {
   stage_col_rows<T, D>(qcol, q_rs, m, q_t, lane);
   stage_col_rows<T, D>(ocol, o_rs, m, k_t, lane);
   if constexpr (LAST) {
-    stage_col_rows<T, DV>(ocol + D, o_rs, m, y_t, lane);
     stage_col_rows<T, DV>(gcol, g_rs, m, g_t, lane);
   }
   const int rk = l32 < m ? l32 : m - 1;
-  V8 krf[D / 16];
+  V8 krf[D / 16], yf[LAST ? DV / 16 : 1];   // kr and y rows k (lane = k) as MFMA operands
   {
     const T* kp = ocol + (int64_t)rk * o_rs + hl * 8;
 #pragma unroll
     for (int ds = 0; ds < D / 16; ++ds) krf[ds] = *(const V8*)(kp + ds * 16);
+    if constexpr (LAST) {
+#pragma unroll
+      for (int ds = 0; ds < DV / 16; ++ds) yf[ds] = *(const V8*)(kp + D + ds * 16);
+    }
   }
   if (hl == 0) {
     const float* ep = p.ent + bb * p.ent_sb + hh * p.ent_sh + j;
@@ -489,12 +492,11 @@ __global__ __launch_bounds__(64 * kLBWaves) void lstep_bwd_kernel(LBParams p) {
   // ---- d attn^T[k][i]
   f32x16 da = f32x16{};
   if constexpr (LAST) {
-    const VMO_LDS char* yrow = y_t + l32 * (DV * 2);
     const VMO_LDS char* grow = g_t + l32 * (DV * 2);
 #pragma unroll
     for (int ds = 0; ds < DV / 16; ++ds) {
       const int off = ((2 * ds + hl) ^ sw) * 16;
-      da = E::mfma(lds_read8<V8>(yrow + off), lds_read8<V8>(grow + off), da);
+      da = E::mfma(yf[ds], lds_read8<V8>(grow + off), da);
     }
     // dy_k = sum_i a[i,k] dz_i -> d out[k, D:]
     to_att(s);

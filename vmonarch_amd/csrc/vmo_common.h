@@ -77,6 +77,13 @@ __device__ __forceinline__ int swz_rows(int r) {
   else return ((r & 3) << 2) | ((r >> 2) & 3);
 }
 
+// XCD-aware block order for a grid of nblocks (a multiple of 8): block b runs on XCD b % 8, so give
+// each XCD a contiguous run of logical blocks (neighbouring tiles / rows then share that XCD's L2).
+__device__ __forceinline__ int xcd_remap(int nblocks) {
+  const int per_xcd = nblocks >> 3;
+  return (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+}
+
 __device__ __forceinline__ float wave_max32(float x) {
   // combine lane l with lane l ^ 32
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
