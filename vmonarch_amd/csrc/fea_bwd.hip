@@ -17,6 +17,9 @@
 //  * fea_bwd_dkdv: one workgroup = 128 keys (32 per wave, K / V rows held as B operands), loop over
 //    32-query stages: S = Q K^T and dP = dO V^T (one key per lane), then dV^T += dO^T P and
 //    dK^T += Q^T dS with dO^T / Q^T read transposed from the staged tiles.
+// Values may come in two parts [v | v1] (VMonarch's [k | v] without a concatenated copy), and when
+// they are k itself or start with it the K operands double as dP's V operands for those columns.
+// Gradients are written in the inputs' dtype or into fp32 buffers (added to or overwritten).
 // P and dS enter the MFMAs as bf16 / fp16 (the reference's dK / dQ dots run in fp32 = tf32 on its
 // hardware; gfx950 has no xf32 MFMA -- parity is checked at the stated gradient tolerance).
 #include <type_traits>
