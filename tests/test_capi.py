@@ -139,3 +139,20 @@ def test_lstep_bwd_rejects_unknown_flags(L):
     a.flags = 2
     assert L.vmo_lstep_bwd(ctypes.byref(a), None) == 1
     assert b"flags" in L.vmo_last_error()
+
+
+def test_fea_bwd_rejects_bad_value_parts(L):
+    from vmonarch_amd import _lib
+    a = _lib.FeaBwdArgs()
+    a.dtype, a.batch, a.heads, a.nq, a.nk, a.d, a.dv = 0, 1, 1, 128, 128, 128, 256
+    v = _lib.View(4096, 128, 128 * 128, 128)
+    a.q = a.k = a.v = a.o = a.grad_o = a.grad_q = a.grad_k = a.grad_v = v
+    a.lse = a.ent = a.grad_ent = 4096
+    a.sm_scale = 0.1
+    a.v1, a.dv1 = _lib.View(8192, 128, 128 * 128, 256), 128    # token stride differs from v's
+    assert L.vmo_fea_bwd(ctypes.byref(a), None) == 1
+    assert b"v1" in L.vmo_last_error()
+    a.v1, a.dv1 = _lib.View(8192, 128, 128 * 128, 128), 64     # parts of unequal width
+    assert L.vmo_fea_bwd(ctypes.byref(a), None) == 2
+    a.dv1 = 256                                                 # no first part left
+    assert L.vmo_fea_bwd(ctypes.byref(a), None) == 1
