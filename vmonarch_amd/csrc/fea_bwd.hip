@@ -257,6 +257,47 @@ __device__ __forceinline__ int grad_mode(int flags, int accum_bit, int f32_bit) 
   return (flags & accum_bit) ? kGradAddF32 : (flags & f32_bit) ? kGradStoreF32 : kGradStore;
 }
 
+// Write a wave's gradient tile -- acc[a][r] is the value at (row l32, column 32 a + 8 (r / 4) +
+// 4 hl + r % 4), the transposed accumulator layout of both kernels -- one 32-column block at a time
+// through a 4 KB LDS patch, so that 8 consecutive lanes write each row's 32-column segment (128 bytes
+// in fp32) instead of every lane writing 8- or 16-byte pieces of 32 rows.  Rows >= nrows are skipped.
+// One wave writes and reads its own patch; LDS accesses of a wave complete in order.
+constexpr int kEpiPatchBytes = 32 * 32 * 4;
+template <bool F16>
+__device__ __forceinline__ void store_acc_rows(VMO_LDS float* patch, const f32x16* acc, int nacc, float f, int mode,
+                                               char* row0, int64_t row_stride_bytes, int nrows, int lane) {
+  using T = typename Elem<F16>::T;
+  using V4 = typename Elem<F16>::V4;
+  const int hl = lane >> 5, l32 = lane & 31, rr0 = lane >> 3, c = lane & 7;
+  const int esize = mode == kGradStore ? 2 : 4;
+  for (int a = 0; a < nacc; ++a) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {   // row l32, 16-byte chunk 2 j + hl, swizzled by row against bank conflicts
+      f32x4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = acc[a][4 * j + e] * f;
+      *(VMO_LDS f32x4*)(patch + l32 * 32 + ((2 * j + hl) ^ (l32 & 7)) * 4) = v;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {   // rows rr0 + 8 i, chunk c: 8 lanes per row
+      const int rr = rr0 + 8 * i;
+      const f32x4 v = *(const VMO_LDS f32x4*)(patch + rr * 32 + (c ^ (rr & 7)) * 4);
+      if (rr < nrows) {
+        char* dst = row0 + rr * row_stride_bytes + (int64_t)(32 * a + 4 * c) * esize;
+        if (mode == kGradStore) {
+          V4 x;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) x[e] = to_elem<T>(v[e]);
+          *(V4*)dst = x;
+        } else {
+          f32x4* ptr = (f32x4*)dst;
+          *ptr = mode == kGradAddF32 ? *ptr + v : v;
+        }
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------------------------------------------
 // Value columns the dq kernel stages per key: all DV, or when the values start with k itself (W0K:
 // values k, or [k | v1]) only the columns after k -- dP's k part reuses the K fragments that
@@ -411,41 +452,18 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
   const int n_full = (kend - kbeg) / kDqBN;   // stages with 64 valid keys
   for (int t = 0; t < n_full; ++t) iteration(t, std::false_type{});
   if (n_full < n_tiles) iteration(n_full, std::true_type{});
-  if (!wave_live || !qvalid) return;
+  __syncthreads();   // every wave is done with the stage ring, which the epilogue patches reuse
+  if (!wave_live) return;
+  VMO_LDS float* patch = (VMO_LDS float*)(smem + wave * kEpiPatchBytes);
+  const int nrows = min(32, p.nq - q0);
   if (p.dq_splits > 1) {   // fp32 partial of this key range; fea_bwd_dq_reduce sums the splits
-    float* pr = p.dq_part + (((int64_t)split * p.problems + prob) * p.nq + qrow) * D;
-#pragma unroll
-    for (int a = 0; a < NA; ++a)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        f32x4 v;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = acc[a][4 * j + e] * p.sm_scale;
-        *(f32x4*)(pr + 32 * a + 8 * j + 4 * hl) = v;
-      }
-  } else if (const int mode = grad_mode(p.accum, VMO_BWD_ACCUM_Q, VMO_BWD_F32_Q); mode != kGradStore) {
-    float* dqr = (float*)p.dq + bb * p.dq_sb + hh * p.dq_sh + (int64_t)qrow * p.dq_sn;
-#pragma unroll
-    for (int a = 0; a < NA; ++a)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        f32x4* ptr = (f32x4*)(dqr + 32 * a + 8 * j + 4 * hl);
-        f32x4 v = mode == kGradAddF32 ? *ptr : f32x4{};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] += acc[a][4 * j + e] * p.sm_scale;
-        *ptr = v;
-      }
+    float* pr = p.dq_part + (((int64_t)split * p.problems + prob) * p.nq + q0) * D;
+    store_acc_rows<F16>(patch, acc, NA, p.sm_scale, kGradStoreF32, (char*)pr, (int64_t)D * 4, nrows, lane);
   } else {
-    T* dqr = (T*)p.dq + bb * p.dq_sb + hh * p.dq_sh + (int64_t)qrow * p.dq_sn;
-#pragma unroll
-    for (int a = 0; a < NA; ++a)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        V4 v;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = to_elem<T>(acc[a][4 * j + e] * p.sm_scale);
-        *(V4*)(dqr + 32 * a + 8 * j + 4 * hl) = v;
-      }
+    const int mode = grad_mode(p.accum, VMO_BWD_ACCUM_Q, VMO_BWD_F32_Q);
+    const int64_t es = mode == kGradStore ? 2 : 4;
+    char* row0 = (char*)p.dq + (bb * p.dq_sb + hh * p.dq_sh + (int64_t)q0 * p.dq_sn) * es;
+    store_acc_rows<F16>(patch, acc, NA, p.sm_scale, mode, row0, p.dq_sn * es, nrows, lane);
   }
 }
 
@@ -673,32 +691,16 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
   const int n_full = p.nq / kKvBM;   // stages with 32 valid queries
   for (int t = 0; t < n_full; ++t) iteration(t, std::false_type{});
   if (n_full < n_tiles) iteration(n_full, std::true_type{});
-  if (!wave_live || !kvalid) return;
+  __syncthreads();   // every wave is done with the stage ring, which the epilogue patches reuse
+  if (!wave_live) return;
+  VMO_LDS float* patch = (VMO_LDS float*)(smem + wave * kEpiPatchBytes);
+  const int nrows = min(32, p.nk - k0);
   // write NACC accumulator blocks times f: stored in T, or added to / stored into an fp32 gradient
   auto put = [&](void* base, int64_t sb, int64_t sh, int64_t sn, int col0, const f32x16* acc, int nacc, float f,
                  int mode) __attribute__((always_inline)) {
-    if (mode != kGradStore) {
-      float* r = (float*)base + bb * sb + hh * sh + (int64_t)krow * sn + col0;
-      for (int a = 0; a < nacc; ++a)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          f32x4* ptr = (f32x4*)(r + 32 * a + 8 * j + 4 * hl);
-          f32x4 v = mode == kGradAddF32 ? *ptr : f32x4{};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] += acc[a][4 * j + e] * f;
-          *ptr = v;
-        }
-    } else {
-      T* r = (T*)base + bb * sb + hh * sh + (int64_t)krow * sn + col0;
-      for (int a = 0; a < nacc; ++a)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          V4 x;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) x[e] = to_elem<T>(acc[a][4 * j + e] * f);
-          *(V4*)(r + 32 * a + 8 * j + 4 * hl) = x;
-        }
-    }
+    const int64_t es = mode == kGradStore ? 2 : 4;
+    char* row0 = (char*)base + (bb * sb + hh * sh + (int64_t)k0 * sn + col0) * es;
+    store_acc_rows<F16>(patch, acc, nacc, f, mode, row0, sn * es, nrows, lane);
   };
   if constexpr (WANT_DK)
     put(p.dk, p.dk_sb, p.dk_sh, p.dk_sn, 0, dk, NK, p.sm_scale, grad_mode(p.accum, VMO_BWD_ACCUM_K, VMO_BWD_F32_K));
@@ -708,7 +710,7 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
 template <bool F16, int D, int DV, int PART, bool W0K>
 static int launch_dkdv(const BwdParams& p, hipStream_t s) {
   constexpr int LDS_KV = dkdv_lds_bytes<D, DV, PART, W0K>();
-  static_assert(LDS_KV <= 160 * 1024, "dkdv LDS");
+  static_assert(LDS_KV <= 160 * 1024 && LDS_KV >= kBwdWaves * kEpiPatchBytes, "dkdv LDS");
   auto kern = fea_bwd_dkdv_kernel<F16, D, DV, PART, W0K>;
   if (LDS_KV > 65536) {
     static bool done = false;
@@ -725,7 +727,7 @@ static int launch_dkdv(const BwdParams& p, hipStream_t s) {
 template <bool F16, int D, int DV, bool V2 = false, bool W0K = false>
 static int launch_bwd(const BwdParams& p, hipStream_t s) {
   constexpr int LDS_DQ = 2 * kDqBN * (D + dq_staged_dv<D, DV, W0K>()) * 2;
-  static_assert(LDS_DQ <= 160 * 1024, "bwd LDS");
+  static_assert(LDS_DQ <= 160 * 1024 && LDS_DQ >= kBwdWaves * kEpiPatchBytes, "bwd LDS");
   if (LDS_DQ > 65536) {
     static bool done = false;
     if (!done) {
