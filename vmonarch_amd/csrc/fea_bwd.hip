@@ -251,53 +251,6 @@ constexpr int dkdv_lds_bytes() {
          (dkdv_k_in_lds<D, DV, PART>() ? kKvBN * D * 2 : 0);
 }
 
-// How a gradient is written: in the inputs' type, or into an fp32 buffer (added to or overwritten).
-enum { kGradStore = 0, kGradAddF32 = 1, kGradStoreF32 = 2 };
-__device__ __forceinline__ int grad_mode(int flags, int accum_bit, int f32_bit) {
-  return (flags & accum_bit) ? kGradAddF32 : (flags & f32_bit) ? kGradStoreF32 : kGradStore;
-}
-
-// Write a wave's gradient tile -- acc[a][r] is the value at (row l32, column 32 a + 8 (r / 4) +
-// 4 hl + r % 4), the transposed accumulator layout of both kernels -- one 32-column block at a time
-// through a 4 KB LDS patch, so that 8 consecutive lanes write each row's 32-column segment (128 bytes
-// in fp32) instead of every lane writing 8- or 16-byte pieces of 32 rows.  Rows >= nrows are skipped.
-// One wave writes and reads its own patch; LDS accesses of a wave complete in order.
-constexpr int kEpiPatchBytes = 32 * 32 * 4;
-template <bool F16>
-__device__ __forceinline__ void store_acc_rows(VMO_LDS float* patch, const f32x16* acc, int nacc, float f, int mode,
-                                               char* row0, int64_t row_stride_bytes, int nrows, int lane) {
-  using T = typename Elem<F16>::T;
-  using V4 = typename Elem<F16>::V4;
-  const int hl = lane >> 5, l32 = lane & 31, rr0 = lane >> 3, c = lane & 7;
-  const int esize = mode == kGradStore ? 2 : 4;
-  for (int a = 0; a < nacc; ++a) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {   // row l32, 16-byte chunk 2 j + hl, swizzled by row against bank conflicts
-      f32x4 v;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = acc[a][4 * j + e] * f;
-      *(VMO_LDS f32x4*)(patch + l32 * 32 + ((2 * j + hl) ^ (l32 & 7)) * 4) = v;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {   // rows rr0 + 8 i, chunk c: 8 lanes per row
-      const int rr = rr0 + 8 * i;
-      const f32x4 v = *(const VMO_LDS f32x4*)(patch + rr * 32 + (c ^ (rr & 7)) * 4);
-      if (rr < nrows) {
-        char* dst = row0 + rr * row_stride_bytes + (int64_t)(32 * a + 4 * c) * esize;
-        if (mode == kGradStore) {
-          V4 x;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) x[e] = to_elem<T>(v[e]);
-          *(V4*)dst = x;
-        } else {
-          f32x4* ptr = (f32x4*)dst;
-          *ptr = mode == kGradAddF32 ? *ptr + v : v;
-        }
-      }
-    }
-  }
-}
-
 // ------------------------------------------------------------------------------------------------
 // Value columns the dq kernel stages per key: all DV, or when the values start with k itself (W0K:
 // values k, or [k | v1]) only the columns after k -- dP's k part reuses the K fragments that

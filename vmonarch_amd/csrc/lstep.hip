@@ -475,17 +475,6 @@ __global__ __launch_bounds__(64 * kLBWaves) void lstep_bwd_kernel(LBParams p) {
       }
     }
   };
-  // store an accumulator (rows w, lane = token row) into a row of width-W features
-  auto store_rows = [&](T* row, const f32x16* acc, int nacc) __attribute__((always_inline)) {
-    for (int a = 0; a < nacc; ++a)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        V4 v;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = to_elem<T>(acc[a][4 * g + e]);
-        *(V4*)(row + 32 * a + 8 * g + 4 * hl) = v;
-      }
-  };
   T* const dcol = (T*)p.dout + bb * p.do_sb + hh * p.do_sh + (int64_t)j * p.do_sn;
   const int64_t do_rs = (int64_t)p.bs * p.do_sn;
 
@@ -507,7 +496,9 @@ __global__ __launch_bounds__(64 * kLBWaves) void lstep_bwd_kernel(LBParams p) {
 #pragma unroll
     for (int a = 0; a < NV; ++a) accy[a] = f32x16{};
     mma_rows_t(accy, g_t, std::integral_constant<int, DV>{}, Bu);
-    if (live && kvalid) store_rows(dcol + (int64_t)k * do_rs + D, accy, NV);
+    // the dz tile is dead now: it takes the row-store patch (whole row segments per store)
+    if (live)
+      store_acc_rows<F16>((VMO_LDS float*)g_t, accy, NV, 1.f, kGradStore, (char*)(dcol + D), do_rs * 2, m, lane);
   } else {
     to_att(s);
     __syncthreads();
@@ -569,18 +560,10 @@ __global__ __launch_bounds__(64 * kLBWaves) void lstep_bwd_kernel(LBParams p) {
     for (int a = 0; a < ND; ++a) accq[a] = f32x16{};
     mma_acc_t(accq, k_t, dl);
     if constexpr (!LAST) mma_acc_t(accq, v_t, s);
-    if (live && ivalid) {
-      float* dqr = p.dq + bb * p.dq_sb + hh * p.dq_sh + (int64_t)(l32 * p.bs + j) * p.dq_sn;
-#pragma unroll
-      for (int a = 0; a < ND; ++a)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          f32x4* ptr = (f32x4*)(dqr + 32 * a + 8 * g + 4 * hl);
-          f32x4 v = p.dq_overwrite ? f32x4{} : *ptr;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] += accq[a][4 * g + e];
-          *ptr = v;
-        }
+    if (live) {   // kr (and dv) tiles dead now: the kr tile takes the row-store patch
+      float* dq0 = p.dq + bb * p.dq_sb + hh * p.dq_sh + (int64_t)j * p.dq_sn;
+      store_acc_rows<F16>((VMO_LDS float*)k_t, accq, ND, 1.f, p.dq_overwrite ? kGradStoreF32 : kGradAddF32,
+                          (char*)dq0, (int64_t)p.bs * p.dq_sn * 4, m, lane);
     }
   }
 
@@ -595,7 +578,8 @@ __global__ __launch_bounds__(64 * kLBWaves) void lstep_bwd_kernel(LBParams p) {
 #pragma unroll
     for (int a = 0; a < ND; ++a) acck[a] = f32x16{};
     mma_rows_t(acck, q_t, std::integral_constant<int, D>{}, Bd);
-    if (live && kvalid) store_rows(dcol + (int64_t)k * do_rs, acck, ND);
+    if (live)   // the q tile is dead now: it takes the row-store patch
+      store_acc_rows<F16>((VMO_LDS float*)q_t, acck, ND, 1.f, kGradStore, (char*)dcol, do_rs * 2, m, lane);
   }
 }
 
