@@ -178,19 +178,13 @@ __global__ __launch_bounds__(256) void lstep_kernel(LParams p) {
         acc[a] = E::mfma(lds_read_tr8<V8>(r0, r0 + 8 * DV * 2), P[ss], acc[a]);
       }
     }
-    const int i = l32;
-    const int tok = i * p.bs + j;
-    if (live && i < m && tok >= p.skip) {
-      T* zr = (T*)p.res + bb * p.res_sb + hh * p.res_sh + (int64_t)tok * p.res_sn;
-#pragma unroll
-      for (int a = 0; a < NACC; ++a)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          V4 v;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = to_elem<T>(acc[a][4 * g + e]);
-          *(V4*)(zr + 32 * a + 8 * g + 4 * hl) = v;
-        }
+    // z rows i (tokens i b + j) from the first one the recompute does not overwrite (token >= skip),
+    // through the y tile (dead now) as the row-store patch
+    if (live) {
+      const int ibeg = p.skip > j ? (p.skip - j + p.bs - 1) / p.bs : 0;
+      T* z0 = (T*)p.res + bb * p.res_sb + hh * p.res_sh + (int64_t)j * p.res_sn;
+      store_acc_rows<F16>((VMO_LDS float*)y_t, acc, NACC, 1.f, kGradStore, (char*)z0, (int64_t)p.bs * p.res_sn * 2,
+                          m, lane, ibeg);
     }
   } else {
     // attn -> LDS as [k][i] (rows i >= m zeroed so they drop out of the sums over i)
@@ -227,19 +221,12 @@ __global__ __launch_bounds__(256) void lstep_kernel(LParams p) {
         acc[a] = E::mfma(lds_read_tr8<V8>(r0, r1), Bu[is], acc[a]);
       }
     }
-    const int k = l32;
-    if (live && k < m) {
+    // u rows k (tokens k b + j) scaled by scale / col_mass, through the q tile (dead now) as the patch
+    if (live) {
       const float f = p.scale / fmaxf(cs, p.min_col_mass);
-      T* ur = (T*)p.res + bb * p.res_sb + hh * p.res_sh + (int64_t)(k * p.bs + j) * p.res_sn;
-#pragma unroll
-      for (int a = 0; a < NACC; ++a)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          V4 v;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = to_elem<T>(acc[a][4 * g + e] * f);
-          *(V4*)(ur + 32 * a + 8 * g + 4 * hl) = v;
-        }
+      T* u0 = (T*)p.res + bb * p.res_sb + hh * p.res_sh + (int64_t)j * p.res_sn;
+      store_acc_rows<F16>((VMO_LDS float*)q_t, acc, NACC, f, kGradStore, (char*)u0, (int64_t)p.bs * p.res_sn * 2, m,
+                          lane);
     }
   }
 }

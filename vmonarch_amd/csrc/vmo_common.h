@@ -178,13 +178,15 @@ __device__ __forceinline__ int grad_mode(int flags, int accum_bit, int f32_bit) 
 // Write a wave's gradient tile -- acc[a][r] is the value at (row l32, column 32 a + 8 (r / 4) +
 // 4 hl + r % 4), the transposed accumulator layout of both kernels -- one 32-column block at a time
 // through a 4 KB LDS patch, so that 8 consecutive lanes write each row's 32-column segment (128 bytes
-// in fp32) instead of every lane writing 8- or 16-byte pieces of 32 rows.  Rows >= nrows are skipped.
+// in fp32) instead of every lane writing 8- or 16-byte pieces of 32 rows.  Only rows rbegin .. nrows-1
+// are written; f may differ per lane (it scales the lane's own row l32).
 // One wave writes and reads its own patch; LDS accesses of a wave complete in order.  Used for the
 // gradient rows of the flash-entropy and L-step backward kernels.
 constexpr int kEpiPatchBytes = 32 * 32 * 4;
 template <bool F16>
 __device__ __forceinline__ void store_acc_rows(VMO_LDS float* patch, const f32x16* acc, int nacc, float f, int mode,
-                                               char* row0, int64_t row_stride_bytes, int nrows, int lane) {
+                                               char* row0, int64_t row_stride_bytes, int nrows, int lane,
+                                               int rbegin = 0) {
   using T = typename Elem<F16>::T;
   using V4 = typename Elem<F16>::V4;
   const int hl = lane >> 5, l32 = lane & 31, rr0 = lane >> 3, c = lane & 7;
@@ -201,7 +203,7 @@ __device__ __forceinline__ void store_acc_rows(VMO_LDS float* patch, const f32x1
     for (int i = 0; i < 4; ++i) {   // rows rr0 + 8 i, chunk c: 8 lanes per row
       const int rr = rr0 + 8 * i;
       const f32x4 v = *(const VMO_LDS f32x4*)(patch + rr * 32 + (c ^ (rr & 7)) * 4);
-      if (rr < nrows) {
+      if (rr >= rbegin && rr < nrows) {
         char* dst = row0 + rr * row_stride_bytes + (int64_t)(32 * a + 4 * c) * esize;
         if (mode == kGradStore) {
           V4 x;
