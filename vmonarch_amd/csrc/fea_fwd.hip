@@ -521,8 +521,13 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
     tile_sync<0>();   // every wave is done with the last max-pass tile before the ring is reused
     prime();
     key_loop();
+    __syncthreads();   // the fallback's ring reads are done before the epilogue patches reuse it
   }
 
+  // the stage ring is free (every wave passed the barrier above): each wave's 4 KB patch for the
+  // row-segment stores of o
+  static_assert(NSLOT * STAGE >= WAVES * kEpiPatchBytes, "epilogue patches");
+  VMO_LDS float* patch = (VMO_LDS float*)(smem + wave * kEpiPatchBytes);
   if (!wave_live) return;
 
 #pragma unroll
@@ -533,20 +538,11 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
     const float log2l = fast_log2(l_tot);
     const float lse = m_run[j] + log2l;
     const int qr = qrow[j];
+    const int qb0 = q0 + 32 * j, nrows = min(32, p.nq - qb0);
     if constexpr (SPLIT) {
-      if (qvalid[j]) {
-        float* orow = p.part_o + (part0 + qr) * (int64_t)(DW0 + DW1);
-#pragma unroll
-        for (int a = 0; a < NA; ++a)
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            f32x4 v;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = acc[j][a][4 * g + e] * inv_l;
-            *(f32x4*)(orow + 32 * a + 8 * g + 4 * hl) = v;
-          }
-        if (hl == 0) p.part_lse[part0 + qr] = lse;
-      }
+      store_acc_rows<F16>(patch, acc[j], NA, inv_l, kGradStoreF32, (char*)(p.part_o + (part0 + qb0) * (int64_t)(DW0 + DW1)),
+                          (int64_t)(DW0 + DW1) * 4, nrows, lane);
+      if (qvalid[j] && hl == 0) p.part_lse[part0 + qr] = lse;
     } else {
       float ent = 0.f;
       if constexpr (ENT == kEntOnline) {
@@ -567,17 +563,8 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
         dot = wave_sum32(dot);
         ent = lse * kLn2 - (c * kLn2) * dot * inv_l;
       }
+      store_acc_rows<F16>(patch, acc[j], NA, inv_l, kGradStore, (char*)(ob + (int64_t)qb0 * o_sn), o_sn * 2, nrows, lane);
       if (qvalid[j]) {
-        T* orow = ob + (int64_t)qr * o_sn;
-#pragma unroll
-        for (int a = 0; a < NA; ++a)
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            V4 v;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = to_elem<T>(acc[j][a][4 * g + e] * inv_l);
-            *(V4*)(orow + 32 * a + 8 * g + 4 * hl) = v;
-          }
         const int64_t si = st0 + qr;
         if (ENT != kEntNone && hl == 0 && p.ent) p.ent[si] = ent;
         if (hl == 0 && p.lse) p.lse[si] = lse;
