@@ -189,7 +189,30 @@ __device__ __forceinline__ void store_acc_rows(VMO_LDS float* patch, const f32x1
                                                int rbegin = 0) {
   using T = typename Elem<F16>::T;
   using V4 = typename Elem<F16>::V4;
+  using V8 = typename Elem<F16>::V8;
   const int hl = lane >> 5, l32 = lane & 31, rr0 = lane >> 3, c = lane & 7;
+  if (mode == kGradStore && nacc % 2 == 0) {
+    // 16-bit rows: two blocks (64 columns) per pass, so that 8 lanes write a whole 128-byte segment
+    VMO_LDS char* pb = (VMO_LDS char*)patch;   // [32 rows][8 chunks of 16 bytes], chunk ^ (row & 7)
+    for (int a = 0; a < nacc; a += 2) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {   // columns 32 h + 8 j + 4 hl .. +3: chunk 4 h + j, half hl
+          V4 x;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) x[e] = to_elem<T>(acc[a + h][4 * j + e] * f);
+          *(VMO_LDS V4*)(pb + l32 * 128 + ((4 * h + j) ^ (l32 & 7)) * 16 + hl * 8) = x;
+        }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {   // rows rr0 + 8 i, chunk c (columns 8 c .. 8 c + 7)
+        const int rr = rr0 + 8 * i;
+        const V8 x = *(const VMO_LDS V8*)(pb + rr * 128 + (c ^ (rr & 7)) * 16);
+        if (rr >= rbegin && rr < nrows) *(V8*)(row0 + rr * row_stride_bytes + (int64_t)(32 * a + 8 * c) * 2) = x;
+      }
+    }
+    return;
+  }
   const int esize = mode == kGradStore ? 2 : 4;
   for (int a = 0; a < nacc; ++a) {
 #pragma unroll
