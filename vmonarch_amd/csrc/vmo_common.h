@@ -169,19 +169,21 @@ __device__ __forceinline__ V8 lds_read_tr8(const VMO_LDS char* p0, const VMO_LDS
 template <class T>
 __device__ __forceinline__ T to_elem(float x) { return static_cast<T>(x); }
 
-// How a gradient is written: in the inputs' type, or into an fp32 buffer (added to or overwritten).
+// How a result row is written: in the inputs' 16-bit type, or into an fp32 buffer (added to or
+// overwritten).
 enum { kGradStore = 0, kGradAddF32 = 1, kGradStoreF32 = 2 };
 __device__ __forceinline__ int grad_mode(int flags, int accum_bit, int f32_bit) {
   return (flags & accum_bit) ? kGradAddF32 : (flags & f32_bit) ? kGradStoreF32 : kGradStore;
 }
 
-// Write a wave's gradient tile -- acc[a][r] is the value at (row l32, column 32 a + 8 (r / 4) +
-// 4 hl + r % 4), the transposed accumulator layout of both kernels -- one 32-column block at a time
-// through a 4 KB LDS patch, so that 8 consecutive lanes write each row's 32-column segment (128 bytes
-// in fp32) instead of every lane writing 8- or 16-byte pieces of 32 rows.  Only rows rbegin .. nrows-1
-// are written; f may differ per lane (it scales the lane's own row l32).
-// One wave writes and reads its own patch; LDS accesses of a wave complete in order.  Used for the
-// gradient rows of the flash-entropy and L-step backward kernels.
+// Write a wave's 32-row result tile -- acc[a][r] is the value at (row l32, column 32 a + 8 (r / 4) +
+// 4 hl + r % 4), the transposed accumulator layout every kernel here ends with -- through a 4 KB LDS
+// patch, so that 8 consecutive lanes write one row's 128-byte segment (32 fp32 or 64 16-bit columns)
+// instead of every lane writing 8- or 16-byte pieces of 32 rows (rows are often far apart: tokens of
+// one grid column, or rows of a strided layout).  Only rows rbegin .. nrows-1 are written; f may differ
+// per lane (it scales the lane's own row l32).  One wave writes and reads its own patch (LDS accesses
+// of a wave complete in order); the caller makes sure no other wave still uses that LDS.  Used by the
+// flash-entropy forward (o) and backward (gradients) and both L-step kernels (u / z, gradients).
 constexpr int kEpiPatchBytes = 32 * 32 * 4;
 template <bool F16>
 __device__ __forceinline__ void store_acc_rows(VMO_LDS float* patch, const f32x16* acc, int nacc, float f, int mode,
