@@ -339,9 +339,10 @@ __global__ __launch_bounds__(64 * kLBWaves) void lstep_bwd_kernel(LBParams p) {
 
   stage_col_rows<T, D>(qcol, q_rs, m, q_t, lane);
   stage_col_rows<T, D>(ocol, o_rs, m, k_t, lane);
-  if constexpr (LAST) {
+  if constexpr (LAST)
     stage_col_rows<T, DV>(gcol, g_rs, m, g_t, lane);
-  }
+  else   // du rows k, into the dv tile: each lane turns its du values into dv in place
+    stage_col_rows<T, D>(gcol, g_rs, m, v_t, lane);
   const int rk = l32 < m ? l32 : m - 1;
   V8 krf[D / 16], yf[LAST ? DV / 16 : 1];   // kr and y rows k (lane = k) as MFMA operands
   {
@@ -498,13 +499,13 @@ __global__ __launch_bounds__(64 * kLBWaves) void lstep_bwd_kernel(LBParams p) {
     mma_rows_t(accv, q_t, std::integral_constant<int, D>{}, Bu);
     const float cm = fmaxf(cs, p.min_col_mass);
     const float f = p.scale / cm;
-    const T* gp = gcol + (int64_t)(kvalid ? k : 0) * g_rs;
     float df = 0.f;
 #pragma unroll
     for (int a = 0; a < ND; ++a)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const V4 d4 = *(const V4*)(gp + 32 * a + 8 * g + 4 * hl);
+        VMO_LDS V4* dvp = (VMO_LDS V4*)(v_t + k * (D * 2) + ((4 * a + g) ^ ksw) * 16 + hl * 8);
+        const V4 d4 = *dvp;   // du[k][32 a + 8 g + 4 hl + 0..3], staged by stage_col_rows' swizzle
         V4 w;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -512,7 +513,7 @@ __global__ __launch_bounds__(64 * kLBWaves) void lstep_bwd_kernel(LBParams p) {
           df = fmaf(du, accv[a][4 * g + e], df);
           w[e] = to_elem<T>(du * f);
         }
-        *(VMO_LDS V4*)(v_t + k * (D * 2) + ((4 * a + g) ^ ksw) * 16 + hl * 8) = w;
+        *dvp = w;
       }
     df = wave_sum32(df);
     if (hl == 0) c_t[k] = (kvalid && cs >= p.min_col_mass) ? -df * f / cm : 0.f;
