@@ -81,6 +81,21 @@ def test_vmonarch_grad_reference_params(m, b, num_iters):
     assert hip_library_loaded()
 
 
+@pytest.mark.parametrize("rt", [0, 50, 230])
+def test_vmonarch_grad_recompute_lengths(rt):
+    """No recompute, a partial first frame, and a recompute reaching into the third frame: the rows
+    the recompute overwrites carry no L-path gradient, every other row keeps it."""
+    g = torch.Generator().manual_seed(40 + rt)
+    m, b = 4, 100
+    q, k, v = (randn_lp(g, 1, 2, m * b, 64) for _ in range(3))
+    do = torch.randn(1, 2, m * b, 64, generator=g)
+    print(f"vmonarch grad rt={rt}", flush=True)
+    _, grads = _grads(q, k, v, do, m, b, 2, rt)
+    ref = vmonarch_attention_grad(*(t.float().numpy() for t in (q, k, v)), do.numpy(), m, b, 2, rt)
+    for gd, gr in zip(grads, ref):
+        assert_close_ref(gd.float().cpu().numpy(), gr, 5e-2)
+
+
 def test_vmonarch_grad_d128_cfg3_shape_sample():
     # cfg3 geometry (m=16, b=256, rt=256) at D = 128, one head
     g = torch.Generator().manual_seed(3)
