@@ -14,7 +14,9 @@
 // HBM stream.  Layouts as in the flash-entropy kernel: logits are computed transposed
 // (L^T = kr q^T) so the softmax over k is in-lane; z = attn y reuses the logits accumulator as
 // the B operand with y^T read by ds_read_tr16_b64; for u the attention matrix goes through LDS
-// once to switch to one-lane-per-k, where the column mass is an in-lane sum.
+// once to switch to one-lane-per-k, where the column mass is an in-lane sum.  The result rows
+// (tokens i b + j, b rows apart) leave through a dead LDS tile as whole row segments
+// (store_acc_rows).  The backward of the step (lstep_bwd_kernel, below) follows the same layout.
 #include <type_traits>
 
 #include "vmo_common.h"
