@@ -220,6 +220,23 @@ def test_fea_backward_reference_params(N, D, Dv):
     _check_grads(grads, refs)
 
 
+@pytest.mark.parametrize("N", [1, 2, 33, 65, 97])
+@pytest.mark.parametrize("D, Dv", [(64, 64), (128, 128), (128, 256)])
+def test_fea_backward_tiny_and_ragged_lengths(N, D, Dv):
+    """Lengths below one stage and one key / query past a stage boundary (the peeled, masked stages)."""
+    from oracle import entropy_attention_grad
+    g = torch.Generator().manual_seed(N + D + Dv)
+    q, k, v = randn_lp(g, 1, 2, N, D), randn_lp(g, 1, 2, N, D), randn_lp(g, 1, 2, N, Dv)
+    do, de = torch.randn(1, 2, N, Dv, generator=g), torch.randn(1, 2, N, generator=g)
+    print(f"fea bwd N={N} D={D} Dv={Dv}", flush=True)
+    grads = _grads(q, k, v, do, de)
+    refs = entropy_attention_grad(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                  do.bfloat16().float().numpy(), de.numpy(), D ** -0.5)
+    if N == 1:   # one key: P = 1, so dq = dk = 0 (up to the fp32 rounding of dP - delta) and dv = do
+        assert float(grads[0].abs().max()) < 1e-4 and float(grads[1].abs().max()) < 1e-4
+    _check_grads(grads if N > 1 else grads[2:], refs if N > 1 else refs[2:])
+
+
 def test_fea_backward_entropy_term_only():
     """do = 0: the gradient is the entropy term alone (dS = dE P (-E - ln P))."""
     from oracle import entropy_attention_grad
