@@ -163,3 +163,16 @@ def test_vmonarch_dit_layout_in_place_and_out():
         z_c = vmonarch_attention(q.contiguous(), k.contiguous(), v.contiguous(), m, b, 2, recompute_tokens=b)
     assert z.stride() == (m * b * H * 128, 128, H * 128, 1)
     assert torch.equal(z, z_c)
+
+
+@pytest.mark.parametrize("m", [32, 33])
+def test_vmonarch_many_frames(m):
+    """m = 32, the widest L-step tile of the fused kernels, and m = 33, which runs the composed path
+    (R-steps in HIP, the L-step as torch ops): both against the oracle."""
+    from vmonarch_amd import vmonarch_attention
+    g = torch.Generator().manual_seed(m)
+    b = 24
+    q, k, v = (randn_lp(g, 1, 2, m * b, 64) for _ in range(3))
+    print(f"vmonarch m={m}", flush=True)
+    z = vmonarch_attention(q.to(DEV), k.to(DEV), v.to(DEV), m, b, 2, recompute_tokens=b)
+    _check(z, vmonarch_oracle(q.float().numpy(), k.float().numpy(), v.float().numpy(), m, b, 2, b))
