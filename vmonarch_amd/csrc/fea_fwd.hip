@@ -254,7 +254,7 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
   // S^T block kb (32 keys) for every query block: K fragments are read once, used QB times.  The
   // reads run kPre fragments ahead of the MFMAs (pinned by sched_group_barrier) so the LDS latency
   // hides behind the previous MFMAs instead of stalling each one.
-  constexpr int kPre = 3;
+  constexpr int kPre = 2;
   auto qk_block = [&](const VMO_LDS char* Ks, int kb2, f32x16 (&x)[QB], auto sched_tag)
       __attribute__((always_inline)) {
     const VMO_LDS char* arow = Ks + (32 * kb2 + l32) * (D * 2);
