@@ -96,6 +96,11 @@ struct TileCopy {
     }
   }
   __device__ __forceinline__ void issue(int row0, int nrows, uint32_t dst) const {
+    // row0 and nrows are uniform, but may arrive in vector registers (the variants that keep the
+    // tile indices in vector registers): without readfirstlane the full-tile test becomes an exec
+    // mask branch and the tile address a vector 64-bit multiply per copy.
+    row0 = __builtin_amdgcn_readfirstlane(row0);
+    nrows = __builtin_amdgcn_readfirstlane(nrows);
     // The per-instruction addresses are loop invariant up to row0; hoisted out of the key loop
     // they would pin dozens of scalar registers.  The empty asm hides where ub comes from, so they
     // are recomputed here (a few scalar adds per copy).
