@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define VMO_ABI_VERSION 5
+#define VMO_ABI_VERSION 6
 
 enum {
   VMO_OK = 0,
@@ -128,10 +128,16 @@ typedef struct vmo_lstep_args {
  */
 /* vmo_fea_bwd_args.flags: the marked gradient is float32 and the kernels add into it (+=, ACCUM) or
  * overwrite it (=, F32); without either bit it has the inputs' dtype.  ACCUM and F32 of the same
- * gradient together are rejected. */
+ * gradient together are rejected.
+ * VMO_BWD_FOLD_K: the values are k, or [k | v1] (v is k: same address and strides), as in the
+ * VMonarch R-steps (vmonarch.py:50, where autograd sums k's two gradients).  grad_k then receives
+ * k's whole gradient, key role plus value role, and grad_v only v1's (dv1 columns; with values k
+ * alone grad_v is not written and may be null).  Built for (d, dv) = (64, 64), (128, 128) and, with
+ * v1, (64, 128), (128, 256); other shapes, or values that do not start with k, are rejected. */
 enum {
   VMO_BWD_ACCUM_Q = 1, VMO_BWD_ACCUM_K = 2, VMO_BWD_ACCUM_V = 4,
-  VMO_BWD_F32_Q = 8, VMO_BWD_F32_K = 16, VMO_BWD_F32_V = 32
+  VMO_BWD_F32_Q = 8, VMO_BWD_F32_K = 16, VMO_BWD_F32_V = 32,
+  VMO_BWD_FOLD_K = 64
 };
 
 typedef struct vmo_fea_bwd_args {

@@ -123,7 +123,7 @@ def test_fea_bwd_rejects_unknown_and_conflicting_flags(L):
     a.q = a.k = a.v = a.o = a.grad_o = a.grad_q = a.grad_k = a.grad_v = v
     a.lse = a.ent = a.grad_ent = 4096
     a.sm_scale = 0.1
-    for flags in (_lib.BWD_ACCUM_K | _lib.BWD_F32_K, _lib.BWD_ACCUM_Q | _lib.BWD_F32_Q, 64):
+    for flags in (_lib.BWD_ACCUM_K | _lib.BWD_F32_K, _lib.BWD_ACCUM_Q | _lib.BWD_F32_Q, 128):
         a.flags = flags
         assert L.vmo_fea_bwd(ctypes.byref(a), None) == 1
         assert b"flags" in L.vmo_last_error()
@@ -156,3 +156,29 @@ def test_fea_bwd_rejects_bad_value_parts(L):
     assert L.vmo_fea_bwd(ctypes.byref(a), None) == 2
     a.dv1 = 256                                                 # no first part left
     assert L.vmo_fea_bwd(ctypes.byref(a), None) == 1
+
+
+def test_fea_bwd_fold_k_needs_values_that_start_with_k(L):
+    """VMO_BWD_FOLD_K is rejected for values other than k, and for shapes without a fold kernel,
+    before anything is launched."""
+    from vmonarch_amd import _lib
+    a = _lib.FeaBwdArgs()
+    a.dtype, a.batch, a.heads, a.nq, a.nk, a.d, a.dv = 0, 1, 1, 128, 128, 128, 128
+    v = _lib.View(4096, 128, 128 * 128, 128)
+    a.q = a.k = a.o = a.grad_o = a.grad_q = a.grad_k = v
+    a.v = _lib.View(8192, 128, 128 * 128, 128)          # not k
+    a.grad_v = _lib.View()                              # values k alone write no grad_v
+    a.lse = a.ent = a.grad_ent = 4096
+    a.sm_scale = 0.1
+    a.flags = _lib.BWD_FOLD_K
+    assert L.vmo_fea_bwd(ctypes.byref(a), None) == 1
+    assert b"FOLD_K" in L.vmo_last_error()
+    a.v = _lib.View(4096, 128, 128 * 128, 256)          # k's address with another token stride
+    assert L.vmo_fea_bwd(ctypes.byref(a), None) == 1
+    # values k at d = dv = 256: a valid request this build has no fold kernel for (rejected in the
+    # dispatch, after the workspace check: a fake, never dereferenced workspace gets it there)
+    a.d = a.dv = 256
+    a.q = a.k = a.v = a.o = a.grad_o = a.grad_q = a.grad_k = _lib.View(4096, 256, 256 * 128, 256)
+    a.workspace, a.workspace_bytes = 1 << 20, L.vmo_fea_bwd_workspace_size(ctypes.byref(a))
+    assert L.vmo_fea_bwd(ctypes.byref(a), None) == 2
+    assert b"FOLD_K" in L.vmo_last_error()

@@ -377,6 +377,53 @@ def test_fea_backward_values_in_two_parts(nq, nk, D):
         assert torch.equal(a, b), "k-first " + name
 
 
+@pytest.mark.parametrize("nq, nk, D, two_parts", [(300, 300, 64, False), (300, 300, 128, False), (40, 4096, 128, False),
+                                                  (300, 300, 64, True), (200, 1000, 128, True)])
+def test_fea_backward_fold_k(nq, nk, D, two_parts):
+    """VMO_BWD_FOLD_K (values k, or [k | v1]): dk holds k's key-role plus value-role gradient, dv only
+    v1's.  Bit for bit the sum of the unfolded fp32 stores (one rounding each for the product and
+    the sum), in the inputs' dtype the rounding of that sum, and added into an fp32 buffer within
+    float32 rounding of the unfolded additions."""
+    from vmonarch_amd.kernel import fea_forward
+    from vmonarch_amd.kernel_bwd import fea_backward_raw
+    g = torch.Generator().manual_seed(11 * nq + nk + D + two_parts)
+    q, k = randn_lp(g, 1, 2, nq, D).to(DEV), randn_lp(g, 1, 2, nk, D).to(DEV)
+    v1 = randn_lp(g, 1, 2, nk, D).to(DEV) if two_parts else None
+    w = torch.cat([k, v1], -1) if two_parts else k
+    do = randn_lp(g, 1, 2, nq, w.shape[-1]).to(DEV)
+    de = torch.randn(1, 2, nq, generator=g).to(DEV)
+    o, lse, ent = fea_forward(q, k, w, None, D ** -0.5)
+    print(f"fea_bwd fold_k nq={nq} nk={nk} D={D} two_parts={two_parts}", flush=True)
+    f32 = dict(device=DEV, dtype=torch.float32)
+    args = (q, k, k, o, lse, ent, do, de, D ** -0.5)
+    # unfolded, fp32 stores
+    dk_ref, dv_ref = torch.empty(1, 2, nk, D, **f32), torch.empty(1, 2, nk, w.shape[-1], **f32)
+    dq_ref, _, _ = fea_backward_raw(*args, dk=dk_ref, dv=dv_ref, overwrite="kv", v1=v1)
+    k_sum = dk_ref + dv_ref[..., :D]
+    # folded, fp32 stores
+    dk, dv = torch.full((1, 2, nk, D), 7.0, **f32), (torch.full((1, 2, nk, D), 7.0, **f32) if two_parts else None)
+    dq, _, dv_out = fea_backward_raw(*args, dk=dk, dv=dv, overwrite="kv", v1=v1, fold_k=True)
+    assert torch.equal(dq, dq_ref)
+    assert torch.equal(dk, k_sum)
+    if two_parts:
+        assert torch.equal(dv_out, dv_ref[..., D:])
+    else:
+        assert dv_out is None
+    # folded, stored in the inputs' dtype
+    _, dk_lp, dv_lp = fea_backward_raw(*args, v1=v1, fold_k=True)
+    assert dk_lp.dtype == q.dtype and torch.equal(dk_lp, k_sum.to(q.dtype))
+    if two_parts:
+        assert dv_lp.shape[-1] == D and torch.equal(dv_lp, dv_ref[..., D:].to(q.dtype))
+    # folded, added into fp32 buffers that already hold a gradient
+    base_k = torch.randn(1, 2, nk, D, generator=g).to(DEV)
+    base_v = torch.randn(1, 2, nk, D, generator=g).to(DEV)
+    dk_acc, dv_acc = base_k.clone(), (base_v.clone() if two_parts else None)
+    fea_backward_raw(*args, dk=dk_acc, dv=dv_acc, v1=v1, fold_k=True)
+    torch.testing.assert_close(dk_acc, base_k + k_sum, rtol=1e-6, atol=1e-6)
+    if two_parts:
+        torch.testing.assert_close(dv_acc, base_v + dv_ref[..., D:], rtol=1e-6, atol=1e-6)
+
+
 @pytest.mark.parametrize("nq, nk, D", [(300, 300, 64), (300, 300, 128), (40, 4096, 128)])
 def test_fea_backward_values_are_keys(nq, nk, D):
     """Values that are k itself (VMonarch's R-steps before the last, vmonarch.py:50): the kernels

@@ -64,6 +64,7 @@ struct BwdParams {
   int dq_total, kv_total;
   int dq_splits, keys_per_split;   // dq workgroups per query tile, each over one key range
   int accum;                       // VMO_BWD_ACCUM_* / VMO_BWD_F32_* bits: that gradient is fp32, added to / stored
+  int fold_k;                      // (values k or [k | v1]) k's value-role gradient goes into dk; dv holds v1's
   float c;          // sm_scale * log2(e)
   float sm_scale;
 };
@@ -655,6 +656,26 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
     char* row0 = (char*)base + (bb * sb + hh * sh + (int64_t)k0 * sn + col0) * es;
     store_acc_rows<F16>(patch, acc, nacc, f, mode, row0, sn * es, nrows, lane);
   };
+  if constexpr (W0K && PART == 0) {
+    if (p.fold_k) {
+      // Value columns [0, D) are k itself: their gradient (dV blocks 0 .. NK-1, laid out like dK's,
+      // features x keys) joins dK here instead of being stored and summed by the caller.  Multiply and
+      // add rounded separately (no contraction into an fma) give the bits of that sum of two fp32 stores.
+      auto fold = [](float key, float s, float val) __attribute__((always_inline)) {
+#pragma clang fp contract(off)
+        return key * s + val;
+      };
+#pragma unroll
+      for (int b = 0; b < NK; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dk[b][r] = fold(dk[b][r], p.sm_scale, dv[b][r]);
+      put(p.dk, p.dk_sb, p.dk_sh, p.dk_sn, 0, dk, NK, 1.0f, grad_mode(p.accum, VMO_BWD_ACCUM_K, VMO_BWD_F32_K));
+      if constexpr (NV > NK)
+        put(p.dv, p.dv_sb, p.dv_sh, p.dv_sn, 0, dv + NK, NV - NK, 1.0f,
+            grad_mode(p.accum, VMO_BWD_ACCUM_V, VMO_BWD_F32_V));
+      return;
+    }
+  }
   if constexpr (WANT_DK)
     put(p.dk, p.dk_sb, p.dk_sh, p.dk_sn, 0, dk, NK, p.sm_scale, grad_mode(p.accum, VMO_BWD_ACCUM_K, VMO_BWD_F32_K));
   put(p.dv, p.dv_sb, p.dv_sh, p.dv_sn, VOFF, dv, NV, 1.0f, grad_mode(p.accum, VMO_BWD_ACCUM_V, VMO_BWD_F32_V));
@@ -716,6 +737,12 @@ static int dispatch_bwd(const BwdParams& p, int d, int dv, hipStream_t s) {
   } else if (p.v0_is_k) {   // values k (VMonarch's R-steps before the last, vmonarch.py:50)
     if (d == 64 && dv == 64) return launch_bwd<F16, 64, 64, false, true>(p, s);
     if (d == 128 && dv == 128) return launch_bwd<F16, 128, 128, false, true>(p, s);
+  }
+  if (p.fold_k)
+    return set_error(VMO_ERR_UNSUPPORTED, "fea_bwd: VMO_BWD_FOLD_K is built for values k with (d, dv) = (64, 64), "
+                     "(128, 128) and values [k | v1] with (64, 128), (128, 256); got d=%d dv=%d", d, dv);
+  if (p.v1 && p.v0_is_k) {
+    return set_error(VMO_ERR_UNSUPPORTED, "fea_bwd: no kernel for d=%d with values [k | v1] of %d", d, dv);
   } else if (p.v1) {   // values in two halves (the caller checked dv1 = dv / 2)
     if (d == 64 && dv == 128) return launch_bwd<F16, 64, 128, true>(p, s);
     if (d == 128 && dv == 256) return launch_bwd<F16, 128, 256, true>(p, s);
@@ -766,8 +793,10 @@ extern "C" int vmo_fea_bwd(const vmo_fea_bwd_args* a, void* stream) {
   if (a->batch < 0 || a->heads < 0 || a->nq < 0 || a->nk < 0) return set_error(VMO_ERR_INVALID, "fea_bwd: sizes");
   if ((int64_t)a->batch * a->heads == 0 || (a->nq == 0 && a->nk == 0)) return VMO_OK;
   if (a->nq == 0 || a->nk == 0) return set_error(VMO_ERR_INVALID, "fea_bwd: nq and nk must both be > 0");
+  // with VMO_BWD_FOLD_K and values k alone there is no grad_v to write
+  const bool fold_k = (a->flags & VMO_BWD_FOLD_K) != 0, no_grad_v = fold_k && a->dv1 == 0;
   if (!view_ok(a->q) || !view_ok(a->k) || !view_ok(a->v) || !view_ok(a->o) || !view_ok(a->grad_o) ||
-      !view_ok(a->grad_q) || !view_ok(a->grad_k) || !view_ok(a->grad_v))
+      !view_ok(a->grad_q) || !view_ok(a->grad_k) || (!no_grad_v && !view_ok(a->grad_v)))
     return set_error(VMO_ERR_INVALID, "fea_bwd: tensors need 16-byte aligned rows");
   if (!a->lse || !a->ent || !a->grad_ent) return set_error(VMO_ERR_INVALID, "fea_bwd: lse / ent / dent required");
   if (a->dv1 < 0 || a->dv1 >= a->dv) return set_error(VMO_ERR_INVALID, "fea_bwd: dv1 = %d with dv = %d", a->dv1, a->dv);
@@ -777,9 +806,15 @@ extern "C" int vmo_fea_bwd(const vmo_fea_bwd_args* a, void* stream) {
         a->v1.stride_n != a->v.stride_n)
       return set_error(VMO_ERR_INVALID, "fea_bwd: v1 needs 16-byte aligned rows and the strides of v");
   }
-  constexpr int kFlags = VMO_BWD_ACCUM_Q | VMO_BWD_ACCUM_K | VMO_BWD_ACCUM_V | VMO_BWD_F32_Q | VMO_BWD_F32_K | VMO_BWD_F32_V;
+  constexpr int kFlags = VMO_BWD_ACCUM_Q | VMO_BWD_ACCUM_K | VMO_BWD_ACCUM_V | VMO_BWD_F32_Q | VMO_BWD_F32_K |
+                         VMO_BWD_F32_V | VMO_BWD_FOLD_K;
   if ((a->flags & ~kFlags) || ((a->flags >> 3) & a->flags & 7))
     return set_error(VMO_ERR_INVALID, "fea_bwd: unknown or conflicting flags 0x%x", (unsigned)a->flags);
+  const bool v0_is_k = a->v.data == a->k.data && a->v.stride_b == a->k.stride_b && a->v.stride_h == a->k.stride_h &&
+                       a->v.stride_n == a->k.stride_n && a->dv - a->dv1 == a->d;
+  if (fold_k && !v0_is_k)
+    return set_error(VMO_ERR_INVALID, "fea_bwd: VMO_BWD_FOLD_K needs values that start with k (v is k: same address "
+                     "and strides, dv - dv1 = d)");
   if (!(a->sm_scale >= 0.f)) return set_error(VMO_ERR_INVALID, "fea_bwd: sm_scale");
   // the tile copies address up to 7 rows from a lane with a 32-bit byte offset
   const int64_t kMaxRowStride = 1ll << 27;
@@ -796,8 +831,8 @@ extern "C" int vmo_fea_bwd(const vmo_fea_bwd_args* a, void* stream) {
   BwdParams p{};
   p.q = a->q.data; p.k = a->k.data; p.v = a->v.data; p.o = a->o.data; p.dO = a->grad_o.data;
   p.v1 = a->dv1 > 0 ? a->v1.data : nullptr;
-  p.v0_is_k = a->v.data == a->k.data && a->v.stride_b == a->k.stride_b && a->v.stride_h == a->k.stride_h &&
-              a->v.stride_n == a->k.stride_n && a->dv - a->dv1 == a->d;
+  p.v0_is_k = v0_is_k;
+  p.fold_k = fold_k;
   p.dq = a->grad_q.data; p.dk = a->grad_k.data; p.dv = a->grad_v.data;
   p.lse = a->lse; p.ent = a->ent; p.dent = a->grad_ent;
   p.alpha = (float*)a->workspace;

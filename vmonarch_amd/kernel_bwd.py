@@ -13,7 +13,8 @@ def _pad_features(t, width):
     return t if t.shape[-1] == width else torch.nn.functional.pad(t, (0, width - t.shape[-1]))
 
 
-def fea_backward_raw(q, k, v, o, lse, ent, do, de, sm_scale, dq=None, dk=None, dv=None, overwrite="", v1=None):
+def fea_backward_raw(q, k, v, o, lse, ent, do, de, sm_scale, dq=None, dk=None, dv=None, overwrite="", v1=None,
+                     fold_k=False):
     """q: (B, H, nq, D); k: (B, H, nk, D); v: (B, H, nk, Dv); o, do: (B, H, nq, Dv);
     lse, ent, de: (B, H, nq) fp32 with unit token stride.  Returns (dq, dk, dv).
 
@@ -21,11 +22,14 @@ def fea_backward_raw(q, k, v, o, lse, ent, do, de, sm_scale, dq=None, dk=None, d
 
     A gradient passed in as a float32 view is accumulated into (+= in the kernels), or overwritten
     when its letter ("q", "k", "v") is in `overwrite`; otherwise it is returned as a new tensor of
-    q's dtype."""
+    q's dtype.
+
+    `fold_k` (v is k, as the VMonarch R-steps pass it): dk receives k's whole gradient, as key and
+    as the first value columns, and dv only v1's (None without v1)."""
     L = _lib.lib()
     B, H, NQ, D = q.shape
     NK, Dv = k.shape[2], v.shape[-1] * (2 if v1 is not None else 1)
-    flags = 0
+    flags = _lib.BWD_FOLD_K if fold_k else 0
     for t, name, acc_bit, f32_bit in ((dq, "q", _lib.BWD_ACCUM_Q, _lib.BWD_F32_Q), (dk, "k", _lib.BWD_ACCUM_K, _lib.BWD_F32_K),
                                       (dv, "v", _lib.BWD_ACCUM_V, _lib.BWD_F32_V)):
         if t is not None:
@@ -35,14 +39,15 @@ def fea_backward_raw(q, k, v, o, lse, ent, do, de, sm_scale, dq=None, dk=None, d
         dq = torch.empty((B, H, NQ, D), device=q.device, dtype=q.dtype)
     if dk is None:
         dk = torch.empty((B, H, NK, D), device=q.device, dtype=q.dtype)
-    if dv is None:
-        dv = torch.empty((B, H, NK, Dv), device=q.device, dtype=q.dtype)
+    if dv is None and not (fold_k and v1 is None):
+        dv = torch.empty((B, H, NK, v1.shape[-1] if fold_k else Dv), device=q.device, dtype=q.dtype)
     a = _lib.FeaBwdArgs()
     a.flags = flags
     a.dtype = _lib.DTYPES[q.dtype]
     a.batch, a.heads, a.nq, a.nk, a.d, a.dv = B, H, NQ, NK, D, Dv
     a.q, a.k, a.v, a.o, a.grad_o = (_lib.view(t) for t in (q, k, v, o, do))
-    a.grad_q, a.grad_k, a.grad_v = _lib.view(dq), _lib.view(dk), _lib.view(dv)
+    a.grad_q, a.grad_k = _lib.view(dq), _lib.view(dk)
+    a.grad_v = _lib.view(dv) if dv is not None else _lib.View()
     assert lse.stride() == ent.stride() and lse.stride(2) == 1 and de.stride(2) == 1
     a.lse, a.ent, a.grad_ent = lse.data_ptr(), ent.data_ptr(), de.data_ptr()
     a.stat_stride_b, a.stat_stride_h = lse.stride(0), lse.stride(1)

@@ -229,14 +229,14 @@ class _VMonarchFunction(torch.autograd.Function):
         dz = _lib.row_aligned(dz.to(dt))
         f32 = torch.float32
         # fp32 gradient buffers, overwritten by the first backward that writes them (the last
-        # iteration's, which covers every token) and added into by every later one: dq, and one
-        # (.., 2D + Dv) buffer holding dk from the key role | dk from the value role (w starts with
-        # k) | dv
+        # iteration's, which covers every token) and added into by every later one.  The R-steps'
+        # values start with k; the kernels add k's value-role gradient to its key-role one
+        # (fold_k), so dk is one buffer, as autograd's sum over k's uses (vmonarch.py:50) is.
         dq = torch.empty((B, H, N, D), device=dev, dtype=f32)
-        g_kv = torch.empty((B, H, N, 2 * D + Dv), device=dev, dtype=f32)
+        dk = torch.empty((B, H, N, D), device=dev, dtype=f32)
+        dv = torch.empty((B, H, N, Dv), device=dev, dtype=f32)
         frames = lambda t: t.reshape(B, H * m, b, *t.shape[3:])   # the R-step's m frames per head
         de = torch.zeros((B, H * m, b), device=dev, dtype=f32)
-        g_fr = frames(g_kv)
         g = dz
         for it in reversed(range(num_iters)):
             last = it == num_iters - 1
@@ -248,20 +248,20 @@ class _VMonarchFunction(torch.autograd.Function):
             gx, _, _ = fea_backward_raw(frames(x), frames(k), frames(k), frames(out), frames(lse), frames(ent),
                                         frames(dout), de, scale if it == 0 else 1.0,
                                         dq=frames(dq) if it == 0 else None,   # R-step 0 read q directly
-                                        dk=g_fr[..., :D], dv=g_fr[..., D:] if last else g_fr[..., D:2 * D],
-                                        overwrite="kv" if last else "", v1=frames(v) if last else None)
+                                        dk=frames(dk), dv=frames(dv) if last else None,
+                                        overwrite="kv" if last else "", v1=frames(v) if last else None, fold_k=True)
             if it > 0:
                 g = gx.view(B, H, N, D)     # dL/du of the previous L-step's output
         if rt > 0:
             # exact attention of the first rt queries (vmonarch.py:66-68)
             zeros = torch.zeros((B, H, rt), device=dev, dtype=f32)
             fea_backward_raw(q[:, :, :rt], k, v, z[:, :, :rt], lse_rt, zeros, _lib.row_aligned(dz[:, :, :rt]), zeros,
-                             scale, dq=dq[:, :, :rt], dk=g_kv[..., :D], dv=g_kv[..., 2 * D:])
+                             scale, dq=dq[:, :, :rt], dk=dk, dv=dv)
         # gradients in the memory order the caller's q, k, v had (the fp32 -> dtype writes place them)
         gq, gk, gv = (_lib.empty_in_order(o, (B, H, N), f, dt, dev) for o, f in zip(ctx.orders, (D, D, Dv)))
         gq.copy_(dq)
-        torch.add(g_kv[..., :D], g_kv[..., D:2 * D], out=gk)
-        gv.copy_(g_kv[..., 2 * D:])
+        gk.copy_(dk)
+        gv.copy_(dv)
         return gq, gk, gv, None, None, None, None, None
 
 
