@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define VMO_ABI_VERSION 6
+#define VMO_ABI_VERSION 7
 
 enum {
   VMO_OK = 0,
@@ -137,7 +137,12 @@ typedef struct vmo_lstep_args {
 enum {
   VMO_BWD_ACCUM_Q = 1, VMO_BWD_ACCUM_K = 2, VMO_BWD_ACCUM_V = 4,
   VMO_BWD_F32_Q = 8, VMO_BWD_F32_K = 16, VMO_BWD_F32_V = 32,
-  VMO_BWD_FOLD_K = 64
+  VMO_BWD_FOLD_K = 64,
+  /* grad_k (grad_v) in the inputs' dtype = grad_k_base (grad_v_base, an fp32 view of the same shape)
+   * + this call's gradient: the last of several calls that sum one gradient writes it once, in the
+   * caller's dtype, instead of adding into fp32 and converting afterwards.  Not with ACCUM / F32 of
+   * the same gradient. */
+  VMO_BWD_SUM_K = 128, VMO_BWD_SUM_V = 256
 };
 
 typedef struct vmo_fea_bwd_args {
@@ -155,13 +160,14 @@ typedef struct vmo_fea_bwd_args {
   float sm_scale;
   void* workspace;
   size_t workspace_bytes;
-  int32_t flags;                   /* VMO_BWD_ACCUM_* | VMO_BWD_F32_* */
+  int32_t flags;                   /* VMO_BWD_ACCUM_* | VMO_BWD_F32_* | VMO_BWD_FOLD_K | VMO_BWD_SUM_* */
   /* Values given in two parts: with dv1 > 0 the value tensor is [v | v1], v holding columns
    * [0, dv - dv1) and v1 (same strides as v) the last dv1 (VMonarch's last R-step, values [k | v],
    * vmonarch.py:50, without the concatenated copy).  Built for dv1 = dv / 2 with (d, dv) = (64, 128)
    * and (128, 256).  grad_v stays one (.., dv) tensor. */
   vmo_view v1;
   int32_t dv1;
+  vmo_view grad_k_base, grad_v_base;   /* fp32, read with VMO_BWD_SUM_K / VMO_BWD_SUM_V */
 } vmo_fea_bwd_args;
 
 /*

@@ -123,7 +123,7 @@ def test_fea_bwd_rejects_unknown_and_conflicting_flags(L):
     a.q = a.k = a.v = a.o = a.grad_o = a.grad_q = a.grad_k = a.grad_v = v
     a.lse = a.ent = a.grad_ent = 4096
     a.sm_scale = 0.1
-    for flags in (_lib.BWD_ACCUM_K | _lib.BWD_F32_K, _lib.BWD_ACCUM_Q | _lib.BWD_F32_Q, 128):
+    for flags in (_lib.BWD_ACCUM_K | _lib.BWD_F32_K, _lib.BWD_ACCUM_Q | _lib.BWD_F32_Q, 512):
         a.flags = flags
         assert L.vmo_fea_bwd(ctypes.byref(a), None) == 1
         assert b"flags" in L.vmo_last_error()
@@ -182,3 +182,24 @@ def test_fea_bwd_fold_k_needs_values_that_start_with_k(L):
     a.workspace, a.workspace_bytes = 1 << 20, L.vmo_fea_bwd_workspace_size(ctypes.byref(a))
     assert L.vmo_fea_bwd(ctypes.byref(a), None) == 2
     assert b"FOLD_K" in L.vmo_last_error()
+
+
+def test_fea_bwd_sum_needs_a_base_and_no_fp32_bits(L):
+    """VMO_BWD_SUM_K / _V write the gradient in the inputs' dtype from an fp32 base: together with
+    ACCUM / F32 of the same gradient, or without the base view, they are rejected."""
+    from vmonarch_amd import _lib
+    a = _lib.FeaBwdArgs()
+    a.dtype, a.batch, a.heads, a.nq, a.nk, a.d, a.dv = 0, 1, 1, 128, 128, 128, 128
+    v = _lib.View(4096, 128, 128 * 128, 128)
+    a.q = a.k = a.v = a.o = a.grad_o = a.grad_q = a.grad_k = a.grad_v = v
+    a.lse = a.ent = a.grad_ent = 4096
+    a.sm_scale = 0.1
+    a.grad_k_base = a.grad_v_base = _lib.View(1 << 16, 128, 128 * 128, 128)
+    for flags in (_lib.BWD_SUM_K | _lib.BWD_ACCUM_K, _lib.BWD_SUM_V | _lib.BWD_F32_V):
+        a.flags = flags
+        assert L.vmo_fea_bwd(ctypes.byref(a), None) == 1
+        assert b"flags" in L.vmo_last_error()
+    a.flags = _lib.BWD_SUM_V
+    a.grad_v_base = _lib.View()
+    assert L.vmo_fea_bwd(ctypes.byref(a), None) == 1
+    assert b"SUM" in L.vmo_last_error()

@@ -424,6 +424,40 @@ def test_fea_backward_fold_k(nq, nk, D, two_parts):
         torch.testing.assert_close(dv_acc, base_v + dv_ref[..., D:], rtol=1e-6, atol=1e-6)
 
 
+@pytest.mark.parametrize("nq, nk, D, Dv, fold", [(300, 300, 128, 128, False), (40, 4096, 128, 128, False),
+                                                (200, 700, 128, 256, False), (77, 300, 64, 64, False),
+                                                (200, 700, 128, 256, True)])
+def test_fea_backward_sum_into_dtype(nq, nk, D, Dv, fold):
+    """VMO_BWD_SUM_K / _V: dk, dv in the inputs' dtype = fp32 base + this call's gradient, bit for bit
+    the dtype rounding of the base plus the call's fp32 store (the dV columns split over two launches
+    at Dv = 256 included; with VMO_BWD_FOLD_K the folded dk and v1's dv)."""
+    from vmonarch_amd.kernel import fea_forward
+    from vmonarch_amd.kernel_bwd import fea_backward_raw
+    g = torch.Generator().manual_seed(13 * nq + nk + D + Dv + fold)
+    q, k = randn_lp(g, 1, 2, nq, D).to(DEV), randn_lp(g, 1, 2, nk, D).to(DEV)
+    if fold:
+        v, v1 = k, randn_lp(g, 1, 2, nk, Dv - D).to(DEV)
+        w = torch.cat([k, v1], -1)
+    else:
+        v = v1 = None
+        w = randn_lp(g, 1, 2, nk, Dv).to(DEV)
+    do = randn_lp(g, 1, 2, nq, Dv).to(DEV)
+    de = torch.randn(1, 2, nq, generator=g).to(DEV)
+    o, lse, ent = fea_forward(q, k, w, None, D ** -0.5)
+    print(f"fea_bwd sum into dtype nq={nq} nk={nk} D={D} Dv={Dv} fold={fold}", flush=True)
+    args = (q, k, v if fold else w, o, lse, ent, do, de, D ** -0.5)
+    f32 = dict(device=DEV, dtype=torch.float32)
+    dvw = Dv - D if fold else Dv
+    dk32, dv32 = torch.empty(1, 2, nk, D, **f32), torch.empty(1, 2, nk, dvw, **f32)
+    dq_ref, _, _ = fea_backward_raw(*args, dk=dk32, dv=dv32, overwrite="kv", v1=v1, fold_k=fold)
+    base_k, base_v = torch.randn(1, 2, nk, D, generator=g).to(DEV), torch.randn(1, 2, nk, dvw, generator=g).to(DEV)
+    dq, dk, dv = fea_backward_raw(*args, v1=v1, fold_k=fold, dk_base=base_k, dv_base=base_v)
+    assert dk.dtype == q.dtype and dv.dtype == q.dtype
+    assert torch.equal(dq, dq_ref.to(q.dtype)) or torch.equal(dq, fea_backward_raw(*args, v1=v1, fold_k=fold)[0])
+    assert torch.equal(dk, (base_k + dk32).to(q.dtype))
+    assert torch.equal(dv, (base_v + dv32).to(q.dtype))
+
+
 @pytest.mark.parametrize("nq, nk, D", [(300, 300, 64), (300, 300, 128), (40, 4096, 128)])
 def test_fea_backward_values_are_keys(nq, nk, D):
     """Values that are k itself (VMonarch's R-steps before the last, vmonarch.py:50): the kernels

@@ -12,7 +12,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libvmonarch_gfx950.so")
-ABI_VERSION = 6
+ABI_VERSION = 7
 DTYPES = {torch.bfloat16: 0, torch.float16: 1}
 
 c_int32, c_int64, c_float, c_void_p, c_size_t = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
@@ -42,13 +42,14 @@ class FeaBwdArgs(ctypes.Structure):
         ("stat_stride_b", c_int64), ("stat_stride_h", c_int64),
         ("grad_ent_stride_b", c_int64), ("grad_ent_stride_h", c_int64),
         ("sm_scale", c_float), ("workspace", c_void_p), ("workspace_bytes", c_size_t), ("flags", c_int32),
-        ("v1", View), ("dv1", c_int32),
+        ("v1", View), ("dv1", c_int32), ("grad_k_base", View), ("grad_v_base", View),
     ]
 
 
 BWD_ACCUM_Q, BWD_ACCUM_K, BWD_ACCUM_V = 1, 2, 4
 BWD_F32_Q, BWD_F32_K, BWD_F32_V = 8, 16, 32
 BWD_FOLD_K = 64   # values k or [k | v1]: k's value-role gradient into grad_k, grad_v holds v1's
+BWD_SUM_K, BWD_SUM_V = 128, 256   # grad (dtype) = fp32 base + this call's gradient
 LSTEP_BWD_OVERWRITE_Q = 1
 
 

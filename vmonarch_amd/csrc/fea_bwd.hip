@@ -65,6 +65,9 @@ struct BwdParams {
   int dq_splits, keys_per_split;   // dq workgroups per query tile, each over one key range
   int accum;                       // VMO_BWD_ACCUM_* / VMO_BWD_F32_* bits: that gradient is fp32, added to / stored
   int fold_k;                      // (values k or [k | v1]) k's value-role gradient goes into dk; dv holds v1's
+  const void* dk_base;             // VMO_BWD_SUM_K / _V: fp32 rows added to dk / dv before their dtype store
+  const void* dv_base;
+  int64_t dkb_sb, dkb_sh, dkb_sn, dvb_sb, dvb_sh, dvb_sn;
   float c;          // sm_scale * log2(e)
   float sm_scale;
 };
@@ -649,13 +652,18 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
   if (!wave_live) return;
   VMO_LDS float* patch = (VMO_LDS float*)(smem + wave * kEpiPatchBytes);
   const int nrows = min(32, p.nk - k0);
-  // write NACC accumulator blocks times f: stored in T, or added to / stored into an fp32 gradient
+  // write NACC accumulator blocks times f: stored in T, added to / stored into an fp32 gradient, or
+  // stored in T as the sum with an fp32 base (src, same column offset)
   auto put = [&](void* base, int64_t sb, int64_t sh, int64_t sn, int col0, const f32x16* acc, int nacc, float f,
-                 int mode) __attribute__((always_inline)) {
-    const int64_t es = mode == kGradStore ? 2 : 4;
+                 int mode, const void* src = nullptr, int64_t ssb = 0, int64_t ssh = 0, int64_t ssn = 0)
+      __attribute__((always_inline)) {
+    const int64_t es = mode == kGradStore || mode == kGradSumStore ? 2 : 4;
     char* row0 = (char*)base + (bb * sb + hh * sh + (int64_t)k0 * sn + col0) * es;
-    store_acc_rows<F16>(patch, acc, nacc, f, mode, row0, sn * es, nrows, lane);
+    const char* src0 = src ? (const char*)src + (bb * ssb + hh * ssh + (int64_t)k0 * ssn + col0) * 4 : nullptr;
+    store_acc_rows<F16>(patch, acc, nacc, f, mode, row0, sn * es, nrows, lane, 0, src0, ssn * 4);
   };
+  const int mode_k = grad_mode(p.accum, VMO_BWD_ACCUM_K, VMO_BWD_F32_K, VMO_BWD_SUM_K);
+  const int mode_v = grad_mode(p.accum, VMO_BWD_ACCUM_V, VMO_BWD_F32_V, VMO_BWD_SUM_V);
   if constexpr (W0K && PART == 0) {
     if (p.fold_k) {
       // Value columns [0, D) are k itself: their gradient (dV blocks 0 .. NK-1, laid out like dK's,
@@ -669,16 +677,16 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
       for (int b = 0; b < NK; ++b)
 #pragma unroll
         for (int r = 0; r < 16; ++r) dk[b][r] = fold(dk[b][r], p.sm_scale, dv[b][r]);
-      put(p.dk, p.dk_sb, p.dk_sh, p.dk_sn, 0, dk, NK, 1.0f, grad_mode(p.accum, VMO_BWD_ACCUM_K, VMO_BWD_F32_K));
+      put(p.dk, p.dk_sb, p.dk_sh, p.dk_sn, 0, dk, NK, 1.0f, mode_k, p.dk_base, p.dkb_sb, p.dkb_sh, p.dkb_sn);
       if constexpr (NV > NK)
-        put(p.dv, p.dv_sb, p.dv_sh, p.dv_sn, 0, dv + NK, NV - NK, 1.0f,
-            grad_mode(p.accum, VMO_BWD_ACCUM_V, VMO_BWD_F32_V));
+        put(p.dv, p.dv_sb, p.dv_sh, p.dv_sn, 0, dv + NK, NV - NK, 1.0f, mode_v, p.dv_base, p.dvb_sb, p.dvb_sh,
+            p.dvb_sn);
       return;
     }
   }
   if constexpr (WANT_DK)
-    put(p.dk, p.dk_sb, p.dk_sh, p.dk_sn, 0, dk, NK, p.sm_scale, grad_mode(p.accum, VMO_BWD_ACCUM_K, VMO_BWD_F32_K));
-  put(p.dv, p.dv_sb, p.dv_sh, p.dv_sn, VOFF, dv, NV, 1.0f, grad_mode(p.accum, VMO_BWD_ACCUM_V, VMO_BWD_F32_V));
+    put(p.dk, p.dk_sb, p.dk_sh, p.dk_sn, 0, dk, NK, p.sm_scale, mode_k, p.dk_base, p.dkb_sb, p.dkb_sh, p.dkb_sn);
+  put(p.dv, p.dv_sb, p.dv_sh, p.dv_sn, VOFF, dv, NV, 1.0f, mode_v, p.dv_base, p.dvb_sb, p.dvb_sh, p.dvb_sn);
 }
 
 template <bool F16, int D, int DV, int PART, bool W0K>
@@ -807,9 +815,15 @@ extern "C" int vmo_fea_bwd(const vmo_fea_bwd_args* a, void* stream) {
       return set_error(VMO_ERR_INVALID, "fea_bwd: v1 needs 16-byte aligned rows and the strides of v");
   }
   constexpr int kFlags = VMO_BWD_ACCUM_Q | VMO_BWD_ACCUM_K | VMO_BWD_ACCUM_V | VMO_BWD_F32_Q | VMO_BWD_F32_K |
-                         VMO_BWD_F32_V | VMO_BWD_FOLD_K;
-  if ((a->flags & ~kFlags) || ((a->flags >> 3) & a->flags & 7))
+                         VMO_BWD_F32_V | VMO_BWD_FOLD_K | VMO_BWD_SUM_K | VMO_BWD_SUM_V;
+  const bool sum_k = (a->flags & VMO_BWD_SUM_K) != 0, sum_v = (a->flags & VMO_BWD_SUM_V) != 0;
+  if ((a->flags & ~kFlags) || ((a->flags >> 3) & a->flags & 7) ||
+      (sum_k && (a->flags & (VMO_BWD_ACCUM_K | VMO_BWD_F32_K))) ||
+      (sum_v && (a->flags & (VMO_BWD_ACCUM_V | VMO_BWD_F32_V))) || (sum_v && no_grad_v))
     return set_error(VMO_ERR_INVALID, "fea_bwd: unknown or conflicting flags 0x%x", (unsigned)a->flags);
+  if ((sum_k && !view_ok(a->grad_k_base)) || (sum_v && !view_ok(a->grad_v_base)))
+    return set_error(VMO_ERR_INVALID, "fea_bwd: VMO_BWD_SUM_K / _V need a grad_k_base / grad_v_base view "
+                     "(fp32, 16-byte aligned rows)");
   const bool v0_is_k = a->v.data == a->k.data && a->v.stride_b == a->k.stride_b && a->v.stride_h == a->k.stride_h &&
                        a->v.stride_n == a->k.stride_n && a->dv - a->dv1 == a->d;
   if (fold_k && !v0_is_k)
@@ -833,6 +847,14 @@ extern "C" int vmo_fea_bwd(const vmo_fea_bwd_args* a, void* stream) {
   p.v1 = a->dv1 > 0 ? a->v1.data : nullptr;
   p.v0_is_k = v0_is_k;
   p.fold_k = fold_k;
+  if (sum_k) {
+    p.dk_base = a->grad_k_base.data;
+    p.dkb_sb = a->grad_k_base.stride_b; p.dkb_sh = a->grad_k_base.stride_h; p.dkb_sn = a->grad_k_base.stride_n;
+  }
+  if (sum_v) {
+    p.dv_base = a->grad_v_base.data;
+    p.dvb_sb = a->grad_v_base.stride_b; p.dvb_sh = a->grad_v_base.stride_h; p.dvb_sn = a->grad_v_base.stride_n;
+  }
   p.dq = a->grad_q.data; p.dk = a->grad_k.data; p.dv = a->grad_v.data;
   p.lse = a->lse; p.ent = a->ent; p.dent = a->grad_ent;
   p.alpha = (float*)a->workspace;

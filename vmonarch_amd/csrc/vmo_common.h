@@ -169,11 +169,13 @@ __device__ __forceinline__ V8 lds_read_tr8(const VMO_LDS char* p0, const VMO_LDS
 template <class T>
 __device__ __forceinline__ T to_elem(float x) { return static_cast<T>(x); }
 
-// How a result row is written: in the inputs' 16-bit type, or into an fp32 buffer (added to or
-// overwritten).
-enum { kGradStore = 0, kGradAddF32 = 1, kGradStoreF32 = 2 };
-__device__ __forceinline__ int grad_mode(int flags, int accum_bit, int f32_bit) {
-  return (flags & accum_bit) ? kGradAddF32 : (flags & f32_bit) ? kGradStoreF32 : kGradStore;
+// How a result row is written: in the inputs' 16-bit type, into an fp32 buffer (added to or
+// overwritten), or in the 16-bit type as the sum with an fp32 base row (the last of several
+// contributions to one gradient).
+enum { kGradStore = 0, kGradAddF32 = 1, kGradStoreF32 = 2, kGradSumStore = 3 };
+__device__ __forceinline__ int grad_mode(int flags, int accum_bit, int f32_bit, int sum_bit = 0) {
+  return (flags & sum_bit) ? kGradSumStore
+         : (flags & accum_bit) ? kGradAddF32 : (flags & f32_bit) ? kGradStoreF32 : kGradStore;
 }
 
 // Write a wave's 32-row result tile -- acc[a][r] is the value at (row l32, column 32 a + 8 (r / 4) +
@@ -188,7 +190,8 @@ constexpr int kEpiPatchBytes = 32 * 32 * 4;
 template <bool F16>
 __device__ __forceinline__ void store_acc_rows(VMO_LDS float* patch, const f32x16* acc, int nacc, float f, int mode,
                                                char* row0, int64_t row_stride_bytes, int nrows, int lane,
-                                               int rbegin = 0) {
+                                               int rbegin = 0, const char* src0 = nullptr,
+                                               int64_t src_stride_bytes = 0) {
   using T = typename Elem<F16>::T;
   using V4 = typename Elem<F16>::V4;
   using V8 = typename Elem<F16>::V8;
@@ -215,7 +218,7 @@ __device__ __forceinline__ void store_acc_rows(VMO_LDS float* patch, const f32x1
     }
     return;
   }
-  const int esize = mode == kGradStore ? 2 : 4;
+  const int esize = mode == kGradStore || mode == kGradSumStore ? 2 : 4;
   for (int a = 0; a < nacc; ++a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {   // row l32, 16-byte chunk 2 j + hl, swizzled by row against bank conflicts
@@ -230,10 +233,15 @@ __device__ __forceinline__ void store_acc_rows(VMO_LDS float* patch, const f32x1
       const f32x4 v = *(const VMO_LDS f32x4*)(patch + rr * 32 + (c ^ (rr & 7)) * 4);
       if (rr >= rbegin && rr < nrows) {
         char* dst = row0 + rr * row_stride_bytes + (int64_t)(32 * a + 4 * c) * esize;
-        if (mode == kGradStore) {
+        if (mode == kGradStore || mode == kGradSumStore) {
+          // (sum: the base row src0 is fp32, same columns; the product came through LDS, so the
+          // sum is its own rounding, as adding the fp32 store of this result would be)
+          const f32x4 b = mode == kGradSumStore
+                              ? *(const f32x4*)(src0 + rr * src_stride_bytes + (int64_t)(32 * a + 4 * c) * 4)
+                              : f32x4{0.f, 0.f, 0.f, 0.f};
           V4 x;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) x[e] = to_elem<T>(v[e]);
+          for (int e = 0; e < 4; ++e) x[e] = to_elem<T>(mode == kGradSumStore ? b[e] + v[e] : v[e]);
           *(V4*)dst = x;
         } else {
           f32x4* ptr = (f32x4*)dst;

@@ -14,7 +14,7 @@ def _pad_features(t, width):
 
 
 def fea_backward_raw(q, k, v, o, lse, ent, do, de, sm_scale, dq=None, dk=None, dv=None, overwrite="", v1=None,
-                     fold_k=False):
+                     fold_k=False, dk_base=None, dv_base=None):
     """q: (B, H, nq, D); k: (B, H, nk, D); v: (B, H, nk, Dv); o, do: (B, H, nq, Dv);
     lse, ent, de: (B, H, nq) fp32 with unit token stride.  Returns (dq, dk, dv).
 
@@ -25,14 +25,21 @@ def fea_backward_raw(q, k, v, o, lse, ent, do, de, sm_scale, dq=None, dk=None, d
     q's dtype.
 
     `fold_k` (v is k, as the VMonarch R-steps pass it): dk receives k's whole gradient, as key and
-    as the first value columns, and dv only v1's (None without v1)."""
+    as the first value columns, and dv only v1's (None without v1).
+
+    `dk_base` / `dv_base` (float32, shaped like dk / dv): dk / dv, in q's dtype, are that base plus
+    this call's gradient (the last of several calls summing one gradient)."""
     L = _lib.lib()
     B, H, NQ, D = q.shape
     NK, Dv = k.shape[2], v.shape[-1] * (2 if v1 is not None else 1)
     flags = _lib.BWD_FOLD_K if fold_k else 0
-    for t, name, acc_bit, f32_bit in ((dq, "q", _lib.BWD_ACCUM_Q, _lib.BWD_F32_Q), (dk, "k", _lib.BWD_ACCUM_K, _lib.BWD_F32_K),
-                                      (dv, "v", _lib.BWD_ACCUM_V, _lib.BWD_F32_V)):
-        if t is not None:
+    for t, name, acc_bit, f32_bit, base in ((dq, "q", _lib.BWD_ACCUM_Q, _lib.BWD_F32_Q, None),
+                                            (dk, "k", _lib.BWD_ACCUM_K, _lib.BWD_F32_K, dk_base),
+                                            (dv, "v", _lib.BWD_ACCUM_V, _lib.BWD_F32_V, dv_base)):
+        if base is not None:
+            assert base.dtype == torch.float32 and (t is None or t.dtype == q.dtype), "base fp32, result q.dtype"
+            flags |= _lib.BWD_SUM_K if name == "k" else _lib.BWD_SUM_V
+        elif t is not None:
             assert t.dtype == torch.float32, "a gradient passed in must be float32"
             flags |= f32_bit if name in overwrite else acc_bit
     if dq is None:
@@ -48,6 +55,12 @@ def fea_backward_raw(q, k, v, o, lse, ent, do, de, sm_scale, dq=None, dk=None, d
     a.q, a.k, a.v, a.o, a.grad_o = (_lib.view(t) for t in (q, k, v, o, do))
     a.grad_q, a.grad_k = _lib.view(dq), _lib.view(dk)
     a.grad_v = _lib.view(dv) if dv is not None else _lib.View()
+    if dk_base is not None:
+        assert dk_base.shape == dk.shape
+        a.grad_k_base = _lib.view(dk_base)
+    if dv_base is not None:
+        assert dv_base.shape == dv.shape
+        a.grad_v_base = _lib.view(dv_base)
     assert lse.stride() == ent.stride() and lse.stride(2) == 1 and de.stride(2) == 1
     a.lse, a.ent, a.grad_ent = lse.data_ptr(), ent.data_ptr(), de.data_ptr()
     a.stat_stride_b, a.stat_stride_h = lse.stride(0), lse.stride(1)

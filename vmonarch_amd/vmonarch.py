@@ -252,16 +252,18 @@ class _VMonarchFunction(torch.autograd.Function):
                                         overwrite="kv" if last else "", v1=frames(v) if last else None, fold_k=True)
             if it > 0:
                 g = gx.view(B, H, N, D)     # dL/du of the previous L-step's output
-        if rt > 0:
-            # exact attention of the first rt queries (vmonarch.py:66-68)
-            zeros = torch.zeros((B, H, rt), device=dev, dtype=f32)
-            fea_backward_raw(q[:, :, :rt], k, v, z[:, :, :rt], lse_rt, zeros, _lib.row_aligned(dz[:, :, :rt]), zeros,
-                             scale, dq=dq[:, :, :rt], dk=dk, dv=dv)
         # gradients in the memory order the caller's q, k, v had (the fp32 -> dtype writes place them)
         gq, gk, gv = (_lib.empty_in_order(o, (B, H, N), f, dt, dev) for o, f in zip(ctx.orders, (D, D, Dv)))
+        if rt > 0:
+            # exact attention of the first rt queries (vmonarch.py:66-68); it reads every key, so its
+            # dK / dV epilogue writes k's and v's final gradients: fp32 sum so far + its own, in dtype
+            zeros = torch.zeros((B, H, rt), device=dev, dtype=f32)
+            fea_backward_raw(q[:, :, :rt], k, v, z[:, :, :rt], lse_rt, zeros, _lib.row_aligned(dz[:, :, :rt]), zeros,
+                             scale, dq=dq[:, :, :rt], dk=gk, dv=gv, dk_base=dk, dv_base=dv)
+        else:
+            gk.copy_(dk)
+            gv.copy_(dv)
         gq.copy_(dq)
-        gk.copy_(dk)
-        gv.copy_(dv)
         return gq, gk, gv, None, None, None, None, None
 
 
