@@ -377,9 +377,14 @@ def test_fea_backward_values_in_two_parts(nq, nk, D):
         assert torch.equal(a, b), "k-first " + name
 
 
-@pytest.mark.parametrize("nq, nk, D, two_parts", [(300, 300, 64, False), (300, 300, 128, False), (40, 4096, 128, False),
-                                                  (300, 300, 64, True), (200, 1000, 128, True)])
-def test_fea_backward_fold_k(nq, nk, D, two_parts):
+@pytest.mark.parametrize("nq, nk, D, two_parts, dt", [(300, 300, 64, False, torch.bfloat16),
+                                                      (300, 300, 128, False, torch.bfloat16),
+                                                      (40, 4096, 128, False, torch.bfloat16),
+                                                      (300, 300, 64, True, torch.bfloat16),
+                                                      (200, 1000, 128, True, torch.bfloat16),
+                                                      (300, 300, 128, False, torch.float16),
+                                                      (200, 1000, 128, True, torch.float16)])
+def test_fea_backward_fold_k(nq, nk, D, two_parts, dt):
     """VMO_BWD_FOLD_K (values k, or [k | v1]): dk holds k's key-role plus value-role gradient, dv only
     v1's.  Bit for bit the sum of the unfolded fp32 stores (one rounding each for the product and
     the sum), in the inputs' dtype the rounding of that sum, and added into an fp32 buffer within
@@ -387,13 +392,13 @@ def test_fea_backward_fold_k(nq, nk, D, two_parts):
     from vmonarch_amd.kernel import fea_forward
     from vmonarch_amd.kernel_bwd import fea_backward_raw
     g = torch.Generator().manual_seed(11 * nq + nk + D + two_parts)
-    q, k = randn_lp(g, 1, 2, nq, D).to(DEV), randn_lp(g, 1, 2, nk, D).to(DEV)
-    v1 = randn_lp(g, 1, 2, nk, D).to(DEV) if two_parts else None
+    q, k = randn_lp(g, 1, 2, nq, D, dtype=dt).to(DEV), randn_lp(g, 1, 2, nk, D, dtype=dt).to(DEV)
+    v1 = randn_lp(g, 1, 2, nk, D, dtype=dt).to(DEV) if two_parts else None
     w = torch.cat([k, v1], -1) if two_parts else k
-    do = randn_lp(g, 1, 2, nq, w.shape[-1]).to(DEV)
+    do = randn_lp(g, 1, 2, nq, w.shape[-1], dtype=dt).to(DEV)
     de = torch.randn(1, 2, nq, generator=g).to(DEV)
     o, lse, ent = fea_forward(q, k, w, None, D ** -0.5)
-    print(f"fea_bwd fold_k nq={nq} nk={nk} D={D} two_parts={two_parts}", flush=True)
+    print(f"fea_bwd fold_k nq={nq} nk={nk} D={D} two_parts={two_parts} {dt}", flush=True)
     f32 = dict(device=DEV, dtype=torch.float32)
     args = (q, k, k, o, lse, ent, do, de, D ** -0.5)
     # unfolded, fp32 stores
@@ -424,27 +429,31 @@ def test_fea_backward_fold_k(nq, nk, D, two_parts):
         torch.testing.assert_close(dv_acc, base_v + dv_ref[..., D:], rtol=1e-6, atol=1e-6)
 
 
-@pytest.mark.parametrize("nq, nk, D, Dv, fold", [(300, 300, 128, 128, False), (40, 4096, 128, 128, False),
-                                                (200, 700, 128, 256, False), (77, 300, 64, 64, False),
-                                                (200, 700, 128, 256, True)])
-def test_fea_backward_sum_into_dtype(nq, nk, D, Dv, fold):
+@pytest.mark.parametrize("nq, nk, D, Dv, fold, dt", [(300, 300, 128, 128, False, torch.bfloat16),
+                                                    (40, 4096, 128, 128, False, torch.bfloat16),
+                                                    (200, 700, 128, 256, False, torch.bfloat16),
+                                                    (77, 300, 64, 64, False, torch.bfloat16),
+                                                    (200, 700, 128, 256, True, torch.bfloat16),
+                                                    (40, 4096, 128, 128, False, torch.float16),
+                                                    (200, 700, 128, 256, True, torch.float16)])
+def test_fea_backward_sum_into_dtype(nq, nk, D, Dv, fold, dt):
     """VMO_BWD_SUM_K / _V: dk, dv in the inputs' dtype = fp32 base + this call's gradient, bit for bit
     the dtype rounding of the base plus the call's fp32 store (the dV columns split over two launches
     at Dv = 256 included; with VMO_BWD_FOLD_K the folded dk and v1's dv)."""
     from vmonarch_amd.kernel import fea_forward
     from vmonarch_amd.kernel_bwd import fea_backward_raw
     g = torch.Generator().manual_seed(13 * nq + nk + D + Dv + fold)
-    q, k = randn_lp(g, 1, 2, nq, D).to(DEV), randn_lp(g, 1, 2, nk, D).to(DEV)
+    q, k = randn_lp(g, 1, 2, nq, D, dtype=dt).to(DEV), randn_lp(g, 1, 2, nk, D, dtype=dt).to(DEV)
     if fold:
-        v, v1 = k, randn_lp(g, 1, 2, nk, Dv - D).to(DEV)
+        v, v1 = k, randn_lp(g, 1, 2, nk, Dv - D, dtype=dt).to(DEV)
         w = torch.cat([k, v1], -1)
     else:
         v = v1 = None
-        w = randn_lp(g, 1, 2, nk, Dv).to(DEV)
-    do = randn_lp(g, 1, 2, nq, Dv).to(DEV)
+        w = randn_lp(g, 1, 2, nk, Dv, dtype=dt).to(DEV)
+    do = randn_lp(g, 1, 2, nq, Dv, dtype=dt).to(DEV)
     de = torch.randn(1, 2, nq, generator=g).to(DEV)
     o, lse, ent = fea_forward(q, k, w, None, D ** -0.5)
-    print(f"fea_bwd sum into dtype nq={nq} nk={nk} D={D} Dv={Dv} fold={fold}", flush=True)
+    print(f"fea_bwd sum into dtype nq={nq} nk={nk} D={D} Dv={Dv} fold={fold} {dt}", flush=True)
     args = (q, k, v if fold else w, o, lse, ent, do, de, D ** -0.5)
     f32 = dict(device=DEV, dtype=torch.float32)
     dvw = Dv - D if fold else Dv
