@@ -10,6 +10,8 @@ Contents
   vmonarch.vmonarch_attention  alternating-minimisation glue (R-step, L-step, recompute)
   vmonarch.lstep_grad          backward of one L-step (entropy bias detached)
   vmonarch.vmonarch_attention_grad  backward of the whole glue (dq, dk, dv)
+  vmonarch.vmonarch_attention_lowp  the glue with the reference's bf16 roundings (how far the
+                                    reference's own bf16 path lands from the fp32 one)
 
 Every function cites the reference file:line it restates.  Arithmetic is numpy float64 by
 default (float32 for the CPU baseline timing).  How each function is pinned:
@@ -22,6 +24,9 @@ default (float32 for the CPU baseline timing).  How each function is pinned:
                           (video_monarch_attention/vmonarch.py:29-69) with its R-step
                           swapped to the fp32 oracle as in tests/test_vmonarch.py:55-61, plus
                           the m=1 / b=1 / rt=N reductions to exact attention.
+  vmonarch_attention_lowp golden vectors written by the reference's own vmonarch_attention run on
+                          bf16 tensors (CPU) around an exact R-step; with the rounding switched
+                          off it is vmonarch_attention.
   lstep_grad,             central finite differences (random directions, float64) of
   vmonarch_attention_grad lstep / vmonarch_attention with the entropy biases frozen at the
                           base point, as the reference's detach (vmonarch.py:26) makes them;
@@ -29,4 +34,4 @@ default (float32 for the CPU baseline timing).  How each function is pinned:
 """
 from .fea import entropy_attention, entropy_attention_grad, exact_attention  # noqa: F401
 from .vmonarch import (vmonarch_attention, row_block_attention, lstep, lstep_grad,  # noqa: F401
-                       vmonarch_attention_grad)
+                       vmonarch_attention_grad, vmonarch_attention_lowp, round_bf16)

@@ -3,6 +3,10 @@
 Restates /root/reference/video_monarch_attention/vmonarch.py:19-69 with the R-step taken by
 the fp32 oracle exactly as the reference's own test does (tests/test_vmonarch.py:55-61), i.e.
 no bf16 rounding anywhere: this is the fp32 reference the GPU path is judged against.
+
+``vmonarch_attention_lowp`` restates the same glue with the roundings the reference's own bf16 run
+makes (the einsums and products of vmonarch.py:47-67 return bf16 tensors), around an exact R-step:
+it tells how far the reference's bf16 path itself lands from the fp32 reference on given inputs.
 """
 import numpy as np
 
@@ -82,6 +86,60 @@ def vmonarch_attention(q, k, v, num_blocks, block_size, num_iters=2, recompute_t
         rt = recompute_tokens
         z = z.copy()
         z[:, :, :rt] = exact_attention(q[:, :, :rt], k, v, None, dtype)
+    return z
+
+
+def round_bf16(x):
+    """Round to the nearest bf16 value (ties to even), returned as float64: what storing an fp32
+    result in a bfloat16 tensor does."""
+    b = np.ascontiguousarray(np.asarray(x, dtype=np.float32)).view(np.uint32).astype(np.uint64)
+    b = (b + 0x7FFF + ((b >> 16) & 1)) & 0xFFFF0000
+    return b.astype(np.uint32).view(np.float32).astype(np.float64)
+
+
+def vmonarch_attention_lowp(q, k, v, num_blocks, block_size, num_iters=2, recompute_tokens=0,
+                            min_col_mass=0.01, rnd=round_bf16):
+    """vmonarch.py:29-69 as the reference runs it on bf16 tensors: every tensor the glue stores in the
+    input dtype is rounded by ``rnd`` where the reference makes it (einsum / product results rounded once,
+    accumulation in float64 here), the softmaxes and col_mass in float, and the R-step exact (its output o
+    rounded as a bf16 kernel stores it, the entropy kept in float).  Cast points:
+      u = q * scale                          (vmonarch.py:47)  rounded
+      out = R-step(u, k, w)                  (vmonarch.py:50)  o rounded, entropy float
+      kr = out[..., :D] * scale              (vmonarch.py:51)  rounded
+      logits = einsum(q, kr).float()         (vmonarch.py:55)  rounded, then float
+      z = einsum(attn.to(dtype), y)          (vmonarch.py:59)  attn rounded, z rounded
+      u = einsum(attn.to(dtype), q)          (vmonarch.py:62)  attn rounded, u rounded
+      u = u * (scale / col_mass).to(dtype)   (vmonarch.py:63)  factor rounded, product rounded
+      SDPA(q[:, :, :rt], k, v)               (vmonarch.py:67)  exact, rounded
+    """
+    q, k, v = (rnd(t) for t in (q, k, v))
+    B, H, N, D = q.shape
+    if N != num_blocks * block_size:
+        raise AssertionError(f"N={N} != {num_blocks} * {block_size}")
+    scale = D ** -0.5
+    m, b = num_blocks, block_size
+    qg, kg, vg = (t.reshape(B, H, m, b, t.shape[-1]) for t in (q, k, v))
+    u = rnd(qg * scale)
+    z = None
+    for it in range(num_iters):
+        last = it == num_iters - 1
+        w = np.concatenate([kg, vg], -1) if last else kg
+        out, ent = entropy_attention(u, kg, w, 1.0)
+        out = rnd(out)
+        kr = rnd(out[..., :D] * scale)
+        logits = rnd(np.einsum("bhijd,bhkjd->bhjik", qg, kr))
+        attn = _softmax(logits + np.swapaxes(ent, -1, -2)[..., None, :])   # - neg_ent
+        if last:
+            z = rnd(np.einsum("bhjik,bhkjd->bhijd", rnd(attn), out[..., D:]))
+        else:
+            col_mass = np.maximum(np.swapaxes(attn.sum(-2), -1, -2), min_col_mass)
+            u = rnd(np.einsum("bhjik,bhijd->bhkjd", rnd(attn), qg))
+            u = rnd(u * rnd(scale / col_mass)[..., None])
+    z = z.reshape(B, H, N, -1)
+    if recompute_tokens > 0:
+        rt = recompute_tokens
+        z = z.copy()
+        z[:, :, :rt] = rnd(exact_attention(q[:, :, :rt], k, v))
     return z
 
 

@@ -54,6 +54,16 @@ def assert_close_elementwise(x, ref, atol=2e-2, rtol=1e-2):
     np.testing.assert_allclose(np.asarray(x, dtype=np.float64), np.asarray(ref, dtype=np.float64), atol=atol, rtol=rtol)
 
 
+def assert_grad_close(g, ref, ref_tol, name=""):
+    """Gradient parity: the reference metric (tests/test_vmonarch.py:22-24) with the reference's own
+    gradient tolerance `ref_tol` AND the stated bf16 class elementwise, |g - ref| <= 2e-2 + 1e-2 |ref|
+    (the same class as o and e)."""
+    g = np.asarray(g, dtype=np.float64)
+    assert np.isfinite(g).all(), f"non-finite gradient {name}"
+    assert_close_ref(g, ref, ref_tol)
+    assert_close_elementwise(g, ref)
+
+
 def hip_library_loaded():
     import os
     from vmonarch_amd import _lib

@@ -10,8 +10,8 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import (assert_close_elementwise, assert_close_ref, golden_names, hip_library_loaded, load_golden,
-                      randn_lp)
+from conftest import (assert_close_elementwise, assert_close_ref, assert_grad_close, golden_names, hip_library_loaded,
+                      load_golden, randn_lp)
 from oracle import entropy_attention
 
 pytestmark = pytest.mark.gpu
@@ -200,9 +200,7 @@ def _grads(q, k, v, do, de, sm_scale=None):
 
 def _check_grads(grads, refs, tol=3e-2):
     for g, r, name in zip(grads, refs, ("dq", "dk", "dv")):
-        g = g.float().cpu().numpy()
-        assert np.isfinite(g).all(), name
-        assert_close_ref(g, r, tol)
+        assert_grad_close(g.float().cpu().numpy(), r, tol, name)
 
 
 @pytest.mark.parametrize("N", [128, 200, 1024])

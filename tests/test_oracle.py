@@ -5,7 +5,8 @@ transposed operand, a wrong einsum index) fails at least one of them:
   * brute-force pure-Python loops on tiny inputs (independent restatement of the formulas);
   * closed forms of the entropy (uniform -> ln n, two keys -> binary entropy, dominant -> 0);
   * central finite differences for the analytic backward;
-  * golden vectors written by the reference's own code (tests/golden/make_golden.py);
+  * golden vectors written by the reference's own code (tests/golden/make_golden.py), including its
+    bf16 run, which pins every rounding point of the reduced-precision restatement;
   * reductions of VMonarch to exact attention (m=1, b=1, rt=N), permutation equivariance
     within a frame, linearity in v.
 """
@@ -15,8 +16,8 @@ import numpy as np
 import pytest
 
 from conftest import assert_close_ref, golden_names, load_golden
-from oracle import (entropy_attention, entropy_attention_grad, exact_attention, lstep, lstep_grad,
-                    vmonarch_attention, vmonarch_attention_grad)
+from oracle import (entropy_attention, entropy_attention_grad, exact_attention, lstep, lstep_grad, round_bf16,
+                    vmonarch_attention, vmonarch_attention_grad, vmonarch_attention_lowp)
 
 
 def brute_entropy_attention(q, k, v, scale):
@@ -241,3 +242,35 @@ def test_vmonarch_rejects_bad_shape_and_zero_iters():
         vmonarch_attention(q, k, v, 5, 3)
     with pytest.raises(UnboundLocalError):
         vmonarch_attention(q, k, v, 4, 3, 0)
+
+
+def test_round_bf16_is_nearest_even():
+    # 1 + 2^-8 lies halfway between the bf16 neighbours 1 and 1 + 2^-7: the tie goes to the even one (1);
+    # 1 + 3 * 2^-8 is the tie between 1 + 2^-7 and 1 + 2^-6 (even: 1 + 2^-6); past a tie, up
+    x = np.array([1.0, 1 + 2.0 ** -8, 1 + 3 * 2.0 ** -8, 1 + 2.0 ** -8 + 2.0 ** -20, -2.5])
+    np.testing.assert_array_equal(round_bf16(x), [1.0, 1.0, 1 + 2.0 ** -6, 1 + 2.0 ** -7, -2.5])
+
+
+@pytest.mark.parametrize("name", golden_names("lowp_vmonarch_"))
+def test_lowp_oracle_matches_reference_bf16_golden(name):
+    """vmonarch_attention_lowp against the reference's own vmonarch_attention run on bf16 tensors: almost
+    every element bit for bit, the rest within about one bf16 step at |z| ~ 1 (the reference's CPU
+    einsums accumulate in another order, which moves a rounding now and then).  Leaving out any one rounding point makes the
+    3-iteration fixture drop from all-exact to at most ~61% exact."""
+    g = load_golden(name)
+    z_ref = g["z"].astype(np.uint16).astype(np.uint32) << 16
+    z_ref = z_ref.view(np.float32).astype(np.float64)
+    args = [int(g[x]) for x in ("num_blocks", "block_size", "num_iters", "recompute_tokens")]
+    z = vmonarch_attention_lowp(g["q"], g["k"], g["v"], *args)
+    exact = float((z == z_ref).mean())
+    assert exact >= (0.99 if args[2] == 3 else 0.9), exact
+    assert np.abs(z - z_ref).max() <= 1e-2   # about one bf16 step at |z| ~ 1
+    # and the fp32 restatement is visibly elsewhere (the roundings matter on these inputs)
+    assert float((vmonarch_attention(g["q"], g["k"], g["v"], *args) == z_ref).mean()) < 0.05
+
+
+def test_lowp_oracle_without_rounding_is_the_fp32_oracle():
+    rng = np.random.default_rng(5)
+    q, k, v = (rng.normal(size=(1, 2, 4 * 24, 32)) for _ in range(3))
+    z = vmonarch_attention_lowp(q, k, v, 4, 24, 2, 24, rnd=lambda x: np.asarray(x, dtype=np.float64))
+    np.testing.assert_allclose(z, vmonarch_attention(q, k, v, 4, 24, 2, 24), rtol=1e-12, atol=1e-12)

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import assert_close_ref, hip_library_loaded, randn_lp
+from conftest import assert_close_ref, assert_grad_close, hip_library_loaded, randn_lp
 from oracle import lstep_grad, vmonarch_attention_grad
 
 pytestmark = pytest.mark.gpu
@@ -77,7 +77,7 @@ def test_vmonarch_grad_reference_params(m, b, num_iters):
     _, grads = _grads(q, k, v, do, m, b, num_iters, b)
     ref = vmonarch_attention_grad(*(t.float().numpy() for t in (q, k, v)), do.numpy(), m, b, num_iters, b)
     for gd, gr in zip(grads, ref):
-        assert_close_ref(gd.float().cpu().numpy(), gr, 5e-2)
+        assert_grad_close(gd.float().cpu().numpy(), gr, 5e-2)
     assert hip_library_loaded()
 
 
@@ -93,7 +93,7 @@ def test_vmonarch_grad_recompute_lengths(rt):
     _, grads = _grads(q, k, v, do, m, b, 2, rt)
     ref = vmonarch_attention_grad(*(t.float().numpy() for t in (q, k, v)), do.numpy(), m, b, 2, rt)
     for gd, gr in zip(grads, ref):
-        assert_close_ref(gd.float().cpu().numpy(), gr, 5e-2)
+        assert_grad_close(gd.float().cpu().numpy(), gr, 5e-2)
 
 
 def test_vmonarch_grad_d128_cfg3_shape_sample():
@@ -107,7 +107,7 @@ def test_vmonarch_grad_d128_cfg3_shape_sample():
     _, grads = _grads(q, k, v, do, m, b, 2, b)
     ref = vmonarch_attention_grad(*(t.float().numpy() for t in (q, k, v)), do.numpy(), m, b, 2, b)
     for gd, gr in zip(grads, ref):
-        assert_close_ref(gd.float().cpu().numpy(), gr, 5e-2)
+        assert_grad_close(gd.float().cpu().numpy(), gr, 5e-2)
 
 
 def test_vmonarch_grad_forward_matches_inference_path():
@@ -174,4 +174,28 @@ def test_vmonarch_fp16_forward_and_grad():
     ref = vmonarch_attention_grad(*(t.float().numpy() for t in (q, k, v)), do.numpy(), m, b, 2, b)
     for gd, gr in zip(grads, ref):
         assert gd.dtype == torch.float16
-        assert_close_ref(gd.float().cpu().numpy(), gr, 5e-2)
+        assert_grad_close(gd.float().cpu().numpy(), gr, 5e-2)
+
+
+def test_vmonarch_grad_cfg4_north_star_head_sample():
+    """The backward bench.py times: cfg4 (21 frames x 1560 tokens, B=1, H=12, D=128, q,k ~ 0.5 N(0,1),
+    v ~ N(0,1), 2 iterations, rt = 1560) with dz ~ N(0,1) in bf16.  The whole problem runs on the GPU;
+    heads 0 and 11 are checked against the oracle's reverse pass in float32 (heads are independent).
+    These gradients are ~1e-2 in size, so of the two bounds the reference metric binds."""
+    B, H, m, b, D = 1, 12, 21, 1560, 128
+    N = m * b
+    g = torch.Generator().manual_seed(0)
+    q = randn_lp(g, B, H, N, D, scale=0.5)
+    k = randn_lp(g, B, H, N, D, scale=0.5)
+    v = randn_lp(g, B, H, N, D)
+    dz = randn_lp(g, B, H, N, D)
+    print("vmonarch grad cfg4: GPU forward + backward", flush=True)
+    _, grads = _grads(q, k, v, dz.float(), m, b, 2, b)
+    grads = [t.float().cpu().numpy() for t in grads]
+    for h in (0, 11):
+        sl = slice(h, h + 1)
+        print(f"vmonarch grad cfg4: oracle head {h}", flush=True)
+        ref = vmonarch_attention_grad(q[:, sl].float().numpy(), k[:, sl].float().numpy(), v[:, sl].float().numpy(),
+                                      dz[:, sl].float().numpy(), m, b, 2, b, dtype=np.float32)
+        for gd, gr, name in zip(grads, ref, ("dq", "dk", "dv")):
+            assert_grad_close(gd[:, sl], gr, 5e-2, name)

@@ -18,8 +18,9 @@
 //    the current tile;
 //  * when w0 aliases k (the VMonarch R-step values [k | v]) the K tile doubles as W0;
 //  * no rescaling in the loop: the reference point m of p = 2^(s c - m) is the max of the first
-//    32 keys and stays fixed; a row whose sum leaves fp32's safe range sends its workgroup through
-//    an exact two-pass fallback.  The entropy identity e = log2 l - h / l holds for any m;
+//    32 keys and stays fixed; a row whose block sum leaves the safe range of the 16-bit type's P
+//    operand sends its workgroup through an exact two-pass fallback.  The entropy identity
+//    e = log2 l - h / l holds for any m;
 //  * tail keys are masked in-kernel (no padding copies, unlike kernel.py:399-400);
 //  * split-KV (num_splits > 1) writes normalised fp32 partials + lse, merged by fea_combine.
 #include <type_traits>
@@ -124,9 +125,14 @@ struct TileCopy {
   }
 };
 
-// Entropy modes: none; online h = sum p (s c - m) (kernel.py:49-50); or, when the first value
-// block is k itself (the VMonarch R-step), from the P.K accumulator at the end:
-//   e = LSE - sm_scale q . (sum_j p_j k_j) / l   (nats)  -- no per-element work in the loop.
+// Entropy modes: none; online h = sum p (s c - m) in fp32 (kernel.py:49-50), e = log2 l - h / l; or,
+// when the first value block is k itself (the VMonarch R-step), from the P.K accumulator at the end:
+//   e = LSE ln2 - sm_scale q . (sum_j p~_j k_j) / l~   (nats), with l~ = sum_j p~_j
+// -- no per-element product in the loop.  p~ is p rounded to the 16-bit type (the MFMA operand), and
+// this mode sums exactly those rounded weights into l (also used for o and the LSE), so the mean logit
+// is a proper average under one distribution.  Normalising the rounded moment by the fp32 sum instead
+// leaves an error of (mean logit) x (relative rounding of the dominant p), several times the 2e-2
+// tolerance on rows with logits of std 4 to 8.
 enum { kEntNone = 0, kEntOnline = 1, kEntFromPK = 2 };
 
 // Workgroups per CU the register budget is sized for: a 256-wide value tensor (its accumulators alone are
@@ -242,10 +248,12 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
 
   const float c = p.scale_log2;
   // Reference point m of x = s c - m (log2 units): the max of the first 32 keys, then fixed.  p = 2^x
-  // is exact in bf16 / fp32 for any x below ~126, so rows whose logits later rise by up to 64 above
-  // that max need no rescaling at all; a block sum beyond 2^64 flags the row and the workgroup redoes
-  // its tile with the exact row max (two passes) -- only for pathological logit ranges.
-  constexpr float kSumLimit = 1.8446744e19f;   // 2^64
+  // is exact in fp32 for any x below ~126 and its bf16 rounding is finite there, so in bf16 rows whose
+  // logits later rise by up to 64 above that max need no rescaling at all; a lane's block sum beyond
+  // 2^64 flags the row and the workgroup redoes its tile with the exact row max (two passes).  fp16
+  // overflows above 65504 (2^16): there a block sum above 65504 -- which any p above 65504 implies --
+  // takes the same exact path, so P never rounds to inf.
+  constexpr float kSumLimit = F16 ? 65504.f : 1.8446744e19f;   // fp16 max / 2^64
   float m_run[QB], l_run[QB], h_run[QB];
   f32x16 acc[QB][NA];
   bool overflow = false;
@@ -292,7 +300,8 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
 
   // x = s c - m; p = 2^x, rounded and packed as two B operands.  The row sums add the fp32 p, as
   // kernel.py:51 does (and with plain adds: v_dot2c_f32_bf16, which would sum the rounded pairs in
-  // one instruction, measured to stall behind a concurrent MFMA of another wave on the SIMD)
+  // one instruction, measured to stall behind a concurrent MFMA of another wave on the SIMD) -- or,
+  // for the P.K entropy, the rounded p~ (the packed halves widened back: a shift or a mask each).
   auto softmax_block = [&](f32x16 (&x)[QB], V8 (&P)[QB][2], int kofs, int nvalid, auto masked_tag)
       __attribute__((always_inline)) {
     constexpr bool MASKED = decltype(masked_tag)::value;
@@ -307,7 +316,10 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
       for (int r = 0; r < 16; r += 2) {
         const float p0 = fast_exp2(x[j][r]), p1 = fast_exp2(x[j][r + 1]);
         const V2 pk = E::pack2(p0, p1);
-        if (r & 2) ls1 += p0 + p1; else ls0 += p0 + p1;
+        float s2;
+        if constexpr (ENT == kEntFromPK) s2 = (float)pk[0] + (float)pk[1];
+        else s2 = p0 + p1;
+        if (r & 2) ls1 += s2; else ls0 += s2;
         if constexpr (ENT == kEntOnline) {
           if (r & 2) hs1 = fmaf(p1, x[j][r + 1], fmaf(p0, x[j][r], hs1));
           else hs0 = fmaf(p1, x[j][r + 1], fmaf(p0, x[j][r], hs0));
@@ -554,7 +566,7 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
         // h = sum_j p_j x_j with p_j = 2^x_j: entropy (bits) = log2 l - h / l
         ent = (log2l - wave_sum32(h_run[j]) * inv_l) * kLn2;
       } else if constexpr (ENT == kEntFromPK) {
-        // sum_j P_j s_j = q . (sum_j p_j k_j) / l, with q re-read in the accumulator's layout
+        // sum_j P~_j s_j = q . (sum_j p~_j k_j) / l~, with q re-read in the accumulator's layout
         const T* qp = qb + (int64_t)(qvalid[j] ? qr : 0) * q_sn + 4 * hl;
         float dot = 0.f;
 #pragma unroll
