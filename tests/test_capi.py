@@ -175,11 +175,11 @@ def test_fea_bwd_fold_k_needs_values_that_start_with_k(L):
     assert b"FOLD_K" in L.vmo_last_error()
     a.v = _lib.View(4096, 128, 128 * 128, 256)          # k's address with another token stride
     assert L.vmo_fea_bwd(ctypes.byref(a), None) == 1
-    # values k at d = dv = 256: a valid request this build has no fold kernel for (rejected in the
-    # dispatch, after the workspace check: a fake, never dereferenced workspace gets it there)
+    # values k at d = dv = 256: a valid request this build has no fold kernel for, rejected by the host
+    # checks (no workspace is passed, so a call that got past them would still stop at the workspace
+    # check and never launch on these made-up addresses)
     a.d = a.dv = 256
     a.q = a.k = a.v = a.o = a.grad_o = a.grad_q = a.grad_k = _lib.View(4096, 256, 256 * 128, 256)
-    a.workspace, a.workspace_bytes = 1 << 20, L.vmo_fea_bwd_workspace_size(ctypes.byref(a))
     assert L.vmo_fea_bwd(ctypes.byref(a), None) == 2
     assert b"FOLD_K" in L.vmo_last_error()
 
@@ -203,3 +203,4 @@ def test_fea_bwd_sum_needs_a_base_and_no_fp32_bits(L):
     a.grad_v_base = _lib.View()
     assert L.vmo_fea_bwd(ctypes.byref(a), None) == 1
     assert b"SUM" in L.vmo_last_error()
+

@@ -829,6 +829,11 @@ extern "C" int vmo_fea_bwd(const vmo_fea_bwd_args* a, void* stream) {
   if (fold_k && !v0_is_k)
     return set_error(VMO_ERR_INVALID, "fea_bwd: VMO_BWD_FOLD_K needs values that start with k (v is k: same address "
                      "and strides, dv - dv1 = d)");
+  // shapes with a fold kernel (dispatch_bwd): rejected here, before any pointer is looked at further
+  if (fold_k && !(a->dv1 == 0 ? ((a->d == 64 && a->dv == 64) || (a->d == 128 && a->dv == 128))
+                              : ((a->d == 64 && a->dv == 128) || (a->d == 128 && a->dv == 256))))
+    return set_error(VMO_ERR_UNSUPPORTED, "fea_bwd: VMO_BWD_FOLD_K is built for values k with (d, dv) = (64, 64), "
+                     "(128, 128) and values [k | v1] with (64, 128), (128, 256); got d=%d dv=%d", a->d, a->dv);
   if (!(a->sm_scale >= 0.f)) return set_error(VMO_ERR_INVALID, "fea_bwd: sm_scale");
   // the tile copies address up to 7 rows from a lane with a 32-bit byte offset
   const int64_t kMaxRowStride = 1ll << 27;
