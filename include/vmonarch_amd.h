@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define VMO_ABI_VERSION 7
+#define VMO_ABI_VERSION 8
 
 enum {
   VMO_OK = 0,
@@ -218,6 +218,20 @@ size_t vmo_fea_fwd_workspace_size(const vmo_fea_fwd_args* args);
 
 /* FlashEntropyAttention forward; see vmo_fea_fwd_args. */
 int vmo_fea_fwd(const vmo_fea_fwd_args* args, void* stream);
+
+/*
+ * Allocation-free variant of vmo_fea_fwd.  No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments and results as vmo_fea_fwd, except that `workspace` /
+ * `workspace_bytes` are ignored: the split-KV partials go to a library-owned static device array of
+ * VMO_FEA_FWD_SCRATCH_BYTES on each GPU (held until the process ends).  A call whose partials need more
+ * (vmo_fea_fwd_workspace_size() > VMO_FEA_FWD_SCRATCH_BYTES) is rejected with VMO_ERR_WORKSPACE before
+ * any launch; calls with num_splits <= 1 use no scratch.  The call allocates nothing and calls no
+ * allocating routine.  All calls on one GPU share its scratch: calls that overlap in time on one GPU
+ * (different streams without ordering, or several host threads) race; order them on one stream.
+ */
+#define VMO_FEA_FWD_SCRATCH_BYTES (32u << 20)
+int vmo_fea_fwd_noalloc(const vmo_fea_fwd_args* args, void* stream);
 
 /* Bytes of workspace vmo_fea_bwd needs for these arguments. */
 size_t vmo_fea_bwd_workspace_size(const vmo_fea_bwd_args* args);

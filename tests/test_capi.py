@@ -28,7 +28,7 @@ def L():
 def test_header_declares_the_entry_points():
     names = _declared_functions()
     for n in ("vmo_abi_version", "vmo_last_error", "vmo_fea_fwd", "vmo_fea_fwd_workspace_size", "vmo_lstep_fwd",
-              "vmo_fea_bwd", "vmo_fea_bwd_workspace_size", "vmo_lstep_bwd"):
+              "vmo_fea_bwd", "vmo_fea_bwd_workspace_size", "vmo_lstep_bwd", "vmo_fea_fwd_noalloc"):
         assert n in names
 
 
@@ -204,3 +204,14 @@ def test_fea_bwd_sum_needs_a_base_and_no_fp32_bits(L):
     assert L.vmo_fea_bwd(ctypes.byref(a), None) == 1
     assert b"SUM" in L.vmo_last_error()
 
+
+def test_fea_fwd_noalloc_rejects_oversized_splits_without_launching(L):
+    """vmo_fea_fwd_noalloc holds the split-KV partials in a fixed library scratch: a call whose partials
+    would not fit is rejected with VMO_ERR_WORKSPACE before any launch (addresses never dereferenced)."""
+    from vmonarch_amd import _lib
+    a = _fwd_args(nq=4096, nk=65536, num_splits=16, heads=8)
+    need = L.vmo_fea_fwd_workspace_size(ctypes.byref(a))
+    assert need > _lib.FEA_FWD_SCRATCH_BYTES
+    assert L.vmo_fea_fwd_noalloc(ctypes.byref(a), None) == 3
+    assert b"scratch" in L.vmo_last_error()
+    assert L.vmo_fea_fwd_noalloc(None, None) == 1

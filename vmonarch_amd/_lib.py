@@ -12,7 +12,8 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libvmonarch_gfx950.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
+FEA_FWD_SCRATCH_BYTES = 32 << 20   # VMO_FEA_FWD_SCRATCH_BYTES: scratch of vmo_fea_fwd_noalloc per GPU
 DTYPES = {torch.bfloat16: 0, torch.float16: 1}
 
 c_int32, c_int64, c_float, c_void_p, c_size_t = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
@@ -93,6 +94,8 @@ def lib():
         L.vmo_fea_fwd_workspace_size.argtypes = [ctypes.POINTER(FeaFwdArgs)]
         L.vmo_fea_fwd.restype = ctypes.c_int
         L.vmo_fea_fwd.argtypes = [ctypes.POINTER(FeaFwdArgs), c_void_p]
+        L.vmo_fea_fwd_noalloc.restype = ctypes.c_int
+        L.vmo_fea_fwd_noalloc.argtypes = [ctypes.POINTER(FeaFwdArgs), c_void_p]
         L.vmo_lstep_fwd.restype = ctypes.c_int
         L.vmo_lstep_fwd.argtypes = [ctypes.POINTER(LstepArgs), c_void_p]
         L.vmo_lstep_bwd.restype = ctypes.c_int

@@ -23,6 +23,7 @@
 //    e = log2 l - h / l holds for any m;
 //  * tail keys are masked in-kernel (no padding copies, unlike kernel.py:399-400);
 //  * split-KV (num_splits > 1) writes normalised fp32 partials + lse, merged by fea_combine.
+#include <mutex>
 #include <type_traits>
 
 #include "vmo_common.h"
@@ -708,9 +709,11 @@ extern "C" size_t vmo_fea_fwd_workspace_size(const vmo_fea_fwd_args* a) {
   return (size_t)vmo::split_layout(a, &s, &kps);
 }
 
-extern "C" int vmo_fea_fwd(const vmo_fea_fwd_args* a, void* stream) {
-  using namespace vmo;
-  clear_error();
+namespace vmo {
+
+// The forward behind both entry points: `workspace` / `workspace_bytes` hold the split-KV partials (the
+// caller's for vmo_fea_fwd, the library's static scratch for vmo_fea_fwd_noalloc).
+static int fea_fwd_impl(const vmo_fea_fwd_args* a, void* workspace, size_t workspace_bytes, void* stream) {
   if (!a) return set_error(VMO_ERR_INVALID, "fea_fwd: null args");
   if (a->dtype != VMO_DTYPE_BF16 && a->dtype != VMO_DTYPE_F16)
     return set_error(VMO_ERR_INVALID, "fea_fwd: dtype %d", a->dtype);
@@ -734,8 +737,9 @@ extern "C" int vmo_fea_fwd(const vmo_fea_fwd_args* a, void* stream) {
   const int64_t ws = split_layout(a, &splits, &kps);
   const bool ent = a->ent != nullptr;
   if (splits > 1 && ent) return set_error(VMO_ERR_UNSUPPORTED, "fea_fwd: split-KV with entropy output");
-  if (splits > 1 && (a->workspace == nullptr || a->workspace_bytes < (size_t)ws || !aligned16(a->workspace)))
-    return set_error(VMO_ERR_WORKSPACE, "fea_fwd: needs %lld workspace bytes", (long long)ws);
+  if (splits > 1 && (workspace == nullptr || workspace_bytes < (size_t)ws || !aligned16(workspace)))
+    return set_error(VMO_ERR_WORKSPACE, "fea_fwd: needs %lld workspace bytes, has %llu", (long long)ws,
+                     (unsigned long long)(workspace ? workspace_bytes : 0));
   const int64_t q_tiles = (a->nq + 32 * kFwdQB * kFwdWavesSmall - 1) / (32 * kFwdQB * kFwdWavesSmall);
   const int64_t problems = (int64_t)a->batch * a->heads * a->frames;
   const int64_t total = problems * splits * q_tiles;   // the most workgroups any variant launches
@@ -747,8 +751,8 @@ extern "C" int vmo_fea_fwd(const vmo_fea_fwd_args* a, void* stream) {
   p.lse = a->lse; p.ent = a->ent;
   if (splits > 1) {
     const int64_t rows = problems * a->nq;
-    p.part_o = (float*)a->workspace;
-    p.part_lse = (float*)((char*)a->workspace + (int64_t)splits * rows * (a->dw0 + a->dw1) * 4);
+    p.part_o = (float*)workspace;
+    p.part_lse = (float*)((char*)workspace + (int64_t)splits * rows * (a->dw0 + a->dw1) * 4);
   }
   p.q_sb = a->q.stride_b; p.q_sh = a->q.stride_h; p.q_sn = a->q.stride_n;
   p.k_sb = a->k.stride_b; p.k_sh = a->k.stride_h; p.k_sn = a->k.stride_n;
@@ -763,4 +767,52 @@ extern "C" int vmo_fea_fwd(const vmo_fea_fwd_args* a, void* stream) {
   hipStream_t s = (hipStream_t)stream;
   if (a->dtype == VMO_DTYPE_F16) return dispatch_fwd<true>(p, a->d, a->dw0, a->dw1, w0k, ent, splits > 1, s);
   return dispatch_fwd<false>(p, a->d, a->dw0, a->dw1, w0k, ent, splits > 1, s);
+}
+
+// Scratch of the allocation-free entry point: split-KV partials (fp32 o and lse of every split), fully
+// written by the split kernels before the merge reads them, so nothing needs clearing between calls.
+// Each GPU the library runs on holds its own copy, at its own address, until the process ends.
+static __device__ __align__(256) char scratch[VMO_FEA_FWD_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+static void* g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mutex;
+
+// Device address of `scratch` on the current device, looked up once per device (in host code the
+// array's name is only a stand-in for the symbol, not a device address).
+static int scratch_on_current_device(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return set_error(VMO_ERR_LAUNCH, "fea_fwd_noalloc: no current HIP device (or device id >= %d)", kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return set_error(VMO_ERR_LAUNCH, "fea_fwd_noalloc: scratch address on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return VMO_OK;
+}
+
+}  // namespace vmo
+
+extern "C" int vmo_fea_fwd(const vmo_fea_fwd_args* a, void* stream) {
+  vmo::clear_error();
+  return vmo::fea_fwd_impl(a, a ? a->workspace : nullptr, a ? a->workspace_bytes : 0, stream);
+}
+
+extern "C" int vmo_fea_fwd_noalloc(const vmo_fea_fwd_args* a, void* stream) {
+  using namespace vmo;
+  clear_error();
+  if (!a) return set_error(VMO_ERR_INVALID, "fea_fwd_noalloc: null args");
+  if (vmo_fea_fwd_workspace_size(a) > VMO_FEA_FWD_SCRATCH_BYTES)
+    return set_error(VMO_ERR_WORKSPACE, "fea_fwd_noalloc: split-KV partials need %llu bytes, the library scratch holds %llu "
+                     "(use fewer splits)", (unsigned long long)vmo_fea_fwd_workspace_size(a),
+                     (unsigned long long)VMO_FEA_FWD_SCRATCH_BYTES);
+  void* ws = nullptr;
+  const int rc = scratch_on_current_device(&ws);
+  if (rc != VMO_OK) return rc;
+  return fea_fwd_impl(a, ws, VMO_FEA_FWD_SCRATCH_BYTES, stream);
 }
