@@ -94,24 +94,29 @@ def test_fea_fwd_empty_problem_is_a_no_op(L):
 
 
 def test_lstep_rejects_too_many_blocks(L):
+    """m = 200 frames: the one-tile kernels stop at 32 and the general ones need more LDS per grid
+    column than a CU has, so the call is refused on the host (the made-up addresses are never used)."""
     from vmonarch_amd import _lib
     a = _lib.LstepArgs()
-    a.dtype, a.batch, a.heads, a.num_blocks, a.block_size, a.d, a.dv = 0, 1, 1, 33, 4, 128, 128
+    a.dtype, a.batch, a.heads, a.num_blocks, a.block_size, a.d, a.dv = 0, 1, 1, 200, 4, 128, 128
     v = _lib.View(4096, 128, 128, 128)
     a.q = a.out = a.res = v
     a.ent = 4096
     assert L.vmo_lstep_fwd(ctypes.byref(a), None) == 2
+    assert b"LDS" in L.vmo_last_error()
+    a.num_blocks, a.d = 40, 100   # head dim not a multiple of 8
+    assert L.vmo_lstep_fwd(ctypes.byref(a), None) != 0
 
 
 def test_lstep_bwd_rejects_too_many_blocks_and_null_args(L):
     from vmonarch_amd import _lib
     a = _lib.LstepBwdArgs()
-    a.dtype, a.batch, a.heads, a.num_blocks, a.block_size, a.d, a.dv = 0, 1, 1, 33, 4, 128, 128
+    a.dtype, a.batch, a.heads, a.num_blocks, a.block_size, a.d, a.dv = 0, 1, 1, 100, 4, 128, 128
     v = _lib.View(4096, 128, 128, 128)
     a.q = a.out = a.grad_res = a.grad_q = a.grad_out = v
     a.ent = 4096
-    assert L.vmo_lstep_bwd(ctypes.byref(a), None) == 2
-    assert b"num_blocks" in L.vmo_last_error()
+    assert L.vmo_lstep_bwd(ctypes.byref(a), None) == 2   # 100 frames: beyond the LDS of a CU
+    assert b"LDS" in L.vmo_last_error()
     assert L.vmo_lstep_bwd(None, None) != 0
 
 

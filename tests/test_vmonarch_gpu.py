@@ -167,8 +167,8 @@ def test_vmonarch_dit_layout_in_place_and_out():
 
 @pytest.mark.parametrize("m", [32, 33])
 def test_vmonarch_many_frames(m):
-    """m = 32, the widest L-step tile of the fused kernels, and m = 33, which runs the composed path
-    (R-steps in HIP, the L-step as torch ops): both against the oracle."""
+    """m = 32, the widest grid of the one-tile L-step kernels, and m = 33, the first that takes the
+    general L-step kernels: both against the oracle."""
     from vmonarch_amd import vmonarch_attention
     g = torch.Generator().manual_seed(m)
     b = 24

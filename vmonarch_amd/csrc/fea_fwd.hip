@@ -181,25 +181,29 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
   // scalar registers, so the per-tile address arithmetic stays scalar.  The variants with eight
   // accumulator blocks are short of registers: for them the extra scalar values cost more (their
   // spills land in the key loop) than the few vector instructions they save.
-  auto uni = [](int v) __attribute__((always_inline)) { return NA >= 8 ? v : __builtin_amdgcn_readfirstlane(v); };
-  const int qt = uni(L % p.q_tiles);
-  const int rest = L / p.q_tiles;
-  const int split = uni(rest % p.splits);
-  const int prob = uni(rest / p.splits);
-  const int f = uni(prob % p.frames);
-  const int bh = prob / p.frames;
-  const int hh = uni(bh % p.heads);
-  const int bb = uni(bh / p.heads);
+  struct Loc { int qt, split, prob, f, hh, bb; };
+  auto locate = [&](int lx, auto scalar_tag) __attribute__((always_inline)) {
+    constexpr bool S = decltype(scalar_tag)::value;
+    auto u = [](int v) __attribute__((always_inline)) { return S ? __builtin_amdgcn_readfirstlane(v) : v; };
+    Loc r;
+    r.qt = u(lx % p.q_tiles);
+    const int rest = lx / p.q_tiles;
+    r.split = u(rest % p.splits);
+    r.prob = u(rest / p.splits);
+    r.f = u(r.prob % p.frames);
+    const int bh = r.prob / p.frames;
+    r.hh = u(bh % p.heads);
+    r.bb = u(bh / p.heads);
+    return r;
+  };
+  const Loc loc = locate(L, std::integral_constant<bool, (NA < 8)>{});
+  const int qt = loc.qt, split = loc.split, f = loc.f, hh = loc.hh, bb = loc.bb;
 
   const T* qb = (const T*)p.q + bb * p.q_sb + hh * p.q_sh + (int64_t)f * p.nq * p.q_sn;
   const T* kb = (const T*)p.k + bb * p.k_sb + hh * p.k_sh + (int64_t)f * p.nk * p.k_sn;
   const T* w0b = (const T*)p.w0 + bb * p.w0_sb + hh * p.w0_sh + (int64_t)f * p.nk * p.w0_sn;
   const T* w1b = DW1 ? (const T*)p.w1 + bb * p.w1_sb + hh * p.w1_sh + (int64_t)f * p.nk * p.w1_sn : nullptr;
-  // epilogue bases, formed here so that the raw strides are dead during the key loop
-  T* const ob = (T*)p.o + bb * p.o_sb + hh * p.o_sh + (int64_t)f * p.nq * p.o_sn;
-  const int64_t o_sn = p.o_sn, q_sn = p.q_sn;
-  const int64_t st0 = bb * p.st_sb + hh * p.st_sh + (int64_t)f * p.nq;
-  const int64_t part0 = (int64_t)(split * p.problems + prob) * p.nq;
+  const int64_t q_sn = p.q_sn;
 
   const int kbeg = split * p.keys_per_split;
   const int kend = min(p.nk, kbeg + p.keys_per_split);
@@ -548,6 +552,19 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
   VMO_LDS float* patch = (VMO_LDS float*)(smem + wave * kEpiPatchBytes);
   if (!wave_live) return;
 
+  // The epilogue derives its indices and row bases again, from an opaque copy of the block's logical
+  // index (scalar registers are free by now): kept from the prologue, the 64-bit bases sat in vector
+  // registers across the whole key loop, and the tightest variants spilled them to scratch.
+  int l_epi = __builtin_amdgcn_readfirstlane(L);
+  asm volatile("" : "+s"(l_epi));
+  const Loc le = locate(l_epi, std::true_type{});
+  T* const ob = (T*)p.o + le.bb * p.o_sb + le.hh * p.o_sh + (int64_t)le.f * p.nq * p.o_sn;
+  const T* const qb_e = (const T*)p.q + le.bb * p.q_sb + le.hh * p.q_sh + (int64_t)le.f * p.nq * p.q_sn;
+  const int64_t o_sn = p.o_sn, q_sn_e = p.q_sn;
+  const int64_t st0 = le.bb * p.st_sb + le.hh * p.st_sh + (int64_t)le.f * p.nq;
+  const int64_t part0 = (int64_t)(le.split * p.problems + le.prob) * p.nq;
+  const int q0_e = le.qt * kBM + wave * 32 * QB;
+
 #pragma unroll
   for (int j = 0; j < QB; ++j) {
     // ---- finalise: combine the two half-waves' partial sums
@@ -555,12 +572,13 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
     const float inv_l = 1.0f / l_tot;
     const float log2l = fast_log2(l_tot);
     const float lse = m_run[j] + log2l;
-    const int qr = qrow[j];
-    const int qb0 = q0 + 32 * j, nrows = min(32, p.nq - qb0);
+    const int qb0 = q0_e + 32 * j, nrows = min(32, p.nq - qb0);
+    const int qr = qb0 + l32;
+    const bool qv = qr < p.nq;
     if constexpr (SPLIT) {
       store_acc_rows<F16>(patch, acc[j], NA, inv_l, kGradStoreF32, (char*)(p.part_o + (part0 + qb0) * (int64_t)(DW0 + DW1)),
                           (int64_t)(DW0 + DW1) * 4, nrows, lane);
-      if (qvalid[j] && hl == 0) p.part_lse[part0 + qr] = lse;
+      if (qv && hl == 0) p.part_lse[part0 + qr] = lse;
     } else {
       float ent = 0.f;
       if constexpr (ENT == kEntOnline) {
@@ -568,7 +586,7 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
         ent = (log2l - wave_sum32(h_run[j]) * inv_l) * kLn2;
       } else if constexpr (ENT == kEntFromPK) {
         // sum_j P~_j s_j = q . (sum_j p~_j k_j) / l~, with q re-read in the accumulator's layout
-        const T* qp = qb + (int64_t)(qvalid[j] ? qr : 0) * q_sn + 4 * hl;
+        const T* qp = qb_e + (int64_t)(qv ? qr : 0) * q_sn_e + 4 * hl;
         float dot = 0.f;
 #pragma unroll
         for (int a = 0; a < NA0; ++a)
@@ -582,7 +600,7 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
         ent = lse * kLn2 - (c * kLn2) * dot * inv_l;
       }
       store_acc_rows<F16>(patch, acc[j], NA, inv_l, kGradStore, (char*)(ob + (int64_t)qb0 * o_sn), o_sn * 2, nrows, lane);
-      if (qvalid[j]) {
+      if (qv) {
         const int64_t si = st0 + qr;
         if (ENT != kEntNone && hl == 0 && p.ent) p.ent[si] = ent;
         if (hl == 0 && p.lse) p.lse[si] = lse;

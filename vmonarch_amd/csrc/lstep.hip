@@ -38,6 +38,7 @@ struct LParams {
   int64_t res_sb, res_sh, res_sn;
   int heads, m, bs, skip;
   int cols_total;
+  int d, dv;                // head dims (the one-tile kernels take them as template parameters)
   float logit_scale_log2;   // scale * log2(e)
   float scale;
   float min_col_mass;
@@ -290,6 +291,7 @@ struct LBParams {
   int64_t do_sb, do_sh, do_sn;
   int heads, m, bs, skip;
   int cols_total;
+  int d, dv;
   float logit_scale_log2;
   float scale;
   float min_col_mass;
@@ -605,6 +607,343 @@ static int dispatch_lstep_bwd(const LBParams& p, int d, int dv, bool last, hipSt
   return set_error(VMO_ERR_UNSUPPORTED, "lstep_bwd: no kernel for d=%d dv=%d last=%d", d, dv, (int)last);
 }
 
+// Head dims the one-tile kernels are built for (with m <= 32).
+static bool one_tile_built(int d, int dv, bool last) {
+  return (d == 64 || d == 128) && (!last || dv == 64 || dv == 128);
+}
+
+// ---------------------------------------------------------------------------------------------
+// General L-step, forward and backward, for the grids the one-tile kernels above do not cover:
+// more than 32 frames (m > 32: HunyuanVideo's 129 frames give 33 latent frames) or head dims other
+// than 64 / 128.  Same mathematics and the same rounding points as the one-tile kernels (logits in
+// fp32 from the 16-bit q and kr, attn rounded to the 16-bit type where it multiplies q or y, the
+// column mass from the fp32 attn; u / z / d out rounded once when stored), but one 256-thread
+// workgroup per grid column with the column's rows staged in LDS and the m x m products on the
+// vector unit in fp32: a column is small (m x D values), so the L2-resident rows are read once and
+// every product is an LDS sweep.  LDS rows are padded by 16 bytes, so that the 16 rows a wave reads
+// at one feature offset fall on 16 distinct bank groups.  Supported: any m whose tiles fit the CU's
+// 160 KB (m <= 64 for every head dim up to 128), d and dv multiples of 8 up to 256.
+constexpr int kLWThreads = 256;
+
+struct LWLayout {   // byte offsets of the per-column LDS arrays
+  int ldq, ldy, ldm;                 // row strides: 16-bit rows (elements), fp32 m x m matrices (floats)
+  int q, k, g, y, a, b, vec, total;  // q rows, kr rows, upstream gradient rows, y rows, two m x m, vectors
+};
+
+__host__ __device__ inline LWLayout lw_layout(int m, int d, int dv, bool last, bool bwd) {
+  LWLayout L;
+  L.ldq = d + 8;
+  L.ldy = dv + 8;
+  L.ldm = m + 1;
+  int off = 0;
+  auto take = [&](int bytes) { const int o = off; off += (bytes + 15) / 16 * 16; return o; };
+  L.q = take(m * L.ldq * 2);
+  L.k = take(m * L.ldq * 2);
+  L.g = bwd ? take(m * (last ? L.ldy : L.ldq) * 2) : 0;
+  L.y = last ? take(m * L.ldy * 2) : 0;
+  L.a = take(m * L.ldm * 4);
+  L.b = bwd ? take(m * L.ldm * 4) : 0;
+  L.vec = take(4 * m * 4);
+  L.total = off;
+  return L;
+}
+
+// rows r < m of F 16-bit values (F % 8 == 0), global row stride rs (elements) -> LDS stride ld
+template <class T>
+__device__ __forceinline__ void lw_stage(VMO_LDS T* dst, int ld, const T* src, int64_t rs, int m, int F, int tid) {
+  const int ch = F / 8;
+  for (int idx = tid; idx < m * ch; idx += kLWThreads) {
+    const int r = idx / ch, c = idx % ch;
+    *(VMO_LDS i32x4*)(dst + r * ld + 8 * c) = *(const i32x4*)(src + r * rs + 8 * c);
+  }
+}
+
+template <class V8>
+__device__ __forceinline__ float lw_dot8(const V8& a, const V8& b, float acc) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc = fmaf((float)a[e], (float)b[e], acc);
+  return acc;
+}
+
+// out[r * ldo + s] = sum_f A[r][f] B[s][f] over F features, r, s < m (rows r: 64 per pass, 4 threads
+// each; a thread takes s = s0 + 4 u, u < 16: its A row chunk is read once per 16 products)
+template <bool F16>
+__device__ __forceinline__ void lw_dots(VMO_LDS float* out, int ldo, const VMO_LDS typename Elem<F16>::T* A, int lda,
+                                        const VMO_LDS typename Elem<F16>::T* B, int ldb, int m, int F, int tid) {
+  using V8 = typename Elem<F16>::V8;
+  for (int r0 = 0; r0 < m; r0 += 64) {
+    const int r = r0 + (tid >> 2);
+    if (r >= m) continue;
+    for (int s0 = tid & 3; s0 < m; s0 += 64) {
+      float acc[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) acc[u] = 0.f;
+      for (int f = 0; f < F; f += 8) {
+        const V8 a = *(const VMO_LDS V8*)(A + r * lda + f);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          const int s = min(s0 + 4 * u, m - 1);
+          const V8 b = *(const VMO_LDS V8*)(B + s * ldb + f);
+          acc[u] = lw_dot8(a, b, acc[u]);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        if (s0 + 4 * u < m) out[r * ldo + s0 + 4 * u] = acc[u];
+    }
+  }
+}
+
+// For every output row r < m and 8-column group fb < F / 8 (4 threads per row, 64 rows per pass):
+// acc[e] = sum_s w(r, s) X[s][8 fb + e] (+ the same for a second weight / row set), then emit(r, fb, acc).
+template <bool F16, class W, class Emit>
+__device__ __forceinline__ void lw_mix(W w, const VMO_LDS typename Elem<F16>::T* X, int ldx, int m, int F, int tid,
+                                       Emit emit) {
+  using V8 = typename Elem<F16>::V8;
+  for (int r0 = 0; r0 < m; r0 += 64) {
+    const int r = r0 + (tid >> 2);
+    if (r >= m) continue;
+    for (int fb = tid & 3; fb < F / 8; fb += 4) {
+      float acc[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+      for (int s = 0; s < m; ++s) {
+        const float ws = w(r, s);
+        const V8 x = *(const VMO_LDS V8*)(X + s * ldx + 8 * fb);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = fmaf(ws, (float)x[e], acc[e]);
+      }
+      emit(r, fb, acc);
+    }
+  }
+}
+
+template <bool F16>
+__device__ __forceinline__ void lw_store8(typename Elem<F16>::T* dst, const float (&x)[8], float f) {
+  using V8 = typename Elem<F16>::V8;
+  V8 v;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = to_elem<typename Elem<F16>::T>(x[e] * f);
+  *(V8*)dst = v;
+}
+
+// attn[i][k] = softmax_k(logit[i][k] * scale * log2 e + ent[k] log2 e) in place, one thread per row i
+__device__ __forceinline__ void lw_softmax_rows(VMO_LDS float* A, int ldm, const VMO_LDS float* ev, int m, float c,
+                                                int tid) {
+  for (int i = tid; i < m; i += kLWThreads) {
+    VMO_LDS float* row = A + i * ldm;
+    float mx = -3.0e38f;
+    for (int k = 0; k < m; ++k) {
+      const float x = fmaf(row[k], c, ev[k]);
+      row[k] = x;
+      mx = fmaxf(mx, x);
+    }
+    float sum = 0.f;
+    for (int k = 0; k < m; ++k) {
+      const float e = fast_exp2(row[k] - mx);
+      row[k] = e;
+      sum += e;
+    }
+    const float inv = 1.0f / sum;
+    for (int k = 0; k < m; ++k) row[k] *= inv;
+  }
+}
+
+template <bool F16, bool LAST>
+__global__ __launch_bounds__(kLWThreads) void lstep_wide_kernel(LParams p) {
+  using T = typename Elem<F16>::T;
+  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  VMO_LDS char* sm = (VMO_LDS char*)smem_raw;
+  const int m = p.m, D = p.d, DV = p.dv, tid = threadIdx.x;
+  const LWLayout L = lw_layout(m, D, DV, LAST, false);
+  VMO_LDS T* qs = (VMO_LDS T*)(sm + L.q);
+  VMO_LDS T* ks = (VMO_LDS T*)(sm + L.k);
+  VMO_LDS T* ys = (VMO_LDS T*)(sm + L.y);
+  VMO_LDS float* A = (VMO_LDS float*)(sm + L.a);
+  VMO_LDS float* ev = (VMO_LDS float*)(sm + L.vec);
+  VMO_LDS float* fk = ev + m;
+
+  const int col = blockIdx.x, bh = col / p.bs, j = col % p.bs, hh = bh % p.heads, bb = bh / p.heads;
+  const T* qcol = (const T*)p.q + bb * p.q_sb + hh * p.q_sh + (int64_t)j * p.q_sn;
+  const T* ocol = (const T*)p.out + bb * p.out_sb + hh * p.out_sh + (int64_t)j * p.out_sn;
+  lw_stage<T>(qs, L.ldq, qcol, (int64_t)p.bs * p.q_sn, m, D, tid);
+  lw_stage<T>(ks, L.ldq, ocol, (int64_t)p.bs * p.out_sn, m, D, tid);
+  if constexpr (LAST) lw_stage<T>(ys, L.ldy, ocol + D, (int64_t)p.bs * p.out_sn, m, DV, tid);
+  const float* ep = p.ent + bb * p.ent_sb + hh * p.ent_sh + j;
+  for (int k = tid; k < m; k += kLWThreads) ev[k] = ep[(int64_t)k * p.bs] * kLog2e;
+  __syncthreads();
+  lw_dots<F16>(A, L.ldm, qs, L.ldq, ks, L.ldq, m, D, tid);   // q_i . kr_k
+  __syncthreads();
+  lw_softmax_rows(A, L.ldm, ev, m, p.logit_scale_log2, tid);
+  __syncthreads();
+  T* rcol = (T*)p.res + bb * p.res_sb + hh * p.res_sh + (int64_t)j * p.res_sn;
+  const int64_t rrs = (int64_t)p.bs * p.res_sn;
+  auto rounded = [](float x) { return (float)to_elem<T>(x); };   // attn as the 16-bit operand
+  if constexpr (LAST) {
+    // z_i = sum_k attn[i][k] y_k, rows whose token the recompute owns left alone
+    lw_mix<F16>([&](int i, int k) { return rounded(A[i * L.ldm + k]); }, ys, L.ldy, m, DV, tid,
+                [&](int i, int fb, const float (&acc)[8]) {
+                  if ((int64_t)i * p.bs + j >= p.skip) lw_store8<F16>(rcol + i * rrs + 8 * fb, acc, 1.f);
+                });
+  } else {
+    // u_k = scale / max(sum_i attn[i][k], min_col_mass) * sum_i attn[i][k] q_i
+    for (int k = tid; k < m; k += kLWThreads) {
+      float c = 0.f;
+      for (int i = 0; i < m; ++i) c += A[i * L.ldm + k];
+      fk[k] = p.scale / fmaxf(c, p.min_col_mass);
+    }
+    __syncthreads();
+    lw_mix<F16>([&](int k, int i) { return rounded(A[i * L.ldm + k]); }, qs, L.ldq, m, D, tid,
+                [&](int k, int fb, const float (&acc)[8]) { lw_store8<F16>(rcol + k * rrs + 8 * fb, acc, fk[k]); });
+  }
+}
+
+// Backward of the general L-step (same mathematics as lstep_bwd_kernel, fp32 products).  With
+// G[k][i] = g_k . q_i (non-last), the column-mass terms need no v_k = sum_i a[i,k] q_i of their own:
+// g_k . v_k = sum_i a[i,k] G[k][i] and dv_k . q_i = f_k G[k][i].
+template <bool F16, bool LAST>
+__global__ __launch_bounds__(kLWThreads) void lstep_wide_bwd_kernel(LBParams p) {
+  using T = typename Elem<F16>::T;
+  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  VMO_LDS char* sm = (VMO_LDS char*)smem_raw;
+  const int m = p.m, D = p.d, DV = p.dv, tid = threadIdx.x;
+  const LWLayout L = lw_layout(m, D, DV, LAST, true);
+  VMO_LDS T* qs = (VMO_LDS T*)(sm + L.q);
+  VMO_LDS T* ks = (VMO_LDS T*)(sm + L.k);
+  VMO_LDS T* gs = (VMO_LDS T*)(sm + L.g);
+  VMO_LDS T* ys = (VMO_LDS T*)(sm + L.y);
+  VMO_LDS float* A = (VMO_LDS float*)(sm + L.a);   // attn[i][k]
+  VMO_LDS float* Bm = (VMO_LDS float*)(sm + L.b);  // d attn[i][k], then dL[i][k]
+  VMO_LDS float* ev = (VMO_LDS float*)(sm + L.vec);
+  VMO_LDS float* fk = ev + m;    // f_k = scale / cm_k (non-last)
+  VMO_LDS float* dck = fk + m;   // dc_k (non-last)
+  VMO_LDS float* rsi = dck + m;  // sum_k a[i,k] da[i,k]
+  const int gw = LAST ? DV : D, ldg = LAST ? L.ldy : L.ldq;
+
+  const int col = blockIdx.x, bh = col / p.bs, j = col % p.bs, hh = bh % p.heads, bb = bh / p.heads;
+  const T* qcol = (const T*)p.q + bb * p.q_sb + hh * p.q_sh + (int64_t)j * p.q_sn;
+  const T* ocol = (const T*)p.out + bb * p.out_sb + hh * p.out_sh + (int64_t)j * p.out_sn;
+  const T* gcol = (const T*)p.g + bb * p.g_sb + hh * p.g_sh + (int64_t)j * p.g_sn;
+  lw_stage<T>(qs, L.ldq, qcol, (int64_t)p.bs * p.q_sn, m, D, tid);
+  lw_stage<T>(ks, L.ldq, ocol, (int64_t)p.bs * p.out_sn, m, D, tid);
+  lw_stage<T>(gs, ldg, gcol, (int64_t)p.bs * p.g_sn, m, gw, tid);
+  if constexpr (LAST) lw_stage<T>(ys, L.ldy, ocol + D, (int64_t)p.bs * p.out_sn, m, DV, tid);
+  const float* ep = p.ent + bb * p.ent_sb + hh * p.ent_sh + j;
+  for (int k = tid; k < m; k += kLWThreads) ev[k] = ep[(int64_t)k * p.bs] * kLog2e;
+  __syncthreads();
+  if constexpr (LAST) {   // z rows of tokens < skip are the recompute's: no gradient reaches the L-path
+    for (int idx = tid; idx < m * (DV / 8); idx += kLWThreads) {
+      const int r = idx / (DV / 8);
+      if ((int64_t)r * p.bs + j < p.skip) *(VMO_LDS i32x4*)(gs + r * ldg + 8 * (idx % (DV / 8))) = i32x4{0, 0, 0, 0};
+    }
+    __syncthreads();
+  }
+  lw_dots<F16>(A, L.ldm, qs, L.ldq, ks, L.ldq, m, D, tid);
+  if constexpr (LAST)
+    lw_dots<F16>(Bm, L.ldm, gs, ldg, ys, L.ldy, m, DV, tid);   // d attn[i][k] = g_i . y_k
+  else
+    lw_dots<F16>(Bm, L.ldm, gs, ldg, qs, L.ldq, m, D, tid);    // G[k][i] = g_k . q_i (rows k)
+  __syncthreads();
+  lw_softmax_rows(A, L.ldm, ev, m, p.logit_scale_log2, tid);
+  __syncthreads();
+  T* dcol = (T*)p.dout + bb * p.do_sb + hh * p.do_sh + (int64_t)j * p.do_sn;
+  const int64_t drs = (int64_t)p.bs * p.do_sn;
+  if constexpr (LAST) {
+    // dy_k = sum_i a[i,k] g_i -> d out[k, D:]
+    lw_mix<F16>([&](int k, int i) { return A[i * L.ldm + k]; }, gs, ldg, m, DV, tid,
+                [&](int k, int fb, const float (&acc)[8]) { lw_store8<F16>(dcol + k * drs + D + 8 * fb, acc, 1.f); });
+  } else {
+    for (int k = tid; k < m; k += kLWThreads) {
+      float c = 0.f, df = 0.f;
+      for (int i = 0; i < m; ++i) {
+        const float a = A[i * L.ldm + k];
+        c += a;
+        df = fmaf(a, Bm[k * L.ldm + i], df);   // g_k . v_k
+      }
+      const float cm = fmaxf(c, p.min_col_mass), f = p.scale / cm;
+      fk[k] = f;
+      dck[k] = c >= p.min_col_mass ? -df * f / cm : 0.f;
+    }
+    __syncthreads();
+  }
+  // softmax backward, row i: rs_i = sum_k a[i,k] da[i,k]; dL[i,k] = scale a[i,k] (da[i,k] - rs_i)
+  // (non-last: da[i,k] = f_k G[k][i] + dc_k, read from the rows-k matrix)
+  auto da_of = [&](int i, int k) {
+    return LAST ? Bm[i * L.ldm + k] : fmaf(fk[k], Bm[k * L.ldm + i], dck[k]);
+  };
+  for (int i = tid; i < m; i += kLWThreads) {
+    float rs = 0.f;
+    for (int k = 0; k < m; ++k) rs = fmaf(A[i * L.ldm + k], da_of(i, k), rs);
+    rsi[i] = rs;
+  }
+  __syncthreads();
+  // dL in place of da: LAST rows i are each written by their own thread after their reads; the
+  // non-last matrix is indexed [k][i], so every thread computes its dL row into registers first
+  if constexpr (LAST) {
+    for (int i = tid; i < m; i += kLWThreads)
+      for (int k = 0; k < m; ++k) Bm[i * L.ldm + k] = p.scale * A[i * L.ldm + k] * (Bm[i * L.ldm + k] - rsi[i]);
+    __syncthreads();
+  } else {
+    // dL[i][k] overwrites G[k][i]: each (k, i) entry is read and written by the same thread only
+    for (int idx = tid; idx < m * m; idx += kLWThreads) {
+      const int k = idx / m, i = idx % m;
+      const float g = Bm[k * L.ldm + i];
+      Bm[k * L.ldm + i] = p.scale * A[i * L.ldm + k] * (fmaf(fk[k], g, dck[k]) - rsi[i]);
+    }
+    __syncthreads();
+  }
+  // dL[i][k] accessor over the layout in use
+  auto dl_of = [&](int i, int k) { return LAST ? Bm[i * L.ldm + k] : Bm[k * L.ldm + i]; };
+  // dq_i (+)= sum_k dL[i,k] kr_k (+ sum_k a[i,k] f_k g_k, non-last)
+  float* dqcol = p.dq + bb * p.dq_sb + hh * p.dq_sh + (int64_t)j * p.dq_sn;
+  const int64_t dqrs = (int64_t)p.bs * p.dq_sn;
+  lw_mix<F16>(dl_of, ks, L.ldq, m, D, tid, [&](int i, int fb, const float (&acc)[8]) {
+    float tot[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) tot[e] = acc[e];
+    if constexpr (!LAST) {
+      using V8 = typename Elem<F16>::V8;
+      for (int k = 0; k < m; ++k) {
+        const float w = A[i * L.ldm + k] * fk[k];
+        const V8 x = *(const VMO_LDS V8*)(gs + k * ldg + 8 * fb);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) tot[e] = fmaf(w, (float)x[e], tot[e]);
+      }
+    }
+    f32x4* dst = (f32x4*)(dqcol + i * dqrs + 8 * fb);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const f32x4 v = f32x4{tot[4 * h], tot[4 * h + 1], tot[4 * h + 2], tot[4 * h + 3]};
+      dst[h] = p.dq_overwrite ? v : dst[h] + v;
+    }
+  });
+  // d kr_k = sum_i dL[i,k] q_i -> d out[k, :D]
+  lw_mix<F16>([&](int k, int i) { return dl_of(i, k); }, qs, L.ldq, m, D, tid,
+              [&](int k, int fb, const float (&acc)[8]) { lw_store8<F16>(dcol + k * drs + 8 * fb, acc, 1.f); });
+}
+
+constexpr int kLWMaxLds = 160 * 1024;
+
+template <class P>
+static int lw_launch(void (*kern)(P), int lds, int cols, hipStream_t s, const char* what, const P& params) {
+  if (lds > 65536 && hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
+    return set_error(VMO_ERR_LAUNCH, "%s: cannot raise the LDS limit to %d bytes", what, lds);
+  hipLaunchKernelGGL(kern, dim3(cols), dim3(kLWThreads), lds, s, params);
+  return launch_status(what);
+}
+
+// The general kernels take any m whose per-column tiles fit the LDS and head dims that are multiples of 8
+// up to 256; VMO_OK when they can run it, else the error to report.
+static int lw_check(int m, int d, int dv, bool last, bool bwd, const char* what) {
+  if (d % 8 != 0 || d > 256 || (last && (dv % 8 != 0 || dv > 256 || dv <= 0)))
+    return set_error(VMO_ERR_UNSUPPORTED, "%s: head dims must be multiples of 8 up to 256 (d=%d dv=%d)", what, d, dv);
+  const int lds = lw_layout(m, d, dv, last, bwd).total;
+  if (lds > kLWMaxLds)
+    return set_error(VMO_ERR_UNSUPPORTED, "%s: %d frames with d=%d dv=%d need %d bytes of LDS per grid column (max %d)",
+                     what, m, d, dv, lds, kLWMaxLds);
+  return VMO_OK;
+}
+
 }  // namespace vmo
 
 extern "C" int vmo_lstep_fwd(const vmo_lstep_args* a, void* stream) {
@@ -615,10 +954,14 @@ extern "C" int vmo_lstep_fwd(const vmo_lstep_args* a, void* stream) {
   if (a->batch < 0 || a->heads < 0 || a->num_blocks < 1 || a->block_size < 1)
     return set_error(VMO_ERR_INVALID, "lstep: bad sizes");
   if ((int64_t)a->batch * a->heads == 0) return VMO_OK;
-  if (a->num_blocks > 32) return set_error(VMO_ERR_UNSUPPORTED, "lstep: num_blocks %d > 32", a->num_blocks);
   if (!view_ok(a->q) || !view_ok(a->out) || !view_ok(a->res) || a->ent == nullptr)
     return set_error(VMO_ERR_INVALID, "lstep: tensors need 16-byte aligned rows");
-  if ((a->d % 8) != 0) return set_error(VMO_ERR_INVALID, "lstep: d");
+  if (a->d <= 0 || (a->d % 8) != 0) return set_error(VMO_ERR_INVALID, "lstep: d");
+  const bool one_tile = a->num_blocks <= 32 && one_tile_built(a->d, a->dv, a->last != 0);
+  if (!one_tile) {
+    const int rc = lw_check(a->num_blocks, a->d, a->dv, a->last != 0, false, "lstep");
+    if (rc != VMO_OK) return rc;
+  }
   const int64_t cols = (int64_t)a->batch * a->heads * a->block_size;
   if (cols > (1ll << 30) || (int64_t)a->num_blocks * a->block_size > (1ll << 30))
     return set_error(VMO_ERR_UNSUPPORTED, "lstep: problem too large");
@@ -630,10 +973,20 @@ extern "C" int vmo_lstep_fwd(const vmo_lstep_args* a, void* stream) {
   p.res_sb = a->res.stride_b; p.res_sh = a->res.stride_h; p.res_sn = a->res.stride_n;
   p.heads = a->heads; p.m = a->num_blocks; p.bs = a->block_size; p.skip = a->last ? a->skip_tokens : 0;
   p.cols_total = (int)cols;
+  p.d = a->d;
+  p.dv = a->last ? a->dv : 0;
   p.logit_scale_log2 = a->scale * kLog2e;
   p.scale = a->scale;
   p.min_col_mass = a->min_col_mass;
   hipStream_t s = (hipStream_t)stream;
+  if (!one_tile) {
+    const int lds = lw_layout(p.m, p.d, p.dv, a->last != 0, false).total;
+    if (a->dtype == VMO_DTYPE_F16)
+      return a->last ? lw_launch(lstep_wide_kernel<true, true>, lds, p.cols_total, s, "lstep_wide", p)
+                     : lw_launch(lstep_wide_kernel<true, false>, lds, p.cols_total, s, "lstep_wide", p);
+    return a->last ? lw_launch(lstep_wide_kernel<false, true>, lds, p.cols_total, s, "lstep_wide", p)
+                   : lw_launch(lstep_wide_kernel<false, false>, lds, p.cols_total, s, "lstep_wide", p);
+  }
   if (a->dtype == VMO_DTYPE_F16) return dispatch_lstep<true>(p, a->d, a->dv, a->last != 0, s);
   return dispatch_lstep<false>(p, a->d, a->dv, a->last != 0, s);
 }
@@ -647,7 +1000,12 @@ extern "C" int vmo_lstep_bwd(const vmo_lstep_bwd_args* a, void* stream) {
   if (a->batch < 0 || a->heads < 0 || a->num_blocks < 1 || a->block_size < 1)
     return set_error(VMO_ERR_INVALID, "lstep_bwd: bad sizes");
   if ((int64_t)a->batch * a->heads == 0) return VMO_OK;
-  if (a->num_blocks > 32) return set_error(VMO_ERR_UNSUPPORTED, "lstep_bwd: num_blocks %d > 32", a->num_blocks);
+  if (a->d <= 0 || (a->d % 8) != 0) return set_error(VMO_ERR_INVALID, "lstep_bwd: d");
+  const bool one_tile = a->num_blocks <= 32 && one_tile_built(a->d, a->dv, a->last != 0);
+  if (!one_tile) {
+    const int rc = lw_check(a->num_blocks, a->d, a->dv, a->last != 0, true, "lstep_bwd");
+    if (rc != VMO_OK) return rc;
+  }
   if (!view_ok(a->q) || !view_ok(a->out) || !view_ok(a->grad_res) || !view_ok(a->grad_out) || a->ent == nullptr ||
       a->grad_q.data == nullptr || ((uintptr_t)a->grad_q.data & 15) != 0 || (a->grad_q.stride_n & 3) != 0 ||
       (a->grad_q.stride_h & 3) != 0 || (a->grad_q.stride_b & 3) != 0)
@@ -668,10 +1026,20 @@ extern "C" int vmo_lstep_bwd(const vmo_lstep_bwd_args* a, void* stream) {
   p.do_sb = a->grad_out.stride_b; p.do_sh = a->grad_out.stride_h; p.do_sn = a->grad_out.stride_n;
   p.heads = a->heads; p.m = a->num_blocks; p.bs = a->block_size; p.skip = a->last ? a->skip_tokens : 0;
   p.cols_total = (int)cols;
+  p.d = a->d;
+  p.dv = a->last ? a->dv : 0;
   p.logit_scale_log2 = a->scale * kLog2e;
   p.scale = a->scale;
   p.min_col_mass = a->min_col_mass;
   hipStream_t s = (hipStream_t)stream;
+  if (!one_tile) {
+    const int lds = lw_layout(p.m, p.d, p.dv, a->last != 0, true).total;
+    if (a->dtype == VMO_DTYPE_F16)
+      return a->last ? lw_launch(lstep_wide_bwd_kernel<true, true>, lds, p.cols_total, s, "lstep_wide_bwd", p)
+                     : lw_launch(lstep_wide_bwd_kernel<true, false>, lds, p.cols_total, s, "lstep_wide_bwd", p);
+    return a->last ? lw_launch(lstep_wide_bwd_kernel<false, true>, lds, p.cols_total, s, "lstep_wide_bwd", p)
+                   : lw_launch(lstep_wide_bwd_kernel<false, false>, lds, p.cols_total, s, "lstep_wide_bwd", p);
+  }
   if (a->dtype == VMO_DTYPE_F16) return dispatch_lstep_bwd<true>(p, a->d, a->dv, a->last != 0, s);
   return dispatch_lstep_bwd<false>(p, a->d, a->dv, a->last != 0, s);
 }

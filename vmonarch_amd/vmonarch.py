@@ -8,15 +8,21 @@ map is approximated by a Monarch matrix built from
   - L: b dense (m x m) blocks, mixing tokens inside each grid column (the L-step);
 fitted by a few steps of alternating minimisation (reference: vmonarch.py:1-11, :29-69).
 
-Two execution paths with identical results (within bf16 tolerance):
-  * fused (default, forward only): every step is a gfx950 HIP kernel -- the R-step reads the
+Execution paths, with identical results within bf16 tolerance:
+  * fused (forward without autograd): every step is a gfx950 HIP kernel -- the R-step reads the
     (B, H, m*b, D) tensors in place as m frames per head (no flatten copy, no torch.cat of
-    [k | v]), the L-step is one fused kernel per iteration, and the recompute of the first
-    tokens is a split-KV flash kernel writing straight into z;
-  * composed: the reference's structure step by step (R-step through the
-    `_row_block_attention` seam, L-step as torch tensor ops), used when autograd needs the graph
-    or when a caller replaced `_row_block_attention` (tests/test_vmonarch.py:59 does).
+    [k | v]), the L-step is one fused kernel per iteration (one MFMA tile per grid column for
+    m <= 32, a general kernel beyond), and the recompute of the first tokens is a split-KV flash
+    kernel writing straight into z;
+  * _VMonarchFunction (autograd): the same forward keeping its activations, and a HIP backward;
+  * head dims the kernels do not take as they are (16, 32; D != Dv with autograd) run either of
+    the above on q, k, v zero-padded to one kernel width;
+  * composed: the reference's structure step by step (R-step through the `_row_block_attention`
+    seam, L-step as torch tensor ops), used when a caller replaced `_row_block_attention`
+    (tests/test_vmonarch.py:59 does), and -- with a RuntimeWarning -- for shapes no HIP path takes.
 """
+import warnings
+
 import torch
 import torch.nn as nn
 
@@ -87,10 +93,34 @@ def _lstep_bwd_launch(q, out, ent, grad_res, grad_q, grad_out, m, b, scale, last
     _lib.check(L.vmo_lstep_bwd(a, _lib.stream_of(q)), "vmo_lstep_bwd")
 
 
+_LDS_BYTES = 160 * 1024   # per CU on gfx950
+
+
+def _lstep_general_lds(m, d, dv, last, bwd):
+    """LDS bytes per grid column of the general L-step kernels (csrc/lstep.hip lw_layout): 16-bit rows of q,
+    kr (and the upstream gradient, y) padded by 16 bytes, one or two fp32 m x (m + 1) matrices, 4 m floats."""
+    r16 = lambda b: (b + 15) // 16 * 16   # noqa: E731
+    ldq, ldy, ldm = d + 8, dv + 8, m + 1
+    total = 2 * r16(m * ldq * 2) + r16(m * ldm * 4) + r16(4 * m * 4)
+    if bwd:
+        total += r16(m * (ldy if last else ldq) * 2) + r16(m * ldm * 4)
+    if last:
+        total += r16(m * ldy * 2)
+    return total
+
+
+def _lstep_supported(m, d, dv, bwd):
+    """Whether the HIP L-steps run this grid: the one-tile MFMA kernels (m <= 32, d and dv in {64, 128}) or the
+    general kernels (any m whose per-column tiles fit the LDS)."""
+    if m <= 32 and d in (64, 128) and dv in (64, 128):
+        return True
+    return all(_lstep_general_lds(m, d, dv, last, bwd) <= _LDS_BYTES for last in (False, True))
+
+
 def _fused_supported(q, k, v, num_blocks):
     D, Dv = q.shape[-1], v.shape[-1]
     return (q.is_cuda and q.dtype in _lib.DTYPES and k.dtype == q.dtype and v.dtype == q.dtype
-            and D in (64, 128) and Dv in (64, 128) and num_blocks <= 32
+            and D in (64, 128) and Dv in (64, 128) and _lstep_supported(num_blocks, D, Dv, False)
             and k.shape == q.shape and v.shape[:-1] == q.shape[:-1])
 
 
@@ -109,13 +139,14 @@ def _side_stream(dev):
     return s
 
 
-def _vmonarch_fused(q, k, v, m, b, num_iters, recompute_tokens, min_col_mass, stage_hook=None):
+def _vmonarch_fused(q, k, v, m, b, num_iters, recompute_tokens, min_col_mass, stage_hook=None, scale=None):
     """All-HIP forward.  `stage_hook(name, phase, stream)`, when given, is called on the host right
     before ("begin") and after ("end") each launch group ("rstep0", "lstep0", ..., "recompute") with
-    the stream it goes to -- used by bench.py to bracket every kernel with events."""
+    the stream it goes to -- used by bench.py to bracket every kernel with events.  `scale` overrides
+    D ** -0.5 (q / k zero-padded past their head dim)."""
     B, H, N, D = q.shape
     Dv = v.shape[-1]
-    scale = D ** -0.5
+    scale = D ** -0.5 if scale is None else scale
     q, k, v = (_lib.row_aligned(t) for t in (q, k, v))
     dev, dt = q.device, q.dtype
     main = torch.cuda.current_stream(dev)
@@ -172,7 +203,8 @@ def _vmonarch_fused(q, k, v, m, b, num_iters, recompute_tokens, min_col_mass, st
 
 def _hip_backward_supported(q, k, v, num_blocks):
     # the last R-step's backward takes the values [k | v] as two equal halves of 64 or 128
-    return _fused_supported(q, k, v, num_blocks) and q.shape[-1] == v.shape[-1]
+    return (_fused_supported(q, k, v, num_blocks) and q.shape[-1] == v.shape[-1]
+            and _lstep_supported(num_blocks, q.shape[-1], v.shape[-1], True))
 
 
 class _VMonarchFunction(torch.autograd.Function):
@@ -188,10 +220,10 @@ class _VMonarchFunction(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, q, k, v, m, b, num_iters, recompute_tokens, min_col_mass):
+    def forward(ctx, q, k, v, m, b, num_iters, recompute_tokens, min_col_mass, scale=None):
         B, H, N, D = q.shape
         Dv = v.shape[-1]
-        scale = D ** -0.5
+        scale = D ** -0.5 if scale is None else scale
         z = _lib.empty_in_layout(q, Dv, q.dtype)
         ctx.orders = tuple(_lib.layout_order(t) for t in (q, k, v))
         # the backward views every head's m frames as one (B, H * m, b) problem set: contiguous copies
@@ -214,17 +246,16 @@ class _VMonarchFunction(torch.autograd.Function):
         if rt > 0:
             _, lse_rt, _ = fea_forward(q[:, :, :rt], k, v, None, scale, o=z[:, :, :rt], want_ent=False,
                                        num_splits=_recompute_splits(B * H, rt, N))
-        ctx.dims = (m, b, num_iters, rt, float(min_col_mass))
+        ctx.dims = (m, b, num_iters, rt, float(min_col_mass), float(scale))
         ctx.save_for_backward(q, k, v, z, lse_rt if lse_rt is not None else z.new_empty(0), *saved)
         return z
 
     @staticmethod
     def backward(ctx, dz):
-        m, b, num_iters, rt, min_col_mass = ctx.dims
+        m, b, num_iters, rt, min_col_mass, scale = ctx.dims
         q, k, v, z, lse_rt, *saved = ctx.saved_tensors
         B, H, N, D = q.shape
         Dv = v.shape[-1]
-        scale = D ** -0.5
         dev, dt = q.device, q.dtype
         dz = _lib.row_aligned(dz.to(dt))
         f32 = torch.float32
@@ -264,7 +295,7 @@ class _VMonarchFunction(torch.autograd.Function):
             gk.copy_(dk)
             gv.copy_(dv)
         gq.copy_(dq)
-        return gq, gk, gv, None, None, None, None, None
+        return gq, gk, gv, None, None, None, None, None, None
 
 
 def _vmonarch_composed(q, k, v, num_blocks, block_size, num_iters, recompute_tokens, min_col_mass):
@@ -294,6 +325,16 @@ def _vmonarch_composed(q, k, v, num_blocks, block_size, num_iters, recompute_tok
     return z
 
 
+def _padded_width(D, Dv):
+    """The kernel width (64 or 128) that q, k and v can all be zero-padded to, or None."""
+    w = max(64, D, Dv)
+    return w if w in (64, 128) else None
+
+
+def _pad_to(t, w):
+    return t if t.shape[-1] == w else torch.nn.functional.pad(t, (0, w - t.shape[-1]))
+
+
 def vmonarch_attention(q, k, v, num_blocks, block_size, num_iters=2, recompute_tokens=0, min_col_mass=0.01):
     """
     Args:
@@ -311,12 +352,30 @@ def vmonarch_attention(q, k, v, num_blocks, block_size, num_iters=2, recompute_t
     if num_iters < 1:
         raise UnboundLocalError("local variable 'z' referenced before assignment")  # as the reference (vmonarch.py:65)
     needs_graph = torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v))
+    Dv = v.shape[-1]
     if _row_block_attention is _ROW_BLOCK_ATTENTION:
+        args = (num_blocks, block_size, num_iters, recompute_tokens, min_col_mass)
         if not needs_graph and _fused_supported(q, k, v, num_blocks):
-            return _vmonarch_fused(q, k, v, num_blocks, block_size, num_iters, recompute_tokens, min_col_mass)
+            return _vmonarch_fused(q, k, v, *args)
         if needs_graph and _hip_backward_supported(q, k, v, num_blocks):
-            return _VMonarchFunction.apply(q, k, v, num_blocks, block_size, num_iters, recompute_tokens,
-                                           min_col_mass)
+            return _VMonarchFunction.apply(q, k, v, *args)
+        # Head dims the kernels do not take as they are (16, 32; or D != Dv with autograd): zero columns
+        # change neither q.k nor P.v, so q, k and v padded to one kernel width give z with zero columns
+        # past Dv, with the softmax scale of the true D; autograd slices the padded gradients back.
+        w = _padded_width(D, Dv)
+        if (w is not None and q.is_cuda and q.dtype in _lib.DTYPES and k.dtype == q.dtype and v.dtype == q.dtype
+                and k.shape == q.shape and v.shape[:-1] == q.shape[:-1]
+                and _lstep_supported(num_blocks, w, w, needs_graph)):
+            qp, kp, vp = (_pad_to(t, w) for t in (q, k, v))
+            if needs_graph:
+                z = _VMonarchFunction.apply(qp, kp, vp, *args, D ** -0.5)
+            else:
+                z = _vmonarch_fused(qp, kp, vp, *args, scale=D ** -0.5)
+            return z if w == Dv else z[..., :Dv].contiguous()
+        if q.is_cuda:
+            warnings.warn(f"vmonarch_amd: no HIP path for num_blocks={num_blocks}, head dims ({D}, {Dv}), {q.dtype}"
+                          f"{' with autograd' if needs_graph else ''}; running the composed path (flash-entropy "
+                          "R-steps in HIP, L-steps and recompute as torch ops)", RuntimeWarning, stacklevel=2)
     if not q.is_cuda:
         raise RuntimeError("vmonarch_amd: vmonarch_attention needs GPU tensors (no CPU path)")
     return _vmonarch_composed(q, k, v, num_blocks, block_size, num_iters, recompute_tokens, min_col_mass)
