@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define VMO_ABI_VERSION 8
+#define VMO_ABI_VERSION 9
 
 enum {
   VMO_OK = 0,
@@ -95,8 +95,10 @@ typedef struct vmo_fea_fwd_args {
  *   last == 1:  z[i,j]  = sum_k attn[i,k] out[k,j,d:d+dv]                (vmonarch.py:57-59)
  * ent is the R-step entropy (the reference subtracts neg_ent = -ent).  `res` receives u
  * (d features) or z (dv features).  With last == 1, tokens n < skip_tokens are not written
- * (the recompute of vmonarch.py:66-68 owns them).  Supported: m <= 32, d in {64, 128},
- * dv in {64, 128}.
+ * (the recompute of vmonarch.py:66-68 owns them).  One MFMA tile per grid column for m <= 32 with d and
+ * dv in {64, 128}; otherwise a general kernel that takes any m whose per-column tiles fit the LDS
+ * (m <= 64 for head dims up to 128) and d, dv multiples of 8 up to 256.  Larger grids are rejected
+ * with VMO_ERR_UNSUPPORTED before any launch.
  */
 typedef struct vmo_lstep_args {
   int32_t dtype;
@@ -168,6 +170,11 @@ typedef struct vmo_fea_bwd_args {
   vmo_view v1;
   int32_t dv1;
   vmo_view grad_k_base, grad_v_base;   /* fp32, read with VMO_BWD_SUM_K / VMO_BWD_SUM_V */
+  /* frames (0 or 1: one): batch * heads * frames problems, as vmo_fea_fwd_args.frames -- frame f of
+   * (b, h) uses query rows [f*nq, (f+1)*nq) of q / o / grad_o / grad_q / lse / ent / grad_ent and key
+   * rows [f*nk, (f+1)*nk) of k / v / v1 / grad_k / grad_v and the bases, so the R-steps' backward reads
+   * a (B, H, m*b, .) tensor in any memory order (a DiT block's (B, N, H, D)) without a copy. */
+  int32_t frames;
 } vmo_fea_bwd_args;
 
 /*
@@ -185,7 +192,8 @@ typedef struct vmo_fea_bwd_args {
  *               grad_out[k,j,:d] = scale sum_i dlogit[i,k] q[i,j]
  * grad_q is float32 and accumulated into (+=); grad_out (the dtype of q) is written.  Replaces
  * the autograd graph of the reference's L-step (batched einsum/softmax/clamp backward); there is
- * no launch site of its own in the reference.  Supported: m <= 32, d in {64, 128}, dv in {64, 128}.
+ * no launch site of its own in the reference.  Supported grids and head dims: as vmo_lstep_args (the
+ * general kernel keeps one more m x m matrix and the gradient rows in LDS: m <= 64 up to head dim 128).
  */
 typedef struct vmo_lstep_bwd_args {
   int32_t dtype;

@@ -12,7 +12,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libvmonarch_gfx950.so")
-ABI_VERSION = 8
+ABI_VERSION = 9
 FEA_FWD_SCRATCH_BYTES = 32 << 20   # VMO_FEA_FWD_SCRATCH_BYTES: scratch of vmo_fea_fwd_noalloc per GPU
 DTYPES = {torch.bfloat16: 0, torch.float16: 1}
 
@@ -43,7 +43,7 @@ class FeaBwdArgs(ctypes.Structure):
         ("stat_stride_b", c_int64), ("stat_stride_h", c_int64),
         ("grad_ent_stride_b", c_int64), ("grad_ent_stride_h", c_int64),
         ("sm_scale", c_float), ("workspace", c_void_p), ("workspace_bytes", c_size_t), ("flags", c_int32),
-        ("v1", View), ("dv1", c_int32), ("grad_k_base", View), ("grad_v_base", View),
+        ("v1", View), ("dv1", c_int32), ("grad_k_base", View), ("grad_v_base", View), ("frames", c_int32),
     ]
 
 

@@ -59,7 +59,7 @@ struct BwdParams {
   int64_t q_sb, q_sh, q_sn, k_sb, k_sh, k_sn, v_sb, v_sh, v_sn, o_sb, o_sh, o_sn, do_sb, do_sh, do_sn;
   int64_t dq_sb, dq_sh, dq_sn, dk_sb, dk_sh, dk_sn, dv_sb, dv_sh, dv_sn;
   int64_t st_sb, st_sh, de_sb, de_sh;
-  int heads, nq, nk, problems;
+  int heads, frames, nq, nk, problems;   // problems = batch * heads * frames
   int dq_tiles, kv_tiles;
   int dq_total, kv_total;
   int dq_splits, keys_per_split;   // dq workgroups per query tile, each over one key range
@@ -284,7 +284,10 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
   const int prob = uni(L / p.dq_tiles / p.dq_splits);
   const int kbeg = split * p.keys_per_split;
   const int kend = min(p.nk, kbeg + p.keys_per_split);
-  const int hh = prob % p.heads, bb = prob / p.heads;
+  // problem (b, h, f): query rows [f nq, (f + 1) nq) and key rows [f nk, (f + 1) nk) of the (b, h) tensors
+  const int fr = uni(prob % p.frames), bh = uni(prob / p.frames);
+  const int hh = uni(bh % p.heads), bb = uni(bh / p.heads);
+  const int64_t qoff = (int64_t)fr * p.nq, koff = (int64_t)fr * p.nk;
   const int tid = threadIdx.x, wave = uni(tid >> 6), lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int q0 = qt * kDqBM + wave * 32;
   const bool wave_live = q0 < p.nq;
@@ -292,16 +295,17 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
   const bool qvalid = qrow < p.nq;
   const int qr = qvalid ? qrow : 0;
 
-  const T* kb = (const T*)p.k + bb * p.k_sb + hh * p.k_sh;
-  const T* vb = (const T*)p.v + bb * p.v_sb + hh * p.v_sh;
+  const T* kb = (const T*)p.k + bb * p.k_sb + hh * p.k_sh + koff * p.k_sn;
+  const T* vb = (const T*)p.v + bb * p.v_sb + hh * p.v_sh + koff * p.v_sn;
+  const T* v1b = (const T*)p.v1 + bb * p.v_sb + hh * p.v_sh + koff * p.v_sn;
 
   // Q^T and dO^T as B operands (one query per lane); delta = o . dO in fp32
   V8 qf[D / 16], dof[DV / 16];
   float delta = 0.f;
   {
-    const T* qp = (const T*)p.q + bb * p.q_sb + hh * p.q_sh + (int64_t)qr * p.q_sn + hl * 8;
-    const T* dp = (const T*)p.dO + bb * p.do_sb + hh * p.do_sh + (int64_t)qr * p.do_sn + hl * 8;
-    const T* op = (const T*)p.o + bb * p.o_sb + hh * p.o_sh + (int64_t)qr * p.o_sn + hl * 8;
+    const T* qp = (const T*)p.q + bb * p.q_sb + hh * p.q_sh + (qoff + qr) * p.q_sn + hl * 8;
+    const T* dp = (const T*)p.dO + bb * p.do_sb + hh * p.do_sh + (qoff + qr) * p.do_sn + hl * 8;
+    const T* op = (const T*)p.o + bb * p.o_sb + hh * p.o_sh + (qoff + qr) * p.o_sn + hl * 8;
 #pragma unroll
     for (int ds = 0; ds < D / 16; ++ds) {
       V8 x = *(const V8*)(qp + ds * 16);
@@ -319,9 +323,9 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
     }
   }
   delta = wave_sum32(delta);
-  const int64_t si = bb * p.st_sb + hh * p.st_sh + qr;
+  const int64_t si = bb * p.st_sb + hh * p.st_sh + qoff + qr;
   const float lse = p.lse[si];
-  const float dE = p.dent[bb * p.de_sb + hh * p.de_sh + qr];
+  const float dE = p.dent[bb * p.de_sb + hh * p.de_sh + qoff + qr];
   float alpha = -delta - dE * p.ent[si];
   float beta = -dE * kLn2;
   float lse_r = lse;
@@ -339,9 +343,9 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
     if constexpr (W0K && DVL == 0)
       return 0;   // values k: nothing beyond the K tile
     else if constexpr (W0K)
-      return BwdTileCopy<T, DVL, kDqBN>((const T*)p.v1 + bb * p.v_sb + hh * p.v_sh, p.v_sn, wave, lane);
+      return BwdTileCopy<T, DVL, kDqBN>(v1b, p.v_sn, wave, lane);
     else if constexpr (V2)
-      return BwdTileCopy2<T, DV, kDqBN>(vb, (const T*)p.v1 + bb * p.v_sb + hh * p.v_sh, p.v_sn, wave, lane);
+      return BwdTileCopy2<T, DV, kDqBN>(vb, v1b, p.v_sn, wave, lane);
     else
       return BwdTileCopy<T, DV, kDqBN>(vb, p.v_sn, wave, lane);
   }();
@@ -419,7 +423,7 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
   } else {
     const int mode = grad_mode(p.accum, VMO_BWD_ACCUM_Q, VMO_BWD_F32_Q);
     const int64_t es = mode == kGradStore ? 2 : 4;
-    char* row0 = (char*)p.dq + (bb * p.dq_sb + hh * p.dq_sh + (int64_t)q0 * p.dq_sn) * es;
+    char* row0 = (char*)p.dq + (bb * p.dq_sb + hh * p.dq_sh + (qoff + q0) * p.dq_sn) * es;
     store_acc_rows<F16>(patch, acc, NA, p.sm_scale, mode, row0, p.dq_sn * es, nrows, lane);
   }
 }
@@ -439,15 +443,16 @@ __global__ __launch_bounds__(256) void fea_bwd_dq_reduce(BwdParams p) {
   f32x4 acc = f32x4{};
   for (int sp = 0; sp < p.dq_splits; ++sp)
     acc += *(const f32x4*)(p.dq_part + (((int64_t)sp * p.problems + prob) * p.nq + qi) * D + 4 * c4);
-  const int hh = prob % p.heads, bb = prob / p.heads;
+  const int fr = prob % p.frames, bh = prob / p.frames, hh = bh % p.heads, bb = bh / p.heads;
+  const int64_t row_q = (int64_t)fr * p.nq + qi;
   if (const int mode = grad_mode(p.accum, VMO_BWD_ACCUM_Q, VMO_BWD_F32_Q); mode != kGradStore) {
-    f32x4* ptr = (f32x4*)((float*)p.dq + bb * p.dq_sb + hh * p.dq_sh + (int64_t)qi * p.dq_sn + 4 * c4);
+    f32x4* ptr = (f32x4*)((float*)p.dq + bb * p.dq_sb + hh * p.dq_sh + row_q * p.dq_sn + 4 * c4);
     *ptr = mode == kGradAddF32 ? *ptr + acc : acc;
   } else {
     V4 v;
 #pragma unroll
     for (int e = 0; e < 4; ++e) v[e] = to_elem<T>(acc[e]);
-    *(V4*)((T*)p.dq + bb * p.dq_sb + hh * p.dq_sh + (int64_t)qi * p.dq_sn + 4 * c4) = v;
+    *(V4*)((T*)p.dq + bb * p.dq_sb + hh * p.dq_sh + row_q * p.dq_sn + 4 * c4) = v;
   }
 }
 
@@ -478,7 +483,9 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
   if (L >= p.kv_total) return;
   auto uni = [](int x) __attribute__((always_inline)) { return __builtin_amdgcn_readfirstlane(x); };
   const int kt = uni(L % p.kv_tiles), prob = uni(L / p.kv_tiles);
-  const int hh = prob % p.heads, bb = prob / p.heads;
+  const int fr = uni(prob % p.frames), bh = uni(prob / p.frames);
+  const int hh = uni(bh % p.heads), bb = uni(bh / p.heads);
+  const int64_t qoff = (int64_t)fr * p.nq, koff = (int64_t)fr * p.nk;
   const int tid = threadIdx.x, wave = uni(tid >> 6), lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int k0 = kt * kKvBN + wave * 32;
   const bool wave_live = k0 < p.nk;
@@ -489,9 +496,9 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
   // K^T and V^T as B operands (one key per lane); V^T from LDS in the V_LDS variants
   V8 kf[K_LDS ? 1 : D / 16], vf[(V_LDS || !WANT_DK || VW == 0) ? 1 : VW / 16];
   {
-    const T* kp = (const T*)p.k + bb * p.k_sb + hh * p.k_sh + (int64_t)kr * p.k_sn + hl * 8;
-    const T* vp = (const T*)p.v + bb * p.v_sb + hh * p.v_sh + (int64_t)kr * p.v_sn + hl * 8;
-    const T* vp1 = p.v1 ? (const T*)p.v1 + bb * p.v_sb + hh * p.v_sh + (int64_t)kr * p.v_sn + hl * 8 : vp;
+    const T* kp = (const T*)p.k + bb * p.k_sb + hh * p.k_sh + (koff + kr) * p.k_sn + hl * 8;
+    const T* vp = (const T*)p.v + bb * p.v_sb + hh * p.v_sh + (koff + kr) * p.v_sn + hl * 8;
+    const T* vp1 = p.v1 ? (const T*)p.v1 + bb * p.v_sb + hh * p.v_sh + (koff + kr) * p.v_sn + hl * 8 : vp;
 #pragma unroll
     for (int ds = 0; ds < (K_LDS ? 0 : D / 16); ++ds) {
       kf[ds] = *(const V8*)(kp + ds * 16);
@@ -512,9 +519,9 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
       }
     }
   }
-  const T* qb = (const T*)p.q + bb * p.q_sb + hh * p.q_sh;
-  const T* dob = (const T*)p.dO + bb * p.do_sb + hh * p.do_sh;
-  const float* lseb = p.lse + bb * p.st_sb + hh * p.st_sh;
+  const T* qb = (const T*)p.q + bb * p.q_sb + hh * p.q_sh + qoff * p.q_sn;
+  const T* dob = (const T*)p.dO + bb * p.do_sb + hh * p.do_sh + qoff * p.do_sn;
+  const float* lseb = p.lse + bb * p.st_sb + hh * p.st_sh + qoff;
   const float* alb = p.alpha + (int64_t)prob * p.nq;
   const float* beb = p.beta + (int64_t)prob * p.nq;
 
@@ -550,18 +557,17 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
   const VMO_LDS char* vt_row = smem + 2 * STAGE + (wave * 32 + l32) * (VW * 2);
   const VMO_LDS char* kt_row = smem + 2 * STAGE + V_TILE + (wave * 32 + l32) * (D * 2);
   if constexpr (V_LDS && VW > 0) {   // this workgroup's 128 V rows, once (landed by the first tile_sync)
-    const T* vb0 = (const T*)p.v + bb * p.v_sb + hh * p.v_sh;
+    const T* vb0 = (const T*)p.v + bb * p.v_sb + hh * p.v_sh + koff * p.v_sn;
+    const T* vb1 = (const T*)p.v1 + bb * p.v_sb + hh * p.v_sh + koff * p.v_sn;
     if constexpr (W0K)
-      stage_rows_n<T, VW, kKvBN>((const T*)p.v1 + bb * p.v_sb + hh * p.v_sh, p.v_sn, kt * kKvBN, p.nk,
-                                 smem_u32 + 2 * STAGE, wave, lane);
+      stage_rows_n<T, VW, kKvBN>(vb1, p.v_sn, kt * kKvBN, p.nk, smem_u32 + 2 * STAGE, wave, lane);
     else if (p.v1)
-      stage_rows_n2<T, DV, kKvBN>(vb0, (const T*)p.v1 + bb * p.v_sb + hh * p.v_sh, p.v_sn, kt * kKvBN, p.nk,
-                                  smem_u32 + 2 * STAGE, wave, lane);
+      stage_rows_n2<T, DV, kKvBN>(vb0, vb1, p.v_sn, kt * kKvBN, p.nk, smem_u32 + 2 * STAGE, wave, lane);
     else
       stage_rows_n<T, DV, kKvBN>(vb0, p.v_sn, kt * kKvBN, p.nk, smem_u32 + 2 * STAGE, wave, lane);
   }
   if constexpr (K_LDS)   // and its 128 K rows
-    stage_rows_n<T, D, kKvBN>((const T*)p.k + bb * p.k_sb + hh * p.k_sh, p.k_sn, kt * kKvBN, p.nk,
+    stage_rows_n<T, D, kKvBN>((const T*)p.k + bb * p.k_sb + hh * p.k_sh + koff * p.k_sn, p.k_sn, kt * kKvBN, p.nk,
                               smem_u32 + 2 * STAGE + V_TILE, wave, lane);
   // one 32-query stage; only a partial last stage masks its queries, and it is peeled out of the loop
   // (both versions inside one loop body made the compiler spill the accumulators)
@@ -658,8 +664,8 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
                  int mode, const void* src = nullptr, int64_t ssb = 0, int64_t ssh = 0, int64_t ssn = 0)
       __attribute__((always_inline)) {
     const int64_t es = mode == kGradStore || mode == kGradSumStore ? 2 : 4;
-    char* row0 = (char*)base + (bb * sb + hh * sh + (int64_t)k0 * sn + col0) * es;
-    const char* src0 = src ? (const char*)src + (bb * ssb + hh * ssh + (int64_t)k0 * ssn + col0) * 4 : nullptr;
+    char* row0 = (char*)base + (bb * sb + hh * sh + (koff + k0) * sn + col0) * es;
+    const char* src0 = src ? (const char*)src + (bb * ssb + hh * ssh + (koff + k0) * ssn + col0) * 4 : nullptr;
     store_acc_rows<F16>(patch, acc, nacc, f, mode, row0, sn * es, nrows, lane, 0, src0, ssn * 4);
   };
   const int mode_k = grad_mode(p.accum, VMO_BWD_ACCUM_K, VMO_BWD_F32_K, VMO_BWD_SUM_K);
@@ -786,7 +792,7 @@ static size_t bwd_stats_bytes(int64_t problems, int nq) { return ((size_t)2 * pr
 extern "C" size_t vmo_fea_bwd_workspace_size(const vmo_fea_bwd_args* a) {
   using namespace vmo;
   if (!a || a->batch <= 0 || a->heads <= 0 || a->nq <= 0 || a->nk <= 0) return 256;
-  const int64_t problems = (int64_t)a->batch * a->heads;
+  const int64_t problems = (int64_t)a->batch * a->heads * (a->frames > 0 ? a->frames : 1);
   const int splits = bwd_dq_splits(problems, a->nq, a->nk);
   size_t bytes = bwd_stats_bytes(problems, a->nq) + 256;
   if (splits > 1) bytes += (size_t)splits * problems * a->nq * (a->d > 0 ? a->d : 0) * 4;
@@ -843,7 +849,8 @@ extern "C" int vmo_fea_bwd(const vmo_fea_bwd_args* a, void* stream) {
   const size_t ws = vmo_fea_bwd_workspace_size(a);
   if (!a->workspace || a->workspace_bytes < ws || !aligned16(a->workspace))
     return set_error(VMO_ERR_WORKSPACE, "fea_bwd: needs %zu workspace bytes", ws);
-  const int64_t problems = (int64_t)a->batch * a->heads;
+  const int frames = a->frames > 0 ? a->frames : 1;
+  const int64_t problems = (int64_t)a->batch * a->heads * frames;
   const int64_t dq_tiles = (a->nq + kDqBM - 1) / kDqBM, kv_tiles = (a->nk + kKvBN - 1) / kKvBN;
   if (problems * dq_tiles > (1ll << 30) || problems * kv_tiles > (1ll << 30))
     return set_error(VMO_ERR_UNSUPPORTED, "fea_bwd: problem too large");
@@ -878,7 +885,7 @@ extern "C" int vmo_fea_bwd(const vmo_fea_bwd_args* a, void* stream) {
   p.dv_sb = a->grad_v.stride_b; p.dv_sh = a->grad_v.stride_h; p.dv_sn = a->grad_v.stride_n;
   p.st_sb = a->stat_stride_b; p.st_sh = a->stat_stride_h;
   p.de_sb = a->grad_ent_stride_b; p.de_sh = a->grad_ent_stride_h;
-  p.heads = a->heads; p.nq = a->nq; p.nk = a->nk; p.problems = (int)problems;
+  p.heads = a->heads; p.frames = frames; p.nq = a->nq; p.nk = a->nk; p.problems = (int)problems;
   p.dq_tiles = (int)dq_tiles; p.kv_tiles = (int)kv_tiles;
   p.dq_total = (int)(problems * dq_tiles * p.dq_splits); p.kv_total = (int)(problems * kv_tiles);
   p.c = a->sm_scale * kLog2e;

@@ -14,14 +14,18 @@ def _pad_features(t, width):
 
 
 def fea_backward_raw(q, k, v, o, lse, ent, do, de, sm_scale, dq=None, dk=None, dv=None, overwrite="", v1=None,
-                     fold_k=False, dk_base=None, dv_base=None):
-    """q: (B, H, nq, D); k: (B, H, nk, D); v: (B, H, nk, Dv); o, do: (B, H, nq, Dv);
-    lse, ent, de: (B, H, nq) fp32 with unit token stride.  Returns (dq, dk, dv).
+                     fold_k=False, dk_base=None, dv_base=None, frames=1):
+    """q: (B, H, F*nq, D); k: (B, H, F*nk, D); v: (B, H, F*nk, Dv); o, do: (B, H, F*nq, Dv);
+    lse, ent, de: (B, H, F*nq) fp32 with unit token stride.  Returns (dq, dk, dv).
+
+    `frames` = F splits every (b, h) into F independent problems of nq queries and nk keys (frame f:
+    rows [f nq, (f + 1) nq) and [f nk, (f + 1) nk)), read in place whatever the memory order.
 
     With `v1` (same shape and strides as v) the values are [v | v1], 2 Dv wide, read in place.
 
     A gradient passed in as a float32 view is accumulated into (+= in the kernels), or overwritten
-    when its letter ("q", "k", "v") is in `overwrite`; otherwise it is returned as a new tensor of
+    when its letter ("q", "k", "v") is in `overwrite`; one passed in q's dtype (a 16-bit view, any
+    strides with a contiguous feature dim) is written; one not passed is returned as a new tensor of
     q's dtype.
 
     `fold_k` (v is k, as the VMonarch R-steps pass it): dk receives k's whole gradient, as key and
@@ -39,8 +43,8 @@ def fea_backward_raw(q, k, v, o, lse, ent, do, de, sm_scale, dq=None, dk=None, d
         if base is not None:
             assert base.dtype == torch.float32 and (t is None or t.dtype == q.dtype), "base fp32, result q.dtype"
             flags |= _lib.BWD_SUM_K if name == "k" else _lib.BWD_SUM_V
-        elif t is not None:
-            assert t.dtype == torch.float32, "a gradient passed in must be float32"
+        elif t is not None and t.dtype != q.dtype:
+            assert t.dtype == torch.float32, "a gradient passed in must be float32 or q's dtype"
             flags |= f32_bit if name in overwrite else acc_bit
     if dq is None:
         dq = torch.empty((B, H, NQ, D), device=q.device, dtype=q.dtype)
@@ -51,7 +55,9 @@ def fea_backward_raw(q, k, v, o, lse, ent, do, de, sm_scale, dq=None, dk=None, d
     a = _lib.FeaBwdArgs()
     a.flags = flags
     a.dtype = _lib.DTYPES[q.dtype]
-    a.batch, a.heads, a.nq, a.nk, a.d, a.dv = B, H, NQ, NK, D, Dv
+    assert NQ % frames == 0 and NK % frames == 0
+    a.batch, a.heads, a.nq, a.nk, a.d, a.dv = B, H, NQ // frames, NK // frames, D, Dv
+    a.frames = frames
     a.q, a.k, a.v, a.o, a.grad_o = (_lib.view(t) for t in (q, k, v, o, do))
     a.grad_q, a.grad_k = _lib.view(dq), _lib.view(dk)
     a.grad_v = _lib.view(dv) if dv is not None else _lib.View()
@@ -90,6 +96,15 @@ def fea_backward(q, k, v, o, lse, ent, do, de, sm_scale, n_valid):
         do = torch.zeros_like(o)
     do = do.to(q.dtype)
     de = de.float()
+    if de.stride(2) != 1:
+        de = de.contiguous()
+    if n == N and Dk == D and Dvk == Dv:
+        # no padding rows, no padded features: the kernels write the gradients once, in the memory order
+        # of the caller's q, k, v (a DiT block's (B, N, H, D) buffers need no copy afterwards)
+        grads = [_lib.empty_in_layout(t, t.shape[-1], q.dtype) for t in (q, k, v)]
+        args = [_lib.row_aligned(t) for t in (q, k, v, o, do)]
+        fea_backward_raw(*args[:4], lse, ent, args[4], de, sm_scale, dq=grads[0], dk=grads[1], dv=grads[2])
+        return tuple(grads)
     dq = torch.zeros_like(q)
     dk = torch.zeros_like(k)
     dv = torch.zeros_like(v)
@@ -100,8 +115,6 @@ def fea_backward(q, k, v, o, lse, ent, do, de, sm_scale, n_valid):
     vx, ox, dox = (_lib.row_aligned(_pad_features(t[:, :, sl], Dvk)) for t in (v, o, do))
     lse_x, ent_x = lse[:, :, sl], ent[:, :, sl]
     de_x = de[:, :, sl]
-    if de_x.stride(2) != 1:
-        de_x = de_x.contiguous()
     gq, gk, gv = fea_backward_raw(qx, kx, vx, ox, lse_x, ent_x, dox, de_x, sm_scale)
     dq[:, :, sl] = gq[..., :D]
     dk[:, :, sl] = gk[..., :D]

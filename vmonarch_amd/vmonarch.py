@@ -48,12 +48,13 @@ _ROW_BLOCK_ATTENTION = _row_block_attention   # the seam as shipped; patched sea
 
 
 def _recompute_splits(problems, nq, nk):
-    q_tiles = (nq + 127) // 128
-    base = problems * q_tiles
-    splits = 1
-    while base * splits < 4 * _NUM_CUS and splits < 16 and nk // (splits * 2) >= 512:
-        splits *= 2
-    return splits
+    """Key splits of the recompute: the fewest that fill ~80% of one round of workgroup slots (two 128-query
+    workgroups per CU), each split keeping >= 512 keys.  Fewer splits write fewer fp32 partials; a split count
+    whose workgroups spill a little into another round leaves that round mostly idle (measured at cfg4, 156
+    query tiles: 3 splits 0.300 ms, 8 splits 0.309 ms, 16 splits 0.336 ms)."""
+    base = problems * ((nq + 127) // 128)
+    want = -(-int(0.8 * 2 * _NUM_CUS) // base)
+    return max(1, min(16, want, nk // 512))
 
 
 def _lstep_launch(q, out, ent, res, m, b, scale, last, skip, min_col_mass):
@@ -226,8 +227,11 @@ class _VMonarchFunction(torch.autograd.Function):
         scale = D ** -0.5 if scale is None else scale
         z = _lib.empty_in_layout(q, Dv, q.dtype)
         ctx.orders = tuple(_lib.layout_order(t) for t in (q, k, v))
-        # the backward views every head's m frames as one (B, H * m, b) problem set: contiguous copies
-        q, k, v = (t.contiguous() for t in (q, k, v))
+        # read in place in any memory order (the backward, like the forward, takes each head's m frames
+        # as m problems of the (B, H, m*b) tensors): no contiguous copies of a DiT block's (B, N, H, D)
+        q, k, v = (_lib.row_aligned(t) for t in (q, k, v))
+        if k.stride() != v.stride():   # the backward reads the values [k | v] as two parts with one set of strides
+            k, v = k.contiguous(), v.contiguous()
         dev, dt = q.device, q.dtype
         rt = min(int(recompute_tokens), N)
         saved = []
@@ -266,8 +270,7 @@ class _VMonarchFunction(torch.autograd.Function):
         dq = torch.empty((B, H, N, D), device=dev, dtype=f32)
         dk = torch.empty((B, H, N, D), device=dev, dtype=f32)
         dv = torch.empty((B, H, N, Dv), device=dev, dtype=f32)
-        frames = lambda t: t.reshape(B, H * m, b, *t.shape[3:])   # the R-step's m frames per head
-        de = torch.zeros((B, H * m, b), device=dev, dtype=f32)
+        de = torch.zeros((B, H, N), device=dev, dtype=f32)
         g = dz
         for it in reversed(range(num_iters)):
             last = it == num_iters - 1
@@ -275,14 +278,13 @@ class _VMonarchFunction(torch.autograd.Function):
             dout = torch.empty_like(out)
             _lstep_bwd_launch(q, out, ent, g, dq, dout, m, b, scale, last, rt if last else 0, min_col_mass,
                               overwrite_q=last)
-            # values k, or [k | v] read from the two tensors in place (vmonarch.py:50)
-            gx, _, _ = fea_backward_raw(frames(x), frames(k), frames(k), frames(out), frames(lse), frames(ent),
-                                        frames(dout), de, scale if it == 0 else 1.0,
-                                        dq=frames(dq) if it == 0 else None,   # R-step 0 read q directly
-                                        dk=frames(dk), dv=frames(dv) if last else None,
-                                        overwrite="kv" if last else "", v1=frames(v) if last else None, fold_k=True)
+            # values k, or [k | v] read from the two tensors in place (vmonarch.py:50); m frames per head
+            gx, _, _ = fea_backward_raw(x, k, k, out, lse, ent, dout, de, scale if it == 0 else 1.0,
+                                        dq=dq if it == 0 else None,   # R-step 0 read q directly
+                                        dk=dk, dv=dv if last else None, overwrite="kv" if last else "",
+                                        v1=v if last else None, fold_k=True, frames=m)
             if it > 0:
-                g = gx.view(B, H, N, D)     # dL/du of the previous L-step's output
+                g = gx                      # dL/du of the previous L-step's output
         # gradients in the memory order the caller's q, k, v had (the fp32 -> dtype writes place them)
         gq, gk, gv = (_lib.empty_in_order(o, (B, H, N), f, dt, dev) for o, f in zip(ctx.orders, (D, D, Dv)))
         if rt > 0:
