@@ -315,21 +315,29 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
 #pragma unroll
       for (int r = 0; r < 16; ++r) x[j][r] = fmaf(x[j][r], c, -m_run[j]);
       if constexpr (MASKED) mask_block(x[j], kofs, nvalid);
-      float ls0 = 0.f, ls1 = 0.f, hs0 = 0.f, hs1 = 0.f;
+      // two partial sums per lane (pairs r % 4 == 0 and == 2), each started from its first term: an
+      // accumulator started at 0 costs an add of +0 per block that the compiler cannot drop (-0 + 0 = +0)
+      float ls0, ls1, hs0, hs1;
       uint32_t w[8];
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
         const float p0 = fast_exp2(x[j][r]), p1 = fast_exp2(x[j][r + 1]);
         const V2 pk = E::pack2(p0, p1);
-        float s2;
-        if constexpr (ENT == kEntFromPK) s2 = (float)pk[0] + (float)pk[1];
-        else s2 = p0 + p1;
-        if (r & 2) ls1 += s2; else ls0 += s2;
-        if constexpr (ENT == kEntOnline) {
-          if (r & 2) hs1 = fmaf(p1, x[j][r + 1], fmaf(p0, x[j][r], hs1));
-          else hs0 = fmaf(p1, x[j][r + 1], fmaf(p0, x[j][r], hs0));
-        }
         w[r / 2] = __builtin_bit_cast(uint32_t, pk);
+        float s2;
+        if constexpr (ENT == kEntFromPK) {
+          // the rounded pair widened back from the packed word itself (left to itself, the compiler
+          // rounds each p a second time, one value per conversion)
+          if constexpr (F16) s2 = (float)pk[0] + (float)pk[1];
+          else s2 = __uint_as_float(w[r / 2] << 16) + __uint_as_float(w[r / 2] & 0xffff0000u);
+        } else {
+          s2 = p0 + p1;
+        }
+        const float h2 = ENT == kEntOnline ? fmaf(p1, x[j][r + 1], p0 * x[j][r]) : 0.f;
+        if (r == 0) { ls0 = s2; hs0 = h2; }
+        else if (r == 2) { ls1 = s2; hs1 = h2; }
+        else if (r & 2) { ls1 += s2; hs1 += h2; }
+        else { ls0 += s2; hs0 += h2; }
       }
       typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
       P[j][0] = __builtin_bit_cast(V8, u32x4{w[0], w[1], w[2], w[3]});
