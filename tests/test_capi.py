@@ -48,11 +48,27 @@ def test_single_hip_runtime_in_process(L):
     assert len(hip) <= 1, hip
 
 
+_DEVICE_BUFFER = []
+
+
+def _addr(offset=0):
+    """Base address for the views of the rejection tests below.  With a GPU visible it lies inside a real
+    64 MiB device buffer that covers every view these tests describe, so a launch that slipped past the
+    host checks would read valid memory and fail an assertion rather than fault the GPU; without a GPU
+    (nothing can launch) it is a made-up page-aligned address."""
+    import torch
+    if not torch.cuda.is_available():
+        return 4096 + offset
+    if not _DEVICE_BUFFER:
+        _DEVICE_BUFFER.append(torch.zeros(64 << 20, dtype=torch.uint8, device="cuda:0"))
+    return _DEVICE_BUFFER[0].data_ptr() + 4096 + offset
+
+
 def _fwd_args(**kw):
     from vmonarch_amd import _lib
     a = _lib.FeaFwdArgs()
     a.dtype, a.batch, a.heads, a.frames, a.nq, a.nk, a.d, a.dw0, a.dw1 = 0, 1, 1, 1, 128, 128, 128, 128, 0
-    v = _lib.View(4096, 128, 128 * 128, 128)
+    v = _lib.View(_addr(), 128, 128 * 128, 128)
     a.q = a.k = a.w0 = a.o = v
     a.sm_scale = 0.1
     a.num_splits = 1
@@ -74,10 +90,10 @@ def test_fea_fwd_rejects_bad_arguments_without_launching(L, field, value, code):
 def test_fea_fwd_rejects_misaligned_rows(L):
     from vmonarch_amd import _lib
     a = _fwd_args()
-    a.q = _lib.View(4096 + 2, 128, 128 * 128, 128)
+    a.q = _lib.View(_addr() + 2, 128, 128 * 128, 128)
     assert L.vmo_fea_fwd(ctypes.byref(a), None) == 1
     a = _fwd_args()
-    a.k = _lib.View(4096, 128, 128 * 128, 100)
+    a.k = _lib.View(_addr(), 128, 128 * 128, 100)
     assert L.vmo_fea_fwd(ctypes.byref(a), None) == 1
 
 
@@ -95,13 +111,13 @@ def test_fea_fwd_empty_problem_is_a_no_op(L):
 
 def test_lstep_rejects_too_many_blocks(L):
     """m = 200 frames: the one-tile kernels stop at 32 and the general ones need more LDS per grid
-    column than a CU has, so the call is refused on the host (the made-up addresses are never used)."""
+    column than a CU has, so the call is refused on the host (the addresses are never dereferenced)."""
     from vmonarch_amd import _lib
     a = _lib.LstepArgs()
     a.dtype, a.batch, a.heads, a.num_blocks, a.block_size, a.d, a.dv = 0, 1, 1, 200, 4, 128, 128
-    v = _lib.View(4096, 128, 128, 128)
+    v = _lib.View(_addr(), 128, 128, 128)
     a.q = a.out = a.res = v
-    a.ent = 4096
+    a.ent = _addr()
     assert L.vmo_lstep_fwd(ctypes.byref(a), None) == 2
     assert b"LDS" in L.vmo_last_error()
     a.num_blocks, a.d = 40, 100   # head dim not a multiple of 8
@@ -112,9 +128,9 @@ def test_lstep_bwd_rejects_too_many_blocks_and_null_args(L):
     from vmonarch_amd import _lib
     a = _lib.LstepBwdArgs()
     a.dtype, a.batch, a.heads, a.num_blocks, a.block_size, a.d, a.dv = 0, 1, 1, 100, 4, 128, 128
-    v = _lib.View(4096, 128, 128, 128)
+    v = _lib.View(_addr(), 128, 128, 128)
     a.q = a.out = a.grad_res = a.grad_q = a.grad_out = v
-    a.ent = 4096
+    a.ent = _addr()
     assert L.vmo_lstep_bwd(ctypes.byref(a), None) == 2   # 100 frames: beyond the LDS of a CU
     assert b"LDS" in L.vmo_last_error()
     assert L.vmo_lstep_bwd(None, None) != 0
@@ -124,9 +140,9 @@ def test_fea_bwd_rejects_unknown_and_conflicting_flags(L):
     from vmonarch_amd import _lib
     a = _lib.FeaBwdArgs()
     a.dtype, a.batch, a.heads, a.nq, a.nk, a.d, a.dv = 0, 1, 1, 128, 128, 128, 128
-    v = _lib.View(4096, 128, 128 * 128, 128)
+    v = _lib.View(_addr(), 128, 128 * 128, 128)
     a.q = a.k = a.v = a.o = a.grad_o = a.grad_q = a.grad_k = a.grad_v = v
-    a.lse = a.ent = a.grad_ent = 4096
+    a.lse = a.ent = a.grad_ent = _addr()
     a.sm_scale = 0.1
     for flags in (_lib.BWD_ACCUM_K | _lib.BWD_F32_K, _lib.BWD_ACCUM_Q | _lib.BWD_F32_Q, 512):
         a.flags = flags
@@ -138,9 +154,9 @@ def test_lstep_bwd_rejects_unknown_flags(L):
     from vmonarch_amd import _lib
     a = _lib.LstepBwdArgs()
     a.dtype, a.batch, a.heads, a.num_blocks, a.block_size, a.d, a.dv = 0, 1, 1, 4, 4, 128, 128
-    v = _lib.View(4096, 128, 128, 128)
+    v = _lib.View(_addr(), 128, 128, 128)
     a.q = a.out = a.grad_res = a.grad_q = a.grad_out = v
-    a.ent = 4096
+    a.ent = _addr()
     a.flags = 2
     assert L.vmo_lstep_bwd(ctypes.byref(a), None) == 1
     assert b"flags" in L.vmo_last_error()
@@ -150,14 +166,14 @@ def test_fea_bwd_rejects_bad_value_parts(L):
     from vmonarch_amd import _lib
     a = _lib.FeaBwdArgs()
     a.dtype, a.batch, a.heads, a.nq, a.nk, a.d, a.dv = 0, 1, 1, 128, 128, 128, 256
-    v = _lib.View(4096, 128, 128 * 128, 128)
+    v = _lib.View(_addr(), 128, 128 * 128, 128)
     a.q = a.k = a.v = a.o = a.grad_o = a.grad_q = a.grad_k = a.grad_v = v
-    a.lse = a.ent = a.grad_ent = 4096
+    a.lse = a.ent = a.grad_ent = _addr()
     a.sm_scale = 0.1
-    a.v1, a.dv1 = _lib.View(8192, 128, 128 * 128, 256), 128    # token stride differs from v's
+    a.v1, a.dv1 = _lib.View(_addr(4096), 128, 128 * 128, 256), 128    # token stride differs from v's
     assert L.vmo_fea_bwd(ctypes.byref(a), None) == 1
     assert b"v1" in L.vmo_last_error()
-    a.v1, a.dv1 = _lib.View(8192, 128, 128 * 128, 128), 64     # parts of unequal width
+    a.v1, a.dv1 = _lib.View(_addr(4096), 128, 128 * 128, 128), 64     # parts of unequal width
     assert L.vmo_fea_bwd(ctypes.byref(a), None) == 2
     a.dv1 = 256                                                 # no first part left
     assert L.vmo_fea_bwd(ctypes.byref(a), None) == 1
@@ -169,22 +185,22 @@ def test_fea_bwd_fold_k_needs_values_that_start_with_k(L):
     from vmonarch_amd import _lib
     a = _lib.FeaBwdArgs()
     a.dtype, a.batch, a.heads, a.nq, a.nk, a.d, a.dv = 0, 1, 1, 128, 128, 128, 128
-    v = _lib.View(4096, 128, 128 * 128, 128)
+    v = _lib.View(_addr(), 128, 128 * 128, 128)
     a.q = a.k = a.o = a.grad_o = a.grad_q = a.grad_k = v
-    a.v = _lib.View(8192, 128, 128 * 128, 128)          # not k
+    a.v = _lib.View(_addr(4096), 128, 128 * 128, 128)          # not k
     a.grad_v = _lib.View()                              # values k alone write no grad_v
-    a.lse = a.ent = a.grad_ent = 4096
+    a.lse = a.ent = a.grad_ent = _addr()
     a.sm_scale = 0.1
     a.flags = _lib.BWD_FOLD_K
     assert L.vmo_fea_bwd(ctypes.byref(a), None) == 1
     assert b"FOLD_K" in L.vmo_last_error()
-    a.v = _lib.View(4096, 128, 128 * 128, 256)          # k's address with another token stride
+    a.v = _lib.View(_addr(), 128, 128 * 128, 256)          # k's address with another token stride
     assert L.vmo_fea_bwd(ctypes.byref(a), None) == 1
     # values k at d = dv = 256: a valid request this build has no fold kernel for, rejected by the host
     # checks (no workspace is passed, so a call that got past them would still stop at the workspace
-    # check and never launch on these made-up addresses)
+    # check and never launch)
     a.d = a.dv = 256
-    a.q = a.k = a.v = a.o = a.grad_o = a.grad_q = a.grad_k = _lib.View(4096, 256, 256 * 128, 256)
+    a.q = a.k = a.v = a.o = a.grad_o = a.grad_q = a.grad_k = _lib.View(_addr(), 256, 256 * 128, 256)
     assert L.vmo_fea_bwd(ctypes.byref(a), None) == 2
     assert b"FOLD_K" in L.vmo_last_error()
 
@@ -195,11 +211,11 @@ def test_fea_bwd_sum_needs_a_base_and_no_fp32_bits(L):
     from vmonarch_amd import _lib
     a = _lib.FeaBwdArgs()
     a.dtype, a.batch, a.heads, a.nq, a.nk, a.d, a.dv = 0, 1, 1, 128, 128, 128, 128
-    v = _lib.View(4096, 128, 128 * 128, 128)
+    v = _lib.View(_addr(), 128, 128 * 128, 128)
     a.q = a.k = a.v = a.o = a.grad_o = a.grad_q = a.grad_k = a.grad_v = v
-    a.lse = a.ent = a.grad_ent = 4096
+    a.lse = a.ent = a.grad_ent = _addr()
     a.sm_scale = 0.1
-    a.grad_k_base = a.grad_v_base = _lib.View(1 << 16, 128, 128 * 128, 128)
+    a.grad_k_base = a.grad_v_base = _lib.View(_addr(1 << 16), 128, 128 * 128, 128)
     for flags in (_lib.BWD_SUM_K | _lib.BWD_ACCUM_K, _lib.BWD_SUM_V | _lib.BWD_F32_V):
         a.flags = flags
         assert L.vmo_fea_bwd(ctypes.byref(a), None) == 1
@@ -212,7 +228,7 @@ def test_fea_bwd_sum_needs_a_base_and_no_fp32_bits(L):
 
 def test_fea_fwd_noalloc_rejects_oversized_splits_without_launching(L):
     """vmo_fea_fwd_noalloc holds the split-KV partials in a fixed library scratch: a call whose partials
-    would not fit is rejected with VMO_ERR_WORKSPACE before any launch (addresses never dereferenced)."""
+    would not fit is rejected with VMO_ERR_WORKSPACE before any launch."""
     from vmonarch_amd import _lib
     a = _fwd_args(nq=4096, nk=65536, num_splits=16, heads=8)
     need = L.vmo_fea_fwd_workspace_size(ctypes.byref(a))
