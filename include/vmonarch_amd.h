@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define VMO_ABI_VERSION 9
+#define VMO_ABI_VERSION 10
 
 enum {
   VMO_OK = 0,
@@ -144,7 +144,15 @@ enum {
    * + this call's gradient: the last of several calls that sum one gradient writes it once, in the
    * caller's dtype, instead of adding into fp32 and converting afterwards.  Not with ACCUM / F32 of
    * the same gradient. */
-  VMO_BWD_SUM_K = 128, VMO_BWD_SUM_V = 256
+  VMO_BWD_SUM_K = 128, VMO_BWD_SUM_V = 256,
+  /* Route for grad_q, results within rounding of each other.  Recompute route: a dq pass recomputes S
+   * and dP.  dS route: the dkdv pass stores dS^T (16-bit, nk and nq rounded up to 32, per problem) in
+   * the workspace and grad_q = sm_scale dS k is a GEMM over it -- no second S and dP, 4 bytes of HBM
+   * traffic per query-key pair instead.  By default the dS route is taken for d = 128 with dv = 256
+   * (where the recompute is dearest) while dS^T of all problems stays within 4 GiB;
+   * VMO_BWD_RECOMPUTE_DQ never takes it, VMO_BWD_DS_DQ takes it for any d in {64, 128} (not both).
+   * vmo_fea_bwd_workspace_size() includes the dS^T bytes when the route is taken. */
+  VMO_BWD_RECOMPUTE_DQ = 512, VMO_BWD_DS_DQ = 1024
 };
 
 typedef struct vmo_fea_bwd_args {
@@ -162,7 +170,8 @@ typedef struct vmo_fea_bwd_args {
   float sm_scale;
   void* workspace;
   size_t workspace_bytes;
-  int32_t flags;                   /* VMO_BWD_ACCUM_* | VMO_BWD_F32_* | VMO_BWD_FOLD_K | VMO_BWD_SUM_* */
+  int32_t flags;                   /* VMO_BWD_ACCUM_* | VMO_BWD_F32_* | VMO_BWD_FOLD_K | VMO_BWD_SUM_* |
+                                      VMO_BWD_RECOMPUTE_DQ | VMO_BWD_DS_DQ */
   /* Values given in two parts: with dv1 > 0 the value tensor is [v | v1], v holding columns
    * [0, dv - dv1) and v1 (same strides as v) the last dv1 (VMonarch's last R-step, values [k | v],
    * vmonarch.py:50, without the concatenated copy).  Built for dv1 = dv / 2 with (d, dv) = (64, 128)

@@ -144,7 +144,8 @@ def test_fea_bwd_rejects_unknown_and_conflicting_flags(L):
     a.q = a.k = a.v = a.o = a.grad_o = a.grad_q = a.grad_k = a.grad_v = v
     a.lse = a.ent = a.grad_ent = _addr()
     a.sm_scale = 0.1
-    for flags in (_lib.BWD_ACCUM_K | _lib.BWD_F32_K, _lib.BWD_ACCUM_Q | _lib.BWD_F32_Q, 512):
+    for flags in (_lib.BWD_ACCUM_K | _lib.BWD_F32_K, _lib.BWD_ACCUM_Q | _lib.BWD_F32_Q, 2048,
+                  _lib.BWD_RECOMPUTE_DQ | _lib.BWD_DS_DQ):
         a.flags = flags
         assert L.vmo_fea_bwd(ctypes.byref(a), None) == 1
         assert b"flags" in L.vmo_last_error()
@@ -236,3 +237,29 @@ def test_fea_fwd_noalloc_rejects_oversized_splits_without_launching(L):
     assert L.vmo_fea_fwd_noalloc(ctypes.byref(a), None) == 3
     assert b"scratch" in L.vmo_last_error()
     assert L.vmo_fea_fwd_noalloc(None, None) == 1
+
+
+def test_fea_bwd_workspace_holds_ds_for_the_ds_route(L):
+    """The dS route keeps dS^T (problems x nk x nq, both rounded up to 32, 16-bit) in the workspace.  It is
+    the default for d = 128 with dv = 256 under the size cap and is taken for any d in {64, 128} with
+    VMO_BWD_DS_DQ; with VMO_BWD_RECOMPUTE_DQ, for other head dims, for dv = d without the flag, or past the
+    cap, only the small recompute-route workspace is asked for."""
+    from vmonarch_amd import _lib
+    a = _lib.FeaBwdArgs()
+    a.dtype, a.batch, a.heads, a.frames, a.nq, a.nk, a.d, a.dv = 0, 1, 3, 7, 1557, 1000, 128, 256
+    with_ds = L.vmo_fea_bwd_workspace_size(ctypes.byref(a))
+    a.flags = _lib.BWD_RECOMPUTE_DQ
+    without = L.vmo_fea_bwd_workspace_size(ctypes.byref(a))
+    assert with_ds - without == 21 * 1024 * 1568 * 2
+    a.flags, a.dv = 0, 128                        # dv = d: the recompute route unless asked for
+    assert L.vmo_fea_bwd_workspace_size(ctypes.byref(a)) == without
+    a.flags = _lib.BWD_DS_DQ
+    assert L.vmo_fea_bwd_workspace_size(ctypes.byref(a)) == with_ds
+    a.flags, a.d, a.dv = _lib.BWD_DS_DQ, 256, 256   # no dS route for d = 256
+    big_d = L.vmo_fea_bwd_workspace_size(ctypes.byref(a))
+    a.flags = _lib.BWD_RECOMPUTE_DQ
+    assert big_d == L.vmo_fea_bwd_workspace_size(ctypes.byref(a))
+    a.flags, a.d, a.dv, a.heads, a.nq, a.nk = 0, 128, 256, 24, 16384, 16384   # 12.9 GB of dS^T: past the cap
+    capped = L.vmo_fea_bwd_workspace_size(ctypes.byref(a))
+    a.flags = _lib.BWD_RECOMPUTE_DQ
+    assert capped == L.vmo_fea_bwd_workspace_size(ctypes.byref(a))

@@ -12,7 +12,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libvmonarch_gfx950.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 FEA_FWD_SCRATCH_BYTES = 32 << 20   # VMO_FEA_FWD_SCRATCH_BYTES: scratch of vmo_fea_fwd_noalloc per GPU
 DTYPES = {torch.bfloat16: 0, torch.float16: 1}
 
@@ -51,6 +51,7 @@ BWD_ACCUM_Q, BWD_ACCUM_K, BWD_ACCUM_V = 1, 2, 4
 BWD_F32_Q, BWD_F32_K, BWD_F32_V = 8, 16, 32
 BWD_FOLD_K = 64   # values k or [k | v1]: k's value-role gradient into grad_k, grad_v holds v1's
 BWD_SUM_K, BWD_SUM_V = 128, 256   # grad (dtype) = fp32 base + this call's gradient
+BWD_RECOMPUTE_DQ, BWD_DS_DQ = 512, 1024   # grad_q route: recompute S and dP / GEMM over a stored dS^T
 LSTEP_BWD_OVERWRITE_Q = 1
 
 

@@ -67,6 +67,8 @@ struct BwdParams {
   int fold_k;                      // (values k or [k | v1]) k's value-role gradient goes into dk; dv holds v1's
   const void* dk_base;             // VMO_BWD_SUM_K / _V: fp32 rows added to dk / dv before their dtype store
   const void* dv_base;
+  void* ds;                        // dS route: dS^T of every problem in 32 x 32 blocks (the inputs' dtype),
+  int ds_kblocks, ds_qblocks;      // (problems, ceil(nk / 32), ceil(nq / 32), 32 keys, 32 queries)
   int64_t dkb_sb, dkb_sh, dkb_sn, dvb_sb, dvb_sh, dvb_sn;
   float c;          // sm_scale * log2(e)
   float sm_scale;
@@ -262,6 +264,23 @@ constexpr int dkdv_lds_bytes() {
 template <int D, int DV, bool W0K>
 constexpr int dq_staged_dv() { return W0K ? DV - D : DV; }
 
+// The dq kernels' epilogue: a wave's 32 rows of dQ (accumulated unscaled, times sm_scale here) as the fp32
+// partial of its key split (summed by fea_bwd_dq_reduce), or into grad_q in the mode the flags ask for.
+template <bool F16, int D>
+__device__ __forceinline__ void store_dq(const BwdParams& p, const f32x16 (&acc)[D / 32], VMO_LDS float* patch,
+                                         int prob, int split, int bb, int hh, int64_t qoff, int q0, int lane) {
+  const int nrows = min(32, p.nq - q0);
+  if (p.dq_splits > 1) {
+    float* pr = p.dq_part + (((int64_t)split * p.problems + prob) * p.nq + q0) * D;
+    store_acc_rows<F16>(patch, acc, D / 32, p.sm_scale, kGradStoreF32, (char*)pr, (int64_t)D * 4, nrows, lane);
+  } else {
+    const int mode = grad_mode(p.accum, VMO_BWD_ACCUM_Q, VMO_BWD_F32_Q);
+    const int64_t es = mode == kGradStore ? 2 : 4;
+    char* row0 = (char*)p.dq + (bb * p.dq_sb + hh * p.dq_sh + (qoff + q0) * p.dq_sn) * es;
+    store_acc_rows<F16>(patch, acc, D / 32, p.sm_scale, mode, row0, p.dq_sn * es, nrows, lane);
+  }
+}
+
 template <bool F16, int D, int DV, bool V2, bool W0K>
 __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq_kernel(BwdParams p) {
   using E = Elem<F16>;
@@ -415,17 +434,7 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
   if (n_full < n_tiles) iteration(n_full, std::true_type{});
   __syncthreads();   // every wave is done with the stage ring, which the epilogue patches reuse
   if (!wave_live) return;
-  VMO_LDS float* patch = (VMO_LDS float*)(smem + wave * kEpiPatchBytes);
-  const int nrows = min(32, p.nq - q0);
-  if (p.dq_splits > 1) {   // fp32 partial of this key range; fea_bwd_dq_reduce sums the splits
-    float* pr = p.dq_part + (((int64_t)split * p.problems + prob) * p.nq + q0) * D;
-    store_acc_rows<F16>(patch, acc, NA, p.sm_scale, kGradStoreF32, (char*)pr, (int64_t)D * 4, nrows, lane);
-  } else {
-    const int mode = grad_mode(p.accum, VMO_BWD_ACCUM_Q, VMO_BWD_F32_Q);
-    const int64_t es = mode == kGradStore ? 2 : 4;
-    char* row0 = (char*)p.dq + (bb * p.dq_sb + hh * p.dq_sh + (qoff + q0) * p.dq_sn) * es;
-    store_acc_rows<F16>(patch, acc, NA, p.sm_scale, mode, row0, p.dq_sn * es, nrows, lane);
-  }
+  store_dq<F16, D>(p, acc, (VMO_LDS float*)(smem + wave * kEpiPatchBytes), prob, split, bb, hh, qoff, q0, lane);
 }
 
 // Sum the split-KV partials of dQ (fixed split order, so the result does not depend on timing) and
@@ -457,7 +466,155 @@ __global__ __launch_bounds__(256) void fea_bwd_dq_reduce(BwdParams p) {
 }
 
 // ------------------------------------------------------------------------------------------------
-template <bool F16, int D, int DV, int PART, bool W0K>
+// The dS route.  For short rows (VMonarch's frame blocks: 1560 keys) the dq kernel above spends most of
+// its MFMAs recomputing S and dP; here the dkdv kernel, which forms dS anyway, stores it (dS^T, in the
+// inputs' dtype -- the value both routes feed the dQ MFMAs), and dQ = sm_scale dS K becomes a GEMM that
+// streams it back.  Three launches: fea_bwd_prep (the per-row scalars the dq kernel's prologue forms),
+// fea_bwd_dkdv with DS, fea_bwd_dq_ds (+ fea_bwd_dq_reduce for key splits).
+
+// delta = o . dO of every query row (fp32), then alpha = -delta - dE E and beta = -dE ln 2 into the
+// workspace; DV / 8 lanes per row, 16 bytes each.
+template <bool F16, int DV>
+__global__ __launch_bounds__(256) void fea_bwd_prep_kernel(BwdParams p) {
+  using T = typename Elem<F16>::T;
+  using V8 = typename Elem<F16>::V8;
+  constexpr int TPR = DV / 8;
+  static_assert(TPR >= 8 && TPR <= 64 && 64 % TPR == 0, "row lanes within one wave");
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t rows = (int64_t)p.problems * p.nq;
+  const int64_t row = gid / TPR;
+  const int part = (int)(gid % TPR);
+  const int64_t rr = row < rows ? row : rows - 1;
+  const int prob = (int)(rr / p.nq), qi = (int)(rr % p.nq);
+  const int fr = prob % p.frames, bh = prob / p.frames, hh = bh % p.heads, bb = bh / p.heads;
+  const int64_t qrow = (int64_t)fr * p.nq + qi;
+  const V8 x = *(const V8*)((const T*)p.dO + bb * p.do_sb + hh * p.do_sh + qrow * p.do_sn + 8 * part);
+  const V8 y = *(const V8*)((const T*)p.o + bb * p.o_sb + hh * p.o_sh + qrow * p.o_sn + 8 * part);
+  float d = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) d = fmaf((float)x[e], (float)y[e], d);
+#pragma unroll
+  for (int m = TPR / 2; m >= 1; m >>= 1) d += __shfl_xor(d, m);
+  if (row < rows && part == 0) {
+    const int64_t si = bb * p.st_sb + hh * p.st_sh + qrow;
+    const float dE = p.dent[bb * p.de_sb + hh * p.de_sh + qrow];
+    p.alpha[row] = -d - dE * p.ent[si];
+    p.beta[row] = -dE * kLn2;
+  }
+}
+
+// dQ from the stored dS^T: one workgroup = 128 queries (32 per wave) of one problem and one key range,
+// 64-key stages of K rows and of dS^T (keys x the tile's 128 query columns, gathered from the 32 x 32
+// blocks) staged by global_load_lds; dQ^T += K^T dS^T with both operands read transposed
+// (ds_read_tr16_b64), so both hold the same 4-key groups.
+template <bool F16, int D>
+__global__ __launch_bounds__(256, 2) void fea_bwd_dq_ds_kernel(BwdParams p) {
+  using E = Elem<F16>;
+  using T = typename E::T;
+  using V8 = typename E::V8;
+  constexpr int K_BYTES = kDqBN * D * 2;
+  constexpr int SRB = kDqBM * 2;   // bytes of one staged dS^T row
+  constexpr int STAGE = K_BYTES + kDqBN * SRB;
+  constexpr int NA = D / 32;
+  extern __shared__ __attribute__((aligned(1024))) char smem_raw[];
+  VMO_LDS char* smem = (VMO_LDS char*)smem_raw;
+
+  const int L = xcd_remap(gridDim.x);
+  if (L >= p.dq_total) return;
+  auto uni = [](int x) __attribute__((always_inline)) { return __builtin_amdgcn_readfirstlane(x); };
+  const int qt = uni(L % p.dq_tiles), split = uni((L / p.dq_tiles) % p.dq_splits);
+  const int prob = uni(L / p.dq_tiles / p.dq_splits);
+  const int kbeg = split * p.keys_per_split;
+  const int kend = min(p.nk, kbeg + p.keys_per_split);
+  const int fr = uni(prob % p.frames), bh = uni(prob / p.frames);
+  const int hh = uni(bh % p.heads), bb = uni(bh / p.heads);
+  const int64_t qoff = (int64_t)fr * p.nq, koff = (int64_t)fr * p.nk;
+  const int tid = threadIdx.x, wave = uni(tid >> 6), lane = tid & 63, hl = lane >> 5;
+  const int q0 = qt * kDqBM + wave * 32;
+  const bool wave_live = q0 < p.nq;
+
+  const T* kb = (const T*)p.k + bb * p.k_sb + hh * p.k_sh + koff * p.k_sn;
+  const int n_tiles = (kend - kbeg + kDqBN - 1) / kDqBN;
+  const uint32_t smem_u32 = (uint32_t)(uintptr_t)smem;
+  const BwdTileCopy<T, D, kDqBN> kcopy(kb, p.k_sn, wave, lane);
+  // The dS^T tile of a stage, [64 keys][128 queries] in LDS with the swz_rows<256> chunk swizzle: wave
+  // instruction i (of 4) fills rows 4 (4 i + wave) .. + 3, lane l row 4 (4 i + wave) + l / 16 at chunk
+  // position l % 16, i.e. the 16 bytes of logical chunk lc = (l % 16) ^ swz(row): 8 queries of query
+  // block 4 qt + lc / 4.  Blocks past the last (the last tile's columns past nq) are clamped to it: they
+  // only feed dQ rows that are never written.  Per lane, the byte offset from the stage's first key block.
+  const uint64_t s_prob = uniform64((uint64_t)(uintptr_t)p.ds + (uint64_t)prob * p.ds_kblocks * p.ds_qblocks * 2048);
+  const int qbs = p.ds_qblocks;
+  uint32_t s_off[4];
+  int s_row[4], s_col[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    s_row[i] = 4 * (4 * i + wave) + lane / 16;
+    const int lc = (lane % 16) ^ swz_rows<SRB>(s_row[i]);
+    s_col[i] = min(qt * 4 + lc / 4, qbs - 1) * 2048 + (lc & 3) * 16;
+    s_off[i] = (uint32_t)(((s_row[i] >> 5) * qbs) * 2048 + (s_row[i] & 31) * 64 + s_col[i]);
+  }
+  auto issue = [&](int t) {
+    const uint32_t st = smem_u32 + (uint32_t)((t & 1) * STAGE);
+    const int row0 = kbeg + t * kDqBN;
+    kcopy.issue(row0, kend, st);
+    if (row0 + kDqBN <= kend) {
+      const uint64_t sbase = s_prob + (uint64_t)(row0 >> 5) * qbs * 2048;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dma16_async_s(sbase, s_off[i], st + K_BYTES + (4 * i + wave) * 1024);
+    } else {   // the last, partial stage: keys past the range repeat its last key (masked below)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int gr = min(row0 + s_row[i], kend - 1);
+        const uint64_t src = s_prob + ((uint64_t)(gr >> 5) * qbs) * 2048 + (gr & 31) * 64 + s_col[i];
+        dma16_async((const void*)(uintptr_t)src, st + K_BYTES + (4 * i + wave) * 1024);
+      }
+    }
+  };
+
+  f32x16 acc[NA];
+#pragma unroll
+  for (int a = 0; a < NA; ++a) acc[a] = f32x16{};
+  const int trow = 4 * hl + ((lane & 15) >> 2);
+  const int tchunk = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+  const int tbyte = (lane & 1) * 8;
+  const int s_tr = tr_offset<SRB>(trow, tchunk, tbyte, wave);   // the wave's 32 query columns
+
+  auto iteration = [&](int t, auto masked_tag) __attribute__((always_inline)) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
+    tile_sync<0>();   // stage t has landed for every wave, and stage t - 1's slot is free
+    if (t + 1 < n_tiles) issue(t + 1);
+    if (!wave_live) return;
+    const VMO_LDS char* Ks = smem + (t & 1) * STAGE;
+    const VMO_LDS char* Ss = Ks + K_BYTES;
+    // dS^T operands of the four 16-key chunks: element e of chunk c is key 16 c + 8 (e / 4) + 4 hl + e % 4
+    V8 G[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) G[c] = tr_pair<V8, SRB>(Ss + 16 * c * SRB, s_tr);
+    if constexpr (MASKED) {   // the staged rows past the key range repeat its last row
+      const int nvalid = kend - kbeg - t * kDqBN;
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (16 * c + 8 * (e >> 2) + 4 * hl + (e & 3) >= nvalid) G[c][e] = to_elem<T>(0.f);
+    }
+    prefetched_chain<4 * NA, kBwdPrefetch>(
+        [&](int i) __attribute__((always_inline)) {
+          return tr_pair<V8, D * 2>(Ks + 16 * (i % 4) * (D * 2), tr_offset<D * 2>(trow, tchunk, tbyte, i / 4));
+        },
+        [&](int i, const V8& x) __attribute__((always_inline)) { acc[i / 4] = E::mfma(x, G[i % 4], acc[i / 4]); });
+  };
+  issue(0);
+  const int n_full = (kend - kbeg) / kDqBN;
+  for (int t = 0; t < n_full; ++t) iteration(t, std::false_type{});
+  if (n_full < n_tiles) iteration(n_full, std::true_type{});
+  __syncthreads();   // every wave is done with the stage ring, which the epilogue patches reuse
+  if (!wave_live) return;
+  store_dq<F16, D>(p, acc, (VMO_LDS float*)(smem + wave * kEpiPatchBytes), prob, split, bb, hh, qoff, q0, lane);
+}
+
+// ------------------------------------------------------------------------------------------------
+template <bool F16, int D, int DV, int PART, bool W0K, bool DS>
 __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea_bwd_dkdv_kernel(BwdParams p) {
   using E = Elem<F16>;
   using T = typename E::T;
@@ -476,6 +633,7 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
   constexpr int VW = dkdv_v_width<D, DV, W0K>();   // V columns held (LDS tile or registers)
   constexpr int V_TILE = V_LDS ? kKvBN * VW * 2 : 0;
   static_assert(!W0K || DV == 2 * D || DV == D, "values k or [k | v1]");
+  static_assert(!DS || PART != 2, "the dS route stores dS from the launch that forms it");
   extern __shared__ __attribute__((aligned(1024))) char smem_raw[];
   VMO_LDS char* smem = (VMO_LDS char*)smem_raw;
 
@@ -527,6 +685,9 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
 
   const int n_tiles = (p.nq + kKvBM - 1) / kKvBM;
   const uint32_t smem_u32 = (uint32_t)(uintptr_t)smem;
+  // dS route: the wave's row of 32 x 32 dS^T blocks (keys k0 .. k0 + 31, one block per query stage)
+  const uint64_t ds_base =
+      DS ? uniform64((uint64_t)(uintptr_t)p.ds + (((uint64_t)prob * p.ds_kblocks + (k0 >> 5)) * p.ds_qblocks) * 2048) : 0;
   const BwdTileCopy<T, D, kKvBM> qcopy(qb, p.q_sn, wave, lane);
   const BwdTileCopy<T, DOW, kKvBM> docopy(dob + VOFF, p.do_sn, wave, lane);
   auto issue = [&](int t) {
@@ -632,6 +793,26 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
         G[r >> 3][r & 7] = to_elem<T>(gv);
       }
     }
+
+    if constexpr (DS) {
+      // The stage's 32 x 32 block of dS^T (unscaled; the dq GEMM applies sm_scale), row = key l32, 64 bytes of
+      // 32 queries.  Lane (l32, hl) holds queries 8 g + 4 hl .. + 3 of G[g / 2]; two permlane32 swaps per
+      // operand trade the halves so that the lower lanes hold whole 8-query chunks 0 and 2 and the upper
+      // lanes chunks 1 and 3: two 16-byte stores per lane, each wave store inside one 2 KB block.  Issued before
+      // the dV / dK MFMAs, which hide their latency from the next stage's wait for its copies.
+      typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+      // a global (not flat) store: a flat one would also hold every later LDS wait (lgkmcnt) until it lands
+      typedef __attribute__((address_space(1))) u32x4 global_u32x4;
+      const uint64_t blk = ds_base + (uint64_t)t * 2048 + l32 * 64 + hl * 16;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        u32x4 w = __builtin_bit_cast(u32x4, G[j]);
+        const auto s0 = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
+        const auto s1 = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+        w = u32x4{s0[0], s1[0], s0[1], s1[1]};
+        *(global_u32x4*)(blk + 32 * j) = w;
+      }
+    }
     // dV^T[dv][key] += dO^T P,  dK^T[d][key] += Q^T dS  (transposed reads of the staged tiles)
     constexpr int NT = 2 * NV + (WANT_DK ? 2 * NK : 0);
     prefetched_chain<NT, kBwdPrefetch>(
@@ -695,11 +876,11 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
   put(p.dv, p.dv_sb, p.dv_sh, p.dv_sn, VOFF, dv, NV, 1.0f, mode_v, p.dv_base, p.dvb_sb, p.dvb_sh, p.dvb_sn);
 }
 
-template <bool F16, int D, int DV, int PART, bool W0K>
+template <bool F16, int D, int DV, int PART, bool W0K, bool DS = false>
 static int launch_dkdv(const BwdParams& p, hipStream_t s) {
   constexpr int LDS_KV = dkdv_lds_bytes<D, DV, PART, W0K>();
   static_assert(LDS_KV <= 160 * 1024 && LDS_KV >= kBwdWaves * kEpiPatchBytes, "dkdv LDS");
-  auto kern = fea_bwd_dkdv_kernel<F16, D, DV, PART, W0K>;
+  auto kern = fea_bwd_dkdv_kernel<F16, D, DV, PART, W0K, DS>;
   if (LDS_KV > 65536) {
     static bool done = false;
     if (!done) {
@@ -712,8 +893,39 @@ static int launch_dkdv(const BwdParams& p, hipStream_t s) {
   return launch_status("fea_bwd_dkdv");
 }
 
+// Head dims the dS route is built for (the host takes it only for these).
+template <int D>
+constexpr bool bwd_ds_built() { return D == 64 || D == 128; }
+
+template <bool F16, int D, int DV, bool W0K>
+static int launch_bwd_ds(const BwdParams& p, hipStream_t s) {
+  const int64_t threads = (int64_t)p.problems * p.nq * (DV / 8);
+  hipLaunchKernelGGL((fea_bwd_prep_kernel<F16, DV>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, p);
+  int rc = launch_status("fea_bwd_prep");
+  if (rc != VMO_OK) return rc;
+  if constexpr (dkdv_parts<D, DV, W0K>() == 1) {
+    rc = launch_dkdv<F16, D, DV, 0, W0K, true>(p, s);
+  } else {
+    rc = launch_dkdv<F16, D, DV, 1, W0K, true>(p, s);
+    if (rc == VMO_OK) rc = launch_dkdv<F16, D, DV, 2, false>(p, s);
+  }
+  if (rc != VMO_OK) return rc;
+  constexpr int LDS = 2 * kDqBN * (D + kDqBM) * 2;
+  static_assert(LDS <= 65536 && LDS >= kBwdWaves * kEpiPatchBytes, "dq_ds LDS");
+  hipLaunchKernelGGL((fea_bwd_dq_ds_kernel<F16, D>), dim3(xcd_grid(p.dq_total)), dim3(256), LDS, s, p);
+  rc = launch_status("fea_bwd_dq_ds");
+  if (rc != VMO_OK || p.dq_splits == 1) return rc;
+  const int64_t rthreads = (int64_t)p.problems * p.nq * (D / 4);
+  hipLaunchKernelGGL((fea_bwd_dq_reduce<F16, D>), dim3((unsigned)((rthreads + 255) / 256)), dim3(256), 0, s, p);
+  return launch_status("fea_bwd_dq_reduce");
+}
+
 template <bool F16, int D, int DV, bool V2 = false, bool W0K = false>
 static int launch_bwd(const BwdParams& p, hipStream_t s) {
+  if (p.ds) {
+    if constexpr (bwd_ds_built<D>()) return launch_bwd_ds<F16, D, DV, W0K>(p, s);
+    return set_error(VMO_ERR_UNSUPPORTED, "fea_bwd: no dS route for d=%d", D);
+  }
   constexpr int LDS_DQ = 2 * kDqBN * (D + dq_staged_dv<D, DV, W0K>()) * 2;
   static_assert(LDS_DQ <= 160 * 1024 && LDS_DQ >= kBwdWaves * kEpiPatchBytes, "bwd LDS");
   if (LDS_DQ > 65536) {
@@ -787,6 +999,23 @@ static int bwd_keys_per_split(int nk, int splits) {
   return ((nk + splits - 1) / splits + kDqBN - 1) / kDqBN * kDqBN;
 }
 static size_t bwd_stats_bytes(int64_t problems, int nq) { return ((size_t)2 * problems * nq * 4 + 255) / 256 * 256; }
+// The dS route (dkdv stores dS^T, dQ is a GEMM over it) trades the dq kernel's recompute of S and dP --
+// 2 (d + dv) flops per query-key pair -- for 4 bytes of HBM traffic per pair (dS^T written and read
+// back).  Measured on the VMonarch cfg4 geometries (1560 x 1560 problems), it wins where the recompute
+// is dearest -- d = 128 with dv = 256 (the last R-step, values [k | v]; its dq kernel runs one wave per
+// SIMD): 1.78 against 1.95-2.0 ms -- and loses for dv = d (R-step 0: 1.27 against 1.07 ms; the recompute
+// backward: 1.08 against 1.04 ms), where the dkdv kernel is already close to the HBM bandwidth it shares
+// with the write stream.  So it is taken by default for d = 128, dv = 256 while dS^T of all problems
+// (32 x 32 blocks, keys and queries rounded up to 32) stays within kBwdDsMaxBytes; VMO_BWD_DS_DQ asks for
+// it at any size with d in {64, 128}, VMO_BWD_RECOMPUTE_DQ never.  Returns the workspace bytes it needs,
+// 0 when not taken.
+constexpr int64_t kBwdDsMaxBytes = 4ll << 30;
+static size_t bwd_ds_bytes(const vmo_fea_bwd_args* a, int64_t problems) {
+  if ((a->flags & VMO_BWD_RECOMPUTE_DQ) || (a->d != 64 && a->d != 128)) return 0;
+  const int64_t total = problems * ((a->nk + 31) / 32) * ((a->nq + 31) / 32) * 2048;
+  if (a->flags & VMO_BWD_DS_DQ) return (size_t)total;
+  return a->d == 128 && a->dv == 256 && total <= kBwdDsMaxBytes ? (size_t)total : 0;
+}
 }  // namespace vmo
 
 extern "C" size_t vmo_fea_bwd_workspace_size(const vmo_fea_bwd_args* a) {
@@ -795,8 +1024,8 @@ extern "C" size_t vmo_fea_bwd_workspace_size(const vmo_fea_bwd_args* a) {
   const int64_t problems = (int64_t)a->batch * a->heads * (a->frames > 0 ? a->frames : 1);
   const int splits = bwd_dq_splits(problems, a->nq, a->nk);
   size_t bytes = bwd_stats_bytes(problems, a->nq) + 256;
-  if (splits > 1) bytes += (size_t)splits * problems * a->nq * (a->d > 0 ? a->d : 0) * 4;
-  return bytes;
+  if (splits > 1) bytes += ((size_t)splits * problems * a->nq * (a->d > 0 ? a->d : 0) * 4 + 255) / 256 * 256;
+  return bytes + bwd_ds_bytes(a, problems);
 }
 
 extern "C" int vmo_fea_bwd(const vmo_fea_bwd_args* a, void* stream) {
@@ -821,11 +1050,13 @@ extern "C" int vmo_fea_bwd(const vmo_fea_bwd_args* a, void* stream) {
       return set_error(VMO_ERR_INVALID, "fea_bwd: v1 needs 16-byte aligned rows and the strides of v");
   }
   constexpr int kFlags = VMO_BWD_ACCUM_Q | VMO_BWD_ACCUM_K | VMO_BWD_ACCUM_V | VMO_BWD_F32_Q | VMO_BWD_F32_K |
-                         VMO_BWD_F32_V | VMO_BWD_FOLD_K | VMO_BWD_SUM_K | VMO_BWD_SUM_V;
+                         VMO_BWD_F32_V | VMO_BWD_FOLD_K | VMO_BWD_SUM_K | VMO_BWD_SUM_V | VMO_BWD_RECOMPUTE_DQ |
+                         VMO_BWD_DS_DQ;
   const bool sum_k = (a->flags & VMO_BWD_SUM_K) != 0, sum_v = (a->flags & VMO_BWD_SUM_V) != 0;
   if ((a->flags & ~kFlags) || ((a->flags >> 3) & a->flags & 7) ||
       (sum_k && (a->flags & (VMO_BWD_ACCUM_K | VMO_BWD_F32_K))) ||
-      (sum_v && (a->flags & (VMO_BWD_ACCUM_V | VMO_BWD_F32_V))) || (sum_v && no_grad_v))
+      (sum_v && (a->flags & (VMO_BWD_ACCUM_V | VMO_BWD_F32_V))) || (sum_v && no_grad_v) ||
+      ((a->flags & VMO_BWD_RECOMPUTE_DQ) && (a->flags & VMO_BWD_DS_DQ)))
     return set_error(VMO_ERR_INVALID, "fea_bwd: unknown or conflicting flags 0x%x", (unsigned)a->flags);
   if ((sum_k && !view_ok(a->grad_k_base)) || (sum_v && !view_ok(a->grad_v_base)))
     return set_error(VMO_ERR_INVALID, "fea_bwd: VMO_BWD_SUM_K / _V need a grad_k_base / grad_v_base view "
@@ -874,6 +1105,13 @@ extern "C" int vmo_fea_bwd(const vmo_fea_bwd_args* a, void* stream) {
   p.dq_splits = bwd_dq_splits(problems, a->nq, a->nk);
   p.keys_per_split = bwd_keys_per_split(a->nk, p.dq_splits);
   p.dq_part = (float*)((char*)a->workspace + bwd_stats_bytes(problems, a->nq));
+  if (bwd_ds_bytes(a, problems)) {   // after the stats and the dq partials
+    size_t off = bwd_stats_bytes(problems, a->nq) + 256;
+    if (p.dq_splits > 1) off += ((size_t)p.dq_splits * problems * a->nq * a->d * 4 + 255) / 256 * 256;
+    p.ds = (char*)a->workspace + off;
+    p.ds_kblocks = (a->nk + 31) / 32;
+    p.ds_qblocks = (a->nq + 31) / 32;
+  }
   p.accum = a->flags;
   p.q_sb = a->q.stride_b; p.q_sh = a->q.stride_h; p.q_sn = a->q.stride_n;
   p.k_sb = a->k.stride_b; p.k_sh = a->k.stride_h; p.k_sn = a->k.stride_n;

@@ -14,7 +14,7 @@ def _pad_features(t, width):
 
 
 def fea_backward_raw(q, k, v, o, lse, ent, do, de, sm_scale, dq=None, dk=None, dv=None, overwrite="", v1=None,
-                     fold_k=False, dk_base=None, dv_base=None, frames=1):
+                     fold_k=False, dk_base=None, dv_base=None, frames=1, dq_route=None):
     """q: (B, H, F*nq, D); k: (B, H, F*nk, D); v: (B, H, F*nk, Dv); o, do: (B, H, F*nq, Dv);
     lse, ent, de: (B, H, F*nq) fp32 with unit token stride.  Returns (dq, dk, dv).
 
@@ -32,11 +32,16 @@ def fea_backward_raw(q, k, v, o, lse, ent, do, de, sm_scale, dq=None, dk=None, d
     as the first value columns, and dv only v1's (None without v1).
 
     `dk_base` / `dv_base` (float32, shaped like dk / dv): dk / dv, in q's dtype, are that base plus
-    this call's gradient (the last of several calls summing one gradient)."""
+    this call's gradient (the last of several calls summing one gradient).
+
+    `dq_route` ("recompute" or "ds"; None lets the library choose) picks how dq is formed: a pass that
+    recomputes S and dP, or a GEMM over dS^T stored by the dk / dv pass (the workspace then holds nk x nq
+    16-bit values per problem)."""
     L = _lib.lib()
     B, H, NQ, D = q.shape
     NK, Dv = k.shape[2], v.shape[-1] * (2 if v1 is not None else 1)
-    flags = _lib.BWD_FOLD_K if fold_k else 0
+    flags = (_lib.BWD_FOLD_K if fold_k else 0) | {None: 0, "recompute": _lib.BWD_RECOMPUTE_DQ,
+                                                   "ds": _lib.BWD_DS_DQ}[dq_route]
     for t, name, acc_bit, f32_bit, base in ((dq, "q", _lib.BWD_ACCUM_Q, _lib.BWD_F32_Q, None),
                                             (dk, "k", _lib.BWD_ACCUM_K, _lib.BWD_F32_K, dk_base),
                                             (dv, "v", _lib.BWD_ACCUM_V, _lib.BWD_F32_V, dv_base)):
