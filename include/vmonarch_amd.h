@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define VMO_ABI_VERSION 10
+#define VMO_ABI_VERSION 11
 
 enum {
   VMO_OK = 0,
@@ -152,7 +152,10 @@ enum {
    * (where the recompute is dearest) while dS^T of all problems stays within 4 GiB;
    * VMO_BWD_RECOMPUTE_DQ never takes it, VMO_BWD_DS_DQ takes it for any d in {64, 128} (not both).
    * vmo_fea_bwd_workspace_size() includes the dS^T bytes when the route is taken. */
-  VMO_BWD_RECOMPUTE_DQ = 512, VMO_BWD_DS_DQ = 1024
+  VMO_BWD_RECOMPUTE_DQ = 512, VMO_BWD_DS_DQ = 1024,
+  /* grad_q in the inputs' dtype = grad_q_base (fp32, shaped like grad_q) + this call's gradient, as
+   * VMO_BWD_SUM_K / _V.  Not with ACCUM_Q / F32_Q. */
+  VMO_BWD_SUM_Q = 2048
 };
 
 typedef struct vmo_fea_bwd_args {
@@ -171,7 +174,7 @@ typedef struct vmo_fea_bwd_args {
   void* workspace;
   size_t workspace_bytes;
   int32_t flags;                   /* VMO_BWD_ACCUM_* | VMO_BWD_F32_* | VMO_BWD_FOLD_K | VMO_BWD_SUM_* |
-                                      VMO_BWD_RECOMPUTE_DQ | VMO_BWD_DS_DQ */
+                                      VMO_BWD_RECOMPUTE_DQ | VMO_BWD_DS_DQ | VMO_BWD_SUM_Q */
   /* Values given in two parts: with dv1 > 0 the value tensor is [v | v1], v holding columns
    * [0, dv - dv1) and v1 (same strides as v) the last dv1 (VMonarch's last R-step, values [k | v],
    * vmonarch.py:50, without the concatenated copy).  Built for dv1 = dv / 2 with (d, dv) = (64, 128)
@@ -184,6 +187,7 @@ typedef struct vmo_fea_bwd_args {
    * rows [f*nk, (f+1)*nk) of k / v / v1 / grad_k / grad_v and the bases, so the R-steps' backward reads
    * a (B, H, m*b, .) tensor in any memory order (a DiT block's (B, N, H, D)) without a copy. */
   int32_t frames;
+  vmo_view grad_q_base;                /* fp32, read with VMO_BWD_SUM_Q */
 } vmo_fea_bwd_args;
 
 /*

@@ -144,7 +144,7 @@ def test_fea_bwd_rejects_unknown_and_conflicting_flags(L):
     a.q = a.k = a.v = a.o = a.grad_o = a.grad_q = a.grad_k = a.grad_v = v
     a.lse = a.ent = a.grad_ent = _addr()
     a.sm_scale = 0.1
-    for flags in (_lib.BWD_ACCUM_K | _lib.BWD_F32_K, _lib.BWD_ACCUM_Q | _lib.BWD_F32_Q, 2048,
+    for flags in (_lib.BWD_ACCUM_K | _lib.BWD_F32_K, _lib.BWD_ACCUM_Q | _lib.BWD_F32_Q, 4096,
                   _lib.BWD_RECOMPUTE_DQ | _lib.BWD_DS_DQ):
         a.flags = flags
         assert L.vmo_fea_bwd(ctypes.byref(a), None) == 1
@@ -207,7 +207,7 @@ def test_fea_bwd_fold_k_needs_values_that_start_with_k(L):
 
 
 def test_fea_bwd_sum_needs_a_base_and_no_fp32_bits(L):
-    """VMO_BWD_SUM_K / _V write the gradient in the inputs' dtype from an fp32 base: together with
+    """VMO_BWD_SUM_Q / _K / _V write the gradient in the inputs' dtype from an fp32 base: together with
     ACCUM / F32 of the same gradient, or without the base view, they are rejected."""
     from vmonarch_amd import _lib
     a = _lib.FeaBwdArgs()
@@ -216,15 +216,19 @@ def test_fea_bwd_sum_needs_a_base_and_no_fp32_bits(L):
     a.q = a.k = a.v = a.o = a.grad_o = a.grad_q = a.grad_k = a.grad_v = v
     a.lse = a.ent = a.grad_ent = _addr()
     a.sm_scale = 0.1
-    a.grad_k_base = a.grad_v_base = _lib.View(_addr(1 << 16), 128, 128 * 128, 128)
-    for flags in (_lib.BWD_SUM_K | _lib.BWD_ACCUM_K, _lib.BWD_SUM_V | _lib.BWD_F32_V):
+    a.grad_q_base = a.grad_k_base = a.grad_v_base = _lib.View(_addr(1 << 16), 128, 128 * 128, 128)
+    for flags in (_lib.BWD_SUM_K | _lib.BWD_ACCUM_K, _lib.BWD_SUM_V | _lib.BWD_F32_V, _lib.BWD_SUM_Q | _lib.BWD_F32_Q,
+                  _lib.BWD_SUM_Q | _lib.BWD_ACCUM_Q):
         a.flags = flags
         assert L.vmo_fea_bwd(ctypes.byref(a), None) == 1
         assert b"flags" in L.vmo_last_error()
-    a.flags = _lib.BWD_SUM_V
-    a.grad_v_base = _lib.View()
-    assert L.vmo_fea_bwd(ctypes.byref(a), None) == 1
-    assert b"SUM" in L.vmo_last_error()
+    for flag, field in ((_lib.BWD_SUM_V, "grad_v_base"), (_lib.BWD_SUM_Q, "grad_q_base")):
+        a.flags = flag
+        saved = getattr(a, field)
+        setattr(a, field, _lib.View())
+        assert L.vmo_fea_bwd(ctypes.byref(a), None) == 1
+        assert b"SUM" in L.vmo_last_error()
+        setattr(a, field, saved)
 
 
 def test_fea_fwd_noalloc_rejects_oversized_splits_without_launching(L):

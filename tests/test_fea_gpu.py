@@ -435,9 +435,10 @@ def test_fea_backward_fold_k(nq, nk, D, two_parts, dt):
                                                     (40, 4096, 128, 128, False, torch.float16),
                                                     (200, 700, 128, 256, True, torch.float16)])
 def test_fea_backward_sum_into_dtype(nq, nk, D, Dv, fold, dt):
-    """VMO_BWD_SUM_K / _V: dk, dv in the inputs' dtype = fp32 base + this call's gradient, bit for bit
-    the dtype rounding of the base plus the call's fp32 store (the dV columns split over two launches
-    at Dv = 256 included; with VMO_BWD_FOLD_K the folded dk and v1's dv)."""
+    """VMO_BWD_SUM_Q / _K / _V: dq, dk, dv in the inputs' dtype = fp32 base + this call's gradient, bit for
+    bit the dtype rounding of the base plus the call's fp32 store (dq from one key range or summed over key
+    splits, both dq routes; the dV columns split over two launches at Dv = 256 included; with
+    VMO_BWD_FOLD_K the folded dk and v1's dv)."""
     from vmonarch_amd.kernel import fea_forward
     from vmonarch_amd.kernel_bwd import fea_backward_raw
     g = torch.Generator().manual_seed(13 * nq + nk + D + Dv + fold)
@@ -455,14 +456,17 @@ def test_fea_backward_sum_into_dtype(nq, nk, D, Dv, fold, dt):
     args = (q, k, v if fold else w, o, lse, ent, do, de, D ** -0.5)
     f32 = dict(device=DEV, dtype=torch.float32)
     dvw = Dv - D if fold else Dv
-    dk32, dv32 = torch.empty(1, 2, nk, D, **f32), torch.empty(1, 2, nk, dvw, **f32)
-    dq_ref, _, _ = fea_backward_raw(*args, dk=dk32, dv=dv32, overwrite="kv", v1=v1, fold_k=fold)
     base_k, base_v = torch.randn(1, 2, nk, D, generator=g).to(DEV), torch.randn(1, 2, nk, dvw, generator=g).to(DEV)
-    dq, dk, dv = fea_backward_raw(*args, v1=v1, fold_k=fold, dk_base=base_k, dv_base=base_v)
-    assert dk.dtype == q.dtype and dv.dtype == q.dtype
-    assert torch.equal(dq, dq_ref.to(q.dtype)) or torch.equal(dq, fea_backward_raw(*args, v1=v1, fold_k=fold)[0])
-    assert torch.equal(dk, (base_k + dk32).to(q.dtype))
-    assert torch.equal(dv, (base_v + dv32).to(q.dtype))
+    base_q = torch.randn(1, 2, nq, D, generator=g).to(DEV)
+    for route in ("recompute", "ds"):
+        dq32, dk32, dv32 = (torch.empty(1, 2, n, w, **f32) for n, w in ((nq, D), (nk, D), (nk, dvw)))
+        fea_backward_raw(*args, dq=dq32, dk=dk32, dv=dv32, overwrite="qkv", v1=v1, fold_k=fold, dq_route=route)
+        dq, dk, dv = fea_backward_raw(*args, v1=v1, fold_k=fold, dq_base=base_q, dk_base=base_k, dv_base=base_v,
+                                      dq_route=route)
+        assert dq.dtype == q.dtype and dk.dtype == q.dtype and dv.dtype == q.dtype
+        assert torch.equal(dq, (base_q + dq32).to(q.dtype)), route
+        assert torch.equal(dk, (base_k + dk32).to(q.dtype)), route
+        assert torch.equal(dv, (base_v + dv32).to(q.dtype)), route
 
 
 @pytest.mark.parametrize("nq, nk, D", [(300, 300, 64), (300, 300, 128), (40, 4096, 128)])

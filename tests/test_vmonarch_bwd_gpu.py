@@ -81,17 +81,19 @@ def test_vmonarch_grad_reference_params(m, b, num_iters):
     assert hip_library_loaded()
 
 
-@pytest.mark.parametrize("rt", [0, 50, 230])
-def test_vmonarch_grad_recompute_lengths(rt):
+@pytest.mark.parametrize("iters, rt", [(2, 0), (2, 50), (2, 230), (1, 0), (1, 100)])
+def test_vmonarch_grad_recompute_lengths(iters, rt):
     """No recompute, a partial first frame, and a recompute reaching into the third frame: the rows
-    the recompute overwrites carry no L-path gradient, every other row keeps it."""
-    g = torch.Generator().manual_seed(40 + rt)
+    the recompute overwrites carry no L-path gradient, every other row keeps it.  With one iteration,
+    R-step 0 is also the last (values [k | v]): the sole writer of dv without a recompute, its last one
+    with."""
+    g = torch.Generator().manual_seed(40 + rt + iters)
     m, b = 4, 100
     q, k, v = (randn_lp(g, 1, 2, m * b, 64) for _ in range(3))
     do = torch.randn(1, 2, m * b, 64, generator=g)
-    print(f"vmonarch grad rt={rt}", flush=True)
-    _, grads = _grads(q, k, v, do, m, b, 2, rt)
-    ref = vmonarch_attention_grad(*(t.float().numpy() for t in (q, k, v)), do.numpy(), m, b, 2, rt)
+    print(f"vmonarch grad iters={iters} rt={rt}", flush=True)
+    _, grads = _grads(q, k, v, do, m, b, iters, rt)
+    ref = vmonarch_attention_grad(*(t.float().numpy() for t in (q, k, v)), do.numpy(), m, b, iters, rt)
     for gd, gr in zip(grads, ref):
         assert_grad_close(gd.float().cpu().numpy(), gr, 5e-2)
 

@@ -12,7 +12,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libvmonarch_gfx950.so")
-ABI_VERSION = 10
+ABI_VERSION = 11
 FEA_FWD_SCRATCH_BYTES = 32 << 20   # VMO_FEA_FWD_SCRATCH_BYTES: scratch of vmo_fea_fwd_noalloc per GPU
 DTYPES = {torch.bfloat16: 0, torch.float16: 1}
 
@@ -44,6 +44,7 @@ class FeaBwdArgs(ctypes.Structure):
         ("grad_ent_stride_b", c_int64), ("grad_ent_stride_h", c_int64),
         ("sm_scale", c_float), ("workspace", c_void_p), ("workspace_bytes", c_size_t), ("flags", c_int32),
         ("v1", View), ("dv1", c_int32), ("grad_k_base", View), ("grad_v_base", View), ("frames", c_int32),
+        ("grad_q_base", View),
     ]
 
 
@@ -52,6 +53,7 @@ BWD_F32_Q, BWD_F32_K, BWD_F32_V = 8, 16, 32
 BWD_FOLD_K = 64   # values k or [k | v1]: k's value-role gradient into grad_k, grad_v holds v1's
 BWD_SUM_K, BWD_SUM_V = 128, 256   # grad (dtype) = fp32 base + this call's gradient
 BWD_RECOMPUTE_DQ, BWD_DS_DQ = 512, 1024   # grad_q route: recompute S and dP / GEMM over a stored dS^T
+BWD_SUM_Q = 2048   # grad_q (dtype) = fp32 base + this call's gradient
 LSTEP_BWD_OVERWRITE_Q = 1
 
 

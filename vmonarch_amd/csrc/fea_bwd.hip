@@ -70,6 +70,8 @@ struct BwdParams {
   void* ds;                        // dS route: dS^T of every problem in 32 x 32 blocks (the inputs' dtype),
   int ds_kblocks, ds_qblocks;      // (problems, ceil(nk / 32), ceil(nq / 32), 32 keys, 32 queries)
   int64_t dkb_sb, dkb_sh, dkb_sn, dvb_sb, dvb_sh, dvb_sn;
+  const void* dq_base;             // VMO_BWD_SUM_Q: fp32 rows added to dq before its dtype store
+  int64_t dqb_sb, dqb_sh, dqb_sn;
   float c;          // sm_scale * log2(e)
   float sm_scale;
 };
@@ -274,10 +276,13 @@ __device__ __forceinline__ void store_dq(const BwdParams& p, const f32x16 (&acc)
     float* pr = p.dq_part + (((int64_t)split * p.problems + prob) * p.nq + q0) * D;
     store_acc_rows<F16>(patch, acc, D / 32, p.sm_scale, kGradStoreF32, (char*)pr, (int64_t)D * 4, nrows, lane);
   } else {
-    const int mode = grad_mode(p.accum, VMO_BWD_ACCUM_Q, VMO_BWD_F32_Q);
-    const int64_t es = mode == kGradStore ? 2 : 4;
+    const int mode = grad_mode(p.accum, VMO_BWD_ACCUM_Q, VMO_BWD_F32_Q, VMO_BWD_SUM_Q);
+    const int64_t es = mode == kGradStore || mode == kGradSumStore ? 2 : 4;
     char* row0 = (char*)p.dq + (bb * p.dq_sb + hh * p.dq_sh + (qoff + q0) * p.dq_sn) * es;
-    store_acc_rows<F16>(patch, acc, D / 32, p.sm_scale, mode, row0, p.dq_sn * es, nrows, lane);
+    const char* src0 = mode == kGradSumStore
+                           ? (const char*)p.dq_base + (bb * p.dqb_sb + hh * p.dqb_sh + (qoff + q0) * p.dqb_sn) * 4
+                           : nullptr;
+    store_acc_rows<F16>(patch, acc, D / 32, p.sm_scale, mode, row0, p.dq_sn * es, nrows, lane, 0, src0, p.dqb_sn * 4);
   }
 }
 
@@ -438,7 +443,7 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
 }
 
 // Sum the split-KV partials of dQ (fixed split order, so the result does not depend on timing) and
-// write grad_q, or store / add them into an fp32 grad_q.
+// write grad_q (with VMO_BWD_SUM_Q: plus its fp32 base row), or store / add them into an fp32 grad_q.
 template <bool F16, int D>
 __global__ __launch_bounds__(256) void fea_bwd_dq_reduce(BwdParams p) {
   using T = typename Elem<F16>::T;
@@ -454,10 +459,13 @@ __global__ __launch_bounds__(256) void fea_bwd_dq_reduce(BwdParams p) {
     acc += *(const f32x4*)(p.dq_part + (((int64_t)sp * p.problems + prob) * p.nq + qi) * D + 4 * c4);
   const int fr = prob % p.frames, bh = prob / p.frames, hh = bh % p.heads, bb = bh / p.heads;
   const int64_t row_q = (int64_t)fr * p.nq + qi;
-  if (const int mode = grad_mode(p.accum, VMO_BWD_ACCUM_Q, VMO_BWD_F32_Q); mode != kGradStore) {
+  const int mode = grad_mode(p.accum, VMO_BWD_ACCUM_Q, VMO_BWD_F32_Q, VMO_BWD_SUM_Q);
+  if (mode == kGradAddF32 || mode == kGradStoreF32) {
     f32x4* ptr = (f32x4*)((float*)p.dq + bb * p.dq_sb + hh * p.dq_sh + row_q * p.dq_sn + 4 * c4);
     *ptr = mode == kGradAddF32 ? *ptr + acc : acc;
   } else {
+    if (mode == kGradSumStore)   // the base plus the (unrounded) sum of the partials, rounded once
+      acc += *(const f32x4*)((const float*)p.dq_base + bb * p.dqb_sb + hh * p.dqb_sh + row_q * p.dqb_sn + 4 * c4);
     V4 v;
 #pragma unroll
     for (int e = 0; e < 4; ++e) v[e] = to_elem<T>(acc[e]);
@@ -1051,16 +1059,19 @@ extern "C" int vmo_fea_bwd(const vmo_fea_bwd_args* a, void* stream) {
   }
   constexpr int kFlags = VMO_BWD_ACCUM_Q | VMO_BWD_ACCUM_K | VMO_BWD_ACCUM_V | VMO_BWD_F32_Q | VMO_BWD_F32_K |
                          VMO_BWD_F32_V | VMO_BWD_FOLD_K | VMO_BWD_SUM_K | VMO_BWD_SUM_V | VMO_BWD_RECOMPUTE_DQ |
-                         VMO_BWD_DS_DQ;
+                         VMO_BWD_DS_DQ | VMO_BWD_SUM_Q;
   const bool sum_k = (a->flags & VMO_BWD_SUM_K) != 0, sum_v = (a->flags & VMO_BWD_SUM_V) != 0;
+  const bool sum_q = (a->flags & VMO_BWD_SUM_Q) != 0;
   if ((a->flags & ~kFlags) || ((a->flags >> 3) & a->flags & 7) ||
       (sum_k && (a->flags & (VMO_BWD_ACCUM_K | VMO_BWD_F32_K))) ||
       (sum_v && (a->flags & (VMO_BWD_ACCUM_V | VMO_BWD_F32_V))) || (sum_v && no_grad_v) ||
+      (sum_q && (a->flags & (VMO_BWD_ACCUM_Q | VMO_BWD_F32_Q))) ||
       ((a->flags & VMO_BWD_RECOMPUTE_DQ) && (a->flags & VMO_BWD_DS_DQ)))
     return set_error(VMO_ERR_INVALID, "fea_bwd: unknown or conflicting flags 0x%x", (unsigned)a->flags);
-  if ((sum_k && !view_ok(a->grad_k_base)) || (sum_v && !view_ok(a->grad_v_base)))
-    return set_error(VMO_ERR_INVALID, "fea_bwd: VMO_BWD_SUM_K / _V need a grad_k_base / grad_v_base view "
-                     "(fp32, 16-byte aligned rows)");
+  if ((sum_k && !view_ok(a->grad_k_base)) || (sum_v && !view_ok(a->grad_v_base)) ||
+      (sum_q && !view_ok(a->grad_q_base)))
+    return set_error(VMO_ERR_INVALID, "fea_bwd: VMO_BWD_SUM_Q / _K / _V need a grad_q_base / grad_k_base / "
+                     "grad_v_base view (fp32, 16-byte aligned rows)");
   const bool v0_is_k = a->v.data == a->k.data && a->v.stride_b == a->k.stride_b && a->v.stride_h == a->k.stride_h &&
                        a->v.stride_n == a->k.stride_n && a->dv - a->dv1 == a->d;
   if (fold_k && !v0_is_k)
@@ -1093,6 +1104,10 @@ extern "C" int vmo_fea_bwd(const vmo_fea_bwd_args* a, void* stream) {
   if (sum_k) {
     p.dk_base = a->grad_k_base.data;
     p.dkb_sb = a->grad_k_base.stride_b; p.dkb_sh = a->grad_k_base.stride_h; p.dkb_sn = a->grad_k_base.stride_n;
+  }
+  if (sum_q) {
+    p.dq_base = a->grad_q_base.data;
+    p.dqb_sb = a->grad_q_base.stride_b; p.dqb_sh = a->grad_q_base.stride_h; p.dqb_sn = a->grad_q_base.stride_n;
   }
   if (sum_v) {
     p.dv_base = a->grad_v_base.data;

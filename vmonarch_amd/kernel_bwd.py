@@ -14,7 +14,7 @@ def _pad_features(t, width):
 
 
 def fea_backward_raw(q, k, v, o, lse, ent, do, de, sm_scale, dq=None, dk=None, dv=None, overwrite="", v1=None,
-                     fold_k=False, dk_base=None, dv_base=None, frames=1, dq_route=None):
+                     fold_k=False, dk_base=None, dv_base=None, frames=1, dq_route=None, dq_base=None):
     """q: (B, H, F*nq, D); k: (B, H, F*nk, D); v: (B, H, F*nk, Dv); o, do: (B, H, F*nq, Dv);
     lse, ent, de: (B, H, F*nq) fp32 with unit token stride.  Returns (dq, dk, dv).
 
@@ -31,8 +31,8 @@ def fea_backward_raw(q, k, v, o, lse, ent, do, de, sm_scale, dq=None, dk=None, d
     `fold_k` (v is k, as the VMonarch R-steps pass it): dk receives k's whole gradient, as key and
     as the first value columns, and dv only v1's (None without v1).
 
-    `dk_base` / `dv_base` (float32, shaped like dk / dv): dk / dv, in q's dtype, are that base plus
-    this call's gradient (the last of several calls summing one gradient).
+    `dq_base` / `dk_base` / `dv_base` (float32, shaped like dq / dk / dv): dq / dk / dv, in q's dtype, are
+    that base plus this call's gradient (the last of several calls summing one gradient).
 
     `dq_route` ("recompute" or "ds"; None lets the library choose) picks how dq is formed: a pass that
     recomputes S and dP, or a GEMM over dS^T stored by the dk / dv pass (the workspace then holds nk x nq
@@ -42,12 +42,12 @@ def fea_backward_raw(q, k, v, o, lse, ent, do, de, sm_scale, dq=None, dk=None, d
     NK, Dv = k.shape[2], v.shape[-1] * (2 if v1 is not None else 1)
     flags = (_lib.BWD_FOLD_K if fold_k else 0) | {None: 0, "recompute": _lib.BWD_RECOMPUTE_DQ,
                                                    "ds": _lib.BWD_DS_DQ}[dq_route]
-    for t, name, acc_bit, f32_bit, base in ((dq, "q", _lib.BWD_ACCUM_Q, _lib.BWD_F32_Q, None),
+    for t, name, acc_bit, f32_bit, base in ((dq, "q", _lib.BWD_ACCUM_Q, _lib.BWD_F32_Q, dq_base),
                                             (dk, "k", _lib.BWD_ACCUM_K, _lib.BWD_F32_K, dk_base),
                                             (dv, "v", _lib.BWD_ACCUM_V, _lib.BWD_F32_V, dv_base)):
         if base is not None:
             assert base.dtype == torch.float32 and (t is None or t.dtype == q.dtype), "base fp32, result q.dtype"
-            flags |= _lib.BWD_SUM_K if name == "k" else _lib.BWD_SUM_V
+            flags |= {"q": _lib.BWD_SUM_Q, "k": _lib.BWD_SUM_K, "v": _lib.BWD_SUM_V}[name]
         elif t is not None and t.dtype != q.dtype:
             assert t.dtype == torch.float32, "a gradient passed in must be float32 or q's dtype"
             flags |= f32_bit if name in overwrite else acc_bit
@@ -66,6 +66,9 @@ def fea_backward_raw(q, k, v, o, lse, ent, do, de, sm_scale, dq=None, dk=None, d
     a.q, a.k, a.v, a.o, a.grad_o = (_lib.view(t) for t in (q, k, v, o, do))
     a.grad_q, a.grad_k = _lib.view(dq), _lib.view(dk)
     a.grad_v = _lib.view(dv) if dv is not None else _lib.View()
+    if dq_base is not None:
+        assert dq_base.shape == dq.shape
+        a.grad_q_base = _lib.view(dq_base)
     if dk_base is not None:
         assert dk_base.shape == dk.shape
         a.grad_k_base = _lib.view(dk_base)

@@ -263,13 +263,31 @@ class _VMonarchFunction(torch.autograd.Function):
         dev, dt = q.device, q.dtype
         dz = _lib.row_aligned(dz.to(dt))
         f32 = torch.float32
-        # fp32 gradient buffers, overwritten by the first backward that writes them (the last
-        # iteration's, which covers every token) and added into by every later one.  The R-steps'
-        # values start with k; the kernels add k's value-role gradient to its key-role one
-        # (fold_k), so dk is one buffer, as autograd's sum over k's uses (vmonarch.py:50) is.
+        # Call order: the L- and R-step backwards from the last iteration down, R-step 0's last of all and the
+        # recompute's (rows [0, rt), vmonarch.py:66-68) just before it.  Every gradient is written once, in
+        # the caller's dtype and memory order, by the last call that contributes to it: the fp32 sum of the
+        # earlier contributions plus its own (VMO_BWD_SUM_*), so no conversion pass follows.  dq: the
+        # L-steps (the first overwrites, the rest add), the recompute, then R-step 0 (x = q).  dk: every
+        # R-step (values start with k: the kernels fold k's value-role gradient into dk, as autograd's sum
+        # over k's uses at vmonarch.py:50 does), the recompute, R-step 0 last.  dv: the last R-step (values
+        # [k | v]) and the recompute.
+        gq, gk, gv = (_lib.empty_in_order(o, (B, H, N), f, dt, dev) for o, f in zip(ctx.orders, (D, D, Dv)))
         dq = torch.empty((B, H, N, D), device=dev, dtype=f32)
-        dk = torch.empty((B, H, N, D), device=dev, dtype=f32)
-        dv = torch.empty((B, H, N, Dv), device=dev, dtype=f32)
+        partial = {"k": torch.empty((B, H, N, D), device=dev, dtype=f32),
+                   "v": torch.empty((B, H, N, Dv), device=dev, dtype=f32)}
+        started = {"k": False, "v": False}
+        final = {"k": gk, "v": gv}
+        v_writers = ([num_iters - 1] if num_iters > 1 else []) + (["rt"] if rt > 0 else []) + ([0] if num_iters == 1 else [])
+
+        def grad_args(x, last_writer):
+            """fea_backward_raw arguments for gradient x ("k" or "v") of one call: into the fp32 partial sum
+            (overwriting it on the first call), or, from its last writer, into the dtype result."""
+            if last_writer:
+                return ({f"d{x}": final[x], f"d{x}_base": partial[x]} if started[x] else {f"d{x}": final[x]}), ""
+            first = not started[x]
+            started[x] = True
+            return {f"d{x}": partial[x]}, (x if first else "")
+
         de = torch.zeros((B, H, N), device=dev, dtype=f32)
         g = dz
         for it in reversed(range(num_iters)):
@@ -278,25 +296,25 @@ class _VMonarchFunction(torch.autograd.Function):
             dout = torch.empty_like(out)
             _lstep_bwd_launch(q, out, ent, g, dq, dout, m, b, scale, last, rt if last else 0, min_col_mass,
                               overwrite_q=last)
+            if it == 0 and rt > 0:
+                # the exact attention of the first rt queries; it reads every key and value
+                zeros = torch.zeros((B, H, rt), device=dev, dtype=f32)
+                kw, ow = grad_args("k", False)
+                kv, ov = grad_args("v", v_writers[-1] == "rt")
+                fea_backward_raw(q[:, :, :rt], k, v, z[:, :, :rt], lse_rt, zeros, _lib.row_aligned(dz[:, :, :rt]), zeros,
+                                 scale, dq=dq[:, :, :rt], overwrite=ow + ov, **kw, **kv)
             # values k, or [k | v] read from the two tensors in place (vmonarch.py:50); m frames per head
-            gx, _, _ = fea_backward_raw(x, k, k, out, lse, ent, dout, de, scale if it == 0 else 1.0,
-                                        dq=dq if it == 0 else None,   # R-step 0 read q directly
-                                        dk=dk, dv=dv if last else None, overwrite="kv" if last else "",
-                                        v1=v if last else None, fold_k=True, frames=m)
+            kw, ow = grad_args("k", it == 0)
+            if last:
+                kv, ov = grad_args("v", v_writers[-1] == it)
+                kw.update(kv)
+                ow += ov
+            if it == 0:   # R-step 0 reads q itself: dq's last contribution
+                kw.update(dq=gq, dq_base=dq)
+            gx, _, _ = fea_backward_raw(x, k, k, out, lse, ent, dout, de, scale if it == 0 else 1.0, overwrite=ow,
+                                        v1=v if last else None, fold_k=True, frames=m, **kw)
             if it > 0:
                 g = gx                      # dL/du of the previous L-step's output
-        # gradients in the memory order the caller's q, k, v had (the fp32 -> dtype writes place them)
-        gq, gk, gv = (_lib.empty_in_order(o, (B, H, N), f, dt, dev) for o, f in zip(ctx.orders, (D, D, Dv)))
-        if rt > 0:
-            # exact attention of the first rt queries (vmonarch.py:66-68); it reads every key, so its
-            # dK / dV epilogue writes k's and v's final gradients: fp32 sum so far + its own, in dtype
-            zeros = torch.zeros((B, H, rt), device=dev, dtype=f32)
-            fea_backward_raw(q[:, :, :rt], k, v, z[:, :, :rt], lse_rt, zeros, _lib.row_aligned(dz[:, :, :rt]), zeros,
-                             scale, dq=dq[:, :, :rt], dk=gk, dv=gv, dk_base=dk, dv_base=dv)
-        else:
-            gk.copy_(dk)
-            gv.copy_(dv)
-        gq.copy_(dq)
         return gq, gk, gv, None, None, None, None, None, None
 
 
