@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define VMO_ABI_VERSION 11
+#define VMO_ABI_VERSION 12
 
 enum {
   VMO_OK = 0,
@@ -188,6 +188,10 @@ typedef struct vmo_fea_bwd_args {
    * a (B, H, m*b, .) tensor in any memory order (a DiT block's (B, N, H, D)) without a copy. */
   int32_t frames;
   vmo_view grad_q_base;                /* fp32, read with VMO_BWD_SUM_Q */
+  /* Optional: delta = rowsum(o * grad_o) per query row, fp32 with the strides below and token stride 1
+   * (vmo_lstep_bwd_args.delta writes it); null: formed here from o and grad_o. */
+  const float* delta;
+  int64_t delta_stride_b, delta_stride_h;
 } vmo_fea_bwd_args;
 
 /*
@@ -225,6 +229,12 @@ typedef struct vmo_lstep_bwd_args {
   float scale;
   float min_col_mass;
   int32_t flags;                   /* VMO_LSTEP_BWD_OVERWRITE_Q: grad_q = dL/dq instead of += */
+  /* Optional (null: not written): delta[token] = sum_f out[token][f] * grad_out[token][f] in fp32 over the
+   * 16-bit values as stored, (B, H, m*b) with token stride 1 -- the per-row sum the flash-entropy backward of
+   * the R-step that produced `out` needs (vmo_fea_bwd_args.delta), formed here from rows this kernel holds
+   * anyway.  Built for the one-tile kernels (m <= 32, d and dv in {64, 128}); other shapes reject it. */
+  float* delta;
+  int64_t delta_stride_b, delta_stride_h;
 } vmo_lstep_bwd_args;
 enum { VMO_LSTEP_BWD_OVERWRITE_Q = 1 };
 

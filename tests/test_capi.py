@@ -134,6 +134,9 @@ def test_lstep_bwd_rejects_too_many_blocks_and_null_args(L):
     assert L.vmo_lstep_bwd(ctypes.byref(a), None) == 2   # 100 frames: beyond the LDS of a CU
     assert b"LDS" in L.vmo_last_error()
     assert L.vmo_lstep_bwd(None, None) != 0
+    a.num_blocks, a.delta = 40, _addr()                  # delta from a general (m > 32) kernel: not built
+    assert L.vmo_lstep_bwd(ctypes.byref(a), None) == 2
+    assert b"delta" in L.vmo_last_error()
 
 
 def test_fea_bwd_rejects_unknown_and_conflicting_flags(L):

@@ -88,3 +88,25 @@ def test_backward_routes_match_oracle_and_each_other(case):
         assert_grad_close(b, ref, 3e-2, f"{name} (recompute route)")
         assert np.abs(a - b).max() <= 1e-2 * np.abs(b).max(), name
     assert hip_library_loaded()
+
+
+@pytest.mark.parametrize("route", ["ds", "recompute"])
+def test_backward_with_given_delta(route):
+    """vmo_fea_bwd_args.delta: rowsum(o * do) handed in (as the L-step backward forms it) instead of formed
+    from o and do -- the same gradients up to the order of that sum."""
+    from vmonarch_amd.kernel import fea_forward
+    from vmonarch_amd.kernel_bwd import fea_backward_raw
+    g = torch.Generator().manual_seed(77)
+    F, n, D = 3, 300, 128
+    q, k = randn_lp(g, 1, 2, F * n, D).to(DEV), randn_lp(g, 1, 2, F * n, D).to(DEV)
+    v1 = randn_lp(g, 1, 2, F * n, D).to(DEV)
+    o, lse, ent = fea_forward(q, k, k, v1, D ** -0.5, frames=F)
+    do = randn_lp(g, 1, 2, F * n, 2 * D).to(DEV)
+    de = torch.randn(1, 2, F * n, generator=g).to(DEV)
+    delta = (o.float() * do.float()).sum(-1)
+    args = (q, k, k, o, lse, ent, do, de, D ** -0.5)
+    ref = fea_backward_raw(*args, v1=v1, frames=F, dq_route=route)
+    got = fea_backward_raw(*args, v1=v1, frames=F, dq_route=route, delta=delta)
+    for a, b, name in zip(got, ref, ("dq", "dk", "dv")):
+        a, b = a.float().cpu().numpy(), b.float().cpu().numpy()
+        assert np.abs(a - b).max() <= 1e-2 * np.abs(b).max(), name

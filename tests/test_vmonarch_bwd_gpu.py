@@ -55,6 +55,16 @@ def test_lstep_bwd_matches_oracle(d, dv, last, m, mcm):
     _lstep_bwd_launch(q.to(DEV), out.to(DEV), ent.to(DEV), grad.to(DEV), dq_inc, dout, m, b, d ** -0.5, last, skip, mcm)
     torch.cuda.synchronize()
     assert torch.equal(dq_ow, dq_inc)
+    # delta = rowsum(out * d out) over the stored 16-bit values, fp32 (the R-step backward's per-row sum);
+    # d out itself is unchanged by asking for it
+    delta = torch.full((B, H, N), float("nan"), device=DEV)
+    dout_d = torch.empty_like(dout)
+    _lstep_bwd_launch(q.to(DEV), out.to(DEV), ent.to(DEV), grad.to(DEV), torch.zeros_like(dq_ow), dout_d, m, b,
+                      d ** -0.5, last, skip, mcm, delta=delta)
+    torch.cuda.synchronize()
+    assert torch.equal(dout_d, dout)
+    ref = (out.double() * dout.cpu().double()).sum(-1)
+    torch.testing.assert_close(delta.cpu().double(), ref, rtol=1e-5, atol=1e-5 * float(ref.abs().max()))
 
 
 def _grads(q, k, v, do, m, b, iters, rt):

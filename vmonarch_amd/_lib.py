@@ -12,7 +12,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libvmonarch_gfx950.so")
-ABI_VERSION = 11
+ABI_VERSION = 12
 FEA_FWD_SCRATCH_BYTES = 32 << 20   # VMO_FEA_FWD_SCRATCH_BYTES: scratch of vmo_fea_fwd_noalloc per GPU
 DTYPES = {torch.bfloat16: 0, torch.float16: 1}
 
@@ -44,7 +44,7 @@ class FeaBwdArgs(ctypes.Structure):
         ("grad_ent_stride_b", c_int64), ("grad_ent_stride_h", c_int64),
         ("sm_scale", c_float), ("workspace", c_void_p), ("workspace_bytes", c_size_t), ("flags", c_int32),
         ("v1", View), ("dv1", c_int32), ("grad_k_base", View), ("grad_v_base", View), ("frames", c_int32),
-        ("grad_q_base", View),
+        ("grad_q_base", View), ("delta", c_void_p), ("delta_stride_b", c_int64), ("delta_stride_h", c_int64),
     ]
 
 
@@ -72,7 +72,7 @@ class LstepBwdArgs(ctypes.Structure):
         ("block_size", c_int32), ("d", c_int32), ("dv", c_int32), ("last", c_int32), ("skip_tokens", c_int32),
         ("q", View), ("out", View), ("ent", c_void_p), ("ent_stride_b", c_int64), ("ent_stride_h", c_int64),
         ("grad_res", View), ("grad_q", View), ("grad_out", View), ("scale", c_float), ("min_col_mass", c_float),
-        ("flags", c_int32),
+        ("flags", c_int32), ("delta", c_void_p), ("delta_stride_b", c_int64), ("delta_stride_h", c_int64),
     ]
 
 

@@ -72,6 +72,8 @@ struct BwdParams {
   int64_t dkb_sb, dkb_sh, dkb_sn, dvb_sb, dvb_sh, dvb_sn;
   const void* dq_base;             // VMO_BWD_SUM_Q: fp32 rows added to dq before its dtype store
   int64_t dqb_sb, dqb_sh, dqb_sn;
+  const float* delta;              // optional rowsum(o * dO) per query (else formed from o and dO)
+  int64_t dl_sb, dl_sh;
   float c;          // sm_scale * log2(e)
   float sm_scale;
 };
@@ -339,14 +341,16 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
 #pragma unroll
     for (int ds = 0; ds < DV / 16; ++ds) {
       V8 x = *(const V8*)(dp + ds * 16);
-      V8 y = *(const V8*)(op + ds * 16);
       dof[ds] = qvalid ? x : V8{};
       asm volatile("" : "+v"(dof[ds]));
+      if (!p.delta) {   // o is read for delta alone
+        V8 y = *(const V8*)(op + ds * 16);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) delta = fmaf((float)x[e], (float)y[e], delta);
+        for (int e = 0; e < 8; ++e) delta = fmaf((float)x[e], (float)y[e], delta);
+      }
     }
   }
-  delta = wave_sum32(delta);
+  delta = p.delta ? p.delta[bb * p.dl_sb + hh * p.dl_sh + qoff + qr] : wave_sum32(delta);
   const int64_t si = bb * p.st_sb + hh * p.st_sh + qoff + qr;
   const float lse = p.lse[si];
   const float dE = p.dent[bb * p.de_sb + hh * p.de_sh + qoff + qr];
@@ -480,8 +484,8 @@ __global__ __launch_bounds__(256) void fea_bwd_dq_reduce(BwdParams p) {
 // streams it back.  Three launches: fea_bwd_prep (the per-row scalars the dq kernel's prologue forms),
 // fea_bwd_dkdv with DS, fea_bwd_dq_ds (+ fea_bwd_dq_reduce for key splits).
 
-// delta = o . dO of every query row (fp32), then alpha = -delta - dE E and beta = -dE ln 2 into the
-// workspace; DV / 8 lanes per row, 16 bytes each.
+// delta = o . dO of every query row (fp32; or the given delta), then alpha = -delta - dE E and
+// beta = -dE ln 2 into the workspace; DV / 8 lanes per row, 16 bytes each.
 template <bool F16, int DV>
 __global__ __launch_bounds__(256) void fea_bwd_prep_kernel(BwdParams p) {
   using T = typename Elem<F16>::T;
@@ -496,13 +500,17 @@ __global__ __launch_bounds__(256) void fea_bwd_prep_kernel(BwdParams p) {
   const int prob = (int)(rr / p.nq), qi = (int)(rr % p.nq);
   const int fr = prob % p.frames, bh = prob / p.frames, hh = bh % p.heads, bb = bh / p.heads;
   const int64_t qrow = (int64_t)fr * p.nq + qi;
-  const V8 x = *(const V8*)((const T*)p.dO + bb * p.do_sb + hh * p.do_sh + qrow * p.do_sn + 8 * part);
-  const V8 y = *(const V8*)((const T*)p.o + bb * p.o_sb + hh * p.o_sh + qrow * p.o_sn + 8 * part);
   float d = 0.f;
+  if (p.delta) {   // given (formed by the L-step backward that wrote dO)
+    d = p.delta[bb * p.dl_sb + hh * p.dl_sh + qrow];
+  } else {
+    const V8 x = *(const V8*)((const T*)p.dO + bb * p.do_sb + hh * p.do_sh + qrow * p.do_sn + 8 * part);
+    const V8 y = *(const V8*)((const T*)p.o + bb * p.o_sb + hh * p.o_sh + qrow * p.o_sn + 8 * part);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) d = fmaf((float)x[e], (float)y[e], d);
+    for (int e = 0; e < 8; ++e) d = fmaf((float)x[e], (float)y[e], d);
 #pragma unroll
-  for (int m = TPR / 2; m >= 1; m >>= 1) d += __shfl_xor(d, m);
+    for (int m = TPR / 2; m >= 1; m >>= 1) d += __shfl_xor(d, m);
+  }
   if (row < rows && part == 0) {
     const int64_t si = bb * p.st_sb + hh * p.st_sh + qrow;
     const float dE = p.dent[bb * p.de_sb + hh * p.de_sh + qrow];
@@ -1105,6 +1113,8 @@ extern "C" int vmo_fea_bwd(const vmo_fea_bwd_args* a, void* stream) {
     p.dk_base = a->grad_k_base.data;
     p.dkb_sb = a->grad_k_base.stride_b; p.dkb_sh = a->grad_k_base.stride_h; p.dkb_sn = a->grad_k_base.stride_n;
   }
+  p.delta = a->delta;
+  p.dl_sb = a->delta_stride_b; p.dl_sh = a->delta_stride_h;
   if (sum_q) {
     p.dq_base = a->grad_q_base.data;
     p.dqb_sb = a->grad_q_base.stride_b; p.dqb_sh = a->grad_q_base.stride_h; p.dqb_sn = a->grad_q_base.stride_n;

@@ -295,6 +295,8 @@ struct LBParams {
   float logit_scale_log2;
   float scale;
   float min_col_mass;
+  float* delta;       // optional: sum_f out * d out per token (one-tile kernels)
+  int64_t dl_sb, dl_sh;
 };
 
 template <int D, int DV, bool LAST>
@@ -470,6 +472,33 @@ __global__ __launch_bounds__(64 * kLBWaves) void lstep_bwd_kernel(LBParams p) {
   T* const dcol = (T*)p.dout + bb * p.do_sb + hh * p.do_sh + (int64_t)j * p.do_sn;
   const int64_t do_rs = (int64_t)p.bs * p.do_sn;
 
+  // delta_k = sum_f out[k][f] d out[k][f] (p.delta): d out's accumulator blocks (lane (k, hl): features 32 a +
+  // 8 g + 4 hl + 0..3), rounded as they are stored, against out's row k held as MFMA operands (features
+  // 16 ds + 8 hl + 0..7).  Two permlane32 swaps per operand trade the middle 4-feature groups between the
+  // halves, so that lane (k, hl) holds features 16 ds + 4 hl + 0..3 (X) and 16 ds + 8 + 4 hl + 0..3 (Y):
+  // groups g = 2 (ds % 2) and 2 (ds % 2) + 1 of block ds / 2.
+  auto row_dot = [&](const V8* rowf, const f32x16* acc, auto nblocks_tag) __attribute__((always_inline)) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    using V2 = typename E::V2;
+    float d = 0.f;
+#pragma unroll
+    for (int ds = 0; ds < 2 * decltype(nblocks_tag)::value; ++ds) {
+      const u32x4 w = __builtin_bit_cast(u32x4, rowf[ds]);
+      const auto s0 = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
+      const auto s1 = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+      const uint32_t xy[4] = {s0[0], s1[0], s0[1], s1[1]};   // X: accumulator rows r0 .. r0+3, Y: r0+4 .. r0+7
+      const int r0 = 8 * (ds & 1);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const V2 x = __builtin_bit_cast(V2, xy[u]);
+        d = fmaf((float)to_elem<T>(acc[ds >> 1][r0 + 2 * u]), (float)x[0], d);
+        d = fmaf((float)to_elem<T>(acc[ds >> 1][r0 + 2 * u + 1]), (float)x[1], d);
+      }
+    }
+    return d;
+  };
+  float dlt = 0.f;
+
   // ---- d attn^T[k][i]
   f32x16 da = f32x16{};
   if constexpr (LAST) {
@@ -488,6 +517,7 @@ __global__ __launch_bounds__(64 * kLBWaves) void lstep_bwd_kernel(LBParams p) {
 #pragma unroll
     for (int a = 0; a < NV; ++a) accy[a] = f32x16{};
     mma_rows_t(accy, g_t, std::integral_constant<int, DV>{}, Bu);
+    if (p.delta) dlt = row_dot(yf, accy, std::integral_constant<int, NV>{});
     // the dz tile is dead now: it takes the row-store patch (whole row segments per store)
     if (live)
       store_acc_rows<F16>((VMO_LDS float*)g_t, accy, NV, 1.f, kGradStore, (char*)(dcol + D), do_rs * 2, m, lane);
@@ -570,6 +600,10 @@ __global__ __launch_bounds__(64 * kLBWaves) void lstep_bwd_kernel(LBParams p) {
 #pragma unroll
     for (int a = 0; a < ND; ++a) acck[a] = f32x16{};
     mma_rows_t(acck, q_t, std::integral_constant<int, D>{}, Bd);
+    if (p.delta) {
+      dlt = wave_sum32(dlt + row_dot(krf, acck, std::integral_constant<int, ND>{}));
+      if (live && kvalid && hl == 0) p.delta[bb * p.dl_sb + hh * p.dl_sh + (int64_t)k * p.bs + j] = dlt;
+    }
     if (live)   // the q tile is dead now: it takes the row-store patch
       store_acc_rows<F16>((VMO_LDS float*)q_t, acck, ND, 1.f, kGradStore, (char*)dcol, do_rs * 2, m, lane);
   }
@@ -1014,7 +1048,12 @@ extern "C" int vmo_lstep_bwd(const vmo_lstep_bwd_args* a, void* stream) {
   if (cols > (1ll << 30) || (int64_t)a->num_blocks * a->block_size > (1ll << 30))
     return set_error(VMO_ERR_UNSUPPORTED, "lstep_bwd: problem too large");
   if (a->flags & ~VMO_LSTEP_BWD_OVERWRITE_Q) return set_error(VMO_ERR_INVALID, "lstep_bwd: unknown flags 0x%x", (unsigned)a->flags);
+  if (a->delta && !one_tile)
+    return set_error(VMO_ERR_UNSUPPORTED, "lstep_bwd: delta is built for the one-tile kernels (m <= 32, d and dv in "
+                     "{64, 128}); got m=%d d=%d dv=%d", a->num_blocks, a->d, a->dv);
   LBParams p{};
+  p.delta = a->delta;
+  p.dl_sb = a->delta_stride_b; p.dl_sh = a->delta_stride_h;
   p.dq_overwrite = (a->flags & VMO_LSTEP_BWD_OVERWRITE_Q) != 0;
   p.q = a->q.data; p.out = a->out.data; p.ent = a->ent; p.g = a->grad_res.data;
   p.dq = (float*)a->grad_q.data; p.dout = a->grad_out.data;

@@ -14,7 +14,7 @@ def _pad_features(t, width):
 
 
 def fea_backward_raw(q, k, v, o, lse, ent, do, de, sm_scale, dq=None, dk=None, dv=None, overwrite="", v1=None,
-                     fold_k=False, dk_base=None, dv_base=None, frames=1, dq_route=None, dq_base=None):
+                     fold_k=False, dk_base=None, dv_base=None, frames=1, dq_route=None, dq_base=None, delta=None):
     """q: (B, H, F*nq, D); k: (B, H, F*nk, D); v: (B, H, F*nk, Dv); o, do: (B, H, F*nq, Dv);
     lse, ent, de: (B, H, F*nq) fp32 with unit token stride.  Returns (dq, dk, dv).
 
@@ -33,6 +33,9 @@ def fea_backward_raw(q, k, v, o, lse, ent, do, de, sm_scale, dq=None, dk=None, d
 
     `dq_base` / `dk_base` / `dv_base` (float32, shaped like dq / dk / dv): dq / dk / dv, in q's dtype, are
     that base plus this call's gradient (the last of several calls summing one gradient).
+
+    `delta` ((B, H, F*nq) fp32, unit token stride): rowsum(o * do) when the caller has it (the L-step
+    backward forms it); otherwise the kernels form it from o and do.
 
     `dq_route` ("recompute" or "ds"; None lets the library choose) picks how dq is formed: a pass that
     recomputes S and dP, or a GEMM over dS^T stored by the dk / dv pass (the workspace then holds nk x nq
@@ -83,6 +86,9 @@ def fea_backward_raw(q, k, v, o, lse, ent, do, de, sm_scale, dq=None, dk=None, d
     if v1 is not None:
         assert v1.shape == v.shape and v1.stride() == v.stride() and v1.dtype == v.dtype
         a.v1, a.dv1 = _lib.view(v1), v1.shape[-1]
+    if delta is not None:
+        assert delta.dtype == torch.float32 and delta.stride(2) == 1
+        a.delta, a.delta_stride_b, a.delta_stride_h = delta.data_ptr(), delta.stride(0), delta.stride(1)
     nbytes = L.vmo_fea_bwd_workspace_size(a)
     ws = torch.empty(nbytes, device=q.device, dtype=torch.uint8)
     a.workspace, a.workspace_bytes = ws.data_ptr(), nbytes

@@ -73,10 +73,15 @@ def _lstep_launch(q, out, ent, res, m, b, scale, last, skip, min_col_mass):
     _lib.check(L.vmo_lstep_fwd(a, _lib.stream_of(q)), "vmo_lstep_fwd")
 
 
+def _lstep_one_tile(m, d, dv, last):
+    """Whether the one-tile L-step kernels take this grid (csrc/lstep.hip one_tile_built)."""
+    return m <= 32 and d in (64, 128) and (not last or dv in (64, 128))
+
+
 def _lstep_bwd_launch(q, out, ent, grad_res, grad_q, grad_out, m, b, scale, last, skip, min_col_mass,
-                      overwrite_q=False):
+                      overwrite_q=False, delta=None):
     """Backward of one L-step (vmo_lstep_bwd): grad_q (fp32) += dL/dq (= with overwrite_q),
-    grad_out = dL/d out."""
+    grad_out = dL/d out; with `delta` ((B, H, N) fp32, one-tile grids only) also rowsum(out * grad_out)."""
     L = _lib.lib()
     B, H, N, D = q.shape
     a = _lib.LstepBwdArgs()
@@ -91,6 +96,9 @@ def _lstep_bwd_launch(q, out, ent, grad_res, grad_q, grad_out, m, b, scale, last
     a.ent_stride_b, a.ent_stride_h = ent.stride(0), ent.stride(1)
     a.scale, a.min_col_mass = float(scale), float(min_col_mass)
     a.flags = _lib.LSTEP_BWD_OVERWRITE_Q if overwrite_q else 0
+    if delta is not None:
+        assert delta.dtype == torch.float32 and delta.stride(2) == 1
+        a.delta, a.delta_stride_b, a.delta_stride_h = delta.data_ptr(), delta.stride(0), delta.stride(1)
     _lib.check(L.vmo_lstep_bwd(a, _lib.stream_of(q)), "vmo_lstep_bwd")
 
 
@@ -289,13 +297,16 @@ class _VMonarchFunction(torch.autograd.Function):
             return {f"d{x}": partial[x]}, (x if first else "")
 
         de = torch.zeros((B, H, N), device=dev, dtype=f32)
+        # rowsum(out * d out), formed by the L-step backward that writes d out (one-tile grids), read by the
+        # R-step backward in place of another pass over both
+        delta = torch.empty((B, H, N), device=dev, dtype=f32) if _lstep_one_tile(m, D, Dv, True) else None
         g = dz
         for it in reversed(range(num_iters)):
             last = it == num_iters - 1
             x, out, lse, ent = saved[4 * it: 4 * it + 4]
             dout = torch.empty_like(out)
             _lstep_bwd_launch(q, out, ent, g, dq, dout, m, b, scale, last, rt if last else 0, min_col_mass,
-                              overwrite_q=last)
+                              overwrite_q=last, delta=delta)
             if it == 0 and rt > 0:
                 # the exact attention of the first rt queries; it reads every key and value
                 zeros = torch.zeros((B, H, rt), device=dev, dtype=f32)
@@ -312,7 +323,7 @@ class _VMonarchFunction(torch.autograd.Function):
             if it == 0:   # R-step 0 reads q itself: dq's last contribution
                 kw.update(dq=gq, dq_base=dq)
             gx, _, _ = fea_backward_raw(x, k, k, out, lse, ent, dout, de, scale if it == 0 else 1.0, overwrite=ow,
-                                        v1=v if last else None, fold_k=True, frames=m, **kw)
+                                        v1=v if last else None, fold_k=True, frames=m, delta=delta, **kw)
             if it > 0:
                 g = gx                      # dL/du of the previous L-step's output
         return gq, gk, gv, None, None, None, None, None, None
