@@ -124,7 +124,7 @@ def backward_timings(steps):
     """Training-side timings (not `value`): the cfg4 VMonarch step with autograd (HIP forward that
     keeps its activations, then the HIP backward: fused L-step backward + flash-entropy backward)
     and the cfg5 flash-entropy forward + backward, (1, 24, 16384, 128) bf16.  Events on the
-    current stream around each half, `steps` timed steps after one warm-up."""
+    current stream around each half, the median of `steps` timed steps after one warm-up."""
     import torch
     from vmonarch_amd import flash_entropy_attention, vmonarch_attention
 
@@ -135,7 +135,7 @@ def backward_timings(steps):
         out = fwd()
         torch.autograd.grad(*grads_of(out))
         torch.cuda.synchronize()
-        tf = tb = 0.0
+        tf, tb = [], []
         for _ in range(steps):
             ev[0].record()
             out = fwd()
@@ -143,9 +143,9 @@ def backward_timings(steps):
             torch.autograd.grad(*grads_of(out))
             ev[2].record()
             torch.cuda.synchronize()
-            tf += ev[0].elapsed_time(ev[1])
-            tb += ev[1].elapsed_time(ev[2])
-        return tf / steps, tb / steps
+            tf.append(ev[0].elapsed_time(ev[1]))
+            tb.append(ev[1].elapsed_time(ev[2]))
+        return sorted(tf)[len(tf) // 2], sorted(tb)[len(tb) // 2]
 
     g = torch.Generator().manual_seed(0)
     q = (torch.randn(B, H, N, D, generator=g) * 0.5).bfloat16().to(dev).requires_grad_()
