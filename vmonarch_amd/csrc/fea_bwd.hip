@@ -491,6 +491,17 @@ __global__ __launch_bounds__(256) void fea_bwd_prep_kernel(BwdParams p) {
   using T = typename Elem<F16>::T;
   using V8 = typename Elem<F16>::V8;
   constexpr int TPR = DV / 8;
+  if (p.delta) {   // given (formed by the L-step backward that wrote dO): one lane per row
+    const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (row >= (int64_t)p.problems * p.nq) return;
+    const int prob = (int)(row / p.nq), qi = (int)(row % p.nq);
+    const int fr = prob % p.frames, bh = prob / p.frames, hh = bh % p.heads, bb = bh / p.heads;
+    const int64_t qrow = (int64_t)fr * p.nq + qi;
+    const float dE = p.dent[bb * p.de_sb + hh * p.de_sh + qrow];
+    p.alpha[row] = -p.delta[bb * p.dl_sb + hh * p.dl_sh + qrow] - dE * p.ent[bb * p.st_sb + hh * p.st_sh + qrow];
+    p.beta[row] = -dE * kLn2;
+    return;
+  }
   static_assert(TPR >= 8 && TPR <= 64 && 64 % TPR == 0, "row lanes within one wave");
   const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t rows = (int64_t)p.problems * p.nq;
@@ -500,17 +511,13 @@ __global__ __launch_bounds__(256) void fea_bwd_prep_kernel(BwdParams p) {
   const int prob = (int)(rr / p.nq), qi = (int)(rr % p.nq);
   const int fr = prob % p.frames, bh = prob / p.frames, hh = bh % p.heads, bb = bh / p.heads;
   const int64_t qrow = (int64_t)fr * p.nq + qi;
+  const V8 x = *(const V8*)((const T*)p.dO + bb * p.do_sb + hh * p.do_sh + qrow * p.do_sn + 8 * part);
+  const V8 y = *(const V8*)((const T*)p.o + bb * p.o_sb + hh * p.o_sh + qrow * p.o_sn + 8 * part);
   float d = 0.f;
-  if (p.delta) {   // given (formed by the L-step backward that wrote dO)
-    d = p.delta[bb * p.dl_sb + hh * p.dl_sh + qrow];
-  } else {
-    const V8 x = *(const V8*)((const T*)p.dO + bb * p.do_sb + hh * p.do_sh + qrow * p.do_sn + 8 * part);
-    const V8 y = *(const V8*)((const T*)p.o + bb * p.o_sb + hh * p.o_sh + qrow * p.o_sn + 8 * part);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) d = fmaf((float)x[e], (float)y[e], d);
+  for (int e = 0; e < 8; ++e) d = fmaf((float)x[e], (float)y[e], d);
 #pragma unroll
-    for (int m = TPR / 2; m >= 1; m >>= 1) d += __shfl_xor(d, m);
-  }
+  for (int m = TPR / 2; m >= 1; m >>= 1) d += __shfl_xor(d, m);
   if (row < rows && part == 0) {
     const int64_t si = bb * p.st_sb + hh * p.st_sh + qrow;
     const float dE = p.dent[bb * p.de_sb + hh * p.de_sh + qrow];
@@ -915,7 +922,7 @@ constexpr bool bwd_ds_built() { return D == 64 || D == 128; }
 
 template <bool F16, int D, int DV, bool W0K>
 static int launch_bwd_ds(const BwdParams& p, hipStream_t s) {
-  const int64_t threads = (int64_t)p.problems * p.nq * (DV / 8);
+  const int64_t threads = (int64_t)p.problems * p.nq * (p.delta ? 1 : DV / 8);
   hipLaunchKernelGGL((fea_bwd_prep_kernel<F16, DV>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, p);
   int rc = launch_status("fea_bwd_prep");
   if (rc != VMO_OK) return rc;
