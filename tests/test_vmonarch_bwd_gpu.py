@@ -242,3 +242,26 @@ def test_vmonarch_training_step_makes_no_layout_copies():
     for gd, gc in zip(g_d, g_c):
         assert torch.equal(gd, gc)
     assert peak_dit <= peak_c + (1 << 20), (peak_dit, peak_c)
+
+
+@pytest.mark.parametrize("d, dv, last", [(64, 64, False), (128, 128, True), (128, 64, True)])
+def test_lstep_bwd_delta_fp16(d, dv, last):
+    """The L-step backward's delta = rowsum(out * d out) in float16 (the half-precision operand pairs of
+    its permlane32 exchange), against the sum over the stored d out."""
+    from vmonarch_amd.vmonarch import _lstep_bwd_launch
+    g = torch.Generator().manual_seed(d + dv + last)
+    B, H, m, b = 1, 2, 21, 30
+    N = m * b
+    wout = d + (dv if last else 0)
+    q, out = randn_lp(g, B, H, N, d, dtype=torch.float16), randn_lp(g, B, H, N, wout, dtype=torch.float16)
+    ent = torch.rand(B, H, N, generator=g) * 3.0
+    grad = randn_lp(g, B, H, N, dv if last else d, dtype=torch.float16)
+    dq = torch.zeros(B, H, N, d, device=DEV)
+    dout = torch.empty((B, H, N, wout), device=DEV, dtype=torch.float16)
+    delta = torch.full((B, H, N), float("nan"), device=DEV)
+    print(f"lstep_bwd delta fp16 d={d} dv={dv} last={last}", flush=True)
+    _lstep_bwd_launch(q.to(DEV), out.to(DEV), ent.to(DEV), grad.to(DEV), dq, dout, m, b, d ** -0.5, last,
+                      b if last else 0, 0.01, delta=delta)
+    torch.cuda.synchronize()
+    ref = (out.double() * dout.cpu().double()).sum(-1)
+    torch.testing.assert_close(delta.cpu().double(), ref, rtol=1e-5, atol=1e-5 * float(ref.abs().max()))
