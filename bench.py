@@ -183,6 +183,8 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--no-backward", action="store_true",
                     help="skip the backward measurements (cfg4 VMonarch fwd+bwd, cfg5 FEA fwd+bwd)")
+    ap.add_argument("--qk-fp8", action="store_true",
+                    help="also time the opt-in fp8 q k^T mode of the R-steps (reported beside `value`, never as it)")
     ap.add_argument("--serial-only", action="store_true",
                     help="time only the serial order (every launch alone; for kernel traces)")
     args = ap.parse_args()
@@ -221,7 +223,7 @@ def main():
     stages.append("recompute")
     production_order = vm._RECOMPUTE_OVERLAP
 
-    def timed_region(order, with_events):
+    def timed_region(order, with_events, fp8=False):
         vm._RECOMPUTE_OVERLAP = order
         step_events = []
 
@@ -231,14 +233,15 @@ def main():
             step_events[-1][(name, phase)] = e
 
         for _ in range(args.warmup):
-            _vmonarch_fused(q, k, v, M, BS, ITERS, RT, mod.min_col_mass)
+            _vmonarch_fused(q, k, v, M, BS, ITERS, RT, mod.min_col_mass, qk_fp8=fp8)
         torch.cuda.synchronize()
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
         ev0.record(stream)
         for _ in range(args.steps):
             step_events.append({})
-            _vmonarch_fused(q, k, v, M, BS, ITERS, RT, mod.min_col_mass, stage_hook=hook if with_events else None)
+            _vmonarch_fused(q, k, v, M, BS, ITERS, RT, mod.min_col_mass, stage_hook=hook if with_events else None,
+                            qk_fp8=fp8)
         ev1.record(stream)
         torch.cuda.synchronize()
         wall = (time.perf_counter() - t0) * 1e3 / args.steps
@@ -275,6 +278,9 @@ def main():
             else:
                 ms, wall_ms, _ = timed_region(production_order, False)
                 ms_serial, _, acc = timed_region("off", True)
+            if args.qk_fp8:
+                ms8, _, _ = timed_region(production_order, False, fp8=True)
+                ms8_serial, _, acc8 = timed_region("off", True, fp8=True)
         finally:
             vm._RECOMPUTE_OVERLAP = production_order
 
@@ -323,6 +329,13 @@ def main():
                      "all_rstep_frac": round(sum(r_flops) / fea_ms / 1e9 / PEAK_BF16_TFLOPS, 4)},
         "kernels": kernels,
     }
+    if args.qk_fp8:
+        result["qk_fp8"] = {
+            "note": "opt-in mode beyond the reference: the R-steps' S = q k^T in fp8 e4m3 (per-row q, per-64-key-tile k "
+                    "scales, k quantized in a pass of its own per R-step); the recompute stays exact; never `value`",
+            "ms_per_step": round(ms8, 4), "ms_per_step_serial": round(ms8_serial, 4),
+            "tflops_same_work": round(total_flops / ms8 / 1e9, 2),
+            "rstep_ms": [round(acc8[n], 4) for n in names], "rstep_ms_bf16": [round(acc[n], 4) for n in names]}
     if not args.no_backward:
         del q, k, v
         result["backward"] = backward_timings(max(3, args.steps // 5))

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define VMO_ABI_VERSION 12
+#define VMO_ABI_VERSION 13
 
 enum {
   VMO_OK = 0,
@@ -82,6 +82,15 @@ typedef struct vmo_fea_fwd_args {
   int32_t num_splits;              /* 1 = no split */
   void* workspace;
   size_t workspace_bytes;
+  /* 1: S = q k^T in fp8 (e4m3; no counterpart in the reference, which computes S in bf16 / fp16): q rows
+   * scaled by their own max |q| / 448 in the kernel, k by one max |k| / 448 per 64-key tile in a pass before it (into the
+   * workspace: vmo_fea_fwd_workspace_size() counts nk * d bytes per problem and the tile scales); P, the
+   * value products, o, the entropy and lse as without it.  Built for the VMonarch R-steps (d = 128, w0 = k,
+   * dw1 in {0, 128}, entropy, num_splits = 1); an approximation: each logit off by up to ~4% of its size
+   * (e4m3's 3-bit mantissa), within the 16-bit tolerances for logits of std <= 0.25, an fp8 class
+   * (6e-2 + 3e-2 |ref| for o, 5e-2 for e) at std 1.  Measured slower than 16-bit S on MI355X (the
+   * R-steps are bound by their tile stream, which the fp8 K tile adds to); 0 is the default. */
+  int32_t qk_fp8;
 } vmo_fea_fwd_args;
 
 /*
@@ -254,10 +263,10 @@ int vmo_fea_fwd(const vmo_fea_fwd_args* args, void* stream);
  * Allocation-free variant of vmo_fea_fwd.  No counterpart in the reference: it is for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc).  Same arguments and results as vmo_fea_fwd, except that `workspace` /
- * `workspace_bytes` are ignored: the split-KV partials go to a library-owned static device array of
- * VMO_FEA_FWD_SCRATCH_BYTES on each GPU (held until the process ends).  A call whose partials need more
- * (vmo_fea_fwd_workspace_size() > VMO_FEA_FWD_SCRATCH_BYTES) is rejected with VMO_ERR_WORKSPACE before
- * any launch; calls with num_splits <= 1 use no scratch.  The call allocates nothing and calls no
+ * `workspace_bytes` are ignored: the split-KV partials (and with qk_fp8 the fp8 keys) go to a library-owned
+ * static device array of VMO_FEA_FWD_SCRATCH_BYTES on each GPU (held until the process ends).  A call whose
+ * workspace needs more (vmo_fea_fwd_workspace_size() > VMO_FEA_FWD_SCRATCH_BYTES) is rejected with
+ * VMO_ERR_WORKSPACE before any launch; calls with num_splits <= 1 and qk_fp8 = 0 use no scratch.  The call allocates nothing and calls no
  * allocating routine.  All calls on one GPU share its scratch: calls that overlap in time on one GPU
  * (different streams without ordering, or several host threads) race; order them on one stream.
  */

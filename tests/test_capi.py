@@ -270,3 +270,23 @@ def test_fea_bwd_workspace_holds_ds_for_the_ds_route(L):
     capped = L.vmo_fea_bwd_workspace_size(ctypes.byref(a))
     a.flags = _lib.BWD_RECOMPUTE_DQ
     assert capped == L.vmo_fea_bwd_workspace_size(ctypes.byref(a))
+
+
+def test_fea_fwd_qk_fp8_workspace_and_rejections(L):
+    """vmo_fea_fwd_args.qk_fp8: the workspace grows by the fp8 keys (problems x nk x d bytes, from a 256-byte
+    boundary) and one float per 64-key tile; values that are not k, d = 64, or a value other than 0 / 1 are
+    rejected before any launch."""
+    from vmonarch_amd import _lib
+    a = _fwd_args(frames=3, nk=1000, heads=2)
+    a.w0 = a.k   # values k (the R-step variants)
+    a.ent = _addr()
+    base = L.vmo_fea_fwd_workspace_size(ctypes.byref(a))
+    a.qk_fp8 = 1
+    assert L.vmo_fea_fwd_workspace_size(ctypes.byref(a)) - base == (6 * 1000 * 128 + 255) // 256 * 256 + 6 * 16 * 4
+    a.qk_fp8 = 2
+    a.workspace, a.workspace_bytes = _addr(1 << 22), 1 << 22
+    assert L.vmo_fea_fwd(ctypes.byref(a), None) == 1
+    a.qk_fp8 = 1
+    a.w0 = _lib.View(_addr(1 << 20), 128, 128 * 128, 128)   # values that are not k
+    assert L.vmo_fea_fwd(ctypes.byref(a), None) == 2
+    assert b"qk_fp8" in L.vmo_last_error()

@@ -60,7 +60,23 @@ struct FwdParams {
   int problems, q_tiles, splits, keys_per_split;
   int total_wg;
   float scale_log2;
+  // fp8 S (QK8 variants): k quantized per problem, rows [nk][128] in the operand order of fea_fp8_keys_kernel,
+  // one scale per 64-key tile (k8_tiles per problem)
+  void* k8;
+  float* k8_scale;
+  int k8_tiles;
 };
+
+// Bytes of one pipeline stage: the K tile, the value tiles the K tile does not double as, and with fp8 S
+// the fp8 K tile (one byte per element).
+template <int D, int DW0, int DW1, bool W0K, bool QK8>
+constexpr int fwd_stage_bytes() { return kFwdBN * (D + (W0K ? 0 : DW0) + DW1) * 2 + (QK8 ? kFwdBN * D : 0); }
+
+// fp8 (e4m3) operand layout of the fp8 S product: a 128-wide row as two 64-dim products; lane half hl of
+// product m takes dims 16 ds + 8 hl + e (ds = 4 m .. 4 m + 3, e = 0 .. 7), which are those the lane holds
+// of the 16-bit q row, as 32 consecutive bytes.  Byte position of dim d in the stored row:
+__host__ __device__ constexpr int fp8_dim_pos(int d) { return 64 * (d / 64) + 32 * ((d / 8) % 2) + 8 * ((d / 16) % 4) + d % 8; }
+constexpr float kFp8Max = 448.f;   // e4m3's largest finite value (the conversion does not saturate: beyond it is NaN)
 
 // LDS ring slots per workgroup: prefetch two tiles ahead when three slots fit the workgroup's share
 // of the CU's 160 KB (two 4-wave workgroups or one 8-wave workgroup per CU), else one ahead.
@@ -145,7 +161,7 @@ constexpr int fwd_min_blocks() {
   return (D >= 256 || DW0 >= 256 || (ENT == kEntOnline && D < DW0) || (DW1 > 0 && DW1 < D)) ? 1 : 8 / WAVES;
 }
 
-template <bool F16, int D, int DW0, int DW1, bool W0K, int ENT, bool SPLIT, int WAVES>
+template <bool F16, int D, int DW0, int DW1, bool W0K, int ENT, bool SPLIT, int WAVES, bool QK8>
 __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES>())) void fea_fwd_kernel(FwdParams p) {
   using E = Elem<F16>;
   using T = typename E::T;
@@ -155,8 +171,10 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
   constexpr int K_BYTES = kFwdBN * D * 2;
   constexpr int W0_BYTES = W0K ? 0 : kFwdBN * DW0 * 2;
   constexpr int W1_BYTES = kFwdBN * DW1 * 2;
-  constexpr int STAGE = K_BYTES + W0_BYTES + W1_BYTES;
+  constexpr int K8_OFF = K_BYTES + W0_BYTES + W1_BYTES;   // the fp8 K tile (QK8)
+  constexpr int STAGE = fwd_stage_bytes<D, DW0, DW1, W0K, QK8>();
   constexpr int NSLOT = fwd_slots(STAGE, WAVES);
+  static_assert(!QK8 || D == 128, "fp8 S is built for 128-wide q / k");
   constexpr int kBM = 32 * kFwdQB * WAVES;   // queries per workgroup
   constexpr int NA0 = DW0 / 32;
   constexpr int NA1 = DW1 / 32;
@@ -164,7 +182,8 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
   constexpr int NDS = D / 16;
   constexpr int QB = kFwdQB;
   // global_load_lds instructions one tile costs each wave (vmcnt units)
-  constexpr int DMA_PER_TILE = kFwdBN * (D + (W0K ? 0 : DW0) + DW1) * 2 / 1024 / WAVES;
+  constexpr int DMA_PER_TILE = STAGE / 1024 / WAVES;
+  static_assert(STAGE % (1024 * WAVES) == 0, "whole copy instructions per wave");
   static_assert(!W0K || DW0 == D, "w0 aliases k");
   static_assert(ENT != kEntFromPK || W0K, "entropy from P.K needs w0 == k");
 
@@ -241,6 +260,9 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
   const TileCopy<T, D, WAVES> kcopy(kb, p.k_sn, wave, lane);
   const TileCopy<T, W0K ? 64 : DW0, WAVES> w0copy(w0b, p.w0_sn, wave, lane);
   const TileCopy<T, DW1 ? DW1 : 64, WAVES> w1copy(w1b, p.w1_sn, wave, lane);
+  // fp8 K rows: 128 bytes, copied as 64 16-bit elements
+  const TileCopy<T, 64, WAVES> k8copy(QK8 ? (const T*)((const char*)p.k8 + (int64_t)loc.prob * p.nk * D) : kb, 64,
+                                      wave, lane);
   auto issue = [&](int t) __attribute__((always_inline)) {
     uint32_t sb = smem_u32;
     asm volatile("" : "+s"(sb));   // keep the LDS destinations from being hoisted (see TileCopy)
@@ -249,6 +271,7 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
     kcopy.issue(row0, p.nk, st);
     if constexpr (!W0K) w0copy.issue(row0, p.nk, st + K_BYTES);
     if constexpr (DW1 > 0) w1copy.issue(row0, p.nk, st + K_BYTES + W0_BYTES);
+    if constexpr (QK8) k8copy.issue(row0, p.nk, st + K8_OFF);
   };
 
   const float c = p.scale_log2;
@@ -260,6 +283,45 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
   // takes the same exact path, so P never rounds to inf.
   constexpr float kSumLimit = F16 ? 65504.f : 1.8446744e19f;   // fp16 max / 2^64
   float m_run[QB], l_run[QB], h_run[QB];
+
+  // x = s cf - m with cf = c -- or, with fp8 S, c times the row's q scale times the tile's k scale (both
+  // positive, so maxima commute with the scaling).  fp8 S: each q row is quantized here, in registers, by
+  // its own max |q| / 448 (the lane pair l, l + 32 holds one row).
+  typedef int i32x8 __attribute__((ext_vector_type(8)));
+  i32x8 qf8[QK8 ? QB : 1][2];
+  float cq[QB], cf[QB];
+#pragma unroll
+  for (int j = 0; j < QB; ++j) {
+    cq[j] = c;
+    if constexpr (QK8) {
+      float amax = 0.f;
+#pragma unroll
+      for (int ds = 0; ds < NDS; ++ds)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf((float)qf[j][ds][e]));
+      amax = wave_max32(amax);
+      const float inv = amax > 0.f ? kFp8Max / amax : 1.f;
+      cq[j] = c * (amax > 0.f ? amax / kFp8Max : 1.f);
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {   // bytes 4 w .. 4 w + 3 of product m: dims 16 (4 m + w / 2) + 8 hl + 4 (w % 2) + 0..3
+          const V8& v = qf[j][4 * m + w / 2];
+          const int e0 = 4 * (w % 2);
+          int word = __builtin_amdgcn_cvt_pk_fp8_f32((float)v[e0] * inv, (float)v[e0 + 1] * inv, 0, false);
+          qf8[j][m][w] = __builtin_amdgcn_cvt_pk_fp8_f32((float)v[e0 + 2] * inv, (float)v[e0 + 3] * inv, word, true);
+        }
+    }
+    cf[j] = cq[j];
+  }
+  const int k8_row0 = QK8 ? __builtin_amdgcn_readfirstlane(loc.prob * p.k8_tiles + kbeg / kFwdBN) : 0;
+  auto tile_scale = [&](int t) __attribute__((always_inline)) {
+    if constexpr (QK8) {
+      const float sk = p.k8_scale[k8_row0 + t];
+#pragma unroll
+      for (int j = 0; j < QB; ++j) cf[j] = cq[j] * sk;
+    }
+  };
   f32x16 acc[QB][NA];
   bool overflow = false;
 
@@ -273,8 +335,29 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
   // reads run kPre fragments ahead of the MFMAs (pinned by sched_group_barrier) so the LDS latency
   // hides behind the previous MFMAs instead of stalling each one.
   constexpr int kPre = 2;
+  const int srow_sw8 = swz_rows<128>(l32);   // fp8 K rows (128 bytes)
   auto qk_block = [&](const VMO_LDS char* Ks, int kb2, f32x16 (&x)[QB], auto sched_tag)
       __attribute__((always_inline)) {
+    if constexpr (QK8) {
+      // S^T = K8 Q8^T: two 32x32x64 fp8 products; lane (key l32, half hl) reads the 32 bytes of product m
+      // as chunks 4 m + 2 hl and + 1 of its key's row
+      const VMO_LDS char* arow8 = Ks + K8_OFF + (32 * kb2 + l32) * 128;
+      i32x8 a8[2];
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const i32x4 lo = *(const VMO_LDS i32x4*)(arow8 + ((4 * m + 2 * hl) ^ srow_sw8) * 16);
+        const i32x4 hi = *(const VMO_LDS i32x4*)(arow8 + ((4 * m + 2 * hl + 1) ^ srow_sw8) * 16);
+        a8[m] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      }
+#pragma unroll
+      for (int j = 0; j < QB; ++j) {
+        x[j] = f32x16{};
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+          x[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8[m], qf8[j][m], x[j], 0, 0, 0, 0, 0, 0);
+      }
+      return;
+    }
     const VMO_LDS char* arow = Ks + (32 * kb2 + l32) * (D * 2);
     V8 a[NDS];
 #pragma unroll
@@ -313,7 +396,7 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
 #pragma unroll
     for (int j = 0; j < QB; ++j) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) x[j][r] = fmaf(x[j][r], c, -m_run[j]);
+      for (int r = 0; r < 16; ++r) x[j][r] = fmaf(x[j][r], cf[j], -m_run[j]);
       if constexpr (MASKED) mask_block(x[j], kofs, nvalid);
       // two partial sums per lane (pairs r % 4 == 0 and == 2), each started from its first term: an
       // accumulator started at 0 costs an add of +0 per block that the compiler cannot drop (-0 + 0 = +0)
@@ -431,7 +514,8 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
     pv_block(Ks, 1, P1, std::true_type{});
   };
 
-  // max over the valid keys of S^T block kb of a stage (raw logits, whole row after the swap)
+  // max over the valid keys of S^T block kb of a stage (whole row after the swap), in units of x (times
+  // cf: the tile's factor)
   auto block_max = [&](const VMO_LDS char* Ks, int kb2, int nvalid, float (&mx)[QB]) __attribute__((always_inline)) {
     f32x16 x[QB];
     qk_block(Ks, kb2, x, std::true_type{});
@@ -441,7 +525,7 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
       float v = x[j][0];
 #pragma unroll
       for (int r = 1; r < 16; ++r) v = fmaxf(v, x[j][r]);
-      mx[j] = fmaxf(mx[j], wave_max32(v));
+      mx[j] = fmaxf(mx[j], wave_max32(v) * cf[j]);
     }
   };
 
@@ -485,6 +569,7 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
         constexpr int S = decltype(slot_tag)::value;
         tile_sync<kSteadyPending>();
         if (t + NSLOT - 1 < n_tiles) issue(t + NSLOT - 1);
+        tile_scale(t);
         if constexpr (kPipe)
           stage_pipe((const VMO_LDS char*)smem + S * STAGE);
         else
@@ -499,9 +584,11 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
       for (; t < n_tiles - 1; ++t) {   // fewer than NSLOT full tiles left
         tile_sync<kSteadyPending>();
         if (t + NSLOT - 1 < n_tiles) issue(t + NSLOT - 1);
+        tile_scale(t);
         stage(slot(t), kFwdBN, std::false_type{}, std::true_type{});
       }
       tile_sync<0>();
+      tile_scale(t);
       const int nvalid = kend - (kbeg + t * kFwdBN);   // 1 .. 64
       if (nvalid == kFwdBN)
         stage(slot(t), nvalid, std::false_type{}, std::true_type{});
@@ -525,14 +612,31 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
     float mx[QB];
 #pragma unroll
     for (int j = 0; j < QB; ++j) mx[j] = kMaskLogit;
+    tile_scale(0);
     if (wave_live) block_max(slot(0), 0, kend - kbeg, mx);
 #pragma unroll
-    for (int j = 0; j < QB; ++j) m_run[j] = mx[j] * c;
+    for (int j = 0; j < QB; ++j) m_run[j] = mx[j];
   }
   reset();
   key_loop();
 
-  if (__syncthreads_or(overflow ? 1 : 0)) {
+  // Workgroup OR of the overflow flags through one word per wave in a ring slot that no wave reads and no
+  // copy fills any more (that of tile n_tiles - NSLOT, or one never used): __syncthreads_or takes a static
+  // LDS word, which the compiler pads to the ring's 1024-byte alignment -- 1 KB that costs the widest
+  // variants their second workgroup per CU.  The second barrier keeps every word until all waves have read
+  // them (a wave past it may refill the ring or write its epilogue patch).
+  auto workgroup_any = [&](bool flag) __attribute__((always_inline)) {
+    VMO_LDS int* words = (VMO_LDS int*)(smem + (n_tiles % NSLOT) * STAGE);
+    const bool wave_any = __builtin_amdgcn_ballot_w64(flag) != 0;
+    if (lane == 0) words[wave] = wave_any ? 1 : 0;
+    __syncthreads();
+    int any = 0;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) any |= words[w];
+    __syncthreads();
+    return any != 0;
+  };
+  if (workgroup_any(overflow)) {
     // exact two-pass fallback for this workgroup: the true row max, then the loop again
     float mx[QB];
 #pragma unroll
@@ -540,13 +644,14 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
     auto max_tile = [&](int t) __attribute__((always_inline)) {
       if (!wave_live) return;
       const int nvalid = kend - (kbeg + t * kFwdBN);
+      tile_scale(t);
       block_max(slot(t), 0, nvalid, mx);
       if (nvalid > 32) block_max(slot(t), 1, nvalid, mx);
     };
     prime();
     for_tiles(max_tile, max_tile);
 #pragma unroll
-    for (int j = 0; j < QB; ++j) m_run[j] = mx[j] * c;
+    for (int j = 0; j < QB; ++j) m_run[j] = mx[j];
     reset();
     tile_sync<0>();   // every wave is done with the last max-pass tile before the ring is reused
     prime();
@@ -650,14 +755,63 @@ __global__ __launch_bounds__(256) void fea_combine_kernel(FwdParams p) {
   if (c4 == 0 && p.lse) p.lse[bb * p.st_sb + hh * p.st_sh + (int64_t)f * p.nq + qi] = M + fast_log2(wsum);
 }
 
-template <bool F16, int D, int DW0, int DW1, bool W0K, int ENT, bool SPLIT, int WAVES>
+// fp8 keys for the fp8-S variants: each 64-key tile of a problem (b, h, f) scaled by its own max |k| / 448
+// (one scale per tile keeps the per-element work of the key loop at one multiply per tile and lane), its
+// 128-dim rows stored in the operand order fp8_dim_pos.  One workgroup per tile, four 16-byte chunks per
+// thread.
+template <bool F16>
+__global__ __launch_bounds__(256) void fea_fp8_keys_kernel(FwdParams p) {
+  using T = typename Elem<F16>::T;
+  using V8 = typename Elem<F16>::V8;
+  const int tile = blockIdx.x, prob = tile / p.k8_tiles, t = tile % p.k8_tiles;
+  const int f = prob % p.frames, bh = prob / p.frames, hh = bh % p.heads, bb = bh / p.heads;
+  const T* kb = (const T*)p.k + bb * p.k_sb + hh * p.k_sh + ((int64_t)f * p.nk + (int64_t)t * kFwdBN) * p.k_sn;
+  const int rows = min(kFwdBN, p.nk - t * kFwdBN);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  V8 v[4];
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {   // chunk tid + 256 i: row / 16, dims 8 (chunk % 16) .. + 7
+    const int id = tid + 256 * i, r = id >> 4, ch = id & 15;
+    v[i] = r < rows ? *(const V8*)(kb + (int64_t)r * p.k_sn + 8 * ch) : V8{};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf((float)v[i][e]));
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m));
+  __shared__ float wmax[4];
+  if (lane == 0) wmax[wave] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  const float inv = amax > 0.f ? kFp8Max / amax : 1.f;
+  if (tid == 0) p.k8_scale[tile] = amax > 0.f ? amax / kFp8Max : 1.f;
+  char* out = (char*)p.k8 + ((int64_t)prob * p.nk + (int64_t)t * kFwdBN) * 128;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int id = tid + 256 * i, r = id >> 4, ch = id & 15;
+    if (r >= rows) continue;
+    const int w0 = __builtin_amdgcn_cvt_pk_fp8_f32((float)v[i][0] * inv, (float)v[i][1] * inv, 0, false);
+    const int w1 = __builtin_amdgcn_cvt_pk_fp8_f32((float)v[i][4] * inv, (float)v[i][5] * inv, 0, false);
+    uint2 b;
+    b.x = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32((float)v[i][2] * inv, (float)v[i][3] * inv, w0, true);
+    b.y = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32((float)v[i][6] * inv, (float)v[i][7] * inv, w1, true);
+    *(uint2*)(out + r * 128 + fp8_dim_pos(8 * ch)) = b;
+  }
+}
+
+template <bool F16, int D, int DW0, int DW1, bool W0K, int ENT, bool SPLIT, int WAVES, bool QK8 = false>
 static int launch_fwd(FwdParams p, hipStream_t stream) {
-  constexpr int STAGE = kFwdBN * (D + (W0K ? 0 : DW0) + DW1) * 2;
+  constexpr int STAGE = fwd_stage_bytes<D, DW0, DW1, W0K, QK8>();
   constexpr int LDS = fwd_slots(STAGE, WAVES) * STAGE;
   constexpr int BM = 32 * kFwdQB * WAVES;
   p.q_tiles = (p.nq + BM - 1) / BM;
   p.total_wg = p.problems * p.splits * p.q_tiles;
-  auto kern = fea_fwd_kernel<F16, D, DW0, DW1, W0K, ENT, SPLIT, WAVES>;
+  auto kern = fea_fwd_kernel<F16, D, DW0, DW1, W0K, ENT, SPLIT, WAVES, QK8>;
+  if constexpr (QK8) {
+    hipLaunchKernelGGL((fea_fp8_keys_kernel<F16>), dim3((unsigned)((int64_t)p.problems * p.k8_tiles)), dim3(256), 0, stream, p);
+    const int rc = launch_status("fea_fp8_keys");
+    if (rc != VMO_OK) return rc;
+  }
   if (LDS > 65536) {
     static bool done = false;   // attribute is per function; idempotent, so a benign race
     if (!done) {
@@ -681,7 +835,21 @@ constexpr int kFwdWavesFor(int, int, int, bool) { return kFwdWavesSmall; }
 
 // Runtime -> template dispatch over the supported shapes.
 template <bool F16>
-static int dispatch_fwd(const FwdParams& p, int d, int dw0, int dw1, bool w0k, bool ent, bool split, hipStream_t s) {
+static int dispatch_fwd(const FwdParams& p, int d, int dw0, int dw1, bool w0k, bool ent, bool split, bool qk8,
+                        hipStream_t s) {
+  if (qk8) {
+    // fp8 S: the VMonarch R-step variants (values k or [k | v], d = 128), with the P.K entropy: e = LSE -
+    // (exact q . sum p k) / l, the LSE from the fp8 logits, so e carries the fp8 error of the row's mean logit
+    // (negligible on the soft rows the mode is for; up to ~2 nats on rows whose logits reach ~80).  The online
+    // entropy (sum p x over the fp8 logits themselves) spills 64-93 dwords in these values-k variants.
+    if (d == 128 && dw0 == 128 && w0k && ent && !split) {
+      if (dw1 == 0) return launch_fwd<F16, 128, 128, 0, true, kEntFromPK, false, kFwdWavesSmall, true>(p, s);
+      if (dw1 == 128) return launch_fwd<F16, 128, 128, 128, true, kEntFromPK, false, kFwdWavesSmall, true>(p, s);
+    }
+    return set_error(VMO_ERR_UNSUPPORTED, "fea_fwd: qk_fp8 is built for the VMonarch R-steps (d = 128, values k or "
+                     "[k | v1] with dw1 = 128, entropy, one split); got d=%d dw0=%d dw1=%d w0_is_k=%d entropy=%d "
+                     "split=%d", d, dw0, dw1, (int)w0k, (int)ent, (int)split);
+  }
 #define VMO_FWD(D_, DW0_, DW1_, W0K_, ENT_, SPLIT_)                                                  \
   if (d == D_ && dw0 == DW0_ && dw1 == DW1_ && w0k == W0K_ && ent == (ENT_ != kEntNone) && split == SPLIT_) \
     return launch_fwd<F16, D_, DW0_, DW1_, W0K_, ENT_, SPLIT_, kFwdWavesFor(D_, DW0_, DW1_, SPLIT_)>(p, s);
@@ -714,6 +882,18 @@ static int dispatch_fwd(const FwdParams& p, int d, int dw0, int dw1, bool w0k, b
                    dw0, dw1, (int)w0k, (int)ent, (int)split);
 }
 
+static int64_t split_layout(const vmo_fea_fwd_args* a, int* splits_out, int* kps_out);
+// Workspace: the split-KV partials, then with qk_fp8 the fp8 keys (problems x nk x d bytes) and their
+// per-tile scales.  *k8_off: where the fp8 keys start.
+static int64_t fwd_workspace(const vmo_fea_fwd_args* a, int* splits, int* kps, int64_t* k8_off) {
+  const int64_t part = (split_layout(a, splits, kps) + 255) / 256 * 256;
+  *k8_off = part;
+  if (!a->qk_fp8) return part;
+  const int64_t problems = (int64_t)a->batch * a->heads * a->frames;
+  const int64_t k8 = (problems * a->nk * a->d + 255) / 256 * 256;
+  return part + k8 + problems * ((a->nk + kFwdBN - 1) / kFwdBN) * 4;
+}
+
 static int64_t split_layout(const vmo_fea_fwd_args* a, int* splits_out, int* kps_out) {
   const int tiles = (a->nk + kFwdBN - 1) / kFwdBN;
   int want = a->num_splits < 1 ? 1 : a->num_splits;
@@ -730,9 +910,10 @@ static int64_t split_layout(const vmo_fea_fwd_args* a, int* splits_out, int* kps
 }  // namespace vmo
 
 extern "C" size_t vmo_fea_fwd_workspace_size(const vmo_fea_fwd_args* a) {
-  if (!a || a->nk <= 0) return 0;
+  if (!a || a->nk <= 0 || a->batch <= 0 || a->heads <= 0 || a->frames <= 0) return 0;
   int s, kps;
-  return (size_t)vmo::split_layout(a, &s, &kps);
+  int64_t k8_off;
+  return (size_t)vmo::fwd_workspace(a, &s, &kps, &k8_off);
 }
 
 namespace vmo {
@@ -760,10 +941,12 @@ static int fea_fwd_impl(const vmo_fea_fwd_args* a, void* workspace, size_t works
                    a->w0.stride_n == a->k.stride_n && a->dw0 == a->d;
   if (a->dw1 > 0 && !w0k) return set_error(VMO_ERR_UNSUPPORTED, "fea_fwd: a second value tensor needs w0 == k");
   int splits, kps;
-  const int64_t ws = split_layout(a, &splits, &kps);
+  int64_t k8_off;
+  const int64_t ws = fwd_workspace(a, &splits, &kps, &k8_off);
   const bool ent = a->ent != nullptr;
   if (splits > 1 && ent) return set_error(VMO_ERR_UNSUPPORTED, "fea_fwd: split-KV with entropy output");
-  if (splits > 1 && (workspace == nullptr || workspace_bytes < (size_t)ws || !aligned16(workspace)))
+  if (a->qk_fp8 != 0 && a->qk_fp8 != 1) return set_error(VMO_ERR_INVALID, "fea_fwd: qk_fp8 is 0 or 1");
+  if (ws > 0 && (workspace == nullptr || workspace_bytes < (size_t)ws || !aligned16(workspace)))
     return set_error(VMO_ERR_WORKSPACE, "fea_fwd: needs %lld workspace bytes, has %llu", (long long)ws,
                      (unsigned long long)(workspace ? workspace_bytes : 0));
   const int64_t q_tiles = (a->nq + 32 * kFwdQB * kFwdWavesSmall - 1) / (32 * kFwdQB * kFwdWavesSmall);
@@ -790,13 +973,20 @@ static int fea_fwd_impl(const vmo_fea_fwd_args* a, void* workspace, size_t works
   p.problems = (int)problems; p.q_tiles = (int)q_tiles; p.splits = splits; p.keys_per_split = kps;
   p.total_wg = (int)total;
   p.scale_log2 = a->sm_scale * kLog2e;
+  if (a->qk_fp8) {
+    p.k8 = (char*)workspace + k8_off;
+    p.k8_tiles = (a->nk + kFwdBN - 1) / kFwdBN;
+    p.k8_scale = (float*)((char*)p.k8 + (problems * a->nk * a->d + 255) / 256 * 256);
+  }
   hipStream_t s = (hipStream_t)stream;
-  if (a->dtype == VMO_DTYPE_F16) return dispatch_fwd<true>(p, a->d, a->dw0, a->dw1, w0k, ent, splits > 1, s);
-  return dispatch_fwd<false>(p, a->d, a->dw0, a->dw1, w0k, ent, splits > 1, s);
+  const bool qk8 = a->qk_fp8 != 0;
+  if (a->dtype == VMO_DTYPE_F16) return dispatch_fwd<true>(p, a->d, a->dw0, a->dw1, w0k, ent, splits > 1, qk8, s);
+  return dispatch_fwd<false>(p, a->d, a->dw0, a->dw1, w0k, ent, splits > 1, qk8, s);
 }
 
 // Scratch of the allocation-free entry point: split-KV partials (fp32 o and lse of every split), fully
-// written by the split kernels before the merge reads them, so nothing needs clearing between calls.
+// written by the split kernels before the merge reads them, and with qk_fp8 the fp8 keys and their scales,
+// fully written by fea_fp8_keys_kernel before the forward reads them, so nothing needs clearing between calls.
 // Each GPU the library runs on holds its own copy, at its own address, until the process ends.
 static __device__ __align__(256) char scratch[VMO_FEA_FWD_SCRATCH_BYTES];
 
@@ -834,8 +1024,8 @@ extern "C" int vmo_fea_fwd_noalloc(const vmo_fea_fwd_args* a, void* stream) {
   clear_error();
   if (!a) return set_error(VMO_ERR_INVALID, "fea_fwd_noalloc: null args");
   if (vmo_fea_fwd_workspace_size(a) > VMO_FEA_FWD_SCRATCH_BYTES)
-    return set_error(VMO_ERR_WORKSPACE, "fea_fwd_noalloc: split-KV partials need %llu bytes, the library scratch holds %llu "
-                     "(use fewer splits)", (unsigned long long)vmo_fea_fwd_workspace_size(a),
+    return set_error(VMO_ERR_WORKSPACE, "fea_fwd_noalloc: the workspace (split-KV partials, fp8 keys) needs %llu bytes, "
+                     "the library scratch holds %llu (use fewer splits, or 16-bit S)", (unsigned long long)vmo_fea_fwd_workspace_size(a),
                      (unsigned long long)VMO_FEA_FWD_SCRATCH_BYTES);
   void* ws = nullptr;
   const int rc = scratch_on_current_device(&ws);

@@ -148,11 +148,13 @@ def _side_stream(dev):
     return s
 
 
-def _vmonarch_fused(q, k, v, m, b, num_iters, recompute_tokens, min_col_mass, stage_hook=None, scale=None):
+def _vmonarch_fused(q, k, v, m, b, num_iters, recompute_tokens, min_col_mass, stage_hook=None, scale=None,
+                    qk_fp8=False):
     """All-HIP forward.  `stage_hook(name, phase, stream)`, when given, is called on the host right
     before ("begin") and after ("end") each launch group ("rstep0", "lstep0", ..., "recompute") with
     the stream it goes to -- used by bench.py to bracket every kernel with events.  `scale` overrides
-    D ** -0.5 (q / k zero-padded past their head dim)."""
+    D ** -0.5 (q / k zero-padded past their head dim).  `qk_fp8`: the R-steps' S in fp8 (the recompute
+    stays exact)."""
     B, H, N, D = q.shape
     Dv = v.shape[-1]
     scale = D ** -0.5 if scale is None else scale
@@ -188,7 +190,7 @@ def _vmonarch_fused(q, k, v, m, b, num_iters, recompute_tokens, min_col_mass, st
         # R-step (vmonarch.py:50): iteration 0 folds u = q * scale into the softmax scale
         x, s = (q, scale) if it == 0 else (u, 1.0)
         hook(f"rstep{it}", "begin", main)
-        out, _, _ = fea_forward(x, k, k, v if last else None, s, frames=m, ent=ent, want_lse=False)
+        out, _, _ = fea_forward(x, k, k, v if last else None, s, frames=m, ent=ent, want_lse=False, qk_fp8=qk_fp8)
         hook(f"rstep{it}", "end", main)
         if rt > 0 and side is None and ((_RECOMPUTE_OVERLAP == "after_r0" and it == 0) or
                                         (_RECOMPUTE_OVERLAP == "after_r1" and last)):
@@ -366,7 +368,8 @@ def _pad_to(t, w):
     return t if t.shape[-1] == w else torch.nn.functional.pad(t, (0, w - t.shape[-1]))
 
 
-def vmonarch_attention(q, k, v, num_blocks, block_size, num_iters=2, recompute_tokens=0, min_col_mass=0.01):
+def vmonarch_attention(q, k, v, num_blocks, block_size, num_iters=2, recompute_tokens=0, min_col_mass=0.01,
+                       qk_fp8=False):
     """
     Args:
         q, k: (B, H, N, D); v: (B, H, N, Dv), with N == num_blocks * block_size.
@@ -375,6 +378,8 @@ def vmonarch_attention(q, k, v, num_blocks, block_size, num_iters=2, recompute_t
         num_iters: alternating-minimization steps.
         recompute_tokens: the first `recompute_tokens` queries use exact attention.
         min_col_mass: lower bound of the column mass of L, for stability.
+        qk_fp8: (beyond the reference) the R-steps' q k^T in fp8 e4m3, forward only, D = 128; the
+            recompute stays exact.  An approximation: logits off by ~1% of their spread.  D = Dv = 128.
     Returns:
         (B, H, N, Dv)
     """
@@ -384,6 +389,16 @@ def vmonarch_attention(q, k, v, num_blocks, block_size, num_iters=2, recompute_t
         raise UnboundLocalError("local variable 'z' referenced before assignment")  # as the reference (vmonarch.py:65)
     needs_graph = torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v))
     Dv = v.shape[-1]
+    if qk_fp8:
+        if needs_graph:
+            raise NotImplementedError("vmonarch_amd: qk_fp8 is forward-only (the backward recomputes S in the "
+                                      "16-bit type); run under torch.no_grad() or without it")
+        if not (_row_block_attention is _ROW_BLOCK_ATTENTION and D == 128 and Dv == 128
+                and _fused_supported(q, k, v, num_blocks)):
+            raise NotImplementedError(f"vmonarch_amd: qk_fp8 is built for the fused HIP path with head dim 128 "
+                                      f"(got D={D}, Dv={Dv}, num_blocks={num_blocks}, {q.dtype})")
+        return _vmonarch_fused(q, k, v, num_blocks, block_size, num_iters, recompute_tokens, min_col_mass,
+                               qk_fp8=True)
     if _row_block_attention is _ROW_BLOCK_ATTENTION:
         args = (num_blocks, block_size, num_iters, recompute_tokens, min_col_mass)
         if not needs_graph and _fused_supported(q, k, v, num_blocks):
@@ -415,16 +430,17 @@ def vmonarch_attention(q, k, v, num_blocks, block_size, num_iters=2, recompute_t
 class VMonarchAttention(nn.Module):
     """Module wrapper (reference vmonarch.py:72-85); holds no parameters."""
 
-    def __init__(self, num_blocks, block_size, num_iters=2, min_col_mass=0.01):
+    def __init__(self, num_blocks, block_size, num_iters=2, min_col_mass=0.01, qk_fp8=False):
         super().__init__()
         self.num_blocks = num_blocks
         self.block_size = block_size
         self.num_iters = num_iters
         self.min_col_mass = min_col_mass
+        self.qk_fp8 = qk_fp8   # beyond the reference: fp8 q k^T in the R-steps (vmonarch_attention)
 
     def forward(self, q, k, v, recompute_tokens=0):
         return vmonarch_attention(q, k, v, self.num_blocks, self.block_size, self.num_iters,
-                                  recompute_tokens, self.min_col_mass)
+                                  recompute_tokens, self.min_col_mass, qk_fp8=self.qk_fp8)
 
     def extra_repr(self):
         return f"num_blocks={self.num_blocks}, block_size={self.block_size}, num_iters={self.num_iters}"
