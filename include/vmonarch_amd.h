@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define VMO_ABI_VERSION 14
+#define VMO_ABI_VERSION 13
 
 enum {
   VMO_OK = 0,
@@ -91,11 +91,6 @@ typedef struct vmo_fea_fwd_args {
    * (6e-2 + 3e-2 |ref| for o, 5e-2 for e) at std 1.  Measured slower than 16-bit S on MI355X (the
    * R-steps are bound by their tile stream, which the fp8 K tile adds to); 0 is the default. */
   int32_t qk_fp8;
-  /* Workgroups of the launch: 0 = one per query tile, or -- when there are more tiles than the GPU holds
-   * workgroups at once -- that many, each running its share of the tiles with the next tile's first key
-   * stages and q rows loaded while the current one finishes.  > 0 caps the count (rounded down to a
-   * multiple of 8, at least 8; a scheduling choice only: every count gives bit-identical results). */
-  int32_t max_blocks;
 } vmo_fea_fwd_args;
 
 /*

@@ -12,7 +12,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libvmonarch_gfx950.so")
-ABI_VERSION = 14
+ABI_VERSION = 13
 FEA_FWD_SCRATCH_BYTES = 32 << 20   # VMO_FEA_FWD_SCRATCH_BYTES: scratch of vmo_fea_fwd_noalloc per GPU
 DTYPES = {torch.bfloat16: 0, torch.float16: 1}
 
@@ -30,7 +30,7 @@ class FeaFwdArgs(ctypes.Structure):
         ("q", View), ("k", View), ("w0", View), ("w1", View), ("o", View),
         ("lse", c_void_p), ("ent", c_void_p), ("stat_stride_b", c_int64), ("stat_stride_h", c_int64),
         ("sm_scale", c_float), ("num_splits", c_int32), ("workspace", c_void_p), ("workspace_bytes", c_size_t),
-        ("qk_fp8", c_int32), ("max_blocks", c_int32),
+        ("qk_fp8", c_int32),
     ]
 
 

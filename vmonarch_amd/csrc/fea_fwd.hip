@@ -65,9 +65,6 @@ struct FwdParams {
   void* k8;
   float* k8_scale;
   int k8_tiles;
-  // dividers of the tile index: query tiles, splits, frames, heads
-  FastDiv fd_qt, fd_sp, fd_fr, fd_hd;
-  int max_blocks;   // host side only: cap on the launch's workgroups (0: the device's resident capacity)
 };
 
 // Bytes of one pipeline stage: the K tile, the value tiles the K tile does not double as, and with fp8 S
@@ -116,11 +113,7 @@ struct TileCopy {
       voff[v] = (uint32_t)((int64_t)(l / CH) * s * 2) + (uint32_t)(((l % CH) ^ swz_rows<W * 2>(r)) * 16);
     }
   }
-  // the tensor's rows of another tile (a persistent workgroup's next problem)
-  __device__ __forceinline__ void rebase(const T* b) { ubase = uniform64((uint64_t)(uintptr_t)b); }
-  __device__ __forceinline__ void issue(int row0, int nrows, uint32_t dst) const { issue_from(ubase, row0, nrows, dst); }
-  // Copies rows row0 .. row0 + 63 of the tensor whose row 0 is at byte address `base` (same row stride).
-  __device__ __forceinline__ void issue_from(uint64_t base, int row0, int nrows, uint32_t dst) const {
+  __device__ __forceinline__ void issue(int row0, int nrows, uint32_t dst) const {
     // row0 and nrows are uniform, but may arrive in vector registers (the variants that keep the
     // tile indices in vector registers): without readfirstlane the full-tile test becomes an exec
     // mask branch and the tile address a vector 64-bit multiply per copy.
@@ -129,7 +122,7 @@ struct TileCopy {
     // The per-instruction addresses are loop invariant up to row0; hoisted out of the key loop
     // they would pin dozens of scalar registers.  The empty asm hides where ub comes from, so they
     // are recomputed here (a few scalar adds per copy).
-    uint64_t ub = uniform64(base);
+    uint64_t ub = ubase;
     asm volatile("" : "+s"(ub));
     if (row0 + kFwdBN <= nrows) {
       const uint64_t tb = ub + (uint64_t)(row0 + wave * RPI) * rbytes;
@@ -198,21 +191,11 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
   VMO_LDS char* smem = (VMO_LDS char*)smem_raw;
   const uint32_t smem_u32 = (uint32_t)(uintptr_t)smem;
 
-  // Tile schedule.  Block b runs on XCD b % 8; XCD x owns the contiguous logical tiles [x T, x T + T),
-  // T = ceil(total / 8) (all query tiles of a problem then share one L2 for their K / W traffic), and its
-  // blocks take them in turn: block (x, i) runs tiles x T + i, x T + i + B, ... (B blocks per XCD).  A grid
-  // of one block per tile runs one tile per block.  A grid of the resident capacity keeps every block alive
-  // across tiles: the next tile's first K / W stages and q rows load while the current tile's outputs are
-  // written, so a tile's start (q load, first copies) overlaps the previous tile's epilogue.
-  // Scalar registers are scarce in the widest variants, so of the schedule only the current tile L stays live
-  // across the key loop; the rest is derived again where it is needed.
-  auto tile_end = [&]() __attribute__((always_inline)) {
-    const int per = (p.total_wg + 7) >> 3;
-    return __builtin_amdgcn_readfirstlane(min(p.total_wg, (int)((blockIdx.x & 7) + 1) * per));
-  };
-  auto next_of = [&](int lx) __attribute__((always_inline)) { return lx + (int)(gridDim.x >> 3); };
-  int L = __builtin_amdgcn_readfirstlane((int)(blockIdx.x & 7) * ((p.total_wg + 7) >> 3) + (int)(blockIdx.x >> 3));
-  if (L >= tile_end()) return;
+  // XCD-aware block -> tile map: block b runs on XCD b % 8, so give each XCD a contiguous run of
+  // logical tiles (all query tiles of a problem then share one L2 for their K / W traffic).
+  const int per_xcd = gridDim.x >> 3;
+  const int L = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  if (L >= p.total_wg) return;
   // Integer division runs on the vector unit; readfirstlane brings the uniform results back to
   // scalar registers, so the per-tile address arithmetic stays scalar.  The variants with eight
   // accumulator blocks are short of registers: for them the extra scalar values cost more (their
@@ -221,95 +204,74 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
   auto locate = [&](int lx, auto scalar_tag) __attribute__((always_inline)) {
     constexpr bool S = decltype(scalar_tag)::value;
     auto u = [](int v) __attribute__((always_inline)) { return S ? __builtin_amdgcn_readfirstlane(v) : v; };
-    lx = u(lx);
     Loc r;
-    const int rest = p.fd_qt.quo(lx);
-    r.qt = u(lx - rest * p.q_tiles);
-    const int prob = p.fd_sp.quo(rest);
-    r.split = u(rest - prob * p.splits);
-    r.prob = u(prob);
-    const int bh = p.fd_fr.quo(prob);
-    r.f = u(prob - bh * p.frames);
-    const int bb = p.fd_hd.quo(bh);
-    r.hh = u(bh - bb * p.heads);
-    r.bb = u(bb);
+    r.qt = u(lx % p.q_tiles);
+    const int rest = lx / p.q_tiles;
+    r.split = u(rest % p.splits);
+    r.prob = u(rest / p.splits);
+    r.f = u(r.prob % p.frames);
+    const int bh = r.prob / p.frames;
+    r.hh = u(bh % p.heads);
+    r.bb = u(bh / p.heads);
     return r;
   };
-  // first row of each tensor for the problem of a tile
-  auto k_base = [&](const Loc& lc) __attribute__((always_inline)) {
-    return (const T*)p.k + lc.bb * p.k_sb + lc.hh * p.k_sh + (int64_t)lc.f * p.nk * p.k_sn;
-  };
-  auto w0_base = [&](const Loc& lc) __attribute__((always_inline)) {
-    return (const T*)p.w0 + lc.bb * p.w0_sb + lc.hh * p.w0_sh + (int64_t)lc.f * p.nk * p.w0_sn;
-  };
-  auto w1_base = [&](const Loc& lc) __attribute__((always_inline)) {
-    return DW1 ? (const T*)p.w1 + lc.bb * p.w1_sb + lc.hh * p.w1_sh + (int64_t)lc.f * p.nk * p.w1_sn : (const T*)p.k;
-  };
-  auto k8_base = [&](const Loc& lc) __attribute__((always_inline)) {
-    return QK8 ? (const T*)((const char*)p.k8 + (int64_t)lc.prob * p.nk * D) : (const T*)p.k;
-  };
-  // key stages of a tile's range (split s: keys [s kps, min(nk, (s + 1) kps)))
-  auto stages_of = [&](int split) __attribute__((always_inline)) {
-    const int kb0 = split * p.keys_per_split;
-    return __builtin_amdgcn_readfirstlane((min(p.nk, kb0 + p.keys_per_split) - kb0 + kFwdBN - 1) / kFwdBN);
-  };
+  const Loc loc = locate(L, std::integral_constant<bool, (NA < 8)>{});
+  const int qt = loc.qt, split = loc.split, f = loc.f, hh = loc.hh, bb = loc.bb;
+
+  const T* qb = (const T*)p.q + bb * p.q_sb + hh * p.q_sh + (int64_t)f * p.nq * p.q_sn;
+  const T* kb = (const T*)p.k + bb * p.k_sb + hh * p.k_sh + (int64_t)f * p.nk * p.k_sn;
+  const T* w0b = (const T*)p.w0 + bb * p.w0_sb + hh * p.w0_sh + (int64_t)f * p.nk * p.w0_sn;
+  const T* w1b = DW1 ? (const T*)p.w1 + bb * p.w1_sb + hh * p.w1_sh + (int64_t)f * p.nk * p.w1_sn : nullptr;
+  const int64_t q_sn = p.q_sn;
+
+  const int kbeg = split * p.keys_per_split;
+  const int kend = min(p.nk, kbeg + p.keys_per_split);
+  // uniform by construction; readfirstlane lets the compiler branch on them with scalar compares
+  const int n_tiles = __builtin_amdgcn_readfirstlane((kend - kbeg + kFwdBN - 1) / kFwdBN);
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  int lane = tid & 63;
-  int hl = lane >> 5;
-  int l32 = lane & 31;
-  // the key loop's operand reads use these (fixed for the kernel; the rest re-derives lane per tile)
-  const int hl_k = hl, l32_k = l32;
-  const int64_t q_sn = p.q_sn;
+  const int lane = tid & 63;
+  const int hl = lane >> 5;
+  const int l32 = lane & 31;
+  // wave owns QB blocks of 32 queries: rows q0 + 32 j + l32
+  const int q0 = qt * kBM + wave * 32 * QB;
+  const bool wave_live = q0 < p.nq;
+  int qrow[QB];
+  bool qvalid[QB];
+#pragma unroll
+  for (int j = 0; j < QB; ++j) {
+    qrow[j] = q0 + 32 * j + l32;
+    qvalid[j] = qrow[j] < p.nq;
+  }
 
-  // K / W tile copies (lane offsets; the tile's rows come with each copy)
-  const TileCopy<T, D, WAVES> kcopy((const T*)p.k, p.k_sn, wave, lane);
-  const TileCopy<T, W0K ? 64 : DW0, WAVES> w0copy((const T*)p.w0, p.w0_sn, wave, lane);
-  const TileCopy<T, DW1 ? DW1 : 64, WAVES> w1copy(DW1 ? (const T*)p.w1 : (const T*)p.k, p.w1_sn, wave, lane);
-  const TileCopy<T, 64, WAVES> k8copy((const T*)p.k, 64, wave, lane);   // fp8 K rows: 128 bytes, as 64 16-bit elements
-
-  // ---- per-tile state: the current tile's key range and tensor bases
-  uint64_t kb_u, w0b_u, w1b_u, k8b_u;
-  int kbeg, n_tiles, k8_row0;
-  auto begin_tile = [&](int lx) __attribute__((always_inline)) {
-    const Loc lc = locate(lx, std::integral_constant<bool, (NA < 8)>{});
-    kb_u = uniform64((uint64_t)(uintptr_t)k_base(lc));
-    w0b_u = uniform64((uint64_t)(uintptr_t)w0_base(lc));
-    w1b_u = uniform64((uint64_t)(uintptr_t)w1_base(lc));
-    k8b_u = uniform64((uint64_t)(uintptr_t)k8_base(lc));
-    kbeg = __builtin_amdgcn_readfirstlane(lc.split * p.keys_per_split);
-    // uniform by construction; readfirstlane lets the compiler branch on them with scalar compares
-    n_tiles = stages_of(lc.split);
-    k8_row0 = QK8 ? __builtin_amdgcn_readfirstlane(lc.prob * p.k8_tiles + kbeg / kFwdBN) : 0;
-    // Opaque from here on: otherwise the compiler, short of scalar registers, recomputes the bases inside the
-    // key loop from reloaded kernel arguments, and each scalar load's wait (lgkmcnt) also waits for the LDS
-    // operand reads in flight.
-    asm volatile("" : "+s"(kb_u), "+s"(w0b_u), "+s"(w1b_u), "+s"(k8b_u));
-    asm volatile("" : "+s"(kbeg), "+s"(n_tiles), "+s"(k8_row0));
-  };
-  auto key_end = [&]() __attribute__((always_inline)) { return min(p.nk, kbeg + p.keys_per_split); };
-  // first query row of this wave in tile lx, and whether the wave has queries there
-  auto wave_q0 = [&](int lx) __attribute__((always_inline)) {
-    lx = __builtin_amdgcn_readfirstlane(lx);
-    return __builtin_amdgcn_readfirstlane((lx - p.fd_qt.quo(lx) * p.q_tiles) * kBM + wave * 32 * QB);
-  };
-  auto wave_live = [&](int lx) __attribute__((always_inline)) { return wave_q0(lx) < p.nq; };
-
-  // Q^T as the B operand: lane (query l32, half hl) holds q[query][16 ds + 8 hl + 0..7].  Rows past the end
-  // read the problem's last row instead (finite data of this same tile, computed and never stored), so the
-  // loads need no select and stay in flight until the first S product.
+  // Q^T as the B operand: lane (query l32, half hl) holds q[query][16 ds + 8 hl + 0..7].
   V8 qf[QB][NDS];
-  auto load_q = [&](int lx) __attribute__((always_inline)) {
-    const Loc lc = locate(lx, std::true_type{});
-    const T* qb = (const T*)p.q + lc.bb * p.q_sb + lc.hh * p.q_sh + (int64_t)lc.f * p.nq * p.q_sn;
-    const int q0 = wave_q0(lx);
 #pragma unroll
-    for (int j = 0; j < QB; ++j) {
-      const T* qp = qb + (int64_t)min(q0 + 32 * j + l32, p.nq - 1) * q_sn + hl * 8;
+  for (int j = 0; j < QB; ++j) {
+    const T* qp = qb + (int64_t)(qvalid[j] ? qrow[j] : 0) * q_sn + hl * 8;
 #pragma unroll
-      for (int ds = 0; ds < NDS; ++ds) qf[j][ds] = *(const V8*)(qp + ds * 16);
+    for (int ds = 0; ds < NDS; ++ds) {
+      V8 v = *(const V8*)(qp + ds * 16);
+      qf[j][ds] = qvalid[j] ? v : V8{};
     }
+  }
+
+  const TileCopy<T, D, WAVES> kcopy(kb, p.k_sn, wave, lane);
+  const TileCopy<T, W0K ? 64 : DW0, WAVES> w0copy(w0b, p.w0_sn, wave, lane);
+  const TileCopy<T, DW1 ? DW1 : 64, WAVES> w1copy(w1b, p.w1_sn, wave, lane);
+  // fp8 K rows: 128 bytes, copied as 64 16-bit elements
+  const TileCopy<T, 64, WAVES> k8copy(QK8 ? (const T*)((const char*)p.k8 + (int64_t)loc.prob * p.nk * D) : kb, 64,
+                                      wave, lane);
+  auto issue = [&](int t) __attribute__((always_inline)) {
+    uint32_t sb = smem_u32;
+    asm volatile("" : "+s"(sb));   // keep the LDS destinations from being hoisted (see TileCopy)
+    const uint32_t st = sb + (uint32_t)((t % NSLOT) * STAGE);
+    const int row0 = kbeg + t * kFwdBN;
+    kcopy.issue(row0, p.nk, st);
+    if constexpr (!W0K) w0copy.issue(row0, p.nk, st + K_BYTES);
+    if constexpr (DW1 > 0) w1copy.issue(row0, p.nk, st + K_BYTES + W0_BYTES);
+    if constexpr (QK8) k8copy.issue(row0, p.nk, st + K8_OFF);
   };
 
   const float c = p.scale_log2;
@@ -328,32 +290,31 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
   typedef int i32x8 __attribute__((ext_vector_type(8)));
   i32x8 qf8[QK8 ? QB : 1][2];
   float cq[QB], cf[QB];
-  auto prep_q = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < QB; ++j) {
-      cq[j] = c;
-      if constexpr (QK8) {
-        float amax = 0.f;
+  for (int j = 0; j < QB; ++j) {
+    cq[j] = c;
+    if constexpr (QK8) {
+      float amax = 0.f;
 #pragma unroll
-        for (int ds = 0; ds < NDS; ++ds)
+      for (int ds = 0; ds < NDS; ++ds)
 #pragma unroll
-          for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf((float)qf[j][ds][e]));
-        amax = wave_max32(amax);
-        const float inv = amax > 0.f ? kFp8Max / amax : 1.f;
-        cq[j] = c * (amax > 0.f ? amax / kFp8Max : 1.f);
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf((float)qf[j][ds][e]));
+      amax = wave_max32(amax);
+      const float inv = amax > 0.f ? kFp8Max / amax : 1.f;
+      cq[j] = c * (amax > 0.f ? amax / kFp8Max : 1.f);
 #pragma unroll
-        for (int m = 0; m < 2; ++m)
+      for (int m = 0; m < 2; ++m)
 #pragma unroll
-          for (int w = 0; w < 8; ++w) {   // bytes 4 w .. 4 w + 3 of product m: dims 16 (4 m + w / 2) + 8 hl + 4 (w % 2) + 0..3
-            const V8& v = qf[j][4 * m + w / 2];
-            const int e0 = 4 * (w % 2);
-            int word = __builtin_amdgcn_cvt_pk_fp8_f32((float)v[e0] * inv, (float)v[e0 + 1] * inv, 0, false);
-            qf8[j][m][w] = __builtin_amdgcn_cvt_pk_fp8_f32((float)v[e0 + 2] * inv, (float)v[e0 + 3] * inv, word, true);
-          }
-      }
-      cf[j] = cq[j];
+        for (int w = 0; w < 8; ++w) {   // bytes 4 w .. 4 w + 3 of product m: dims 16 (4 m + w / 2) + 8 hl + 4 (w % 2) + 0..3
+          const V8& v = qf[j][4 * m + w / 2];
+          const int e0 = 4 * (w % 2);
+          int word = __builtin_amdgcn_cvt_pk_fp8_f32((float)v[e0] * inv, (float)v[e0 + 1] * inv, 0, false);
+          qf8[j][m][w] = __builtin_amdgcn_cvt_pk_fp8_f32((float)v[e0 + 2] * inv, (float)v[e0 + 3] * inv, word, true);
+        }
     }
-  };
+    cf[j] = cq[j];
+  }
+  const int k8_row0 = QK8 ? __builtin_amdgcn_readfirstlane(loc.prob * p.k8_tiles + kbeg / kFwdBN) : 0;
   auto tile_scale = [&](int t) __attribute__((always_inline)) {
     if constexpr (QK8) {
       const float sk = p.k8_scale[k8_row0 + t];
@@ -380,12 +341,12 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
     if constexpr (QK8) {
       // S^T = K8 Q8^T: two 32x32x64 fp8 products; lane (key l32, half hl) reads the 32 bytes of product m
       // as chunks 4 m + 2 hl and + 1 of its key's row
-      const VMO_LDS char* arow8 = Ks + K8_OFF + (32 * kb2 + l32_k) * 128;
+      const VMO_LDS char* arow8 = Ks + K8_OFF + (32 * kb2 + l32) * 128;
       i32x8 a8[2];
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
-        const i32x4 lo = *(const VMO_LDS i32x4*)(arow8 + ((4 * m + 2 * hl_k) ^ srow_sw8) * 16);
-        const i32x4 hi = *(const VMO_LDS i32x4*)(arow8 + ((4 * m + 2 * hl_k + 1) ^ srow_sw8) * 16);
+        const i32x4 lo = *(const VMO_LDS i32x4*)(arow8 + ((4 * m + 2 * hl) ^ srow_sw8) * 16);
+        const i32x4 hi = *(const VMO_LDS i32x4*)(arow8 + ((4 * m + 2 * hl + 1) ^ srow_sw8) * 16);
         a8[m] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       }
 #pragma unroll
@@ -397,10 +358,10 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
       }
       return;
     }
-    const VMO_LDS char* arow = Ks + (32 * kb2 + l32_k) * (D * 2);
+    const VMO_LDS char* arow = Ks + (32 * kb2 + l32) * (D * 2);
     V8 a[NDS];
 #pragma unroll
-    for (int ds = 0; ds < NDS; ++ds) a[ds] = lds_read8<V8>(arow + ((2 * ds + hl_k) ^ srow_sw) * 16);
+    for (int ds = 0; ds < NDS; ++ds) a[ds] = lds_read8<V8>(arow + ((2 * ds + hl) ^ srow_sw) * 16);
 #pragma unroll
     for (int j = 0; j < QB; ++j) x[j] = f32x16{};
 #pragma unroll
@@ -578,28 +539,11 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
     }
   };
 
-  // ---- the ring.  Stage t of a tile sits in slot t % NSLOT.  The epilogue patches take the last slot (or,
-  // when a stage is smaller than the four patches, LDS past the ring: fwd_lds_bytes), which the next tile's
-  // first stages, copied during the epilogue, leave free.
-  constexpr bool kPatchInRing = STAGE >= WAVES * kEpiPatchBytes;
-  constexpr int kPatchOff = kPatchInRing ? (NSLOT - 1) * STAGE : NSLOT * STAGE;
-
-  auto issue = [&](int t) __attribute__((always_inline)) {
-    uint32_t sb = smem_u32;
-    asm volatile("" : "+s"(sb));   // keep the LDS destinations from being hoisted (see TileCopy)
-    const uint32_t st = sb + (uint32_t)((t % NSLOT) * STAGE);
-    const int row0 = kbeg + t * kFwdBN;
-    kcopy.issue_from(kb_u, row0, p.nk, st);
-    if constexpr (!W0K) w0copy.issue_from(w0b_u, row0, p.nk, st + K_BYTES);
-    if constexpr (DW1 > 0) w1copy.issue_from(w1b_u, row0, p.nk, st + K_BYTES + W0_BYTES);
-    if constexpr (QK8) k8copy.issue_from(k8b_u, row0, p.nk, st + K8_OFF);
-  };
-
   // Tiles t = 0 .. n_tiles-1 flow through an NSLOT-slot LDS ring; prime() issues tiles 0 ..
   // NSLOT-2.  At the top of tile t this wave's copies of tile t have landed -- only those of tile
-  // t+1 may still be in flight (three slots) -- and after the barrier every wave's copies have, and
-  // the slot of tile t-1 is free for tile t + NSLOT - 1.  Only the last tile can be partial, so it
-  // is peeled: the steady-state body is one straight path and the accumulators stay in place
+  // t+1 may still be in flight (three slots) -- and after the barrier every wave's copies have,
+  // and the slot of tile t-1 is free for tile t + NSLOT - 1.  Only the last tile can be partial, so
+  // it is peeled: the steady-state body is one straight path and the accumulators stay in place
   // across iterations.  Waves without queries still take part in every barrier and tile copy.
   constexpr int kSteadyPending = NSLOT == 3 ? DMA_PER_TILE : 0;
   auto slot = [&](int t) __attribute__((always_inline)) { return (const VMO_LDS char*)smem + (t % NSLOT) * STAGE; };
@@ -617,8 +561,8 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
     tile_sync<0>();
     last_body(t);
   };
-  auto key_loop = [&](bool live) __attribute__((always_inline)) {
-    if (live) {
+  auto key_loop = [&]() __attribute__((always_inline)) {
+    if (wave_live) {
       // Full tiles in groups of NSLOT: tile t + S sits in ring slot S, a compile-time offset that
       // folds into the LDS reads' immediate field (no per-read address arithmetic in the loop).
       auto full_tile = [&](int t, auto slot_tag) __attribute__((always_inline)) {
@@ -645,7 +589,7 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
       }
       tile_sync<0>();
       tile_scale(t);
-      const int nvalid = key_end() - (kbeg + t * kFwdBN);   // 1 .. 64
+      const int nvalid = kend - (kbeg + t * kFwdBN);   // 1 .. 64
       if (nvalid == kFwdBN)
         stage(slot(t), nvalid, std::false_type{}, std::true_type{});
       else if (nvalid > 32)
@@ -656,6 +600,25 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
       for_tiles([](int) {}, [](int) {});
     }
   };
+
+  // m from the first 32 keys of the range (tile 0 stays in slot 0 for the loop)
+  prime();
+  if constexpr (NSLOT == 3) {
+    if (n_tiles > 1) tile_sync<DMA_PER_TILE>(); else tile_sync<0>();
+  } else {
+    tile_sync<0>();
+  }
+  {
+    float mx[QB];
+#pragma unroll
+    for (int j = 0; j < QB; ++j) mx[j] = kMaskLogit;
+    tile_scale(0);
+    if (wave_live) block_max(slot(0), 0, kend - kbeg, mx);
+#pragma unroll
+    for (int j = 0; j < QB; ++j) m_run[j] = mx[j];
+  }
+  reset();
+  key_loop();
 
   // Workgroup OR of the overflow flags through one word per wave in a ring slot that no wave reads and no
   // copy fills any more (that of tile n_tiles - NSLOT, or one never used): __syncthreads_or takes a static
@@ -673,174 +636,89 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
     __syncthreads();
     return any != 0;
   };
-
-  // sum_j p~_j q . k_j (the P.K entropy) with q from the B-operand registers: the accumulator's lane (row l32,
-  // half hl) holds dims 32 a + 8 g + 4 hl + 0..3 and qf[ds] dims 16 ds + 8 hl + 0..7, so one permlane32 swap of
-  // dwords (0, 2) and one of (1, 3) per ds hand every lane dims 16 ds + 4 hl + 0..3 (g = 2 (ds % 2)) and
-  // 16 ds + 8 + 4 hl + 0..3 (g + 1) of its row.
-  auto pk_dot = [&](int j) __attribute__((always_inline)) {
-    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-    float d = 0.f;
+  if (workgroup_any(overflow)) {
+    // exact two-pass fallback for this workgroup: the true row max, then the loop again
+    float mx[QB];
 #pragma unroll
-    for (int ds = 0; ds < NDS; ++ds) {
-      const u32x4 w = __builtin_bit_cast(u32x4, qf[j][ds]);
-      const auto s0 = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
-      const auto s1 = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
-      const uint32_t xy[4] = {s0[0], s1[0], s0[1], s1[1]};
-      const int r0 = 8 * (ds & 1);
+    for (int j = 0; j < QB; ++j) mx[j] = kMaskLogit;
+    auto max_tile = [&](int t) __attribute__((always_inline)) {
+      if (!wave_live) return;
+      const int nvalid = kend - (kbeg + t * kFwdBN);
+      tile_scale(t);
+      block_max(slot(t), 0, nvalid, mx);
+      if (nvalid > 32) block_max(slot(t), 1, nvalid, mx);
+    };
+    prime();
+    for_tiles(max_tile, max_tile);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const V2 x = __builtin_bit_cast(V2, xy[u]);
-        d = fmaf((float)x[0], acc[j][ds >> 1][r0 + 2 * u], d);
-        d = fmaf((float)x[1], acc[j][ds >> 1][r0 + 2 * u + 1], d);
-      }
-    }
-    return wave_sum32(d);
-  };
-
-  // The tile's outputs.  The epilogue derives its indices and row bases again, from an opaque copy of the
-  // tile's logical index (scalar registers are free by now): kept from the prologue, the 64-bit bases sat in
-  // vector registers across the whole key loop, and the tightest variants spilled them to scratch.
-  // `between` runs once the first two accumulator blocks are stored (the next tile's q loads, which then take
-  // registers those blocks no longer need).
-  auto epilogue = [&](int lx, VMO_LDS float* patch, const float (&pkdot)[QB], auto&& between) __attribute__((always_inline)) {
-    int l_epi = __builtin_amdgcn_readfirstlane(lx);
-    asm volatile("" : "+s"(l_epi));
-    // lane indices from an opaque copy as well: derived from the loop-invariant lane id, the epilogue's
-    // per-lane offsets would be hoisted out of the tile loop and held in registers across the key loop
-    int lane = threadIdx.x & 63;
-    asm volatile("" : "+v"(lane));
-    const int hl = lane >> 5, l32 = lane & 31;
-    const Loc le = locate(l_epi, std::true_type{});
-    T* const ob = (T*)p.o + le.bb * p.o_sb + le.hh * p.o_sh + (int64_t)le.f * p.nq * p.o_sn;
-    const int64_t o_sn = p.o_sn;
-    const int64_t st0 = le.bb * p.st_sb + le.hh * p.st_sh + (int64_t)le.f * p.nq;
-    const int64_t part0 = (int64_t)(le.split * p.problems + le.prob) * p.nq;
-    const int q0_e = le.qt * kBM + wave * 32 * QB;
-#pragma unroll
-    for (int j = 0; j < QB; ++j) {
-      // ---- finalise: combine the two half-waves' partial sums
-      const float l_tot = wave_sum32(l_run[j]);
-      const float inv_l = 1.0f / l_tot;
-      const float log2l = fast_log2(l_tot);
-      const float lse = m_run[j] + log2l;
-      const int qb0 = q0_e + 32 * j, nrows = min(32, p.nq - qb0);
-      const int qr = qb0 + l32;
-      const bool qv = qr < p.nq;
-      constexpr int NA_FIRST = NA >= 4 ? 2 : NA;   // blocks stored before `between` (j = 0)
-      if constexpr (SPLIT) {
-        char* const prow = (char*)(p.part_o + (part0 + qb0) * (int64_t)(DW0 + DW1));
-        store_acc_rows<F16>(patch, acc[j], NA_FIRST, inv_l, kGradStoreF32, prow, (int64_t)(DW0 + DW1) * 4, nrows, lane);
-        if (j == 0) between();
-        if constexpr (NA_FIRST < NA)
-          store_acc_rows<F16>(patch, acc[j] + NA_FIRST, NA - NA_FIRST, inv_l, kGradStoreF32, prow + NA_FIRST * 32 * 4,
-                              (int64_t)(DW0 + DW1) * 4, nrows, lane);
-        if (qv && hl == 0) p.part_lse[part0 + qr] = lse;
-      } else {
-        float ent = 0.f;
-        if constexpr (ENT == kEntOnline) {
-          // h = sum_j p_j x_j with p_j = 2^x_j: entropy (bits) = log2 l - h / l
-          ent = (log2l - wave_sum32(h_run[j]) * inv_l) * kLn2;
-        } else if constexpr (ENT == kEntFromPK) {
-          // sum_j P~_j s_j = q . (sum_j p~_j k_j) / l~
-          ent = lse * kLn2 - (c * kLn2) * pkdot[j] * inv_l;
-        }
-        char* const orow = (char*)(ob + (int64_t)qb0 * o_sn);
-        store_acc_rows<F16>(patch, acc[j], NA_FIRST, inv_l, kGradStore, orow, o_sn * 2, nrows, lane);
-        if (j == 0) between();
-        if constexpr (NA_FIRST < NA)
-          store_acc_rows<F16>(patch, acc[j] + NA_FIRST, NA - NA_FIRST, inv_l, kGradStore, orow + NA_FIRST * 32 * 2,
-                              o_sn * 2, nrows, lane);
-        if (qv) {
-          const int64_t si = st0 + qr;
-          if (ENT != kEntNone && hl == 0 && p.ent) p.ent[si] = ent;
-          if (hl == 0 && p.lse) p.lse[si] = lse;
-        }
-      }
-    }
-  };
-
-  // ---- first tile: q rows and the first stages, then the block's tiles in turn
-  begin_tile(L);
-  load_q(L);
-  prime();
-  prep_q();
-  if (NSLOT == 3 && n_tiles > 1) tile_sync<DMA_PER_TILE>(); else tile_sync<0>();
-  for (;;) {
-    // lane indices from an opaque copy in every tile: values derived from them are then not loop
-    // invariant, so the compiler computes them where they are used instead of holding them across tiles
-    lane = tid & 63;
-    asm volatile("" : "+v"(lane));
-    hl = lane >> 5;
-    l32 = lane & 31;
-    const bool live = wave_live(L);
-    // m from the first 32 keys of the range (tile 0 stays in slot 0 for the loop)
-    {
-      float mx[QB];
-#pragma unroll
-      for (int j = 0; j < QB; ++j) mx[j] = kMaskLogit;
-      tile_scale(0);
-      if (live) block_max(slot(0), 0, key_end() - kbeg, mx);
-#pragma unroll
-      for (int j = 0; j < QB; ++j) m_run[j] = mx[j];
-    }
+    for (int j = 0; j < QB; ++j) m_run[j] = mx[j];
     reset();
-    overflow = false;
-    key_loop(live);
+    tile_sync<0>();   // every wave is done with the last max-pass tile before the ring is reused
+    prime();
+    key_loop();
+    __syncthreads();   // the fallback's ring reads are done before the epilogue patches reuse it
+  }
 
-    if (workgroup_any(overflow)) {
-      // exact two-pass fallback for this tile: the true row max, then the loop again
-      float mx[QB];
-#pragma unroll
-      for (int j = 0; j < QB; ++j) mx[j] = kMaskLogit;
-      auto max_tile = [&](int t) __attribute__((always_inline)) {
-        if (!live) return;
-        const int nvalid = key_end() - (kbeg + t * kFwdBN);
-        tile_scale(t);
-        block_max(slot(t), 0, nvalid, mx);
-        if (nvalid > 32) block_max(slot(t), 1, nvalid, mx);
-      };
-      prime();
-      for_tiles(max_tile, max_tile);
-#pragma unroll
-      for (int j = 0; j < QB; ++j) m_run[j] = mx[j];
-      reset();
-      tile_sync<0>();   // every wave is done with the last max-pass tile before the ring is reused
-      prime();
-      key_loop(live);
-      __syncthreads();   // the fallback's ring reads are done before the next tile's copies and the patches
-    }
+  // the stage ring is free (every wave passed the barrier above): each wave's 4 KB patch for the
+  // row-segment stores of o
+  static_assert(NSLOT * STAGE >= WAVES * kEpiPatchBytes, "epilogue patches");
+  VMO_LDS float* patch = (VMO_LDS float*)(smem + wave * kEpiPatchBytes);
+  if (!wave_live) return;
 
-    // Every wave is past the key loop (the vote's barriers): the ring is free.  The entropy dot is the last use
-    // of this tile's q registers; then the next tile's first stages and q rows load while this tile's outputs
-    // are written.
-    float pkdot[QB];
+  // The epilogue derives its indices and row bases again, from an opaque copy of the block's logical
+  // index (scalar registers are free by now): kept from the prologue, the 64-bit bases sat in vector
+  // registers across the whole key loop, and the tightest variants spilled them to scratch.
+  int l_epi = __builtin_amdgcn_readfirstlane(L);
+  asm volatile("" : "+s"(l_epi));
+  const Loc le = locate(l_epi, std::true_type{});
+  T* const ob = (T*)p.o + le.bb * p.o_sb + le.hh * p.o_sh + (int64_t)le.f * p.nq * p.o_sn;
+  const T* const qb_e = (const T*)p.q + le.bb * p.q_sb + le.hh * p.q_sh + (int64_t)le.f * p.nq * p.q_sn;
+  const int64_t o_sn = p.o_sn, q_sn_e = p.q_sn;
+  const int64_t st0 = le.bb * p.st_sb + le.hh * p.st_sh + (int64_t)le.f * p.nq;
+  const int64_t part0 = (int64_t)(le.split * p.problems + le.prob) * p.nq;
+  const int q0_e = le.qt * kBM + wave * 32 * QB;
+
 #pragma unroll
-    for (int j = 0; j < QB; ++j) pkdot[j] = 0.f;
-    if constexpr (ENT == kEntFromPK) {
-      if (live) {
+  for (int j = 0; j < QB; ++j) {
+    // ---- finalise: combine the two half-waves' partial sums
+    const float l_tot = wave_sum32(l_run[j]);
+    const float inv_l = 1.0f / l_tot;
+    const float log2l = fast_log2(l_tot);
+    const float lse = m_run[j] + log2l;
+    const int qb0 = q0_e + 32 * j, nrows = min(32, p.nq - qb0);
+    const int qr = qb0 + l32;
+    const bool qv = qr < p.nq;
+    if constexpr (SPLIT) {
+      store_acc_rows<F16>(patch, acc[j], NA, inv_l, kGradStoreF32, (char*)(p.part_o + (part0 + qb0) * (int64_t)(DW0 + DW1)),
+                          (int64_t)(DW0 + DW1) * 4, nrows, lane);
+      if (qv && hl == 0) p.part_lse[part0 + qr] = lse;
+    } else {
+      float ent = 0.f;
+      if constexpr (ENT == kEntOnline) {
+        // h = sum_j p_j x_j with p_j = 2^x_j: entropy (bits) = log2 l - h / l
+        ent = (log2l - wave_sum32(h_run[j]) * inv_l) * kLn2;
+      } else if constexpr (ENT == kEntFromPK) {
+        // sum_j P~_j s_j = q . (sum_j p~_j k_j) / l~, with q re-read in the accumulator's layout
+        const T* qp = qb_e + (int64_t)(qv ? qr : 0) * q_sn_e + 4 * hl;
+        float dot = 0.f;
 #pragma unroll
-        for (int j = 0; j < QB; ++j) pkdot[j] = pk_dot(j);
+        for (int a = 0; a < NA0; ++a)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const V4 qv = *(const V4*)(qp + 32 * a + 8 * g);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dot = fmaf((float)qv[e], acc[j][a][4 * g + e], dot);
+          }
+        dot = wave_sum32(dot);
+        ent = lse * kLn2 - (c * kLn2) * dot * inv_l;
+      }
+      store_acc_rows<F16>(patch, acc[j], NA, inv_l, kGradStore, (char*)(ob + (int64_t)qb0 * o_sn), o_sn * 2, nrows, lane);
+      if (qv) {
+        const int64_t si = st0 + qr;
+        if (ENT != kEntNone && hl == 0 && p.ent) p.ent[si] = ent;
+        if (hl == 0 && p.lse) p.lse[si] = lse;
       }
     }
-    const int l_cur = L;
-    const int l_next = next_of(L);
-    const bool more = l_next < tile_end();
-    VMO_LDS float* patch = (VMO_LDS float*)(smem + kPatchOff + wave * kEpiPatchBytes);
-    if (more) {
-      L = l_next;
-      begin_tile(L);
-      prime();   // slots 0 .. NSLOT - 2; the patches sit past them
-    }
-    if (live) {
-      epilogue(l_cur, patch, pkdot, [&]() __attribute__((always_inline)) { if (more) load_q(L); });
-    } else if (more) {
-      load_q(L);
-    }
-    if (!more) break;
-    prep_q();
-    tile_sync<0>();   // the first stages and the q rows have landed (and the epilogue's stores); every wave
-                      // is done with its patch before tile NSLOT - 1 refills that slot
   }
 }
 
@@ -921,39 +799,13 @@ __global__ __launch_bounds__(256) void fea_fp8_keys_kernel(FwdParams p) {
   }
 }
 
-// LDS of a forward workgroup: the stage ring, then the four epilogue patches when a stage is smaller than them
-// (else they take the ring's last slot).
-template <int D, int DW0, int DW1, bool W0K, bool QK8, int WAVES>
-constexpr int fwd_lds_bytes() {
-  constexpr int stage = fwd_stage_bytes<D, DW0, DW1, W0K, QK8>();
-  return fwd_slots(stage, WAVES) * stage + (stage >= WAVES * kEpiPatchBytes ? 0 : WAVES * kEpiPatchBytes);
-}
-
-constexpr int kMaxDevices = 64;
-
-// Compute units of the current device (looked up once per device).
-static int device_cus() {
-  static int cus[kMaxDevices];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
-  if (cus[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    cus[dev] = n;
-  }
-  return cus[dev];
-}
-
 template <bool F16, int D, int DW0, int DW1, bool W0K, int ENT, bool SPLIT, int WAVES, bool QK8 = false>
 static int launch_fwd(FwdParams p, hipStream_t stream) {
-  constexpr int LDS = fwd_lds_bytes<D, DW0, DW1, W0K, QK8, WAVES>();
+  constexpr int STAGE = fwd_stage_bytes<D, DW0, DW1, W0K, QK8>();
+  constexpr int LDS = fwd_slots(STAGE, WAVES) * STAGE;
   constexpr int BM = 32 * kFwdQB * WAVES;
   p.q_tiles = (p.nq + BM - 1) / BM;
   p.total_wg = p.problems * p.splits * p.q_tiles;
-  p.fd_qt.init(p.q_tiles);
-  p.fd_sp.init(p.splits);
-  p.fd_fr.init(p.frames);
-  p.fd_hd.init(p.heads);
   auto kern = fea_fwd_kernel<F16, D, DW0, DW1, W0K, ENT, SPLIT, WAVES, QK8>;
   if constexpr (QK8) {
     hipLaunchKernelGGL((fea_fp8_keys_kernel<F16>), dim3((unsigned)((int64_t)p.problems * p.k8_tiles)), dim3(256), 0, stream, p);
@@ -968,28 +820,7 @@ static int launch_fwd(FwdParams p, hipStream_t stream) {
       done = true;
     }
   }
-  // One block per tile, or -- when there are more tiles than the GPU holds blocks at once -- as many blocks
-  // as it holds, each running its share of the tiles with the stage ring carried from one tile into the
-  // next (the fp8 variants, whose ring fills the LDS share, run one tile per block unless max_blocks asks
-  // for fewer blocks; their blocks then start the ring again for every tile).
-  int grid = xcd_grid(p.total_wg);
-  if constexpr (!QK8) {
-    static int resident[kMaxDevices];   // blocks the device holds at once (idempotent, so a benign race)
-    int dev = 0;
-    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices) {
-      if (resident[dev] == 0) {
-        int per_cu = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)kern, 64 * WAVES, LDS) == hipSuccess &&
-            per_cu > 0)
-          resident[dev] = per_cu * device_cus();
-        else
-          resident[dev] = -1;
-      }
-      if (resident[dev] >= 8 && grid > resident[dev]) grid = resident[dev] / 8 * 8;
-    }
-  }
-  if (p.max_blocks > 0 && grid > p.max_blocks) grid = max(8, p.max_blocks / 8 * 8);
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * WAVES), LDS, stream, p);
+  hipLaunchKernelGGL(kern, dim3(xcd_grid(p.total_wg)), dim3(64 * WAVES), LDS, stream, p);
   int rc = launch_status("fea_fwd");
   if (rc != VMO_OK || !SPLIT) return rc;
   constexpr int DWT = DW0 + DW1;
@@ -1142,8 +973,6 @@ static int fea_fwd_impl(const vmo_fea_fwd_args* a, void* workspace, size_t works
   p.problems = (int)problems; p.q_tiles = (int)q_tiles; p.splits = splits; p.keys_per_split = kps;
   p.total_wg = (int)total;
   p.scale_log2 = a->sm_scale * kLog2e;
-  if (a->max_blocks < 0) return set_error(VMO_ERR_INVALID, "fea_fwd: max_blocks must be >= 0");
-  p.max_blocks = a->max_blocks;
   if (a->qk_fp8) {
     p.k8 = (char*)workspace + k8_off;
     p.k8_tiles = (a->nk + kFwdBN - 1) / kFwdBN;
@@ -1161,6 +990,7 @@ static int fea_fwd_impl(const vmo_fea_fwd_args* a, void* workspace, size_t works
 // Each GPU the library runs on holds its own copy, at its own address, until the process ends.
 static __device__ __align__(256) char scratch[VMO_FEA_FWD_SCRATCH_BYTES];
 
+constexpr int kMaxDevices = 64;
 static void* g_scratch_ptr[kMaxDevices];
 static std::mutex g_scratch_mutex;
 

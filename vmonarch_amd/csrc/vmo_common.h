@@ -84,22 +84,6 @@ __device__ __forceinline__ int xcd_remap(int nblocks) {
   return (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
 }
 
-// Division by a run-time invariant divisor d >= 1 for numerators below 2^31 (Granlund & Montgomery, "Division
-// by invariant integers using multiplication", PLDI 1994): q = (mulhi(n, m) + n) >> s with s = ceil(log2 d) and
-// m = floor(2^32 (2^s - d) / d) + 1, set up on the host.  With a uniform numerator the quotient stays on the
-// scalar unit; the compiler's own division by a kernel argument is vector code whose reciprocal it keeps in
-// vector registers for the whole kernel.
-struct FastDiv {
-  uint32_t d, m, s;
-  __host__ void init(uint32_t div) {
-    d = div < 1 ? 1 : div;
-    s = 0;
-    while ((1ull << s) < d) ++s;
-    m = (uint32_t)((((1ull << 32) * ((1ull << s) - d)) / d) + 1);
-  }
-  __device__ __forceinline__ int quo(int n) const { return (int)((__umulhi((uint32_t)n, m) + (uint32_t)n) >> s); }
-};
-
 __device__ __forceinline__ float wave_max32(float x) {
   // combine lane l with lane l ^ 32
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);

@@ -28,15 +28,14 @@ def _kernel_width(d):
 
 
 def fea_forward(q, k, w0, w1, sm_scale, frames=1, o=None, lse=None, ent=None, want_ent=True, want_lse=True,
-                num_splits=1, qk_fp8=False, max_blocks=0):
+                num_splits=1, qk_fp8=False):
     """Launch the flash-entropy forward.
 
     q: (B, H, F*nq, D); k, w0: (B, H, F*nk, .); w1: optional second value tensor (requires w0 is k).
     Returns (o, lse, ent): o (B, H, F*nq, Dw0 + Dw1) in q.dtype; lse (log2 units) and ent (nats)
     (B, H, F*nq) fp32, or None when not wanted.  o / lse / ent may be passed in as (strided) views
     to write into; lse / ent views need a unit token stride.  `qk_fp8`: S = q k^T in fp8 (the VMonarch
-    R-step variants only; vmo_fea_fwd_args.qk_fp8).  `max_blocks`: cap on the launch's workgroups
-    (vmo_fea_fwd_args.max_blocks; results do not depend on it).
+    R-step variants only; vmo_fea_fwd_args.qk_fp8).
     """
     L = _lib.lib()
     B, H, NQ, D = q.shape
@@ -69,7 +68,6 @@ def fea_forward(q, k, w0, w1, sm_scale, frames=1, o=None, lse=None, ent=None, wa
     a.sm_scale = float(sm_scale)
     a.num_splits = int(num_splits)
     a.qk_fp8 = int(bool(qk_fp8))
-    a.max_blocks = int(max_blocks)
     ws = None
     nbytes = L.vmo_fea_fwd_workspace_size(a)
     if nbytes:
