@@ -386,7 +386,10 @@ def test_fea_backward_fold_k(nq, nk, D, two_parts, dt):
     """VMO_BWD_FOLD_K (values k, or [k | v1]): dk holds k's key-role plus value-role gradient, dv only
     v1's.  Bit for bit the sum of the unfolded fp32 stores (one rounding each for the product and
     the sum), in the inputs' dtype the rounding of that sum, and added into an fp32 buffer within
-    float32 rounding of the unfolded additions."""
+    float32 rounding of the unfolded additions -- except for [k | v1] at d = 128, whose folded launch
+    accumulates both gradients of k in one set of registers with dS rounded after its sm_scale factor
+    (and stores dS^T that way for the dq GEMM): there dk and dq agree with the unfolded results within
+    1e-2 of their largest element (measured ~1e-3), and v1's gradient stays bit for bit."""
     from vmonarch_amd.kernel import fea_forward
     from vmonarch_amd.kernel_bwd import fea_backward_raw
     g = torch.Generator().manual_seed(11 * nq + nk + D + two_parts)
@@ -399,6 +402,15 @@ def test_fea_backward_fold_k(nq, nk, D, two_parts, dt):
     print(f"fea_bwd fold_k nq={nq} nk={nk} D={D} two_parts={two_parts} {dt}", flush=True)
     f32 = dict(device=DEV, dtype=torch.float32)
     args = (q, k, k, o, lse, ent, do, de, D ** -0.5)
+    exact = not (two_parts and D == 128)
+
+    def same(x, ref, name):
+        if exact:
+            assert torch.equal(x, ref), name
+        else:
+            err = float((x.float() - ref.float()).abs().max())
+            assert err <= 1e-2 * float(ref.float().abs().max()), f"{name}: {err}"
+
     # unfolded, fp32 stores
     dk_ref, dv_ref = torch.empty(1, 2, nk, D, **f32), torch.empty(1, 2, nk, w.shape[-1], **f32)
     dq_ref, _, _ = fea_backward_raw(*args, dk=dk_ref, dv=dv_ref, overwrite="kv", v1=v1)
@@ -406,15 +418,16 @@ def test_fea_backward_fold_k(nq, nk, D, two_parts, dt):
     # folded, fp32 stores
     dk, dv = torch.full((1, 2, nk, D), 7.0, **f32), (torch.full((1, 2, nk, D), 7.0, **f32) if two_parts else None)
     dq, _, dv_out = fea_backward_raw(*args, dk=dk, dv=dv, overwrite="kv", v1=v1, fold_k=True)
-    assert torch.equal(dq, dq_ref)
-    assert torch.equal(dk, k_sum)
+    same(dq, dq_ref, "dq")
+    same(dk, k_sum, "dk")
     if two_parts:
         assert torch.equal(dv_out, dv_ref[..., D:])
     else:
         assert dv_out is None
     # folded, stored in the inputs' dtype
     _, dk_lp, dv_lp = fea_backward_raw(*args, v1=v1, fold_k=True)
-    assert dk_lp.dtype == q.dtype and torch.equal(dk_lp, k_sum.to(q.dtype))
+    assert dk_lp.dtype == q.dtype
+    same(dk_lp, k_sum.to(q.dtype), "dk in the inputs' dtype")
     if two_parts:
         assert dv_lp.shape[-1] == D and torch.equal(dv_lp, dv_ref[..., D:].to(q.dtype))
     # folded, added into fp32 buffers that already hold a gradient
@@ -422,7 +435,10 @@ def test_fea_backward_fold_k(nq, nk, D, two_parts, dt):
     base_v = torch.randn(1, 2, nk, D, generator=g).to(DEV)
     dk_acc, dv_acc = base_k.clone(), (base_v.clone() if two_parts else None)
     fea_backward_raw(*args, dk=dk_acc, dv=dv_acc, v1=v1, fold_k=True)
-    torch.testing.assert_close(dk_acc, base_k + k_sum, rtol=1e-6, atol=1e-6)
+    if exact:
+        torch.testing.assert_close(dk_acc, base_k + k_sum, rtol=1e-6, atol=1e-6)
+    else:
+        torch.testing.assert_close(dk_acc, base_k + dk, rtol=1e-6, atol=1e-6)   # the folded fp32 store above
     if two_parts:
         torch.testing.assert_close(dv_acc, base_v + dv_ref[..., D:], rtol=1e-6, atol=1e-6)
 

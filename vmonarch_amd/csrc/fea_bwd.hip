@@ -76,6 +76,7 @@ struct BwdParams {
   int64_t dl_sb, dl_sh;
   float c;          // sm_scale * log2(e)
   float sm_scale;
+  float ds_scale;   // factor of the dq GEMM over a stored dS^T: sm_scale, or 1 when the stored dS carries it
 };
 
 // Copy rows row0 .. row0 + ROWS - 1 (clamped to nrows - 1) of a row-major (token, W) tensor into an
@@ -236,14 +237,19 @@ constexpr int bwd_waves_per_simd() { return D + DV > 320 ? 1 : 2; }
 // one wave per SIMD without moving accumulators).
 template <int D, int DV, bool W0K>
 constexpr int dkdv_parts() { return DV > 128 && !(W0K && D == 128 && DV == 256) ? 2 : 1; }
+// PART 3: values [k | v1] with VMO_BWD_FOLD_K at 128 / 256, the first of two launches (PART 2 gives v1's
+// gradient): dK and k's value-role gradient accumulate in one set of registers -- dK = sm_scale dS^T Q +
+// P^T dO[:, :D] with dS entering the MFMA already times sm_scale -- so that the launch holds 64 accumulator
+// registers instead of the 192 of PART 0 (dK and all 256 dV columns) and runs two waves per SIMD with K and
+// V1 as register operands.
 template <int DV, int PART>
 constexpr int dkdv_do_width() { return PART == 2 ? DV / 2 : DV; }   // dO columns staged per stage
 template <int DV, int PART>
-constexpr int dkdv_dv_width() { return PART == 0 ? DV : DV / 2; }   // dV columns accumulated
+constexpr int dkdv_dv_width() { return PART == 0 ? DV : PART == 3 ? 0 : DV / 2; }   // dV columns accumulated
 // dkdv variants that read the V operand of dP = dO V^T from an LDS copy of the workgroup's 128 V rows
 // instead of holding it in registers (128 / 128 and the 256-wide value variants would otherwise spill).
 template <int D, int DV, int PART>
-constexpr bool dkdv_v_in_lds() { return PART != 2 && D + DV >= 256; }
+constexpr bool dkdv_v_in_lds() { return PART != 2 && PART != 3 && D + DV >= 256; }
 // ... and of K for S = Q K^T, in the first part of the 128 / 256 variant
 template <int D, int DV, int PART>
 constexpr bool dkdv_k_in_lds() { return PART == 1 && D == 128 && DV == 256; }
@@ -272,11 +278,12 @@ constexpr int dq_staged_dv() { return W0K ? DV - D : DV; }
 // partial of its key split (summed by fea_bwd_dq_reduce), or into grad_q in the mode the flags ask for.
 template <bool F16, int D>
 __device__ __forceinline__ void store_dq(const BwdParams& p, const f32x16 (&acc)[D / 32], VMO_LDS float* patch,
-                                         int prob, int split, int bb, int hh, int64_t qoff, int q0, int lane) {
+                                         int prob, int split, int bb, int hh, int64_t qoff, int q0, int lane,
+                                         float scale) {
   const int nrows = min(32, p.nq - q0);
   if (p.dq_splits > 1) {
     float* pr = p.dq_part + (((int64_t)split * p.problems + prob) * p.nq + q0) * D;
-    store_acc_rows<F16>(patch, acc, D / 32, p.sm_scale, kGradStoreF32, (char*)pr, (int64_t)D * 4, nrows, lane);
+    store_acc_rows<F16>(patch, acc, D / 32, scale, kGradStoreF32, (char*)pr, (int64_t)D * 4, nrows, lane);
   } else {
     const int mode = grad_mode(p.accum, VMO_BWD_ACCUM_Q, VMO_BWD_F32_Q, VMO_BWD_SUM_Q);
     const int64_t es = mode == kGradStore || mode == kGradSumStore ? 2 : 4;
@@ -284,7 +291,7 @@ __device__ __forceinline__ void store_dq(const BwdParams& p, const f32x16 (&acc)
     const char* src0 = mode == kGradSumStore
                            ? (const char*)p.dq_base + (bb * p.dqb_sb + hh * p.dqb_sh + (qoff + q0) * p.dqb_sn) * 4
                            : nullptr;
-    store_acc_rows<F16>(patch, acc, D / 32, p.sm_scale, mode, row0, p.dq_sn * es, nrows, lane, 0, src0, p.dqb_sn * 4);
+    store_acc_rows<F16>(patch, acc, D / 32, scale, mode, row0, p.dq_sn * es, nrows, lane, 0, src0, p.dqb_sn * 4);
   }
 }
 
@@ -443,7 +450,8 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
   if (n_full < n_tiles) iteration(n_full, std::true_type{});
   __syncthreads();   // every wave is done with the stage ring, which the epilogue patches reuse
   if (!wave_live) return;
-  store_dq<F16, D>(p, acc, (VMO_LDS float*)(smem + wave * kEpiPatchBytes), prob, split, bb, hh, qoff, q0, lane);
+  store_dq<F16, D>(p, acc, (VMO_LDS float*)(smem + wave * kEpiPatchBytes), prob, split, bb, hh, qoff, q0, lane,
+                   p.sm_scale);
 }
 
 // Sum the split-KV partials of dQ (fixed split order, so the result does not depend on timing) and
@@ -633,7 +641,8 @@ __global__ __launch_bounds__(256, 2) void fea_bwd_dq_ds_kernel(BwdParams p) {
   if (n_full < n_tiles) iteration(n_full, std::true_type{});
   __syncthreads();   // every wave is done with the stage ring, which the epilogue patches reuse
   if (!wave_live) return;
-  store_dq<F16, D>(p, acc, (VMO_LDS float*)(smem + wave * kEpiPatchBytes), prob, split, bb, hh, qoff, q0, lane);
+  store_dq<F16, D>(p, acc, (VMO_LDS float*)(smem + wave * kEpiPatchBytes), prob, split, bb, hh, qoff, q0, lane,
+                   p.ds_scale);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -657,6 +666,8 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
   constexpr int V_TILE = V_LDS ? kKvBN * VW * 2 : 0;
   static_assert(!W0K || DV == 2 * D || DV == D, "values k or [k | v1]");
   static_assert(!DS || PART != 2, "the dS route stores dS from the launch that forms it");
+  static_assert(PART != 3 || (W0K && DV == 2 * D), "the folded launch is for values [k | v1]");
+  constexpr bool FOLD = PART == 3;   // k's value-role gradient in the dK accumulators
   extern __shared__ __attribute__((aligned(1024))) char smem_raw[];
   VMO_LDS char* smem = (VMO_LDS char*)smem_raw;
 
@@ -727,11 +738,12 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
     }
   };
 
-  f32x16 dk[NK], dv[NV];
+  f32x16 dk[NK], dv[NV > 0 ? NV : 1];
 #pragma unroll
   for (int a = 0; a < NK; ++a) dk[a] = f32x16{};
 #pragma unroll
   for (int a = 0; a < NV; ++a) dv[a] = f32x16{};
+  const float gs = FOLD ? p.sm_scale : 1.f;   // dS enters the dK MFMAs times this
   const float c = p.c;
   const int qsw = swz_rows<D * 2>(l32), dsw = swz_rows<DOW * 2>(l32), vsw = swz_rows<(VW > 0 ? VW : D) * 2>(l32);
   const int trow = 4 * hl + ((lane & 15) >> 2);
@@ -811,6 +823,7 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
         const float x = fmaf(s[r], c, -lv[e]);
         float pv = fast_exp2(x);
         float gv = WANT_DK ? pv * (dp[r] + fmaf(bv[e], x, av[e])) : 0.f;
+        if constexpr (FOLD) gv *= gs;
         if (MASKED && 8 * g + 4 * hl + e >= nvalid) { pv = 0.f; gv = 0.f; }
         P[r >> 3][r & 7] = to_elem<T>(pv);
         G[r >> 3][r & 7] = to_elem<T>(gv);
@@ -818,7 +831,8 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
     }
 
     if constexpr (DS) {
-      // The stage's 32 x 32 block of dS^T (unscaled; the dq GEMM applies sm_scale), row = key l32, 64 bytes of
+      // The stage's 32 x 32 block of dS^T (unscaled -- the dq GEMM applies sm_scale -- or with FOLD times
+      // sm_scale already, and the dq GEMM then applies p.ds_scale = 1), row = key l32, 64 bytes of
       // 32 queries.  Lane (l32, hl) holds queries 8 g + 4 hl .. + 3 of G[g / 2]; two permlane32 swaps per
       // operand trade the halves so that the lower lanes hold whole 8-query chunks 0 and 2 and the upper
       // lanes chunks 1 and 3: two 16-byte stores per lane, each wave store inside one 2 KB block.  Issued before
@@ -836,20 +850,23 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
         *(global_u32x4*)(blk + 32 * j) = w;
       }
     }
-    // dV^T[dv][key] += dO^T P,  dK^T[d][key] += Q^T dS  (transposed reads of the staged tiles)
-    constexpr int NT = 2 * NV + (WANT_DK ? 2 * NK : 0);
+    // dV^T[dv][key] += dO^T P,  dK^T[d][key] += Q^T dS  (transposed reads of the staged tiles); with FOLD the
+    // first 2 NK products are dO[:, :D]^T P into the dK accumulators
+    constexpr int NPV = FOLD ? NK : NV;   // accumulator blocks that take dO^T P
+    constexpr int NT = 2 * NPV + (WANT_DK ? 2 * NK : 0);
     prefetched_chain<NT, kBwdPrefetch>(
         [&](int i) __attribute__((always_inline)) {
-          if (i < 2 * NV)
+          if (i < 2 * NPV)
             return tr_pair<V8, DOW * 2>(dOs + 16 * (i % 2) * (DOW * 2), tr_offset<DOW * 2>(trow, tchunk, tbyte, i / 2));
-          const int j = i - 2 * NV;
+          const int j = i - 2 * NPV;
           return tr_pair<V8, D * 2>(Qs + 16 * (j % 2) * (D * 2), tr_offset<D * 2>(trow, tchunk, tbyte, j / 2));
         },
         [&](int i, const V8& x) __attribute__((always_inline)) {
-          if (i < 2 * NV) {
-            dv[i / 2] = E::mfma(x, P[i % 2], dv[i / 2]);
+          if (i < 2 * NPV) {
+            if constexpr (FOLD) dk[i / 2] = E::mfma(x, P[i % 2], dk[i / 2]);
+            else dv[i / 2] = E::mfma(x, P[i % 2], dv[i / 2]);
           } else if constexpr (WANT_DK) {
-            const int j = i - 2 * NV;
+            const int j = i - 2 * NPV;
             dk[j / 2] = E::mfma(x, G[j % 2], dk[j / 2]);
           }
         });
@@ -874,6 +891,10 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
   };
   const int mode_k = grad_mode(p.accum, VMO_BWD_ACCUM_K, VMO_BWD_F32_K, VMO_BWD_SUM_K);
   const int mode_v = grad_mode(p.accum, VMO_BWD_ACCUM_V, VMO_BWD_F32_V, VMO_BWD_SUM_V);
+  if constexpr (FOLD) {   // dK in natural units already (dS times sm_scale); v1's gradient is PART 2's
+    put(p.dk, p.dk_sb, p.dk_sh, p.dk_sn, 0, dk, NK, 1.0f, mode_k, p.dk_base, p.dkb_sb, p.dkb_sh, p.dkb_sn);
+    return;
+  }
   if constexpr (W0K && PART == 0) {
     if (p.fold_k) {
       // Value columns [0, D) are k itself: their gradient (dV blocks 0 .. NK-1, laid out like dK's,
@@ -896,7 +917,9 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
   }
   if constexpr (WANT_DK)
     put(p.dk, p.dk_sb, p.dk_sh, p.dk_sn, 0, dk, NK, p.sm_scale, mode_k, p.dk_base, p.dkb_sb, p.dkb_sh, p.dkb_sn);
-  put(p.dv, p.dv_sb, p.dv_sh, p.dv_sn, VOFF, dv, NV, 1.0f, mode_v, p.dv_base, p.dvb_sb, p.dvb_sh, p.dvb_sn);
+  // (PART 2 after the folded PART 3: dv holds v1's gradient alone, from its column 0)
+  const int vcol = PART == 2 && p.fold_k ? 0 : VOFF;
+  put(p.dv, p.dv_sb, p.dv_sh, p.dv_sn, vcol, dv, NV, 1.0f, mode_v, p.dv_base, p.dvb_sb, p.dvb_sh, p.dvb_sn);
 }
 
 template <bool F16, int D, int DV, int PART, bool W0K, bool DS = false>
@@ -926,7 +949,14 @@ static int launch_bwd_ds(const BwdParams& p, hipStream_t s) {
   hipLaunchKernelGGL((fea_bwd_prep_kernel<F16, DV>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, p);
   int rc = launch_status("fea_bwd_prep");
   if (rc != VMO_OK) return rc;
-  if constexpr (dkdv_parts<D, DV, W0K>() == 1) {
+  if constexpr (W0K && D == 128 && DV == 256) {
+    if (p.fold_k) {   // folded dK with dS^T stored times sm_scale (p.ds_scale = 1), then v1's gradient
+      rc = launch_dkdv<F16, D, DV, 3, true, true>(p, s);
+      if (rc == VMO_OK) rc = launch_dkdv<F16, D, DV, 2, false>(p, s);
+    } else {
+      rc = launch_dkdv<F16, D, DV, 0, W0K, true>(p, s);
+    }
+  } else if constexpr (dkdv_parts<D, DV, W0K>() == 1) {
     rc = launch_dkdv<F16, D, DV, 0, W0K, true>(p, s);
   } else {
     rc = launch_dkdv<F16, D, DV, 1, W0K, true>(p, s);
@@ -969,7 +999,14 @@ static int launch_bwd(const BwdParams& p, hipStream_t s) {
     rc = launch_status("fea_bwd_dq_reduce");
     if (rc != VMO_OK) return rc;
   }
-  if constexpr (dkdv_parts<D, DV, W0K>() == 1) {
+  if constexpr (W0K && D == 128 && DV == 256) {
+    if (p.fold_k) {
+      rc = launch_dkdv<F16, D, DV, 3, true>(p, s);
+      if (rc != VMO_OK) return rc;
+      return launch_dkdv<F16, D, DV, 2, false>(p, s);
+    }
+    return launch_dkdv<F16, D, DV, 0, W0K>(p, s);
+  } else if constexpr (dkdv_parts<D, DV, W0K>() == 1) {
     return launch_dkdv<F16, D, DV, 0, W0K>(p, s);
   } else {
     rc = launch_dkdv<F16, D, DV, 1, W0K>(p, s);
@@ -1160,6 +1197,8 @@ extern "C" int vmo_fea_bwd(const vmo_fea_bwd_args* a, void* stream) {
   p.dq_total = (int)(problems * dq_tiles * p.dq_splits); p.kv_total = (int)(problems * kv_tiles);
   p.c = a->sm_scale * kLog2e;
   p.sm_scale = a->sm_scale;
+  // the folded launch for values [k | v1] at 128 / 256 stores dS^T times sm_scale
+  p.ds_scale = fold_k && a->dv1 > 0 && a->d == 128 ? 1.0f : a->sm_scale;
   hipStream_t s = (hipStream_t)stream;
   if (a->dtype == VMO_DTYPE_F16) return dispatch_bwd<true>(p, a->d, a->dv, s);
   return dispatch_bwd<false>(p, a->d, a->dv, s);
