@@ -665,6 +665,36 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
   VMO_LDS float* patch = (VMO_LDS float*)(smem + wave * kEpiPatchBytes);
   if (!wave_live) return;
 
+  // sum_j p~_j q . k_j (the P.K entropy) from the B-operand q registers (rows past the end hold zeros): the
+  // accumulator's lane (row l32, half hl) holds dims 32 a + 8 g + 4 hl + 0..3 and qf[ds] dims 16 ds + 8 hl +
+  // 0..7, so one permlane32 swap of dwords (0, 2) and one of (1, 3) per ds hand every lane dims 16 ds + 4 hl
+  // + 0..3 (g = 2 (ds % 2)) and 16 ds + 8 + 4 hl + 0..3 (g + 1) of its row.  (Re-reading q in the
+  // accumulator's layout instead cost the launch a second pass over q, 100 MB at cfg4.)
+  float pkdot[QB];
+#pragma unroll
+  for (int j = 0; j < QB; ++j) {
+    pkdot[j] = 0.f;
+    if constexpr (ENT == kEntFromPK) {
+      typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+      float d = 0.f;
+#pragma unroll
+      for (int ds = 0; ds < NDS; ++ds) {
+        const u32x4 w = __builtin_bit_cast(u32x4, qf[j][ds]);
+        const auto s0 = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
+        const auto s1 = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+        const uint32_t xy[4] = {s0[0], s1[0], s0[1], s1[1]};
+        const int r0 = 8 * (ds & 1);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const V2 x = __builtin_bit_cast(V2, xy[u]);
+          d = fmaf((float)x[0], acc[j][ds >> 1][r0 + 2 * u], d);
+          d = fmaf((float)x[1], acc[j][ds >> 1][r0 + 2 * u + 1], d);
+        }
+      }
+      pkdot[j] = wave_sum32(d);
+    }
+  }
+
   // The epilogue derives its indices and row bases again, from an opaque copy of the block's logical
   // index (scalar registers are free by now): kept from the prologue, the 64-bit bases sat in vector
   // registers across the whole key loop, and the tightest variants spilled them to scratch.
@@ -672,8 +702,7 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
   asm volatile("" : "+s"(l_epi));
   const Loc le = locate(l_epi, std::true_type{});
   T* const ob = (T*)p.o + le.bb * p.o_sb + le.hh * p.o_sh + (int64_t)le.f * p.nq * p.o_sn;
-  const T* const qb_e = (const T*)p.q + le.bb * p.q_sb + le.hh * p.q_sh + (int64_t)le.f * p.nq * p.q_sn;
-  const int64_t o_sn = p.o_sn, q_sn_e = p.q_sn;
+  const int64_t o_sn = p.o_sn;
   const int64_t st0 = le.bb * p.st_sb + le.hh * p.st_sh + (int64_t)le.f * p.nq;
   const int64_t part0 = (int64_t)(le.split * p.problems + le.prob) * p.nq;
   const int q0_e = le.qt * kBM + wave * 32 * QB;
@@ -698,19 +727,8 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
         // h = sum_j p_j x_j with p_j = 2^x_j: entropy (bits) = log2 l - h / l
         ent = (log2l - wave_sum32(h_run[j]) * inv_l) * kLn2;
       } else if constexpr (ENT == kEntFromPK) {
-        // sum_j P~_j s_j = q . (sum_j p~_j k_j) / l~, with q re-read in the accumulator's layout
-        const T* qp = qb_e + (int64_t)(qv ? qr : 0) * q_sn_e + 4 * hl;
-        float dot = 0.f;
-#pragma unroll
-        for (int a = 0; a < NA0; ++a)
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const V4 qv = *(const V4*)(qp + 32 * a + 8 * g);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) dot = fmaf((float)qv[e], acc[j][a][4 * g + e], dot);
-          }
-        dot = wave_sum32(dot);
-        ent = lse * kLn2 - (c * kLn2) * dot * inv_l;
+        // sum_j P~_j s_j = q . (sum_j p~_j k_j) / l~
+        ent = lse * kLn2 - (c * kLn2) * pkdot[j] * inv_l;
       }
       store_acc_rows<F16>(patch, acc[j], NA, inv_l, kGradStore, (char*)(ob + (int64_t)qb0 * o_sn), o_sn * 2, nrows, lane);
       if (qv) {
