@@ -272,7 +272,9 @@ static int dispatch_lstep(const LParams& p, int d, int dv, bool last, hipStream_
 // [k][i] wherever a product needs one lane per k.  dq is accumulated (read-modify-write) into an
 // fp32 buffer, since every L-step and the R-step chain add to it; d out is written.
 // Columns (waves) per workgroup: one, so that the LDS a wave needs (29 KB at 128 / 128) is the whole
-// allocation unit and five waves share a CU (two per workgroup fitted four).
+// allocation unit and five waves share a CU (two per workgroup fitted four).  The register budget is
+// sized for two waves per SIMD: left free, the compiler took 316 registers at 128 / 128 (one wave per
+// SIMD, four per CU); within 256 it needs 176-224 and spills none.
 constexpr int kLBWaves = 1;
 
 struct LBParams {
@@ -312,7 +314,7 @@ struct LBLds {
 };
 
 template <bool F16, int D, int DV, bool LAST>
-__global__ __launch_bounds__(64 * kLBWaves) void lstep_bwd_kernel(LBParams p) {
+__global__ __launch_bounds__(64 * kLBWaves, 2) void lstep_bwd_kernel(LBParams p) {
   using E = Elem<F16>;
   using T = typename E::T;
   using V8 = typename E::V8;
