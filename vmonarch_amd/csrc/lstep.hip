@@ -368,6 +368,24 @@ __global__ __launch_bounds__(64 * kLBWaves, 2) void lstep_bwd_kernel(LBParams p)
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  // Non-last steps add to dq (the last one overwrites it): its fp32 rows are loaded now, in the layout of
+  // the final store (lane: rows rr0 + 8 i, 4 columns at 32 a + 4 c), so that the read's latency hides
+  // behind the whole column's work instead of stalling that store.  (The last step keeps the generic
+  // store: these 64 registers would spill its operands.)
+  float* const dq0 = p.dq + bb * p.dq_sb + hh * p.dq_sh + (int64_t)j * p.dq_sn;
+  const int64_t dq_rs = (int64_t)p.bs * p.dq_sn;
+  f32x4 dq_pre[LAST ? 1 : ND][4];
+  if constexpr (!LAST) {
+    const bool dq_add = !p.dq_overwrite;
+#pragma unroll
+    for (int a = 0; a < ND; ++a)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int rr = (lane >> 3) + 8 * i;
+        dq_pre[a][i] = (dq_add && live && rr < m) ? *(const f32x4*)(dq0 + rr * dq_rs + 32 * a + 4 * (lane & 7))
+                                                 : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+  }
   if constexpr (LAST) {
     // z rows of tokens < skip are overwritten by the recompute: no gradient reaches the L-path
     constexpr int CH = DV / 8;
@@ -584,10 +602,28 @@ __global__ __launch_bounds__(64 * kLBWaves, 2) void lstep_bwd_kernel(LBParams p)
     for (int a = 0; a < ND; ++a) accq[a] = f32x16{};
     mma_acc_t(accq, k_t, dl);
     if constexpr (!LAST) mma_acc_t(accq, v_t, s);
-    if (live) {   // kr (and dv) tiles dead now: the kr tile takes the row-store patch
-      float* dq0 = p.dq + bb * p.dq_sb + hh * p.dq_sh + (int64_t)j * p.dq_sn;
+    if (LAST && live) {   // kr tile dead now: it takes the row-store patch
       store_acc_rows<F16>((VMO_LDS float*)k_t, accq, ND, 1.f, p.dq_overwrite ? kGradStoreF32 : kGradAddF32,
-                          (char*)dq0, (int64_t)p.bs * p.dq_sn * 4, m, lane);
+                          (char*)dq0, dq_rs * 4, m, lane);
+    } else if (live) {   // kr and dv tiles dead now: the kr tile takes the row-store patch, dq_pre the add
+      VMO_LDS float* patch = (VMO_LDS float*)k_t;
+      const int rr0 = lane >> 3, c = lane & 7;
+#pragma unroll
+      for (int a = 0; a < ND; ++a) {
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {   // row l32, 16-byte chunk 2 jj + hl, swizzled by row
+          f32x4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = accq[a][4 * jj + e];
+          *(VMO_LDS f32x4*)(patch + l32 * 32 + ((2 * jj + hl) ^ (l32 & 7)) * 4) = v;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {   // rows rr0 + 8 i, chunk c: 8 lanes per row
+          const int rr = rr0 + 8 * i;
+          const f32x4 v = *(const VMO_LDS f32x4*)(patch + rr * 32 + (c ^ (rr & 7)) * 4);
+          if (rr < m) *(f32x4*)(dq0 + rr * dq_rs + 32 * a + 4 * c) = v + dq_pre[LAST ? 0 : a][i];
+        }
+      }
     }
   }
 
