@@ -54,12 +54,13 @@ struct LLds {
 };
 
 // Stage 32 rows (row i = token i*bs + j, clamped to i < m) of width W into a swizzled tile.
-template <class T, int W>
+template <class T, int W, int ROWS = 32>
 __device__ __forceinline__ void stage_col_rows(const T* __restrict__ colbase, int64_t row_stride, int m,
                                                VMO_LDS char* dst, int lane) {
   constexpr int CH = W / 8;
   constexpr int RPI = 64 / CH;
-  constexpr int NI = 32 / RPI;
+  constexpr int NI = ROWS / RPI;
+  static_assert(ROWS % RPI == 0, "whole copy instructions");
 #pragma unroll
   for (int inst = 0; inst < NI; ++inst) {
     const int r = inst * RPI + lane / CH;
@@ -301,25 +302,38 @@ struct LBParams {
   int64_t dl_sb, dl_sh;
 };
 
-template <int D, int DV, bool LAST>
+// ROWS: rows held per tile, 32 or (for m <= 24) 24.  The MFMAs take 32 rows of a tile; with 24 tile rows
+// their reads of rows 24..31 land in the first 8 rows of the next tile (q -> kr -> dz / dv, all 16-bit, so
+// finite) or, past the last, in a zeroed pad, and those rows only ever meet zero factors (attention rows
+// and columns past m).  The row-store patches (fp32 / 16-bit words, kEpiPatchBytes) therefore go where no
+// later read lands: see the ALIAS-marked stores.  Built for the 128-wide tiles (6 KB, each holding a patch),
+// where the smaller tiles let six waves share a CU instead of five.
+template <int D, int DV, bool LAST, int ROWS>
 struct LBLds {
-  static constexpr int QT = 32 * D * 2;               // q rows i
-  static constexpr int KT = 32 * D * 2;               // kr rows k
-  static constexpr int GT = LAST ? 32 * DV * 2 : 0;   // dz rows i
-  static constexpr int VT = LAST ? 0 : 32 * D * 2;    // dv rows k
-  static constexpr int AT = 32 * kAttStride * 4;      // an m x m matrix as [k][i]
+  static constexpr int QT = ROWS * D * 2;                 // q rows i
+  static constexpr int KT = ROWS * D * 2;                 // kr rows k
+  static constexpr int GT = LAST ? ROWS * DV * 2 : 0;     // dz rows i
+  static constexpr int VT = LAST ? 0 : ROWS * D * 2;      // dv rows k
+  static constexpr int PT = (32 - ROWS) * (LAST ? DV : D) * 2;   // zeroed pad after the last tile
+  static constexpr int AT = 32 * kAttStride * 4;          // an m x m matrix as [k][i]
   static constexpr int ET = 32 * 4;
   static constexpr int CT = 32 * 4;
-  static constexpr int PER_WAVE = QT + KT + GT + VT + AT + ET + CT;   // y is read into registers
+  static constexpr int PER_WAVE = QT + KT + GT + VT + PT + AT + ET + CT;   // y is read into registers
+  // the aliased first 8 rows of a tile, and a patch in the rest of the dz tile
+  static constexpr int ALIAS = (32 - ROWS) * D * 2;
+  static_assert(ROWS == 32 || (ROWS == 24 && D == 128 && (!LAST || DV == 128)), "tile rows");
+  static_assert(QT >= kEpiPatchBytes && (LAST ? GT - ALIAS >= kEpiPatchBytes : VT >= kEpiPatchBytes), "patch room");
 };
+template <int D, int DV, bool LAST>
+constexpr bool lbwd_rows24() { return D == 128 && (!LAST || DV == 128); }
 
-template <bool F16, int D, int DV, bool LAST>
+template <bool F16, int D, int DV, bool LAST, int ROWS>
 __global__ __launch_bounds__(64 * kLBWaves, 2) void lstep_bwd_kernel(LBParams p) {
   using E = Elem<F16>;
   using T = typename E::T;
   using V8 = typename E::V8;
   using V4 = typename E::V4;
-  using LL = LBLds<D, DV, LAST>;
+  using LL = LBLds<D, DV, LAST, ROWS>;
   constexpr int ND = D / 32;
   constexpr int NV = DV / 32;
 
@@ -331,7 +345,8 @@ __global__ __launch_bounds__(64 * kLBWaves, 2) void lstep_bwd_kernel(LBParams p)
   VMO_LDS char* k_t = q_t + LL::QT;
   VMO_LDS char* g_t = k_t + LL::KT;
   VMO_LDS char* v_t = g_t + LL::GT;
-  VMO_LDS float* att = (VMO_LDS float*)(v_t + LL::VT);
+  VMO_LDS char* pad = v_t + LL::VT;
+  VMO_LDS float* att = (VMO_LDS float*)(pad + LL::PT);
   VMO_LDS float* e_t = att + 32 * kAttStride;
   VMO_LDS float* c_t = e_t + 32;
 
@@ -345,12 +360,13 @@ __global__ __launch_bounds__(64 * kLBWaves, 2) void lstep_bwd_kernel(LBParams p)
   const T* ocol = (const T*)p.out + bb * p.out_sb + hh * p.out_sh + (int64_t)j * p.out_sn;
   const T* gcol = (const T*)p.g + bb * p.g_sb + hh * p.g_sh + (int64_t)j * p.g_sn;
 
-  stage_col_rows<T, D>(qcol, q_rs, m, q_t, lane);
-  stage_col_rows<T, D>(ocol, o_rs, m, k_t, lane);
+  stage_col_rows<T, D, ROWS>(qcol, q_rs, m, q_t, lane);
+  stage_col_rows<T, D, ROWS>(ocol, o_rs, m, k_t, lane);
   if constexpr (LAST)
-    stage_col_rows<T, DV>(gcol, g_rs, m, g_t, lane);
+    stage_col_rows<T, DV, ROWS>(gcol, g_rs, m, g_t, lane);
   else   // du rows k, into the dv tile: each lane turns its du values into dv in place
-    stage_col_rows<T, D>(gcol, g_rs, m, v_t, lane);
+    stage_col_rows<T, D, ROWS>(gcol, g_rs, m, v_t, lane);
+  for (int o = lane * 16; o < LL::PT; o += 64 * 16) *(VMO_LDS i32x4*)(pad + o) = i32x4{0, 0, 0, 0};
   const int rk = l32 < m ? l32 : m - 1;
   V8 krf[D / 16], yf[LAST ? DV / 16 : 1];   // kr and y rows k (lane = k) as MFMA operands
   {
@@ -374,13 +390,14 @@ __global__ __launch_bounds__(64 * kLBWaves, 2) void lstep_bwd_kernel(LBParams p)
   // store: these 64 registers would spill its operands.)
   float* const dq0 = p.dq + bb * p.dq_sb + hh * p.dq_sh + (int64_t)j * p.dq_sn;
   const int64_t dq_rs = (int64_t)p.bs * p.dq_sn;
-  f32x4 dq_pre[LAST ? 1 : ND][4];
+  constexpr int DQ_RG = ROWS / 8;   // row groups that can hold rows < m
+  f32x4 dq_pre[LAST ? 1 : ND][DQ_RG];
   if constexpr (!LAST) {
     const bool dq_add = !p.dq_overwrite;
 #pragma unroll
     for (int a = 0; a < ND; ++a)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < DQ_RG; ++i) {
         const int rr = (lane >> 3) + 8 * i;
         dq_pre[a][i] = (dq_add && live && rr < m) ? *(const f32x4*)(dq0 + rr * dq_rs + 32 * a + 4 * (lane & 7))
                                                  : f32x4{0.f, 0.f, 0.f, 0.f};
@@ -389,7 +406,7 @@ __global__ __launch_bounds__(64 * kLBWaves, 2) void lstep_bwd_kernel(LBParams p)
   if constexpr (LAST) {
     // z rows of tokens < skip are overwritten by the recompute: no gradient reaches the L-path
     constexpr int CH = DV / 8;
-    for (int idx = lane; idx < 32 * CH; idx += 64) {
+    for (int idx = lane; idx < ROWS * CH; idx += 64) {
       const int r = idx / CH;
       if (r * p.bs + j < p.skip) *(VMO_LDS i32x4*)(g_t + r * (DV * 2) + (idx % CH) * 16) = i32x4{0, 0, 0, 0};
     }
@@ -538,9 +555,11 @@ __global__ __launch_bounds__(64 * kLBWaves, 2) void lstep_bwd_kernel(LBParams p)
     for (int a = 0; a < NV; ++a) accy[a] = f32x16{};
     mma_rows_t(accy, g_t, std::integral_constant<int, DV>{}, Bu);
     if (p.delta) dlt = row_dot(yf, accy, std::integral_constant<int, NV>{});
-    // the dz tile is dead now: it takes the row-store patch (whole row segments per store)
+    // the dz tile is dead now: it takes the row-store patch (whole row segments per store), past its first
+    // rows, which the kr tile's reads of rows ROWS.. still land in (ALIAS)
     if (live)
-      store_acc_rows<F16>((VMO_LDS float*)g_t, accy, NV, 1.f, kGradStore, (char*)(dcol + D), do_rs * 2, m, lane);
+      store_acc_rows<F16>((VMO_LDS float*)(g_t + LL::ALIAS), accy, NV, 1.f, kGradStore, (char*)(dcol + D), do_rs * 2,
+                          m, lane);
   } else {
     to_att(s);
     __syncthreads();
@@ -567,7 +586,7 @@ __global__ __launch_bounds__(64 * kLBWaves, 2) void lstep_bwd_kernel(LBParams p)
           df = fmaf(du, accv[a][4 * g + e], df);
           w[e] = to_elem<T>(du * f);
         }
-        *dvp = w;
+        *dvp = w;   // rows k >= ROWS: the pad, which stays zero (du = 0 there)
       }
     df = wave_sum32(df);
     if (hl == 0) c_t[k] = (kvalid && cs >= p.min_col_mass) ? -df * f / cm : 0.f;
@@ -602,11 +621,13 @@ __global__ __launch_bounds__(64 * kLBWaves, 2) void lstep_bwd_kernel(LBParams p)
     for (int a = 0; a < ND; ++a) accq[a] = f32x16{};
     mma_acc_t(accq, k_t, dl);
     if constexpr (!LAST) mma_acc_t(accq, v_t, s);
-    if (LAST && live) {   // kr tile dead now: it takes the row-store patch
-      store_acc_rows<F16>((VMO_LDS float*)k_t, accq, ND, 1.f, p.dq_overwrite ? kGradStoreF32 : kGradAddF32,
+    // the dz (dv) tile is dead now and takes the row-store patch: not the kr tile, whose first rows the q
+    // tile's reads of rows ROWS.. still land in (ALIAS)
+    if (LAST && live) {
+      store_acc_rows<F16>((VMO_LDS float*)g_t, accq, ND, 1.f, p.dq_overwrite ? kGradStoreF32 : kGradAddF32,
                           (char*)dq0, dq_rs * 4, m, lane);
-    } else if (live) {   // kr and dv tiles dead now: the kr tile takes the row-store patch, dq_pre the add
-      VMO_LDS float* patch = (VMO_LDS float*)k_t;
+    } else if (live) {   // dq_pre holds the rows added to
+      VMO_LDS float* patch = (VMO_LDS float*)v_t;
       const int rr0 = lane >> 3, c = lane & 7;
 #pragma unroll
       for (int a = 0; a < ND; ++a) {
@@ -618,7 +639,7 @@ __global__ __launch_bounds__(64 * kLBWaves, 2) void lstep_bwd_kernel(LBParams p)
           *(VMO_LDS f32x4*)(patch + l32 * 32 + ((2 * jj + hl) ^ (l32 & 7)) * 4) = v;
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {   // rows rr0 + 8 i, chunk c: 8 lanes per row
+        for (int i = 0; i < DQ_RG; ++i) {   // rows rr0 + 8 i, chunk c: 8 lanes per row
           const int rr = rr0 + 8 * i;
           const f32x4 v = *(const VMO_LDS f32x4*)(patch + rr * 32 + (c ^ (rr & 7)) * 4);
           if (rr < m) *(f32x4*)(dq0 + rr * dq_rs + 32 * a + 4 * c) = v + dq_pre[LAST ? 0 : a][i];
@@ -647,11 +668,11 @@ __global__ __launch_bounds__(64 * kLBWaves, 2) void lstep_bwd_kernel(LBParams p)
   }
 }
 
-template <bool F16, int D, int DV, bool LAST>
+template <bool F16, int D, int DV, bool LAST, int ROWS>
 static int launch_lstep_bwd(const LBParams& p, hipStream_t s) {
-  constexpr int LDS = LBLds<D, DV, LAST>::PER_WAVE * kLBWaves;
+  constexpr int LDS = LBLds<D, DV, LAST, ROWS>::PER_WAVE * kLBWaves;
   static_assert(LDS <= 160 * 1024, "lstep_bwd LDS");
-  auto kern = lstep_bwd_kernel<F16, D, DV, LAST>;
+  auto kern = lstep_bwd_kernel<F16, D, DV, LAST, ROWS>;
   if (LDS > 65536) {
     static bool done = false;   // attribute is per function; idempotent, so a benign race
     if (!done) {
@@ -667,8 +688,11 @@ static int launch_lstep_bwd(const LBParams& p, hipStream_t s) {
 
 template <bool F16>
 static int dispatch_lstep_bwd(const LBParams& p, int d, int dv, bool last, hipStream_t s) {
-#define VMO_LB(D_, DV_, LAST_) \
-  if (d == D_ && (!LAST_ || dv == DV_) && last == LAST_) return launch_lstep_bwd<F16, D_, DV_, LAST_>(p, s);
+#define VMO_LB(D_, DV_, LAST_)                                        \
+  if (d == D_ && (!LAST_ || dv == DV_) && last == LAST_)              \
+    return p.m <= 24 && lbwd_rows24<D_, DV_, LAST_>()                 \
+               ? launch_lstep_bwd<F16, D_, DV_, LAST_, lbwd_rows24<D_, DV_, LAST_>() ? 24 : 32>(p, s) \
+               : launch_lstep_bwd<F16, D_, DV_, LAST_, 32>(p, s);
   VMO_LB(64, 64, false)
   VMO_LB(128, 128, false)
   VMO_LB(64, 64, true)
