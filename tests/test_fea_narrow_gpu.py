@@ -1,0 +1,91 @@
+"""The 32-wide flash-entropy forward kernel (heads of at most 32; 16-wide heads zero-padded to 32 by the
+caller) against the CPU oracle: the reference's narrow head dims (kernel.py:324), ragged N, fp16, frames,
+the no-entropy variant called through the C ABI, and the exact two-pass path of the fixed reference point.
+Tolerances as tests/test_fea_gpu.py: the reference metric (2e-2 * max|ref|) and elementwise 2e-2 + 1e-2 |ref|."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close_elementwise, assert_close_ref, hip_library_loaded, randn_lp
+from oracle import entropy_attention
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+LOG2E = 1.4426950408889634
+
+
+def _check(o, e, o_ref, e_ref):
+    o, e = o.float().cpu().numpy(), e.float().cpu().numpy()
+    assert np.isfinite(o).all() and np.isfinite(e).all()
+    for x, ref in ((o, o_ref), (e, e_ref)):
+        if np.abs(ref).max() > 0:   # (one key: every entropy is 0, and the relative metric has no scale)
+            assert_close_ref(x, ref, 2e-2)
+        assert_close_elementwise(x, ref)
+
+
+@pytest.mark.parametrize("D, Dv", [(32, 32), (16, 16), (16, 32), (32, 16)])
+@pytest.mark.parametrize("N", [1, 77, 300, 1024])
+def test_narrow_heads_forward(D, Dv, N):
+    from vmonarch_amd import flash_entropy_attention
+    g = torch.Generator().manual_seed(1000 + 10 * D + Dv + N)
+    q, k, v = randn_lp(g, 2, 3, N, D), randn_lp(g, 2, 3, N, D), randn_lp(g, 2, 3, N, Dv)
+    print(f"narrow forward D={D} Dv={Dv} N={N}", flush=True)
+    o, e = flash_entropy_attention(q.to(DEV), k.to(DEV), v.to(DEV))
+    assert o.shape == (2, 3, N, Dv)
+    o_ref, e_ref = entropy_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), D ** -0.5)
+    _check(o, e, o_ref, e_ref)
+    assert hip_library_loaded()
+
+
+def test_narrow_heads_forward_fp16():
+    from vmonarch_amd import flash_entropy_attention
+    g = torch.Generator().manual_seed(7)
+    q, k, v = (randn_lp(g, 1, 2, 500, 32, dtype=torch.float16) for _ in range(3))
+    o, e = flash_entropy_attention(q.to(DEV), k.to(DEV), v.to(DEV))
+    assert o.dtype == torch.float16
+    o_ref, e_ref = entropy_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), 32 ** -0.5)
+    _check(o, e, o_ref, e_ref)
+
+
+@pytest.mark.parametrize("want_ent", [True, False])
+def test_32_wide_kernel_through_the_c_abi(want_ent):
+    """fea_forward on 32-wide tensors (no padding: the library rejects widths it has no kernel for), three
+    frames of 200 queries and 170 keys, with and without the entropy output."""
+    from vmonarch_amd.kernel import fea_forward
+    g = torch.Generator().manual_seed(11)
+    F, nq, nk = 3, 200, 170
+    q, k, v = randn_lp(g, 1, 2, F * nq, 32), randn_lp(g, 1, 2, F * nk, 32), randn_lp(g, 1, 2, F * nk, 32)
+    o, lse, ent = fea_forward(q.to(DEV), k.to(DEV), v.to(DEV), None, 0.2, frames=F, want_ent=want_ent)
+    assert (ent is not None) == want_ent
+    for f in range(F):
+        qs, ks, vs = (t[:, :, f * n:(f + 1) * n].float().numpy() for t, n in ((q, nq), (k, nk), (v, nk)))
+        o_ref, e_ref = entropy_attention(qs, ks, vs, 0.2)
+        o_f = o[:, :, f * nq:(f + 1) * nq].float().cpu().numpy()
+        assert_close_ref(o_f, o_ref, 2e-2)
+        assert_close_elementwise(o_f, o_ref)
+        s = np.einsum("bhqd,bhkd->bhqk", qs.astype(np.float64), ks.astype(np.float64)) * 0.2 * LOG2E
+        lse_ref = np.log2(np.exp2(s - s.max(-1, keepdims=True)).sum(-1)) + s.max(-1)
+        np.testing.assert_allclose(lse[:, :, f * nq:(f + 1) * nq].cpu().numpy(), lse_ref, atol=2e-2, rtol=1e-3)
+        if want_ent:
+            e_f = ent[:, :, f * nq:(f + 1) * nq].cpu().numpy()
+            assert_close_elementwise(e_f, e_ref)
+
+
+def test_narrow_heads_reference_point_overflow():
+    """Keys 70+ log2 units above the max of the first 32 keys take the exact two-pass path (bf16)."""
+    from vmonarch_amd import flash_entropy_attention
+    g = torch.Generator().manual_seed(12)
+    N, D = 300, 32
+    q = torch.randn(1, 2, N, D, generator=g)
+    q[:, :, : N // 2] += 1.0
+    k = torch.randn(1, 2, N, D, generator=g)
+    for j in (40, 290):   # one in the first stage, one in the last partial stage
+        k[:, :, j] = 4.0 + 0.05 * torch.randn(1, 2, D, generator=g)
+    v = torch.randn(1, 2, N, D, generator=g)
+    q, k, v = q.bfloat16(), k.bfloat16(), v.bfloat16()
+    sm = 1.0
+    s = (q.double() @ k.double().transpose(-1, -2)) * sm * LOG2E
+    assert float((s.amax(-1) - s[..., :32].amax(-1)).max()) > 70.0, "inputs do not reach the fallback"
+    o, e = flash_entropy_attention(q.to(DEV), k.to(DEV), v.to(DEV), sm)
+    o_ref, e_ref = entropy_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), sm)
+    _check(o, e, o_ref, e_ref)

@@ -98,7 +98,7 @@ struct TileCopy {
   static constexpr int RPI = 64 / CH;    // rows per wave instruction
   static constexpr int NI = kFwdBN / RPI / WAVES;
   static constexpr int NV = (WAVES * RPI) % 16 == 0 ? 1 : 2;   // distinct lane offsets
-  static_assert(CH >= 8 && NI >= 1 && RPI >= 2, "tile shape");
+  static_assert(CH >= 4 && NI >= 1 && RPI >= 2, "tile shape");
   uint64_t ubase;     // base as a scalar byte address
   uint64_t rbytes;    // bytes per row
   uint32_t voff[NV];
@@ -871,7 +871,10 @@ static int dispatch_fwd(const FwdParams& p, int d, int dw0, int dw1, bool w0k, b
 #define VMO_FWD(D_, DW0_, DW1_, W0K_, ENT_, SPLIT_)                                                  \
   if (d == D_ && dw0 == DW0_ && dw1 == DW1_ && w0k == W0K_ && ent == (ENT_ != kEntNone) && split == SPLIT_) \
     return launch_fwd<F16, D_, DW0_, DW1_, W0K_, ENT_, SPLIT_, kFwdWavesFor(D_, DW0_, DW1_, SPLIT_)>(p, s);
-  // standalone flash_entropy_attention (kernel.py:384-402): online entropy
+  // standalone flash_entropy_attention (kernel.py:384-402): online entropy (32 / 32 also takes 16-wide heads,
+  // zero-padded by the caller)
+  VMO_FWD(32, 32, 0, false, kEntOnline, false)
+  VMO_FWD(32, 32, 0, false, kEntNone, false)
   VMO_FWD(64, 64, 0, false, kEntOnline, false)
   VMO_FWD(64, 128, 0, false, kEntOnline, false)
   VMO_FWD(64, 256, 0, false, kEntOnline, false)

@@ -63,17 +63,20 @@ template <> struct Elem<true> {
 __device__ __forceinline__ int swz(int row) { return ((row & 3) << 1) | ((row >> 2) & 1); }
 
 // Bank-conflict-free chunk swizzle for gfx950's 64-bank LDS (256 bytes per cycle), for tiles with
-// RB-byte rows (RB = 128, 256 or 512): chunk c of row r is stored at chunk c ^ swz_rows<RB>(r).
+// RB-byte rows (RB = 64, 128, 256 or 512): chunk c of row r is stored at chunk c ^ swz_rows<RB>(r).
 //  * ds_read_b128 of 16 consecutive rows at one logical chunk (an MFMA A operand, 16 lanes per
 //    cycle) hits 16 distinct 16-byte bank groups: for RB >= 256 the map r -> f(r) is a bijection
 //    on r mod 16; for RB = 128 (two rows per bank line) it is a bijection on each row parity.
 //  * ds_read_tr16_b64 of 4 aligned rows x 4 aligned chunks (32 lanes per cycle) hits 16 distinct
 //    groups: f(r) >> 2 differs between the rows that share a bank line position.
+//  * RB = 64 (four rows per bank line, four chunks per row): f(r) = (r / 4) % 4, so 16 consecutive rows at
+//    one logical chunk take the 16 (row % 4, chunk) positions of a bank line.
 // f(r + 8) = f(r) ^ 2 and f(r + 16) = f(r).
 template <int RB>
 __device__ __forceinline__ int swz_rows(int r) {
-  static_assert(RB == 128 || RB == 256 || RB == 512, "row width");
-  if constexpr (RB == 128) return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+  static_assert(RB == 64 || RB == 128 || RB == 256 || RB == 512, "row width");
+  if constexpr (RB == 64) return (r >> 2) & 3;
+  else if constexpr (RB == 128) return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
   else return ((r & 3) << 2) | ((r >> 2) & 3);
 }
 

@@ -22,9 +22,12 @@ def _pad_features(t, width):
     return torch.nn.functional.pad(t, (0, width - t.shape[-1]))
 
 
-def _kernel_width(d):
-    # kernels exist for 64 / 128 (q, k) and 64 / 128 / 256 (values); narrower dims are zero-padded
-    return 64 if d < 64 else d
+def _kernel_widths(d, dv):
+    """Head dims of the forward kernel that serves (d, dv): 32 / 32 for heads of at most 32 (16 zero-padded to
+    32), else 64 / 128 (q, k) and 64 / 128 / 256 (values), narrower dims zero-padded to 64."""
+    if d <= 32 and dv <= 32:
+        return 32, 32
+    return (64 if d < 64 else d), (64 if dv < 64 else dv)
 
 
 def fea_forward(q, k, w0, w1, sm_scale, frames=1, o=None, lse=None, ent=None, want_ent=True, want_lse=True,
@@ -96,7 +99,7 @@ class _FlashEntropyAttention(torch.autograd.Function):
         if not q.is_cuda:
             raise RuntimeError("vmonarch_amd: flash_entropy_attention needs GPU tensors (no CPU path)")
         n = int(n_valid)
-        Dk, Dvk = _kernel_width(D), _kernel_width(Dv)
+        Dk, Dvk = _kernel_widths(D, Dv)
         qx, kx, vx = (_lib.row_aligned(_pad_features(t[:, :, :n], w)) for t, w in ((q, Dk), (k, Dk), (v, Dvk)))
         ent = torch.empty((B, H, N), device=q.device, dtype=torch.float32)
         lse = torch.empty((B, H, N), device=q.device, dtype=torch.float32)
