@@ -1,13 +1,14 @@
-"""The 32-wide flash-entropy forward kernel (heads of at most 32; 16-wide heads zero-padded to 32 by the
-caller) against the CPU oracle: the reference's narrow head dims (kernel.py:324), ragged N, fp16, frames,
-the no-entropy variant called through the C ABI, and the exact two-pass path of the fixed reference point.
-Tolerances as tests/test_fea_gpu.py: the reference metric (2e-2 * max|ref|) and elementwise 2e-2 + 1e-2 |ref|."""
+"""The 32-wide flash-entropy kernels (heads of at most 32; 16-wide heads zero-padded to 32 by the caller)
+against the CPU oracle: the reference's narrow head dims (kernel.py:324), ragged N, fp16, frames, the
+no-entropy variant called through the C ABI, the exact two-pass path of the fixed reference point, and the
+gradients (dq with key splits at N = 4096).  Tolerances as tests/test_fea_gpu.py: the reference metric
+(2e-2 * max|ref|, gradients 3e-2) and elementwise 2e-2 + 1e-2 |ref|."""
 import numpy as np
 import pytest
 import torch
 
-from conftest import assert_close_elementwise, assert_close_ref, hip_library_loaded, randn_lp
-from oracle import entropy_attention
+from conftest import assert_close_elementwise, assert_close_ref, assert_grad_close, hip_library_loaded, randn_lp
+from oracle import entropy_attention, entropy_attention_grad
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -89,3 +90,24 @@ def test_narrow_heads_reference_point_overflow():
     o, e = flash_entropy_attention(q.to(DEV), k.to(DEV), v.to(DEV), sm)
     o_ref, e_ref = entropy_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), sm)
     _check(o, e, o_ref, e_ref)
+
+
+@pytest.mark.parametrize("D, Dv, N", [(32, 32, 77), (32, 32, 300), (32, 32, 4096), (16, 32, 300), (32, 16, 300),
+                                      (16, 16, 129)])
+def test_narrow_heads_backward(D, Dv, N):
+    """Gradients of the loss of tests/test_vmonarch.py:35 through the 32-wide dq and dk/dv kernels (N = 4096:
+    the dq kernel splits the keys four ways and reduces the partials)."""
+    from vmonarch_amd import flash_entropy_attention
+    g = torch.Generator().manual_seed(2000 + 10 * D + Dv + N)
+    q, k, v = randn_lp(g, 1, 2, N, D), randn_lp(g, 1, 2, N, D), randn_lp(g, 1, 2, N, Dv)
+    do, de = torch.randn(1, 2, N, Dv, generator=g), torch.randn(1, 2, N, generator=g)
+    print(f"narrow backward D={D} Dv={Dv} N={N}", flush=True)
+    leaves = [t.to(DEV).requires_grad_() for t in (q, k, v)]
+    o, e = flash_entropy_attention(*leaves)
+    grads = torch.autograd.grad((o.float() * do.to(DEV)).sum() + (e * de.to(DEV)).sum(), leaves)
+    refs = entropy_attention_grad(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                  do.bfloat16().float().numpy(), de.numpy(), D ** -0.5)
+    for gd, gr, t, name in zip(grads, refs, leaves, ("dq", "dk", "dv")):
+        assert gd.shape == t.shape and gd.dtype == t.dtype
+        assert_grad_close(gd.float().cpu().numpy(), gr, 3e-2, name)
+    assert hip_library_loaded()

@@ -130,9 +130,11 @@ template <class T, int W, int ROWS>
 struct BwdTileCopy {
   static constexpr int CH = W / 8;
   static constexpr int RPI = 64 / CH;
-  static constexpr int NI = ROWS / RPI / kBwdWaves;
+  static constexpr int TI = ROWS / RPI;   // copy instructions per tile: a narrow tile has fewer than the waves
+  static constexpr int NI = (TI + kBwdWaves - 1) / kBwdWaves;   // ... and waves wave < TI copy it
   static constexpr int NV = (kBwdWaves * RPI) % 16 == 0 ? 1 : 2;   // distinct lane offsets (swizzle period 16)
-  static_assert(CH >= 8 && NI >= 1 && RPI >= 2, "tile shape");
+  static_assert(CH >= 4 && TI >= 1 && RPI >= 2 && ROWS % RPI == 0 && (TI % kBwdWaves == 0 || TI < kBwdWaves),
+                "tile shape");
   uint64_t ubase, rbytes;
   uint32_t voff[NV];
   int wave, lane;
@@ -149,6 +151,7 @@ struct BwdTileCopy {
   __device__ __forceinline__ void issue(int row0, int nrows, uint32_t dst) const {
     uint64_t ub = ubase;
     asm volatile("" : "+s"(ub));   // recomputed per call: hoisted, the addresses would pin scalar registers
+    if (TI < kBwdWaves && wave >= TI) return;   // (wave-uniform)
     if (row0 + ROWS <= nrows) {
       const uint64_t tb = ub + (uint64_t)(row0 + wave * RPI) * rbytes;
 #pragma unroll
@@ -262,9 +265,11 @@ template <int D, int DV, bool W0K>
 constexpr int dkdv_v_width() { return W0K ? DV - D : DV; }
 template <int D, int DV, int PART, bool W0K>
 constexpr int dkdv_lds_bytes() {
-  return 2 * (kKvBM * (D + dkdv_do_width<DV, PART>()) * 2 + 512) +
-         (dkdv_v_in_lds<D, DV, PART>() ? kKvBN * dkdv_v_width<D, DV, W0K>() * 2 : 0) +
-         (dkdv_k_in_lds<D, DV, PART>() ? kKvBN * D * 2 : 0);
+  // (at least the four waves' epilogue patches: the narrow heads' stages are smaller)
+  constexpr int ring = 2 * (kKvBM * (D + dkdv_do_width<DV, PART>()) * 2 + 512) +
+                       (dkdv_v_in_lds<D, DV, PART>() ? kKvBN * dkdv_v_width<D, DV, W0K>() * 2 : 0) +
+                       (dkdv_k_in_lds<D, DV, PART>() ? kKvBN * D * 2 : 0);
+  return ring > kBwdWaves * kEpiPatchBytes ? ring : kBwdWaves * kEpiPatchBytes;
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -1034,6 +1039,7 @@ static int dispatch_bwd(const BwdParams& p, int d, int dv, hipStream_t s) {
     if (d == 128 && dv == 256) return launch_bwd<F16, 128, 256, true>(p, s);
     return set_error(VMO_ERR_UNSUPPORTED, "fea_bwd: no kernel for d=%d with values in two parts of %d", d, dv / 2);
   }
+  if (d == 32 && dv == 32) return launch_bwd<F16, 32, 32>(p, s);   // heads of at most 32 (16: zero-padded)
   if (d == 64 && dv == 64) return launch_bwd<F16, 64, 64>(p, s);
   if (d == 64 && dv == 128) return launch_bwd<F16, 64, 128>(p, s);
   if (d == 128 && dv == 64) return launch_bwd<F16, 128, 64>(p, s);
