@@ -143,8 +143,9 @@ typedef struct vmo_lstep_args {
  * VMO_BWD_FOLD_K: the values are k, or [k | v1] (v is k: same address and strides), as in the
  * VMonarch R-steps (vmonarch.py:50, where autograd sums k's two gradients).  grad_k then receives
  * k's whole gradient, key role plus value role, and grad_v only v1's (dv1 columns; with values k
- * alone grad_v is not written and may be null).  Built for (d, dv) = (64, 64), (128, 128) and, with
- * v1, (64, 128), (128, 256); other shapes, or values that do not start with k, are rejected. */
+ * alone grad_v is not written and may be null).  Built for (d, dv) = (32, 32), (64, 64), (128, 128) and,
+ * with v1, (32, 64), (64, 128), (128, 256); other shapes, or values that do not start with k, are
+ * rejected. */
 enum {
   VMO_BWD_ACCUM_Q = 1, VMO_BWD_ACCUM_K = 2, VMO_BWD_ACCUM_V = 4,
   VMO_BWD_F32_Q = 8, VMO_BWD_F32_K = 16, VMO_BWD_F32_V = 32,

@@ -8,7 +8,8 @@ import pytest
 import torch
 
 from conftest import assert_close_elementwise, assert_close_ref, assert_grad_close, hip_library_loaded, randn_lp
-from oracle import entropy_attention, entropy_attention_grad
+from oracle import entropy_attention, entropy_attention_grad, vmonarch_attention as vmonarch_oracle
+from oracle import vmonarch_attention_grad
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -110,4 +111,34 @@ def test_narrow_heads_backward(D, Dv, N):
     for gd, gr, t, name in zip(grads, refs, leaves, ("dq", "dk", "dv")):
         assert gd.shape == t.shape and gd.dtype == t.dtype
         assert_grad_close(gd.float().cpu().numpy(), gr, 3e-2, name)
+    assert hip_library_loaded()
+
+
+@pytest.mark.parametrize("m, b, rt", [(21, 100, 100), (8, 77, 30)])
+def test_vmonarch_head_dim_32_native(m, b, rt):
+    """VMonarch at D = Dv = 32 on the 32-wide flash-entropy kernels (R-steps with values k and [k | v], the
+    split-KV recompute) and the general L-step kernels, no padding: z and the gradients against the oracle
+    (reference metric 3e-2 / 5e-2 as tests/test_vmonarch.py:64-66, and elementwise)."""
+    import vmonarch_amd.vmonarch as vm
+    from vmonarch_amd import vmonarch_attention
+    g = torch.Generator().manual_seed(3000 + m + b)
+    q, k, v = (randn_lp(g, 1, 2, m * b, 32) for _ in range(3))
+    do = torch.randn(1, 2, m * b, 32, generator=g)
+    assert vm._fused_supported(q.to(DEV), k.to(DEV), v.to(DEV), m)
+    print(f"vmonarch D=32 m={m} b={b} rt={rt}", flush=True)
+    with torch.no_grad():
+        z = vmonarch_attention(q.to(DEV), k.to(DEV), v.to(DEV), m, b, 2, recompute_tokens=rt)
+    qn, kn, vn = (t.float().numpy() for t in (q, k, v))
+    z_ref = vmonarch_oracle(qn, kn, vn, m, b, 2, rt)
+    zz = z.float().cpu().numpy()
+    assert np.isfinite(zz).all()
+    assert_close_ref(zz, z_ref, 3e-2)
+    assert_close_elementwise(zz, z_ref)
+    leaves = [t.to(DEV).requires_grad_() for t in (q, k, v)]
+    zg = vmonarch_attention(*leaves, m, b, 2, recompute_tokens=rt)
+    assert type(zg.grad_fn).__name__ == "_VMonarchFunctionBackward"
+    grads = torch.autograd.grad((zg.float() * do.to(DEV)).sum(), leaves)
+    refs = vmonarch_attention_grad(qn, kn, vn, do.numpy(), m, b, 2, rt)
+    for gd, gr, name in zip(grads, refs, ("dq", "dk", "dv")):
+        assert_grad_close(gd.float().cpu().numpy(), gr, 5e-2, name)
     assert hip_library_loaded()

@@ -984,7 +984,8 @@ static int launch_bwd(const BwdParams& p, hipStream_t s) {
     if constexpr (bwd_ds_built<D>()) return launch_bwd_ds<F16, D, DV, W0K>(p, s);
     return set_error(VMO_ERR_UNSUPPORTED, "fea_bwd: no dS route for d=%d", D);
   }
-  constexpr int LDS_DQ = 2 * kDqBN * (D + dq_staged_dv<D, DV, W0K>()) * 2;
+  constexpr int RING_DQ = 2 * kDqBN * (D + dq_staged_dv<D, DV, W0K>()) * 2;
+  constexpr int LDS_DQ = RING_DQ > kBwdWaves * kEpiPatchBytes ? RING_DQ : kBwdWaves * kEpiPatchBytes;   // + patches
   static_assert(LDS_DQ <= 160 * 1024 && LDS_DQ >= kBwdWaves * kEpiPatchBytes, "bwd LDS");
   if (LDS_DQ > 65536) {
     static bool done = false;
@@ -1023,15 +1024,17 @@ static int launch_bwd(const BwdParams& p, hipStream_t s) {
 template <bool F16>
 static int dispatch_bwd(const BwdParams& p, int d, int dv, hipStream_t s) {
   if (p.v1 && p.v0_is_k) {   // values [k | v1]
+    if (d == 32 && dv == 64) return launch_bwd<F16, 32, 64, true, true>(p, s);
     if (d == 64 && dv == 128) return launch_bwd<F16, 64, 128, true, true>(p, s);
     if (d == 128 && dv == 256) return launch_bwd<F16, 128, 256, true, true>(p, s);
   } else if (p.v0_is_k) {   // values k (VMonarch's R-steps before the last, vmonarch.py:50)
+    if (d == 32 && dv == 32) return launch_bwd<F16, 32, 32, false, true>(p, s);
     if (d == 64 && dv == 64) return launch_bwd<F16, 64, 64, false, true>(p, s);
     if (d == 128 && dv == 128) return launch_bwd<F16, 128, 128, false, true>(p, s);
   }
   if (p.fold_k)
-    return set_error(VMO_ERR_UNSUPPORTED, "fea_bwd: VMO_BWD_FOLD_K is built for values k with (d, dv) = (64, 64), "
-                     "(128, 128) and values [k | v1] with (64, 128), (128, 256); got d=%d dv=%d", d, dv);
+    return set_error(VMO_ERR_UNSUPPORTED, "fea_bwd: VMO_BWD_FOLD_K is built for values k with (d, dv) = (32, 32), (64, 64), "
+                     "(128, 128) and values [k | v1] with (32, 64), (64, 128), (128, 256); got d=%d dv=%d", d, dv);
   if (p.v1 && p.v0_is_k) {
     return set_error(VMO_ERR_UNSUPPORTED, "fea_bwd: no kernel for d=%d with values [k | v1] of %d", d, dv);
   } else if (p.v1) {   // values in two halves (the caller checked dv1 = dv / 2)
@@ -1136,10 +1139,11 @@ extern "C" int vmo_fea_bwd(const vmo_fea_bwd_args* a, void* stream) {
     return set_error(VMO_ERR_INVALID, "fea_bwd: VMO_BWD_FOLD_K needs values that start with k (v is k: same address "
                      "and strides, dv - dv1 = d)");
   // shapes with a fold kernel (dispatch_bwd): rejected here, before any pointer is looked at further
-  if (fold_k && !(a->dv1 == 0 ? ((a->d == 64 && a->dv == 64) || (a->d == 128 && a->dv == 128))
-                              : ((a->d == 64 && a->dv == 128) || (a->d == 128 && a->dv == 256))))
-    return set_error(VMO_ERR_UNSUPPORTED, "fea_bwd: VMO_BWD_FOLD_K is built for values k with (d, dv) = (64, 64), "
-                     "(128, 128) and values [k | v1] with (64, 128), (128, 256); got d=%d dv=%d", a->d, a->dv);
+  if (fold_k && !(a->dv1 == 0 ? ((a->d == 32 || a->d == 64 || a->d == 128) && a->dv == a->d)
+                              : ((a->d == 32 || a->d == 64 || a->d == 128) && a->dv == 2 * a->d)))
+    return set_error(VMO_ERR_UNSUPPORTED, "fea_bwd: VMO_BWD_FOLD_K is built for values k with (d, dv) = (32, 32), "
+                     "(64, 64), (128, 128) and values [k | v1] with (32, 64), (64, 128), (128, 256); got d=%d dv=%d",
+                     a->d, a->dv);
   if (!(a->sm_scale >= 0.f)) return set_error(VMO_ERR_INVALID, "fea_bwd: sm_scale");
   // the tile copies address up to 7 rows from a lane with a 32-bit byte offset
   const int64_t kMaxRowStride = 1ll << 27;

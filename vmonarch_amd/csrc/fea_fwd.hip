@@ -661,7 +661,7 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
 
   // the stage ring is free (every wave passed the barrier above): each wave's 4 KB patch for the
   // row-segment stores of o
-  static_assert(NSLOT * STAGE >= WAVES * kEpiPatchBytes, "epilogue patches");
+  // (the launch allocates at least the patches: the narrow heads' rings are smaller)
   VMO_LDS float* patch = (VMO_LDS float*)(smem + wave * kEpiPatchBytes);
   if (!wave_live) return;
 
@@ -820,7 +820,8 @@ __global__ __launch_bounds__(256) void fea_fp8_keys_kernel(FwdParams p) {
 template <bool F16, int D, int DW0, int DW1, bool W0K, int ENT, bool SPLIT, int WAVES, bool QK8 = false>
 static int launch_fwd(FwdParams p, hipStream_t stream) {
   constexpr int STAGE = fwd_stage_bytes<D, DW0, DW1, W0K, QK8>();
-  constexpr int LDS = fwd_slots(STAGE, WAVES) * STAGE;
+  constexpr int LDS = fwd_slots(STAGE, WAVES) * STAGE > WAVES * kEpiPatchBytes ? fwd_slots(STAGE, WAVES) * STAGE
+                                                                              : WAVES * kEpiPatchBytes;
   constexpr int BM = 32 * kFwdQB * WAVES;
   p.q_tiles = (p.nq + BM - 1) / BM;
   p.total_wg = p.problems * p.splits * p.q_tiles;
@@ -883,6 +884,8 @@ static int dispatch_fwd(const FwdParams& p, int d, int dw0, int dw1, bool w0k, b
   VMO_FWD(128, 256, 0, false, kEntOnline, false)
   VMO_FWD(256, 256, 0, false, kEntOnline, false)
   // VMonarch R-step (vmonarch.py:50): values k, or [k | v]; entropy from the P.K accumulator
+  VMO_FWD(32, 32, 0, true, kEntFromPK, false)
+  VMO_FWD(32, 32, 32, true, kEntFromPK, false)
   VMO_FWD(64, 64, 0, true, kEntFromPK, false)
   VMO_FWD(64, 64, 64, true, kEntFromPK, false)
   VMO_FWD(64, 64, 128, true, kEntFromPK, false)
@@ -894,6 +897,7 @@ static int dispatch_fwd(const FwdParams& p, int d, int dw0, int dw1, bool w0k, b
   VMO_FWD(64, 128, 0, false, kEntNone, false)
   VMO_FWD(128, 64, 0, false, kEntNone, false)
   VMO_FWD(128, 128, 0, false, kEntNone, false)
+  VMO_FWD(32, 32, 0, false, kEntNone, true)
   VMO_FWD(64, 64, 0, false, kEntNone, true)
   VMO_FWD(64, 128, 0, false, kEntNone, true)
   VMO_FWD(128, 64, 0, false, kEntNone, true)

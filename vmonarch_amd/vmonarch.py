@@ -128,8 +128,10 @@ def _lstep_supported(m, d, dv, bwd):
 
 def _fused_supported(q, k, v, num_blocks):
     D, Dv = q.shape[-1], v.shape[-1]
+    # flash-entropy kernels at 64 / 128 (either dim) or 32 / 32; 32-wide L-steps on the general kernels
     return (q.is_cuda and q.dtype in _lib.DTYPES and k.dtype == q.dtype and v.dtype == q.dtype
-            and D in (64, 128) and Dv in (64, 128) and _lstep_supported(num_blocks, D, Dv, False)
+            and ((D in (64, 128) and Dv in (64, 128)) or D == Dv == 32)
+            and _lstep_supported(num_blocks, D, Dv, False)
             and k.shape == q.shape and v.shape[:-1] == q.shape[:-1])
 
 
@@ -359,7 +361,9 @@ def _vmonarch_composed(q, k, v, num_blocks, block_size, num_iters, recompute_tok
 
 
 def _padded_width(D, Dv):
-    """The kernel width (64 or 128) that q, k and v can all be zero-padded to, or None."""
+    """The kernel width (32, 64 or 128) that q, k and v can all be zero-padded to, or None."""
+    if D <= 32 and Dv <= 32:
+        return 32
     w = max(64, D, Dv)
     return w if w in (64, 128) else None
 
@@ -405,7 +409,7 @@ def vmonarch_attention(q, k, v, num_blocks, block_size, num_iters=2, recompute_t
             return _vmonarch_fused(q, k, v, *args)
         if needs_graph and _hip_backward_supported(q, k, v, num_blocks):
             return _VMonarchFunction.apply(q, k, v, *args)
-        # Head dims the kernels do not take as they are (16, 32; or D != Dv with autograd): zero columns
+        # Head dims the kernels do not take as they are (16, mixes with 16 / 32, or D != Dv with autograd): zero columns
         # change neither q.k nor P.v, so q, k and v padded to one kernel width give z with zero columns
         # past Dv, with the softmax scale of the true D; autograd slices the padded gradients back.
         w = _padded_width(D, Dv)
