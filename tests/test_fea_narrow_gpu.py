@@ -142,3 +142,25 @@ def test_vmonarch_head_dim_32_native(m, b, rt):
     for gd, gr, name in zip(grads, refs, ("dq", "dk", "dv")):
         assert_grad_close(gd.float().cpu().numpy(), gr, 5e-2, name)
     assert hip_library_loaded()
+
+
+@pytest.mark.parametrize("D, Dv", [(32, 64), (32, 128), (64, 32), (128, 32), (16, 64), (16, 256), (32, 256)])
+def test_narrow_and_wide_head_mixes(D, Dv):
+    """A 32-wide (or 16-wide) dim with a wider one: the 32 / 64, 32 / 128, 64 / 32 and 128 / 32 kernels, and
+    32 / 256 through q, k zero-padded to 64; o, e and the gradients against the oracle."""
+    from vmonarch_amd import flash_entropy_attention
+    g = torch.Generator().manual_seed(4000 + D + 3 * Dv)
+    N = 333
+    q, k, v = randn_lp(g, 1, 2, N, D), randn_lp(g, 1, 2, N, D), randn_lp(g, 1, 2, N, Dv)
+    do, de = torch.randn(1, 2, N, Dv, generator=g), torch.randn(1, 2, N, generator=g)
+    print(f"head mix D={D} Dv={Dv}", flush=True)
+    leaves = [t.to(DEV).requires_grad_() for t in (q, k, v)]
+    o, e = flash_entropy_attention(*leaves)
+    qn, kn, vn = (t.float().numpy() for t in (q, k, v))
+    o_ref, e_ref = entropy_attention(qn, kn, vn, D ** -0.5)
+    _check(o.detach(), e.detach(), o_ref, e_ref)
+    grads = torch.autograd.grad((o.float() * do.to(DEV)).sum() + (e * de.to(DEV)).sum(), leaves)
+    refs = entropy_attention_grad(qn, kn, vn, do.bfloat16().float().numpy(), de.numpy(), D ** -0.5)
+    for gd, gr, t, name in zip(grads, refs, leaves, ("dq", "dk", "dv")):
+        assert gd.shape == t.shape
+        assert_grad_close(gd.float().cpu().numpy(), gr, 3e-2, name)

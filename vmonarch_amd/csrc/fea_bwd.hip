@@ -515,7 +515,7 @@ __global__ __launch_bounds__(256) void fea_bwd_prep_kernel(BwdParams p) {
     p.beta[row] = -dE * kLn2;
     return;
   }
-  static_assert(TPR >= 8 && TPR <= 64 && 64 % TPR == 0, "row lanes within one wave");
+  static_assert(TPR >= 2 && TPR <= 64 && 64 % TPR == 0, "row lanes within one wave");
   const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t rows = (int64_t)p.problems * p.nq;
   const int64_t row = gid / TPR;
@@ -1042,7 +1042,11 @@ static int dispatch_bwd(const BwdParams& p, int d, int dv, hipStream_t s) {
     if (d == 128 && dv == 256) return launch_bwd<F16, 128, 256, true>(p, s);
     return set_error(VMO_ERR_UNSUPPORTED, "fea_bwd: no kernel for d=%d with values in two parts of %d", d, dv / 2);
   }
-  if (d == 32 && dv == 32) return launch_bwd<F16, 32, 32>(p, s);   // heads of at most 32 (16: zero-padded)
+  if (d == 32 && dv == 32) return launch_bwd<F16, 32, 32>(p, s);   // 32-wide dims (16: zero-padded to 32)
+  if (d == 32 && dv == 64) return launch_bwd<F16, 32, 64>(p, s);
+  if (d == 32 && dv == 128) return launch_bwd<F16, 32, 128>(p, s);
+  if (d == 64 && dv == 32) return launch_bwd<F16, 64, 32>(p, s);
+  if (d == 128 && dv == 32) return launch_bwd<F16, 128, 32>(p, s);
   if (d == 64 && dv == 64) return launch_bwd<F16, 64, 64>(p, s);
   if (d == 64 && dv == 128) return launch_bwd<F16, 64, 128>(p, s);
   if (d == 128 && dv == 64) return launch_bwd<F16, 128, 64>(p, s);

@@ -875,6 +875,10 @@ static int dispatch_fwd(const FwdParams& p, int d, int dw0, int dw1, bool w0k, b
   // standalone flash_entropy_attention (kernel.py:384-402): online entropy (32 / 32 also takes 16-wide heads,
   // zero-padded by the caller)
   VMO_FWD(32, 32, 0, false, kEntOnline, false)
+  VMO_FWD(32, 64, 0, false, kEntOnline, false)
+  VMO_FWD(32, 128, 0, false, kEntOnline, false)
+  VMO_FWD(64, 32, 0, false, kEntOnline, false)
+  VMO_FWD(128, 32, 0, false, kEntOnline, false)
   VMO_FWD(32, 32, 0, false, kEntNone, false)
   VMO_FWD(64, 64, 0, false, kEntOnline, false)
   VMO_FWD(64, 128, 0, false, kEntOnline, false)

@@ -23,11 +23,14 @@ def _pad_features(t, width):
 
 
 def _kernel_widths(d, dv):
-    """Head dims of the forward kernel that serves (d, dv): 32 / 32 for heads of at most 32 (16 zero-padded to
-    32), else 64 / 128 (q, k) and 64 / 128 / 256 (values), narrower dims zero-padded to 64."""
-    if d <= 32 and dv <= 32:
-        return 32, 32
-    return (64 if d < 64 else d), (64 if dv < 64 else dv)
+    """Head dims of the flash-entropy kernels (forward and backward) that serve (d, dv): each dim of at most 32
+    runs 32 wide (16 zero-padded to 32), wider ones as they are (64, 128, 256); the 32 / 256 pair, which has
+    no kernel, takes q and k zero-padded to 64."""
+    w = lambda x: 32 if x <= 32 else x   # noqa: E731
+    dk, dvk = w(d), w(dv)
+    if dk == 32 and dvk == 256:
+        dk = 64
+    return dk, dvk
 
 
 def fea_forward(q, k, w0, w1, sm_scale, frames=1, o=None, lse=None, ent=None, want_ent=True, want_lse=True,

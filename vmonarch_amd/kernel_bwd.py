@@ -100,12 +100,10 @@ def fea_backward(q, k, v, o, lse, ent, do, de, sm_scale, n_valid):
     B, H, N, D = q.shape
     Dv = v.shape[-1]
     n = int(n_valid)
-    if D <= 32 and Dv <= 32:   # the 32-wide kernels (16-wide heads zero-padded to 32)
-        Dk = Dvk = 32
-    else:                      # narrower dims of a wider head zero-padded to 64
-        Dk = 64 if D < 64 else D
-        Dvk = 64 if Dv < 64 else Dv
-    if not ((Dk in (32, 64, 128) and Dvk in (32, 64, 128, 256)) or (Dk == 256 and Dvk == 256)):
+    from .kernel import _kernel_widths
+    Dk, Dvk = _kernel_widths(D, Dv)
+    if not ((Dk in (32, 64, 128) and Dvk in (32, 64, 128, 256) and (Dk, Dvk) != (32, 256))
+            or (Dk == 256 and Dvk == 256)):
         raise NotImplementedError(f"vmonarch_amd: backward for head dims ({D}, {Dv}) is not built")
     if de is None:
         de = torch.zeros((B, H, N), device=q.device, dtype=torch.float32)
