@@ -11,8 +11,9 @@ padding and softmax excluded) in the production launch order, where the exact re
 second stream beside the R/L chain.  `roofline` is the dominant kernel (the flash-entropy R-step
 launch with values [k | v]) and `kernels` every launch, timed with HIP events on the launch stream
 inside a second timed region that runs the same launches serially (each alone on the GPU);
-`ms_per_step_serial` is that region's step time.  `cpu_baseline` times the CPU oracle (numpy
-restatement of the reference) on a bounded sample of the same workload on this host.
+`ms_per_step_serial` is that region's step time.  `graph` times the production-order step replayed
+from a HIP graph (captured once; checked bit for bit against the eager step).  `cpu_baseline` times
+the CPU oracle (numpy restatement of the reference) on a bounded sample of the same workload on this host.
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--cpu-heads 2 | --no-cpu-baseline]
     python bench.py --copy-calibration     # a plain 1 GiB device copy, x5 (for HBM counter scaling)
@@ -252,6 +253,34 @@ def main():
                     per[s] += evs[(s, "begin")].elapsed_time(evs[(s, "end")]) / len(step_events)
         return ev0.elapsed_time(ev1) / args.steps, wall, per
 
+    def graph_region():
+        """The production-order step captured once in a HIP graph (torch.cuda.CUDAGraph; the recompute's
+        second stream joins the capture) and replayed `steps` times: the same launches without the host
+        issuing them one by one.  Checked bit for bit against the eager step."""
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                _vmonarch_fused(q, k, v, M, BS, ITERS, RT, mod.min_col_mass)
+        stream.wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            z_graph = _vmonarch_fused(q, k, v, M, BS, ITERS, RT, mod.min_col_mass)
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record(stream)
+        for _ in range(args.steps):
+            graph.replay()
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        if not torch.equal(z_graph, _vmonarch_fused(q, k, v, M, BS, ITERS, RT, mod.min_col_mass)):
+            raise RuntimeError("bench: the graph replay differs from the eager step")
+        del graph, z_graph
+        return ev0.elapsed_time(ev1) / args.steps
+
     with torch.no_grad():
         for _ in range(args.warmup):
             z_api = mod(q, k, v, recompute_tokens=RT)
@@ -283,6 +312,7 @@ def main():
                 ms8_serial, _, acc8 = timed_region("off", True, fp8=True)
         finally:
             vm._RECOMPUTE_OVERLAP = production_order
+        ms_graph = None if args.serial_only else graph_region()
 
     r_flops, l_flops, l_bytes, rec_flops = algorithmic_work()
     total_flops = sum(r_flops) + ITERS * l_flops + rec_flops
@@ -329,6 +359,9 @@ def main():
                      "all_rstep_frac": round(sum(r_flops) / fea_ms / 1e9 / PEAK_BF16_TFLOPS, 4)},
         "kernels": kernels,
     }
+    if ms_graph is not None:
+        result["graph"] = {"note": "the same production-order step replayed from a HIP graph (captured once); not `value`",
+                           "ms_per_step": round(ms_graph, 4), "tflops": round(total_flops / ms_graph / 1e9, 2)}
     if args.qk_fp8:
         result["qk_fp8"] = {
             "note": "opt-in mode beyond the reference: the R-steps' S = q k^T in fp8 e4m3 (per-row q, per-64-key-tile k "
