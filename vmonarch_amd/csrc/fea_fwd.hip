@@ -201,21 +201,22 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
   // accumulator blocks are short of registers: for them the extra scalar values cost more (their
   // spills land in the key loop) than the few vector instructions they save.
   struct Loc { int qt, split, prob, f, hh, bb; };
-  auto locate = [&](int lx, auto scalar_tag) __attribute__((always_inline)) {
+  struct Div { int q_tiles, splits, frames, heads; };
+  auto locate = [&](int lx, const Div& dv, auto scalar_tag) __attribute__((always_inline)) {
     constexpr bool S = decltype(scalar_tag)::value;
     auto u = [](int v) __attribute__((always_inline)) { return S ? __builtin_amdgcn_readfirstlane(v) : v; };
     Loc r;
-    r.qt = u(lx % p.q_tiles);
-    const int rest = lx / p.q_tiles;
-    r.split = u(rest % p.splits);
-    r.prob = u(rest / p.splits);
-    r.f = u(r.prob % p.frames);
-    const int bh = r.prob / p.frames;
-    r.hh = u(bh % p.heads);
-    r.bb = u(bh / p.heads);
+    r.qt = u(lx % dv.q_tiles);
+    const int rest = lx / dv.q_tiles;
+    r.split = u(rest % dv.splits);
+    r.prob = u(rest / dv.splits);
+    r.f = u(r.prob % dv.frames);
+    const int bh = r.prob / dv.frames;
+    r.hh = u(bh % dv.heads);
+    r.bb = u(bh / dv.heads);
     return r;
   };
-  const Loc loc = locate(L, std::integral_constant<bool, (NA < 8)>{});
+  const Loc loc = locate(L, Div{p.q_tiles, p.splits, p.frames, p.heads}, std::integral_constant<bool, (NA < 8)>{});
   const int qt = loc.qt, split = loc.split, f = loc.f, hh = loc.hh, bb = loc.bb;
 
   const T* qb = (const T*)p.q + bb * p.q_sb + hh * p.q_sh + (int64_t)f * p.nq * p.q_sn;
@@ -698,9 +699,12 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
   // The epilogue derives its indices and row bases again, from an opaque copy of the block's logical
   // index (scalar registers are free by now): kept from the prologue, the 64-bit bases sat in vector
   // registers across the whole key loop, and the tightest variants spilled them to scratch.
+  // The divisors are opaque copies too: the division's reciprocal (a vector value) would otherwise be kept
+  // from the prologue, and the [k | v] variant spilled it across the loop.
   int l_epi = __builtin_amdgcn_readfirstlane(L);
-  asm volatile("" : "+s"(l_epi));
-  const Loc le = locate(l_epi, std::true_type{});
+  Div d_epi{p.q_tiles, p.splits, p.frames, p.heads};
+  asm volatile("" : "+s"(l_epi), "+s"(d_epi.q_tiles), "+s"(d_epi.splits), "+s"(d_epi.frames), "+s"(d_epi.heads));
+  const Loc le = locate(l_epi, d_epi, std::true_type{});
   T* const ob = (T*)p.o + le.bb * p.o_sb + le.hh * p.o_sh + (int64_t)le.f * p.nq * p.o_sn;
   const int64_t o_sn = p.o_sn;
   const int64_t st0 = le.bb * p.st_sb + le.hh * p.st_sh + (int64_t)le.f * p.nq;
