@@ -164,3 +164,43 @@ def test_narrow_and_wide_head_mixes(D, Dv):
     for gd, gr, t, name in zip(grads, refs, leaves, ("dq", "dk", "dv")):
         assert gd.shape == t.shape
         assert_grad_close(gd.float().cpu().numpy(), gr, 3e-2, name)
+
+
+@pytest.mark.parametrize("D, Dv", [(32, 32), (32, 64), (64, 32)])
+def test_narrow_heads_backward_fp16(D, Dv):
+    """fp16 through the 32-wide dq and dk/dv kernels (and a mix with a 64-wide dim)."""
+    from vmonarch_amd import flash_entropy_attention
+    g = torch.Generator().manual_seed(5000 + D + Dv)
+    N = 300
+    q, k, v = (randn_lp(g, 1, 2, N, d, dtype=torch.float16) for d in (D, D, Dv))
+    do, de = torch.randn(1, 2, N, Dv, generator=g), torch.randn(1, 2, N, generator=g)
+    leaves = [t.to(DEV).requires_grad_() for t in (q, k, v)]
+    o, e = flash_entropy_attention(*leaves)
+    assert o.dtype == torch.float16
+    grads = torch.autograd.grad((o.float() * do.to(DEV)).sum() + (e * de.to(DEV)).sum(), leaves)
+    refs = entropy_attention_grad(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                  do.half().float().numpy(), de.numpy(), D ** -0.5)
+    for gd, gr, t, name in zip(grads, refs, leaves, ("dq", "dk", "dv")):
+        assert gd.dtype == torch.float16
+        assert_grad_close(gd.float().cpu().numpy(), gr, 3e-2, name)
+
+
+def test_vmonarch_head_dim_32_fp16():
+    """VMonarch at D = Dv = 32 in fp16, forward and gradients."""
+    from vmonarch_amd import vmonarch_attention
+    g = torch.Generator().manual_seed(5100)
+    m, b, rt = 8, 100, 100
+    q, k, v = (randn_lp(g, 1, 2, m * b, 32, dtype=torch.float16) for _ in range(3))
+    do = torch.randn(1, 2, m * b, 32, generator=g)
+    leaves = [t.to(DEV).requires_grad_() for t in (q, k, v)]
+    z = vmonarch_attention(*leaves, m, b, 2, recompute_tokens=rt)
+    assert z.dtype == torch.float16 and type(z.grad_fn).__name__ == "_VMonarchFunctionBackward"
+    qn, kn, vn = (t.float().numpy() for t in (q, k, v))
+    zz = z.detach().float().cpu().numpy()
+    z_ref = vmonarch_oracle(qn, kn, vn, m, b, 2, rt)
+    assert_close_ref(zz, z_ref, 3e-2)
+    assert_close_elementwise(zz, z_ref)
+    grads = torch.autograd.grad((z.float() * do.to(DEV)).sum(), leaves)
+    refs = vmonarch_attention_grad(qn, kn, vn, do.numpy(), m, b, 2, rt)
+    for gd, gr, name in zip(grads, refs, ("dq", "dk", "dv")):
+        assert_grad_close(gd.float().cpu().numpy(), gr, 5e-2, name)
