@@ -1,0 +1,67 @@
+"""Seeded random VMonarch shapes against the CPU oracle: frames m (one-tile and general L-steps), block sizes,
+head dims 32 / 64 / 128 (and D != Dv), 1-3 iterations, recompute rows, bf16 and fp16, contiguous and
+(B, N, H, D)-strided inputs; z, and with autograd the gradients, through the HIP path (no composed-path
+warning).  Tolerances as tests/test_vmonarch.py:64-66 (z 3e-2, gradients 5e-2) beside elementwise
+2e-2 + 1e-2 |ref| for z."""
+import warnings
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close_elementwise, assert_close_ref, assert_grad_close, hip_library_loaded, randn_lp
+from oracle import vmonarch_attention as vmonarch_oracle
+from oracle import vmonarch_attention_grad
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+DIMS = [(32, 32), (64, 64), (128, 128), (64, 128), (128, 64)]
+
+
+def _case(seed):
+    rng = np.random.default_rng(seed)
+    D, Dv = DIMS[seed % len(DIMS)]
+    m = int(rng.choice([2, 3, 5, 8, 13, 21, 32, 40]))
+    b = int(rng.integers(8, 97))
+    iters = int(rng.integers(1, 4))
+    rt = int(rng.choice([0, b, int(rng.integers(1, b + 1))]))
+    dtype = torch.float16 if rng.random() < 0.3 else torch.bfloat16
+    dit = bool(rng.random() < 0.4)
+    return D, Dv, m, b, iters, rt, dtype, dit
+
+
+@pytest.mark.parametrize("seed", range(14))
+def test_fuzz_vmonarch(seed):
+    from vmonarch_amd import vmonarch_attention
+    D, Dv, m, b, iters, rt, dtype, dit = _case(seed)
+    g = torch.Generator().manual_seed(seed)
+    B, H, N = 1, 2, m * b
+
+    def tensor(d):
+        t = randn_lp(g, B, N, H, d, dtype=dtype) if dit else randn_lp(g, B, H, N, d, dtype=dtype)
+        t = t.to(DEV)
+        return t.transpose(1, 2) if dit else t
+
+    q, k, v = tensor(D), tensor(D), tensor(Dv)
+    do = torch.randn(B, H, N, Dv, generator=g)
+    print(f"fuzz vmonarch seed={seed} D={D} Dv={Dv} m={m} b={b} iters={iters} rt={rt} {dtype} dit={dit}", flush=True)
+    qn, kn, vn = (t.float().cpu().numpy() for t in (q, k, v))
+    z_ref = vmonarch_oracle(qn, kn, vn, m, b, iters, rt)
+    with warnings.catch_warnings():
+        warnings.simplefilter("error", RuntimeWarning)   # the composed path warns: it must not be taken
+        with torch.no_grad():
+            z = vmonarch_attention(q, k, v, m, b, iters, recompute_tokens=rt)
+        zz = z.float().cpu().numpy()
+        assert np.isfinite(zz).all()
+        assert_close_ref(zz, z_ref, 3e-2)
+        assert_close_elementwise(zz, z_ref)
+        leaves = [t.detach().requires_grad_() for t in (q, k, v)]
+        zg = vmonarch_attention(*leaves, m, b, iters, recompute_tokens=rt)
+    if D == Dv:   # the same kernels with and without autograd (D != Dv pads to one width for the backward)
+        assert torch.equal(zg.detach(), z)
+    grads = torch.autograd.grad((zg.float() * do.to(DEV)).sum(), leaves)
+    refs = vmonarch_attention_grad(qn, kn, vn, do.numpy(), m, b, iters, rt)
+    for gd, gr, t, name in zip(grads, refs, leaves, ("dq", "dk", "dv")):
+        assert gd.shape == t.shape and gd.dtype == t.dtype
+        assert_grad_close(gd.float().cpu().numpy(), gr, 5e-2, name)
+    assert hip_library_loaded()
