@@ -370,13 +370,19 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
 #pragma unroll
       for (int j = 0; j < QB; ++j) x[j] = E::mfma(a[ds], qf[j][ds], x[j]);
     if constexpr (decltype(sched_tag)::value) {
+      constexpr int NV = int(decltype(sched_tag)::value) - 1;
       __builtin_amdgcn_sched_group_barrier(0x100, kPre, 0);
 #pragma unroll
       for (int ds = 0; ds < NDS - kPre; ++ds) {
         __builtin_amdgcn_sched_group_barrier(0x008, QB, 0);
+        if constexpr (NV > 0) __builtin_amdgcn_sched_group_barrier(0x402, NV, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
-      __builtin_amdgcn_sched_group_barrier(0x008, QB * kPre, 0);
+#pragma unroll
+      for (int ds = 0; ds < kPre; ++ds) {
+        __builtin_amdgcn_sched_group_barrier(0x008, QB, 0);
+        if constexpr (NV > 0) __builtin_amdgcn_sched_group_barrier(0x402, NV, 0);
+      }
     }
   };
 
@@ -461,14 +467,20 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
 #pragma unroll
         for (int j = 0; j < QB; ++j) acc[j][a0 + a] = E::mfma(wt[2 * a + h2], P[j][h2], acc[j][a0 + a]);
     if constexpr (decltype(sched_tag)::value) {
+      constexpr int NV = int(decltype(sched_tag)::value) - 1;
       constexpr int kPreOps = 2;
       __builtin_amdgcn_sched_group_barrier(0x100, 2 * kPreOps, 0);
 #pragma unroll
       for (int o = 0; o < NOP - kPreOps; ++o) {
         __builtin_amdgcn_sched_group_barrier(0x008, QB, 0);
+        if constexpr (NV > 0) __builtin_amdgcn_sched_group_barrier(0x402, NV, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
       }
-      __builtin_amdgcn_sched_group_barrier(0x008, QB * kPreOps, 0);
+#pragma unroll
+      for (int o = 0; o < kPreOps; ++o) {
+        __builtin_amdgcn_sched_group_barrier(0x008, QB, 0);
+        if constexpr (NV > 0) __builtin_amdgcn_sched_group_barrier(0x402, NV, 0);
+      }
     }
   };
   auto pv_block = [&](const VMO_LDS char* Ks, int kb2, const V8 (&P)[QB][2], auto sched_tag)
@@ -480,9 +492,9 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
               kb2, P, sched_tag);
   };
 
-  // One 64-key stage, as two 32-key blocks in sequence: S(kb) -> softmax(kb) -> PV(kb).  Only one
-  // block's logits and P are live at a time (the [k | v] variant holds 128 accumulator registers);
-  // the second wave on the SIMD (another workgroup) overlaps its MFMAs with this wave's softmax.
+  // One 64-key stage, as two 32-key blocks in sequence: S(kb) -> softmax(kb) -> PV(kb), with one
+  // block's logits and P live at a time: the partial last tile, and the 256-wide value tensors (more
+  // than eight accumulator blocks), whose softmax only the second wave on the SIMD overlaps.
   auto stage = [&](const VMO_LDS char* Ks, int nvalid, auto masked_tag, auto hi_tag) __attribute__((always_inline)) {
     constexpr bool HI = decltype(hi_tag)::value;
 #pragma unroll
@@ -498,18 +510,27 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
   // A full 64-key stage with the two 32-key blocks software-pipelined inside the wave: the S MFMAs
   // of block 1 are independent of the softmax of block 0, and the P.V MFMAs of block 0 of the
   // softmax of block 1, so the scheduler can interleave each pair (sched_barrier keeps the three
-  // regions apart).  Needs one more S and P block live, so it is used where the accumulators leave
-  // room (at most four accumulator blocks).
-  constexpr bool kPipe = NA <= 4;
+  // regions apart).  Needs one more S and P block live: up to eight accumulator blocks.  With more
+  // than four ([k | v] values, 128 accumulator registers) the compiler, left to itself, hoists the
+  // overlapped regions' operand reads and spills; pinned instead, each MFMA of S block 1 is followed
+  // by 9 softmax instructions of block 0 and each of P.V block 0 by 5 of block 1 (about 72 vector
+  // instructions per softmax block), with the operand reads two ahead: no spills, and R-step 1
+  // ~1% faster than the sequential stage (the interleave counts 5/3 and 14/8 and three reads
+  // ahead measured the same).
+  constexpr bool kPipe = NA <= 8;
+  constexpr bool kPipeSched = NA > 4;
+  constexpr int kSchQk = 9, kSchPv = 5;
   auto stage_pipe = [&](const VMO_LDS char* Ks) __attribute__((always_inline)) {
     f32x16 x0[QB], x1[QB];
     V8 P0[QB][2], P1[QB][2];
     qk_block(Ks, 0, x0, std::true_type{});
     __builtin_amdgcn_sched_barrier(0);
-    qk_block(Ks, 1, x1, std::false_type{});
+    if constexpr (kPipeSched) qk_block(Ks, 1, x1, std::integral_constant<int, 1 + kSchQk>{});
+    else qk_block(Ks, 1, x1, std::false_type{});
     softmax_block(x0, P0, 0, kFwdBN, std::false_type{});
     __builtin_amdgcn_sched_barrier(0);
-    pv_block(Ks, 0, P0, std::false_type{});
+    if constexpr (kPipeSched) pv_block(Ks, 0, P0, std::integral_constant<int, 1 + kSchPv>{});
+    else pv_block(Ks, 0, P0, std::false_type{});
     softmax_block(x1, P1, 32, kFwdBN, std::false_type{});
     __builtin_amdgcn_sched_barrier(0);
     pv_block(Ks, 1, P1, std::true_type{});
