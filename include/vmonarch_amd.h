@@ -65,9 +65,11 @@ typedef struct vmo_view {
  * ent / lse may be NULL.  num_splits > 1 splits the keys of each problem into num_splits
  * ranges (split-KV, for problems with few query tiles such as the recompute of
  * vmonarch.py:66-68); it needs ent == NULL and a workspace of
- * vmo_fea_fwd_workspace_size() bytes.  Supported: d in {64, 128} with dw0 in {64, 128, 256}, and d = dw0 = 256
- * (entropy output, no split);
- * dw1 in {0, 64, 128} (dw1 > 0 only with w0 aliasing k); sm_scale >= 0.
+ * vmo_fea_fwd_workspace_size() bytes.  Supported (d, dw0): with entropy output and one split, d in {64, 128}
+ * with dw0 in {64, 128, 256}, (256, 256), and the 32-wide (32, 32), (32, 64), (32, 128), (64, 32), (128, 32);
+ * without entropy, one split or several, (32, 32), (64, 64), (64, 128), (128, 64), (128, 128).  Values that
+ * start with k (w0 aliasing k, entropy, one split): d = dw0 in {32, 64, 128} with dw1 in {0, d}, and
+ * dw1 = 128 at d = 64, dw1 = 64 at d = 128.  sm_scale >= 0.
  */
 typedef struct vmo_fea_fwd_args {
   int32_t dtype;
@@ -135,7 +137,8 @@ typedef struct vmo_lstep_args {
  *   grad_q = sm_scale dS k,  grad_k = sm_scale dS^T q,  grad_v = P^T grad_o
  * with P rebuilt from `lse` (log2 units, as written by vmo_fea_fwd).  nq queries attend to nk
  * keys per (batch, head) (nq != nk allowed).  Supported: d in {64, 128} with dv in {64, 128, 256},
- * and d = dv = 256.  Needs vmo_fea_bwd_workspace_size() bytes of workspace.
+ * d = dv = 256, and the 32-wide (32, 32), (32, 64), (32, 128), (64, 32), (128, 32).  Needs
+ * vmo_fea_bwd_workspace_size() bytes of workspace.
  */
 /* vmo_fea_bwd_args.flags: the marked gradient is float32 and the kernels add into it (+=, ACCUM) or
  * overwrite it (=, F32); without either bit it has the inputs' dtype.  ACCUM and F32 of the same
