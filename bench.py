@@ -15,7 +15,7 @@ inside a second timed region that runs the same launches serially (each alone on
 from a HIP graph (captured once; checked bit for bit against the eager step).  `cpu_baseline` times
 the CPU oracle (numpy restatement of the reference) on a bounded sample of the same workload on this host.
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--cpu-heads 2 | --no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--cpu-heads 6 | --no-cpu-baseline]
     python bench.py --copy-calibration     # a plain 1 GiB device copy, x5 (for HBM counter scaling)
     python bench.py --serial-only ...      # only the serial-order region (what kernel traces use)
 
@@ -179,7 +179,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--cpu-heads", type=int, default=2)
+    ap.add_argument("--cpu-heads", type=int, default=6)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--no-backward", action="store_true",
