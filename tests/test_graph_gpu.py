@@ -21,14 +21,15 @@ def _warm(fn):
     torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("m, b, D, rt", [(4, 256, 64, 256), (21, 120, 128, 120)])
-def test_vmonarch_forward_replays_from_a_graph(m, b, D, rt):
+@pytest.mark.parametrize("m, b, D, rt, dtype", [(4, 256, 64, 256, torch.bfloat16), (21, 120, 128, 120, torch.bfloat16),
+                                                (8, 100, 32, 100, torch.bfloat16), (21, 120, 128, 60, torch.float16)])
+def test_vmonarch_forward_replays_from_a_graph(m, b, D, rt, dtype):
     from vmonarch_amd import vmonarch_attention
     g = torch.Generator().manual_seed(31 + m + D)
-    q, k, v = (randn_lp(g, 1, 2, m * b, D, scale=0.5).to(DEV) for _ in range(3))
-    inputs = [[randn_lp(g, 1, 2, m * b, D, scale=0.5).to(DEV) for _ in range(3)] for _ in range(3)]
+    q, k, v = (randn_lp(g, 1, 2, m * b, D, scale=0.5, dtype=dtype).to(DEV) for _ in range(3))
+    inputs = [[randn_lp(g, 1, 2, m * b, D, scale=0.5, dtype=dtype).to(DEV) for _ in range(3)] for _ in range(3)]
     run = lambda: vmonarch_attention(q, k, v, m, b, 2, recompute_tokens=rt)   # noqa: E731
-    print(f"graph vmonarch m={m} b={b} D={D}", flush=True)
+    print(f"graph vmonarch m={m} b={b} D={D} rt={rt} {dtype}", flush=True)
     with torch.no_grad():
         _warm(run)
         graph = torch.cuda.CUDAGraph()
