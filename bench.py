@@ -89,9 +89,12 @@ def cpu_baseline(heads, repeats=3):
     r, l_flops, _, rec = algorithmic_work()
     flops = (sum(r) + ITERS * l_flops + rec) * heads / H
     return {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "implementation": "numpy restatement (oracle/, float32) of the reference's pure-PyTorch fp32 path "
+                              "(tests/test_vmonarch.py:12-15 as the R-step of vmonarch.py:29-69); not torch itself",
             "ms_full_workload": round(t * H / heads * 1e3, 1),
-            "sample": f"{heads} of {H} heads of the north-star workload (heads are independent), oracle/ numpy "
-                      f"float32 on {cores} threads, median of {repeats} after a 2-frame warm-up; {t:.2f} s per run",
+            "sample": f"numpy restatement: {heads} of {H} heads of the north-star workload (heads are independent), "
+                      f"oracle/ numpy float32 on {cores} threads, median of {repeats} after a 2-frame warm-up; "
+                      f"{t:.2f} s per run",
             "cfg1": {"workload": "flash_entropy_attention forward (1, 2, 1024, 64) fp32, BASELINE configs[0]",
                      "ms": round(t1 * 1e3, 3), "gflops": round(f1 / t1 / 1e9, 2), "cores": cores}}
 

@@ -161,10 +161,12 @@ enum {
   /* Route for grad_q, results within rounding of each other.  Recompute route: a dq pass recomputes S
    * and dP.  dS route: the dkdv pass stores dS^T (16-bit, nk and nq rounded up to 32, per problem) in
    * the workspace and grad_q = sm_scale dS k is a GEMM over it -- no second S and dP, 4 bytes of HBM
-   * traffic per query-key pair instead.  By default the dS route is taken for d = 128 with dv = 256
-   * (where the recompute is dearest) while dS^T of all problems stays within 4 GiB;
-   * VMO_BWD_RECOMPUTE_DQ never takes it, VMO_BWD_DS_DQ takes it for any d in {64, 128} (not both).
-   * vmo_fea_bwd_workspace_size() includes the dS^T bytes when the route is taken. */
+   * traffic per query-key pair instead.  Its workspace is 2 bytes per query-key pair (the recompute
+   * route needs O(nq)), so by default it is taken only for d = 128 with dv = 256 (where the recompute
+   * is dearest) on short problems -- nq and nk at most 4096, the VMonarch R-step's frames -- while dS^T
+   * of all problems stays within 2 GiB; a long standalone backward stays on the recompute route.
+   * VMO_BWD_RECOMPUTE_DQ never takes it, VMO_BWD_DS_DQ takes it at any size for d in {64, 128} (not
+   * both).  vmo_fea_bwd_workspace_size() includes the dS^T bytes when the route is taken. */
   VMO_BWD_RECOMPUTE_DQ = 512, VMO_BWD_DS_DQ = 1024,
   /* grad_q in the inputs' dtype = grad_q_base (fp32, shaped like grad_q) + this call's gradient, as
    * VMO_BWD_SUM_K / _V.  Not with ACCUM_Q / F32_Q. */
@@ -273,6 +275,10 @@ int vmo_fea_fwd(const vmo_fea_fwd_args* args, void* stream);
  * VMO_ERR_WORKSPACE before any launch; calls with num_splits <= 1 and qk_fp8 = 0 use no scratch.  The call allocates nothing and calls no
  * allocating routine.  All calls on one GPU share its scratch: calls that overlap in time on one GPU
  * (different streams without ordering, or several host threads) race; order them on one stream.
+ * Set-up: the first call on a device looks up the scratch's device address (hipGetSymbolAddress, which
+ * may load the library's code object and its scratch on that device).  Make that first call outside any
+ * graph capture -- one uncaptured call per device (any arguments, e.g. an empty problem) -- and every
+ * later call, captured or not, launches its kernels only.
  */
 #define VMO_FEA_FWD_SCRATCH_BYTES (32u << 20)
 int vmo_fea_fwd_noalloc(const vmo_fea_fwd_args* args, void* stream);

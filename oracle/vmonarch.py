@@ -98,7 +98,7 @@ def round_bf16(x):
 
 
 def vmonarch_attention_lowp(q, k, v, num_blocks, block_size, num_iters=2, recompute_tokens=0,
-                            min_col_mass=0.01, rnd=round_bf16):
+                            min_col_mass=0.01, rnd=round_bf16, keep_fp32=()):
     """vmonarch.py:29-69 as the reference runs it on bf16 tensors: every tensor the glue stores in the
     input dtype is rounded by ``rnd`` where the reference makes it (einsum / product results rounded once,
     accumulation in float64 here), the softmaxes and col_mass in float, and the R-step exact (its output o
@@ -111,6 +111,9 @@ def vmonarch_attention_lowp(q, k, v, num_blocks, block_size, num_iters=2, recomp
       u = einsum(attn.to(dtype), q)          (vmonarch.py:62)  attn rounded, u rounded
       u = u * (scale / col_mass).to(dtype)   (vmonarch.py:63)  factor rounded, product rounded
       SDPA(q[:, :, :rt], k, v)               (vmonarch.py:67)  exact, rounded
+    ``keep_fp32`` names cast points to skip ("u0": the first u, "kr", "logits"): with all three the glue
+    rounds where the HIP kernels round (they fold q * scale and out * scale into their fp32 softmax factors
+    and keep the L-step logits in fp32), the reference's path minus those three roundings.
     """
     q, k, v = (rnd(t) for t in (q, k, v))
     B, H, N, D = q.shape
@@ -119,15 +122,19 @@ def vmonarch_attention_lowp(q, k, v, num_blocks, block_size, num_iters=2, recomp
     scale = D ** -0.5
     m, b = num_blocks, block_size
     qg, kg, vg = (t.reshape(B, H, m, b, t.shape[-1]) for t in (q, k, v))
-    u = rnd(qg * scale)
+    unknown = set(keep_fp32) - {"u0", "kr", "logits"}
+    if unknown:
+        raise ValueError(f"keep_fp32: unknown cast points {sorted(unknown)}")
+    keep = lambda name, x: x if name in keep_fp32 else rnd(x)   # noqa: E731
+    u = keep("u0", qg * scale)
     z = None
     for it in range(num_iters):
         last = it == num_iters - 1
         w = np.concatenate([kg, vg], -1) if last else kg
         out, ent = entropy_attention(u, kg, w, 1.0)
         out = rnd(out)
-        kr = rnd(out[..., :D] * scale)
-        logits = rnd(np.einsum("bhijd,bhkjd->bhjik", qg, kr))
+        kr = keep("kr", out[..., :D] * scale)
+        logits = keep("logits", np.einsum("bhijd,bhkjd->bhjik", qg, kr))
         attn = _softmax(logits + np.swapaxes(ent, -1, -2)[..., None, :])   # - neg_ent
         if last:
             z = rnd(np.einsum("bhjik,bhkjd->bhijd", rnd(attn), out[..., D:]))

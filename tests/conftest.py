@@ -54,6 +54,13 @@ def assert_close_elementwise(x, ref, atol=2e-2, rtol=1e-2):
     np.testing.assert_allclose(np.asarray(x, dtype=np.float64), np.asarray(ref, dtype=np.float64), atol=atol, rtol=rtol)
 
 
+def elementwise_margin(x, ref, atol=2e-2, rtol=1e-2):
+    """max |x - ref| / (atol + rtol |ref|): the elementwise class holds where this is <= 1."""
+    x = np.asarray(x, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    return float((np.abs(x - ref) / (atol + rtol * np.abs(ref))).max())
+
+
 def assert_grad_close(g, ref, ref_tol, name=""):
     """Gradient parity: the reference metric (tests/test_vmonarch.py:22-24) with the reference's own
     gradient tolerance `ref_tol` AND the stated bf16 class elementwise, |g - ref| <= 2e-2 + 1e-2 |ref|

@@ -272,6 +272,28 @@ def test_fea_bwd_workspace_holds_ds_for_the_ds_route(L):
     assert capped == L.vmo_fea_bwd_workspace_size(ctypes.byref(a))
 
 
+@pytest.mark.parametrize("heads, n", [(8, 16384), (1, 8192), (2, 4100)])
+def test_fea_bwd_long_standalone_backward_stays_on_the_recompute_route(L, heads, n):
+    """A standalone flash_entropy_attention backward at d = 128, dv = 256 with long sequences -- (1, 8, 16384)
+    would need exactly 4 GiB of dS^T, (1, 1, 8192) 128 MiB -- takes the recompute route (O(nq) workspace) by
+    default: the dS route is the default only for the short frame problems it was measured on (nq, nk <= 4096),
+    as VMonarch's R-step passes them (cfg4: 252 problems of 1560 x 1560, 1.24 GB)."""
+    from vmonarch_amd import _lib
+    a = _lib.FeaBwdArgs()
+    a.dtype, a.batch, a.heads, a.frames, a.nq, a.nk, a.d, a.dv = 0, 1, heads, 1, n, n, 128, 256
+    default = L.vmo_fea_bwd_workspace_size(ctypes.byref(a))
+    a.flags = _lib.BWD_RECOMPUTE_DQ
+    assert default == L.vmo_fea_bwd_workspace_size(ctypes.byref(a))
+    assert default < 64 << 20
+    a.flags = _lib.BWD_DS_DQ   # still available on request
+    assert L.vmo_fea_bwd_workspace_size(ctypes.byref(a)) - default == heads * ((n + 31) // 32) ** 2 * 2048
+    # the cfg4 R-step geometry keeps the dS route
+    a.flags, a.heads, a.frames, a.nq, a.nk = 0, 12, 21, 1560, 1560
+    with_ds = L.vmo_fea_bwd_workspace_size(ctypes.byref(a))
+    a.flags = _lib.BWD_RECOMPUTE_DQ
+    assert with_ds - L.vmo_fea_bwd_workspace_size(ctypes.byref(a)) == 252 * 49 * 49 * 2048
+
+
 def test_fea_fwd_qk_fp8_workspace_and_rejections(L):
     """vmo_fea_fwd_args.qk_fp8: the workspace grows by the fp8 keys (problems x nk x d bytes, from a 256-byte
     boundary) and one float per 64-key tile; values that are not k, d = 64, or a value other than 0 / 1 are

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import (assert_close_elementwise, assert_close_ref, assert_grad_close, golden_names, hip_library_loaded,
+from conftest import (assert_close_elementwise, elementwise_margin, assert_close_ref, assert_grad_close, golden_names, hip_library_loaded,
                       load_golden, randn_lp)
 from oracle import entropy_attention
 
@@ -263,17 +263,24 @@ def test_fea_backward_padding_rows_get_zero_grad():
 
 
 def test_fea_backward_cfg5_head_sample():
-    """BASELINE cfg5: B=1, H=24, N=16384, D=128 fwd+bwd on the GPU; heads 0 and 23 against the oracle."""
+    """BASELINE cfg5: B=1, H=24, N=16384, D=128 fwd+bwd on the GPU; heads 0 and 23 against the oracle.  With
+    dO, dE ~ N(0,1) the gradients over 16384 soft keys are ~1e-2, below the elementwise class's 2e-2 atol;
+    the gradients are linear in (dO, dE), so both are scaled by 128 (a power of two: exact in bf16 and fp32,
+    and every rounding in the kernels commutes with it) to bring them to O(1), where the elementwise
+    2e-2 / 1e-2 class binds beside the reference metric."""
     from oracle import entropy_attention_grad
     g = torch.Generator().manual_seed(0)
     q, k, v = (randn_lp(g, 1, 24, 16384, 128) for _ in range(3))
-    do, de = torch.randn(1, 24, 16384, 128, generator=g), torch.randn(1, 24, 16384, generator=g)
+    do, de = torch.randn(1, 24, 16384, 128, generator=g) * 128, torch.randn(1, 24, 16384, generator=g) * 128
     grads = _grads(q, k, v, do, de)
     for h in (0, 23):
         sl = slice(h, h + 1)
         refs = entropy_attention_grad(q[:, sl].float().numpy(), k[:, sl].float().numpy(), v[:, sl].float().numpy(),
                                       do[:, sl].bfloat16().float().numpy(), de[:, sl].numpy(), 128 ** -0.5,
                                       dtype=np.float32)
+        for gd, gr, name in zip(grads, refs, ("dq", "dk", "dv")):
+            print(f"  cfg5 head {h} {name}: max|ref| {np.abs(gr).max():.3f}, elementwise margin "
+                  f"{elementwise_margin(gd[:, sl].float().cpu().numpy(), gr):.3f} (<= 1 passes)", flush=True)
         _check_grads([t[:, sl] for t in grads], refs)
 
 

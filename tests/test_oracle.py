@@ -274,3 +274,28 @@ def test_lowp_oracle_without_rounding_is_the_fp32_oracle():
     q, k, v = (rng.normal(size=(1, 2, 4 * 24, 32)) for _ in range(3))
     z = vmonarch_attention_lowp(q, k, v, 4, 24, 2, 24, rnd=lambda x: np.asarray(x, dtype=np.float64))
     np.testing.assert_allclose(z, vmonarch_attention(q, k, v, 4, 24, 2, 24), rtol=1e-12, atol=1e-12)
+
+
+def test_lowp_oracle_keep_fp32_drops_exactly_the_named_roundings():
+    """keep_fp32 skips the named cast points: with rounding switched off everywhere else and the three named
+    points kept in fp32 the result is the fp32 oracle; each of the three, rounded on its own beside the others
+    kept, moves z visibly; and on sharp inputs the variant without them (the HIP rounding points) is nearer to
+    the fp32 result than the reference's full bf16 path (golden-pinned above)."""
+    rng = np.random.default_rng(7)
+    q, k, v = (rng.normal(size=(1, 2, 4 * 24, 32)) * s for s in (3.0, 3.0, 1.0))
+    args = (4, 24, 2, 24)
+    z32 = vmonarch_attention(q, k, v, *args)
+    names = ("u0", "kr", "logits")
+
+    ident = lambda x: np.asarray(x, dtype=np.float64)   # noqa: E731
+    z_keep = vmonarch_attention_lowp(q, k, v, *args, rnd=ident, keep_fp32=names)
+    np.testing.assert_allclose(z_keep, z32, rtol=1e-12, atol=1e-12)
+    base = np.abs(vmonarch_attention_lowp(q, k, v, *args) - z32).max()
+    hip = np.abs(vmonarch_attention_lowp(q, k, v, *args, keep_fp32=names) - z32).max()
+    assert hip < base
+    for name in names:   # each of the three, rounded on its own, moves z
+        others = tuple(n for n in names if n != name)
+        z_one = vmonarch_attention_lowp(q, k, v, *args, keep_fp32=others)
+        assert np.abs(z_one - vmonarch_attention_lowp(q, k, v, *args, keep_fp32=names)).max() > 1e-3, name
+    with pytest.raises(ValueError):
+        vmonarch_attention_lowp(q, k, v, *args, keep_fp32=("scale",))

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import assert_close_ref, assert_grad_close, hip_library_loaded, randn_lp
+from conftest import elementwise_margin, assert_close_ref, assert_grad_close, hip_library_loaded, randn_lp
 from oracle import lstep_grad, vmonarch_attention_grad
 
 pytestmark = pytest.mark.gpu
@@ -191,17 +191,20 @@ def test_vmonarch_fp16_forward_and_grad():
 
 def test_vmonarch_grad_cfg4_north_star_head_sample():
     """The backward bench.py times: cfg4 (21 frames x 1560 tokens, B=1, H=12, D=128, q,k ~ 0.5 N(0,1),
-    v ~ N(0,1), 2 iterations, rt = 1560) with dz ~ N(0,1) in bf16.  The whole problem runs on the GPU;
-    heads 0 and 11 are checked against the oracle's reverse pass in float32 (heads are independent).
-    These gradients are ~1e-2 in size, so of the two bounds the reference metric binds."""
+    v ~ N(0,1), 2 iterations, rt = 1560).  The whole problem runs on the GPU; heads 0 and 11 are checked
+    against the oracle's reverse pass in float32 (heads are independent).  With dz ~ N(0,1) these gradients
+    are ~1e-2 in size, below the elementwise class's 2e-2 atol, so that bound could not fail; gradients are
+    linear in dz, so dz is scaled by 128 (a power of two: exact in bf16, and every rounding in the kernels
+    commutes with it) to bring them to O(1), where both the reference metric and the elementwise
+    2e-2 / 1e-2 class bind."""
     B, H, m, b, D = 1, 12, 21, 1560, 128
     N = m * b
     g = torch.Generator().manual_seed(0)
     q = randn_lp(g, B, H, N, D, scale=0.5)
     k = randn_lp(g, B, H, N, D, scale=0.5)
     v = randn_lp(g, B, H, N, D)
-    dz = randn_lp(g, B, H, N, D)
-    print("vmonarch grad cfg4: GPU forward + backward", flush=True)
+    dz = randn_lp(g, B, H, N, D) * 128
+    print("vmonarch grad cfg4: GPU forward + backward (dz x 128)", flush=True)
     _, grads = _grads(q, k, v, dz.float(), m, b, 2, b)
     grads = [t.float().cpu().numpy() for t in grads]
     for h in (0, 11):
@@ -210,6 +213,8 @@ def test_vmonarch_grad_cfg4_north_star_head_sample():
         ref = vmonarch_attention_grad(q[:, sl].float().numpy(), k[:, sl].float().numpy(), v[:, sl].float().numpy(),
                                       dz[:, sl].float().numpy(), m, b, 2, b, dtype=np.float32)
         for gd, gr, name in zip(grads, ref, ("dq", "dk", "dv")):
+            print(f"  {name}: max|ref| {np.abs(gr).max():.3f}, elementwise margin "
+                  f"{elementwise_margin(gd[:, sl], gr):.3f} (<= 1 passes)", flush=True)
             assert_grad_close(gd[:, sl], gr, 5e-2, name)
 
 

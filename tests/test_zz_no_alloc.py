@@ -82,3 +82,36 @@ def test_noalloc_forward_rejects_calls_beyond_its_scratch():
     assert L.vmo_fea_fwd_workspace_size(ctypes.byref(a)) > _lib.FEA_FWD_SCRATCH_BYTES
     assert L.vmo_fea_fwd_noalloc(ctypes.byref(a), _lib.stream_of(q)) == 3
     assert b"scratch" in L.vmo_last_error()
+
+
+def test_noalloc_forward_replays_from_a_hip_graph():
+    """vmo_fea_fwd_noalloc with split-KV captured in a torch.cuda.CUDAGraph (after one uncaptured call, which
+    looks up the scratch address on this device): every replay -- with eager work and a sentinel fill of the
+    outputs between replays -- gives o and LSE bit for bit equal to an eager vmo_fea_fwd with a caller
+    workspace.  The forward records no memset node (its partials are written in full before the merge reads
+    them), so nothing in the graph depends on state a replay leaves behind."""
+    from vmonarch_amd import _lib
+    L = _lib.lib()
+    g = torch.Generator().manual_seed(78)
+    nq, nk, splits = 300, 6000, 8
+    q, k, v = (randn_lp(g, 1, 3, n, 128).to(DEV) for n in (nq, nk, nk))
+    (o_ref, lse_ref, _), _ = _run_both(q, k, v, splits)   # eager reference; also the uncaptured set-up call
+    o = torch.empty_like(o_ref)
+    lse = torch.empty_like(lse_ref)
+    a = _args(q, k, v, o, lse, None, splits, 128 ** -0.5)
+    a.workspace, a.workspace_bytes = None, 0
+    graph = torch.cuda.CUDAGraph()
+    print("noalloc forward: capture", flush=True)
+    with torch.cuda.graph(graph):
+        _lib.check(L.vmo_fea_fwd_noalloc(ctypes.byref(a), _lib.stream_of(q)), "vmo_fea_fwd_noalloc (captured)")
+    for rep in range(3):
+        o.fill_(7.0)
+        lse.fill_(7.0)
+        # eager work between replays that also uses the scratch: a smaller split-KV call
+        q2, k2, v2 = (randn_lp(g, 1, 2, n, 128).to(DEV) for n in (100, 1500, 1500))
+        _run_both(q2, k2, v2, 3)
+        print(f"noalloc forward: replay {rep}", flush=True)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o, o_ref) and torch.equal(lse, lse_ref), f"replay {rep}"
+    del graph

@@ -1078,16 +1078,21 @@ static size_t bwd_stats_bytes(int64_t problems, int nq) { return ((size_t)2 * pr
 // is dearest -- d = 128 with dv = 256 (the last R-step, values [k | v]; its dq kernel runs one wave per
 // SIMD): 1.78 against 1.95-2.0 ms -- and loses for dv = d (R-step 0: 1.27 against 1.07 ms; the recompute
 // backward: 1.08 against 1.04 ms), where the dkdv kernel is already close to the HBM bandwidth it shares
-// with the write stream.  So it is taken by default for d = 128, dv = 256 while dS^T of all problems
-// (32 x 32 blocks, keys and queries rounded up to 32) stays within kBwdDsMaxBytes; VMO_BWD_DS_DQ asks for
-// it at any size with d in {64, 128}, VMO_BWD_RECOMPUTE_DQ never.  Returns the workspace bytes it needs,
-// 0 when not taken.
-constexpr int64_t kBwdDsMaxBytes = 4ll << 30;
+// with the write stream.  Its workspace grows as nq x nk per problem (2 bytes per query-key pair), while the
+// recompute route needs O(nq) memory, so it is taken by default only where it was measured to win: d = 128,
+// dv = 256, short problems (nq and nk at most kBwdDsMaxLen, the VMonarch R-step's frames) and dS^T of all
+// problems (32 x 32 blocks, keys and queries rounded up to 32) within kBwdDsMaxBytes.  A long standalone
+// flash_entropy_attention backward (nq = nk = 16384 and more) stays on the recompute route whatever its
+// dims.  VMO_BWD_DS_DQ asks for the dS route at any size with d in {64, 128}, VMO_BWD_RECOMPUTE_DQ never.
+// Returns the workspace bytes it needs, 0 when not taken.
+constexpr int64_t kBwdDsMaxBytes = 2ll << 30;
+constexpr int kBwdDsMaxLen = 4096;
 static size_t bwd_ds_bytes(const vmo_fea_bwd_args* a, int64_t problems) {
   if ((a->flags & VMO_BWD_RECOMPUTE_DQ) || (a->d != 64 && a->d != 128)) return 0;
   const int64_t total = problems * ((a->nk + 31) / 32) * ((a->nq + 31) / 32) * 2048;
   if (a->flags & VMO_BWD_DS_DQ) return (size_t)total;
-  return a->d == 128 && a->dv == 256 && total <= kBwdDsMaxBytes ? (size_t)total : 0;
+  const bool short_problems = a->nq <= kBwdDsMaxLen && a->nk <= kBwdDsMaxLen;
+  return a->d == 128 && a->dv == 256 && short_problems && total <= kBwdDsMaxBytes ? (size_t)total : 0;
 }
 }  // namespace vmo
 

@@ -114,7 +114,7 @@ class _FlashEntropyAttention(torch.autograd.Function):
             o_k = torch.empty((B, H, N, Dvk), device=q.device, dtype=q.dtype)
             if n > 0:
                 fea_forward(qx, kx, vx, None, sm_scale, o=o_k[:, :, :n], lse=lse[:, :, :n], ent=ent[:, :, :n])
-            o = o_k[..., :Dv].contiguous()
+            o = _lib.empty_in_layout(q, Dv, q.dtype).copy_(o_k[..., :Dv])   # the caller's layout, as above
         if n < N:   # padding rows (kernel.py:352-353)
             o[:, :, n:] = 0
             ent[:, :, n:] = 0

@@ -421,7 +421,11 @@ def vmonarch_attention(q, k, v, num_blocks, block_size, num_iters=2, recompute_t
                 z = _VMonarchFunction.apply(qp, kp, vp, *args, D ** -0.5)
             else:
                 z = _vmonarch_fused(qp, kp, vp, *args, scale=D ** -0.5)
-            return z if w == Dv else z[..., :Dv].contiguous()
+            if w == Dv:
+                return z
+            # the first Dv columns, in the caller's memory order like every other path's z (a DiT block's
+            # (B, N, H, Dv) buffer needs no permute copy afterwards); copy_ keeps the autograd graph
+            return _lib.empty_in_layout(q, Dv, q.dtype).copy_(z[..., :Dv])
         if q.is_cuda:
             warnings.warn(f"vmonarch_amd: no HIP path for num_blocks={num_blocks}, head dims ({D}, {Dv}), {q.dtype}"
                           f"{' with autograd' if needs_graph else ''}; running the composed path (flash-entropy "
