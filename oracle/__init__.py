@@ -32,6 +32,6 @@ default (float32 for the CPU baseline timing).  How each function is pinned:
                           base point, as the reference's detach (vmonarch.py:26) makes them;
                           with and without the col_mass clamp active, 1-3 iterations, rt 0 and b.
 """
-from .fea import entropy_attention, entropy_attention_grad, exact_attention  # noqa: F401
+from .fea import entropy_attention, entropy_attention_grad, exact_attention, kernel_rounding_attention  # noqa: F401
 from .vmonarch import (vmonarch_attention, row_block_attention, lstep, lstep_grad,  # noqa: F401
                        vmonarch_attention_grad, vmonarch_attention_lowp, round_bf16)

@@ -63,3 +63,24 @@ def entropy_attention_grad(q, k, v, do, de, sm_scale=None, dtype=np.float64):
     dk = sm_scale * (np.swapaxes(ds, -1, -2) @ q)
     dv = np.swapaxes(p, -1, -2) @ do
     return dq, dk, dv
+
+
+def kernel_rounding_attention(q, k, w, sm_scale, rnd, entropy_from_pk=True, first_keys=32, dtype=np.float64):
+    """Where the gfx950 flash-entropy kernels round (not the reference's algorithm: an emulation of this
+    build's kernels, used to tell their rounding apart from the reference's in tests).  Relative to the max m
+    of the row's first `first_keys` logits, p = exp(s - m) is rounded once (``rnd``) where it enters P.W as
+    the MFMA operand p~.  With ``entropy_from_pk`` (the VMonarch R-step, values starting with k) the row sum is
+    l~ = sum p~, o = sum p~ w / l~ and e = m + ln l~ - sum p~ s / l~; otherwise (the recompute) l = sum p,
+    o = sum p~ w / l.  With an identity ``rnd`` both are exactly softmax(s) w and -sum P ln P.
+    Returns (o, e); e is None without ``entropy_from_pk``."""
+    q, k, w = _f(q, dtype), _f(k, dtype), _f(w, dtype)
+    s = sm_scale * (q @ np.swapaxes(k, -1, -2))
+    m = s[..., :first_keys].max(-1, keepdims=True)
+    p = np.exp(s - m)
+    pt = rnd(p)
+    if entropy_from_pk:
+        l = pt.sum(-1, keepdims=True)
+        e = m[..., 0] + np.log(l[..., 0]) - (pt * s).sum(-1) / l[..., 0]
+        return (pt @ w) / l, e
+    return (pt @ w) / p.sum(-1, keepdims=True), None
+

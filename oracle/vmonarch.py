@@ -10,7 +10,7 @@ it tells how far the reference's bf16 path itself lands from the fp32 reference 
 """
 import numpy as np
 
-from .fea import entropy_attention, entropy_attention_grad, exact_attention
+from .fea import entropy_attention, entropy_attention_grad, exact_attention, kernel_rounding_attention
 
 
 def row_block_attention(x, k, w, dtype=np.float64):
@@ -98,7 +98,7 @@ def round_bf16(x):
 
 
 def vmonarch_attention_lowp(q, k, v, num_blocks, block_size, num_iters=2, recompute_tokens=0,
-                            min_col_mass=0.01, rnd=round_bf16, keep_fp32=()):
+                            min_col_mass=0.01, rnd=round_bf16, keep_fp32=(), kernel_p=False):
     """vmonarch.py:29-69 as the reference runs it on bf16 tensors: every tensor the glue stores in the
     input dtype is rounded by ``rnd`` where the reference makes it (einsum / product results rounded once,
     accumulation in float64 here), the softmaxes and col_mass in float, and the R-step exact (its output o
@@ -111,9 +111,13 @@ def vmonarch_attention_lowp(q, k, v, num_blocks, block_size, num_iters=2, recomp
       u = einsum(attn.to(dtype), q)          (vmonarch.py:62)  attn rounded, u rounded
       u = u * (scale / col_mass).to(dtype)   (vmonarch.py:63)  factor rounded, product rounded
       SDPA(q[:, :, :rt], k, v)               (vmonarch.py:67)  exact, rounded
-    ``keep_fp32`` names cast points to skip ("u0": the first u, "kr", "logits"): with all three the glue
-    rounds where the HIP kernels round (they fold q * scale and out * scale into their fp32 softmax factors
-    and keep the L-step logits in fp32), the reference's path minus those three roundings.
+    ``keep_fp32`` names cast points to skip ("u0": the first u, "kr", "logits"; "u": the u update rounded
+    once, as the product of the fp32 einsum and the fp32 factor, instead of three times): with all four the
+    glue rounds where this build's HIP kernels round (they fold q * scale and out * scale into their fp32
+    softmax factors, keep the L-step logits in fp32 and round u once when they store it).  ``kernel_p`` takes
+    the R-steps and the recompute as the flash-entropy kernels round them (fea.kernel_rounding_attention:
+    P rounded where it enters P.W) instead of exactly.  Both are emulations of this build, not of the
+    reference: the reference's own bf16 path is the default (no keep_fp32, kernel_p False).
     """
     q, k, v = (rnd(t) for t in (q, k, v))
     B, H, N, D = q.shape
@@ -122,7 +126,7 @@ def vmonarch_attention_lowp(q, k, v, num_blocks, block_size, num_iters=2, recomp
     scale = D ** -0.5
     m, b = num_blocks, block_size
     qg, kg, vg = (t.reshape(B, H, m, b, t.shape[-1]) for t in (q, k, v))
-    unknown = set(keep_fp32) - {"u0", "kr", "logits"}
+    unknown = set(keep_fp32) - {"u0", "kr", "logits", "u"}
     if unknown:
         raise ValueError(f"keep_fp32: unknown cast points {sorted(unknown)}")
     keep = lambda name, x: x if name in keep_fp32 else rnd(x)   # noqa: E731
@@ -131,7 +135,10 @@ def vmonarch_attention_lowp(q, k, v, num_blocks, block_size, num_iters=2, recomp
     for it in range(num_iters):
         last = it == num_iters - 1
         w = np.concatenate([kg, vg], -1) if last else kg
-        out, ent = entropy_attention(u, kg, w, 1.0)
+        if kernel_p:
+            out, ent = kernel_rounding_attention(u, kg, w, 1.0, rnd)
+        else:
+            out, ent = entropy_attention(u, kg, w, 1.0)
         out = rnd(out)
         kr = keep("kr", out[..., :D] * scale)
         logits = keep("logits", np.einsum("bhijd,bhkjd->bhjik", qg, kr))
@@ -140,13 +147,16 @@ def vmonarch_attention_lowp(q, k, v, num_blocks, block_size, num_iters=2, recomp
             z = rnd(np.einsum("bhjik,bhkjd->bhijd", rnd(attn), out[..., D:]))
         else:
             col_mass = np.maximum(np.swapaxes(attn.sum(-2), -1, -2), min_col_mass)
-            u = rnd(np.einsum("bhjik,bhijd->bhkjd", rnd(attn), qg))
-            u = rnd(u * rnd(scale / col_mass)[..., None])
+            u = keep("u", np.einsum("bhjik,bhijd->bhkjd", rnd(attn), qg))
+            u = rnd(u * keep("u", scale / col_mass)[..., None])
     z = z.reshape(B, H, N, -1)
     if recompute_tokens > 0:
         rt = recompute_tokens
         z = z.copy()
-        z[:, :, :rt] = rnd(exact_attention(q[:, :, :rt], k, v))
+        if kernel_p:
+            z[:, :, :rt] = rnd(kernel_rounding_attention(q[:, :, :rt], k, v, D ** -0.5, rnd, entropy_from_pk=False)[0])
+        else:
+            z[:, :, :rt] = rnd(exact_attention(q[:, :, :rt], k, v))
     return z
 
 

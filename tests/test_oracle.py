@@ -288,7 +288,7 @@ def test_lowp_oracle_keep_fp32_drops_exactly_the_named_roundings():
     names = ("u0", "kr", "logits")
 
     ident = lambda x: np.asarray(x, dtype=np.float64)   # noqa: E731
-    z_keep = vmonarch_attention_lowp(q, k, v, *args, rnd=ident, keep_fp32=names)
+    z_keep = vmonarch_attention_lowp(q, k, v, *args, rnd=ident, keep_fp32=names + ("u",), kernel_p=True)
     np.testing.assert_allclose(z_keep, z32, rtol=1e-12, atol=1e-12)
     base = np.abs(vmonarch_attention_lowp(q, k, v, *args) - z32).max()
     hip = np.abs(vmonarch_attention_lowp(q, k, v, *args, keep_fp32=names) - z32).max()
@@ -299,3 +299,29 @@ def test_lowp_oracle_keep_fp32_drops_exactly_the_named_roundings():
         assert np.abs(z_one - vmonarch_attention_lowp(q, k, v, *args, keep_fp32=names)).max() > 1e-3, name
     with pytest.raises(ValueError):
         vmonarch_attention_lowp(q, k, v, *args, keep_fp32=("scale",))
+
+
+@pytest.mark.parametrize("from_pk", [True, False])
+def test_kernel_rounding_attention(from_pk):
+    """The emulation of the kernels' P rounding: exactly the fp32 oracle with an identity rounding (any
+    reference point m), and with bf16 rounding of p within the bounds the rounding allows: o moves by at most
+    ~2 x 2^-8 max|w| (the weights p~ / sum p~ of the R-step are perturbed by <= 2^-8 relative) or 2^-9 max|w|
+    (the recompute's sum p~ w / sum p), and the R-step entropy by at most ~2^-8 (max s - min s)."""
+    from oracle import kernel_rounding_attention, round_bf16
+    rng = np.random.default_rng(11)
+    q, k = rng.normal(size=(2, 3, 40, 16)) * 1.5, rng.normal(size=(2, 3, 70, 16)) * 1.5
+    w = rng.normal(size=(2, 3, 70, 24))
+    o_ref, e_ref = entropy_attention(q, k, w, 0.5)
+    ident = lambda x: x   # noqa: E731
+    for first in (1, 32, 70):
+        o, e = kernel_rounding_attention(q, k, w, 0.5, ident, entropy_from_pk=from_pk, first_keys=first)
+        np.testing.assert_allclose(o, o_ref, rtol=1e-10, atol=1e-10)
+        if from_pk:
+            np.testing.assert_allclose(e, e_ref, rtol=1e-10, atol=1e-10)
+    o, e = kernel_rounding_attention(q, k, w, 0.5, round_bf16, entropy_from_pk=from_pk)
+    err = np.abs(o - o_ref).max()
+    assert 0 < err <= (2 * 2.0 ** -8 if from_pk else 2.0 ** -9) * np.abs(w).max(), err
+    if from_pk:
+        s = 0.5 * (q @ np.swapaxes(k, -1, -2))
+        spread = (s.max(-1) - s.min(-1)).max()
+        assert 0 < np.abs(e - e_ref).max() <= 2.0 ** -8 * spread
