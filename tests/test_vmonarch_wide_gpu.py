@@ -26,8 +26,8 @@ def _r5(t, m, b):
     return t.float().cpu().numpy().reshape(B, H, m, b, F)
 
 
-@pytest.mark.parametrize("m", [33, 48, 64])
-@pytest.mark.parametrize("d, dv", [(64, 64), (128, 128), (32, 32), (128, 64), (256, 256)])
+@pytest.mark.parametrize("m", [7, 33, 48, 64, 65, 96, 128])
+@pytest.mark.parametrize("d, dv", [(64, 64), (128, 128), (32, 32), (128, 64), (32, 128), (256, 256)])
 @pytest.mark.parametrize("last", [False, True])
 def test_general_lstep_forward_matches_oracle(m, d, dv, last):
     from vmonarch_amd.vmonarch import _lstep_launch, _lstep_supported

@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libvmonarch_gfx950.so")
-SOURCES = ["capi.hip", "fea_fwd.hip", "fea_bwd.hip", "lstep.hip"]
+SOURCES = ["capi.hip", "fea_fwd.hip", "fea_bwd.hip", "lstep.hip", "lstep_mb.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-mcode-object-version=5",

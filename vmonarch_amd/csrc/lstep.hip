@@ -21,28 +21,14 @@
 
 #include "vmo_common.h"
 #include "vmo_host.h"
+#include "lstep_params.h"
 
 namespace vmo {
 
 constexpr int kLWaves = 4;   // columns per workgroup
 constexpr int kAttStride = 36;   // floats per row of the LDS attention tile (bank-conflict pad)
 
-struct LParams {
-  const void* q;
-  const void* out;
-  const float* ent;
-  void* res;
-  int64_t q_sb, q_sh, q_sn;
-  int64_t out_sb, out_sh, out_sn;
-  int64_t ent_sb, ent_sh;
-  int64_t res_sb, res_sh, res_sn;
-  int heads, m, bs, skip;
-  int cols_total;
-  int d, dv;                // head dims (the one-tile kernels take them as template parameters)
-  float logit_scale_log2;   // scale * log2(e)
-  float scale;
-  float min_col_mass;
-};
+
 
 template <int D, int DV, bool LAST>
 struct LLds {
@@ -278,29 +264,7 @@ static int dispatch_lstep(const LParams& p, int d, int dv, bool last, hipStream_
 // SIMD, four per CU); within 256 it needs 176-224 and spills none.
 constexpr int kLBWaves = 1;
 
-struct LBParams {
-  const void* q;
-  const void* out;
-  const float* ent;
-  const void* g;
-  float* dq;
-  int dq_overwrite;   // dq = dL/dq instead of +=
-  void* dout;
-  int64_t q_sb, q_sh, q_sn;
-  int64_t out_sb, out_sh, out_sn;
-  int64_t ent_sb, ent_sh;
-  int64_t g_sb, g_sh, g_sn;
-  int64_t dq_sb, dq_sh, dq_sn;
-  int64_t do_sb, do_sh, do_sn;
-  int heads, m, bs, skip;
-  int cols_total;
-  int d, dv;
-  float logit_scale_log2;
-  float scale;
-  float min_col_mass;
-  float* delta;       // optional: sum_f out * d out per token (one-tile kernels)
-  int64_t dl_sb, dl_sh;
-};
+
 
 // ROWS: rows held per tile, 32 or (for m <= 24) 24.  The MFMAs take 32 rows of a tile; with 24 tile rows
 // their reads of rows 24..31 land in the first 8 rows of the next tile (q -> kr -> dz / dv, all 16-bit, so
@@ -1054,7 +1018,8 @@ extern "C" int vmo_lstep_fwd(const vmo_lstep_args* a, void* stream) {
     return set_error(VMO_ERR_INVALID, "lstep: tensors need 16-byte aligned rows");
   if (a->d <= 0 || (a->d % 8) != 0) return set_error(VMO_ERR_INVALID, "lstep: d");
   const bool one_tile = a->num_blocks <= 32 && one_tile_built(a->d, a->dv, a->last != 0);
-  if (!one_tile) {
+  const bool multi_block = !one_tile && mb_lstep_check(a->num_blocks, a->d, a->dv, a->last != 0, false);
+  if (!one_tile && !multi_block) {
     const int rc = lw_check(a->num_blocks, a->d, a->dv, a->last != 0, false, "lstep");
     if (rc != VMO_OK) return rc;
   }
@@ -1075,6 +1040,7 @@ extern "C" int vmo_lstep_fwd(const vmo_lstep_args* a, void* stream) {
   p.scale = a->scale;
   p.min_col_mass = a->min_col_mass;
   hipStream_t s = (hipStream_t)stream;
+  if (multi_block) return mb_lstep_fwd(p, a->dtype == VMO_DTYPE_F16, a->d, a->dv, a->last != 0, s);
   if (!one_tile) {
     const int lds = lw_layout(p.m, p.d, p.dv, a->last != 0, false).total;
     if (a->dtype == VMO_DTYPE_F16)

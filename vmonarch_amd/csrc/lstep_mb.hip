@@ -1,0 +1,305 @@
+// Multi-block fused L-step for gfx950: grids of more than 32 frames (and head dims 32 / 64 / 128 at any
+// frame count up to kMbMaxFrames), on MFMA.
+//
+// Reference: video_monarch_attention/vmonarch.py:51-63 -- per grid column j (the same spatial position in
+// all m frames) an m x m attention over the frames:
+//   attn[i, k] = softmax_k(scale q_i . kr_k + ent_k),  kr = out[..., :D]
+//   last:      z_i = sum_k attn[i, k] y_k,  y = out[..., D:]
+//   otherwise: u_k = scale / max(sum_i attn[i, k], min_col_mass) * sum_i attn[i, k] q_i
+// (the one-tile kernels in lstep.hip take m <= 32 in a single 32 x 32 MFMA tile per column).
+//
+// Here one 4-wave workgroup owns a column: its q, kr (and y) rows -- tokens i b + j, i < m -- are staged
+// whole into swizzled LDS tiles of M = 32 * MB rows (MB = ceil(m / 32) <= kMbMaxBlocks; rows past m repeat
+// the last row, finite data whose weights are exact zeros), and the m x m products run on
+// v_mfma_f32_32x32x16 in 32 x 32 blocks:
+//   * last: wave w owns query block w.  S^T blocks (keys x queries: one query row per lane) for every key
+//     block, softmax over all of them in registers (max, sum, normalise: the attention is rounded to the
+//     16-bit type only once normalised, as the reference's attn.to(y.dtype)), then z^T += Y^T P^T with the
+//     S^T accumulators as the B operand and Y^T read by ds_read_tr16_b64, whose 4-row groups match the
+//     accumulator's (no key permutation);
+//   * otherwise two passes: (1) wave w computes the log-sum-exp of its query block's rows (S^T blocks as
+//     above) into LDS; (2) wave w owns key block w: L blocks (queries x keys: one key per lane) = Q Kr^T for
+//     every query block, attn = exp2(L c + ent_k - lse_i) exactly normalised, the column mass as an in-lane
+//     sum of the fp32 attn, and u^T += Q^T attn with Q^T by transposed reads.
+// Rounding points as the one-tile kernels: logits in fp32 from the 16-bit q and kr, attn rounded to the
+// 16-bit type where it multiplies q or y, the column mass from the fp32 attn, u / z rounded once when stored.
+// Results leave through per-wave LDS patches as whole row segments (store_acc_rows).
+#include "vmo_common.h"
+#include "vmo_host.h"
+#include "lstep_params.h"
+
+namespace vmo {
+
+constexpr int kMbWaves = 4;
+constexpr int kMbMaxBlocks = 4;                  // one 32-row block per wave
+constexpr int kMbMaxFrames = 32 * kMbMaxBlocks;  // m <= 128
+
+// Byte offsets of a column's LDS arrays.  The row-store patches (kEpiPatchBytes per wave) reuse the start
+// of the allocation once every wave has passed the barrier that ends the compute.
+struct MbLayout {
+  int q, k, y, g, e, lse, vec2, vec3, total;
+};
+__host__ __device__ inline MbLayout mb_layout(int M, int d, int dv, bool last, bool bwd) {
+  MbLayout L;
+  int off = 0;
+  auto take = [&](int bytes) { const int o = off; off += (bytes + 255) / 256 * 256; return o; };
+  L.q = take(M * d * 2);
+  L.k = take(M * d * 2);
+  L.y = last ? take(M * dv * 2) : 0;
+  L.g = bwd ? take(M * (last ? dv : d) * 2) : 0;
+  L.e = take(M * 4);
+  L.lse = take(M * 4);
+  L.vec2 = bwd ? take(M * 4) : 0;
+  L.vec3 = bwd ? take(M * 4) : 0;
+  L.total = off > kMbWaves * kEpiPatchBytes ? off : kMbWaves * kEpiPatchBytes;
+  return L;
+}
+
+// Stage M rows of W 16-bit values (row r < m: src + r rs; rows past m repeat row m - 1) into a tile whose
+// chunk c of row r sits at chunk c ^ swz_rows(r): wave instruction inst covers rows inst RPI .. + RPI - 1,
+// lane l lands at byte 16 l of its 1 KB and so loads global chunk (l % CH) ^ swz_rows(row).
+template <class T, int W>
+__device__ __forceinline__ void mb_stage(const T* src, int64_t rs, int m, int M, VMO_LDS char* dst, int wave,
+                                         int lane) {
+  constexpr int RB = W * 2, CH = RB / 16, RPI = 64 / CH;
+  const int c = lane % CH;
+  for (int inst = wave; inst * RPI < M; inst += kMbWaves) {
+    const int r = inst * RPI + lane / CH;
+    const int rr = r < m ? r : m - 1;
+    g2l_16(src + (int64_t)rr * rs + (c ^ swz_rows<RB>(r)) * 8, dst + inst * 1024);
+  }
+}
+
+// Row-read MFMA operand: lane (row l32 of a 32-row block at `rows`, half hl) gets elements 16 ds + 8 hl .. + 7.
+template <class V8, int RB>
+__device__ __forceinline__ V8 mb_row8(const VMO_LDS char* rows, int l32, int hl, int ds) {
+  return lds_read8<V8>(rows + l32 * RB + ((2 * ds + hl) ^ swz_rows<RB>(l32)) * 16);
+}
+
+// Transposed MFMA A operand for the 32 columns 32 a .. 32 a + 31 of a row-major tile, K step h2 (16 rows) of
+// the 32-row block at `rows`: the rows are taken in the S^T / L accumulator's order (rows 4 hl + 0..3 and
+// 8 + 4 hl + 0..3 of the step), so that accumulator rows 8 h2 .. 8 h2 + 7, rounded, are the B operand.
+template <class V8, int RB>
+__device__ __forceinline__ V8 mb_tr8(const VMO_LDS char* rows, int lane, int a, int h2) {
+  const int hl = lane >> 5;
+  const int trow = 4 * hl + ((lane & 15) >> 2);
+  const int tchunk = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+  const int tbyte = (lane & 1) * 8;
+  const int c0 = trow * RB + (((4 * a + tchunk) ^ swz_rows<RB>(trow)) * 16 + tbyte);
+  const VMO_LDS char* rp = rows + 16 * h2 * RB;
+  return lds_read_tr8<V8>(rp + c0, rp + 8 * RB + (c0 ^ 32));
+}
+
+// Accumulator rows 8 h2 .. 8 h2 + 7 of x, times f, rounded to the 16-bit type: a B operand.
+template <class T, class V8>
+__device__ __forceinline__ V8 mb_pack(const f32x16& x, int h2, float f) {
+  V8 v;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = to_elem<T>(x[8 * h2 + e] * f);
+  return v;
+}
+
+template <bool F16, int D, int DV, bool LAST>
+__global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_kernel(LParams p) {
+  using E = Elem<F16>;
+  using T = typename E::T;
+  using V8 = typename E::V8;
+  constexpr int NDS = D / 16;
+  constexpr int NACC = (LAST ? DV : D) / 32;
+  constexpr int RBD = D * 2, RBY = DV * 2;
+  extern __shared__ __attribute__((aligned(1024))) char smem_raw[];
+  VMO_LDS char* sm = (VMO_LDS char*)smem_raw;
+
+  const int m = p.m, MB = (m + 31) / 32, M = 32 * MB;
+  const MbLayout Lo = mb_layout(M, D, DV, LAST, false);
+  VMO_LDS char* q_t = sm + Lo.q;
+  VMO_LDS char* k_t = sm + Lo.k;
+  VMO_LDS char* y_t = sm + Lo.y;
+  VMO_LDS float* e_t = (VMO_LDS float*)(sm + Lo.e);
+  VMO_LDS float* lse_t = (VMO_LDS float*)(sm + Lo.lse);
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int hl = lane >> 5, l32 = lane & 31;
+
+  const int col = blockIdx.x, bh = col / p.bs, j = col % p.bs, hh = bh % p.heads, bb = bh / p.heads;
+  const int64_t q_rs = (int64_t)p.bs * p.q_sn, o_rs = (int64_t)p.bs * p.out_sn, r_rs = (int64_t)p.bs * p.res_sn;
+  const T* qcol = (const T*)p.q + bb * p.q_sb + hh * p.q_sh + (int64_t)j * p.q_sn;
+  const T* ocol = (const T*)p.out + bb * p.out_sb + hh * p.out_sh + (int64_t)j * p.out_sn;
+  T* rcol = (T*)p.res + bb * p.res_sb + hh * p.res_sh + (int64_t)j * p.res_sn;
+
+  mb_stage<T, D>(qcol, q_rs, m, M, q_t, wave, lane);
+  mb_stage<T, D>(ocol, o_rs, m, M, k_t, wave, lane);
+  if constexpr (LAST) mb_stage<T, DV>(ocol + D, o_rs, m, M, y_t, wave, lane);
+  const float* ep = p.ent + bb * p.ent_sb + hh * p.ent_sh + j;
+  for (int k = tid; k < M; k += 64 * kMbWaves) e_t[k] = k < m ? ep[(int64_t)k * p.bs] * kLog2e : -1.0e30f;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  const float c = p.logit_scale_log2;
+  // S^T blocks of query block ib against every key block, biased and in log2 units (keys past m at -1e30):
+  // x[kb][r] for key 32 kb + 8 (r / 4) + 4 hl + r % 4 and query 32 ib + l32; returns the row max.
+  auto s_blocks = [&](int ib, f32x16 (&x)[kMbMaxBlocks]) __attribute__((always_inline)) {
+    V8 qb[NDS];
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds) qb[ds] = mb_row8<V8, RBD>(q_t + 32 * ib * RBD, l32, hl, ds);
+    float mx = -3.0e38f;
+#pragma unroll
+    for (int kb = 0; kb < kMbMaxBlocks; ++kb) {
+      if (kb >= MB) break;
+      x[kb] = f32x16{};
+#pragma unroll
+      for (int ds = 0; ds < NDS; ++ds) x[kb] = E::mfma(mb_row8<V8, RBD>(k_t + 32 * kb * RBD, l32, hl, ds), qb[ds], x[kb]);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 ev = *(const VMO_LDS f32x4*)(e_t + 32 * kb + 8 * g + 4 * hl);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          x[kb][4 * g + e] = fmaf(x[kb][4 * g + e], c, ev[e]);
+          mx = fmaxf(mx, x[kb][4 * g + e]);
+        }
+      }
+    }
+    return wave_max32(mx);
+  };
+
+  f32x16 acc[NACC];
+#pragma unroll
+  for (int a = 0; a < NACC; ++a) acc[a] = f32x16{};
+  const int blk = wave;            // this wave's query block (last) or key block (otherwise)
+  const bool busy = blk < MB;
+  float fscale = 1.f;
+
+  if constexpr (LAST) {
+    if (busy) {
+      f32x16 x[kMbMaxBlocks];
+      const float mx = s_blocks(blk, x);
+      float sum = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < kMbMaxBlocks; ++kb) {
+        if (kb >= MB) break;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          x[kb][r] = fast_exp2(x[kb][r] - mx);
+          sum += x[kb][r];
+        }
+      }
+      const float inv = 1.0f / wave_sum32(sum);
+      // z^T[dv][i] = sum_k y^T[dv][k] attn^T[k][i]
+#pragma unroll
+      for (int kb = 0; kb < kMbMaxBlocks; ++kb) {
+        if (kb >= MB) break;
+        const V8 P0 = mb_pack<T, V8>(x[kb], 0, inv), P1 = mb_pack<T, V8>(x[kb], 1, inv);
+#pragma unroll
+        for (int a = 0; a < NACC; ++a) {
+          acc[a] = E::mfma(mb_tr8<V8, RBY>(y_t + 32 * kb * RBY, lane, a, 0), P0, acc[a]);
+          acc[a] = E::mfma(mb_tr8<V8, RBY>(y_t + 32 * kb * RBY, lane, a, 1), P1, acc[a]);
+        }
+      }
+    }
+  } else {
+    // pass 1: row log-sum-exp (log2 units) of every query row; rows past m get +1e30 (zero attention)
+    if (busy) {
+      f32x16 x[kMbMaxBlocks];
+      const float mx = s_blocks(blk, x);
+      float sum = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < kMbMaxBlocks; ++kb) {
+        if (kb >= MB) break;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sum += fast_exp2(x[kb][r] - mx);
+      }
+      const float lse = mx + fast_log2(wave_sum32(sum));
+      if (hl == 0) lse_t[32 * blk + l32] = 32 * blk + l32 < m ? lse : 1.0e30f;
+    }
+    __syncthreads();
+    // pass 2: key block blk; one key per lane
+    if (busy) {
+      V8 kb_op[NDS];
+#pragma unroll
+      for (int ds = 0; ds < NDS; ++ds) kb_op[ds] = mb_row8<V8, RBD>(k_t + 32 * blk * RBD, l32, hl, ds);
+      const float ek = e_t[32 * blk + l32];
+      float cm = 0.f;
+#pragma unroll
+      for (int ib = 0; ib < kMbMaxBlocks; ++ib) {
+        if (ib >= MB) break;
+        // L[i][k] = q_i . kr_k: A = q rows (lane = query row), B = kr rows (lane = key)
+        f32x16 x = f32x16{};
+#pragma unroll
+        for (int ds = 0; ds < NDS; ++ds) x = E::mfma(mb_row8<V8, RBD>(q_t + 32 * ib * RBD, l32, hl, ds), kb_op[ds], x);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 lv = *(const VMO_LDS f32x4*)(lse_t + 32 * ib + 8 * g + 4 * hl);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float a = fast_exp2(fmaf(x[4 * g + e], c, ek - lv[e]));
+            x[4 * g + e] = a;
+            cm += a;
+          }
+        }
+        // u^T[d][k] += sum_i q^T[d][i] attn[i][k]
+        const V8 P0 = mb_pack<T, V8>(x, 0, 1.f), P1 = mb_pack<T, V8>(x, 1, 1.f);
+#pragma unroll
+        for (int a = 0; a < NACC; ++a) {
+          acc[a] = E::mfma(mb_tr8<V8, RBD>(q_t + 32 * ib * RBD, lane, a, 0), P0, acc[a]);
+          acc[a] = E::mfma(mb_tr8<V8, RBD>(q_t + 32 * ib * RBD, lane, a, 1), P1, acc[a]);
+        }
+      }
+      fscale = p.scale / fmaxf(wave_sum32(cm), p.min_col_mass);
+    }
+  }
+
+  __syncthreads();   // every wave is done with the tiles: the patches reuse them
+  if (!busy) return;
+  VMO_LDS float* patch = (VMO_LDS float*)(sm + wave * kEpiPatchBytes);
+  const int nrows = min(32, m - 32 * blk);
+  if constexpr (LAST) {
+    // z rows i from the first one the recompute does not overwrite (token i b + j >= skip)
+    const int ibeg = p.skip > j ? (p.skip - j + p.bs - 1) / p.bs : 0;
+    store_acc_rows<F16>(patch, acc, NACC, 1.f, kGradStore, (char*)(rcol + 32 * blk * r_rs), r_rs * 2, nrows, lane,
+                        max(0, ibeg - 32 * blk));
+  } else {
+    store_acc_rows<F16>(patch, acc, NACC, fscale, kGradStore, (char*)(rcol + 32 * blk * r_rs), r_rs * 2, nrows, lane);
+  }
+}
+
+// Head-dim pairs the multi-block kernels are built for.
+static bool mb_dims(int d, int dv, bool last) {
+  const auto ok = [](int x) { return x == 32 || x == 64 || x == 128; };
+  return ok(d) && (!last || ok(dv));
+}
+
+int mb_lstep_check(int m, int d, int dv, bool last, bool bwd) {
+  if (!mb_dims(d, dv, last) || m < 1 || m > kMbMaxFrames) return 0;
+  return mb_layout(32 * ((m + 31) / 32), d, last ? dv : 0, last, bwd).total <= 160 * 1024;
+}
+
+template <bool F16, int D, int DV, bool LAST>
+static int launch_mb(const LParams& p, hipStream_t s) {
+  const int M = 32 * ((p.m + 31) / 32);
+  const int lds = mb_layout(M, D, DV, LAST, false).total;
+  auto kern = lstep_mb_kernel<F16, D, DV, LAST>;
+  if (lds > 65536 && hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
+    return set_error(VMO_ERR_LAUNCH, "lstep_mb: cannot raise the LDS limit to %d bytes", lds);
+  hipLaunchKernelGGL(kern, dim3(p.cols_total), dim3(64 * kMbWaves), lds, s, p);
+  return launch_status("lstep_mb");
+}
+
+template <bool F16>
+static int dispatch_mb(const LParams& p, int d, int dv, bool last, hipStream_t s) {
+#define VMO_MB(D_, DV_)                                                                   \
+  if (d == D_ && dv == DV_ && last) return launch_mb<F16, D_, DV_, true>(p, s);
+#define VMO_MB_U(D_) \
+  if (d == D_ && !last) return launch_mb<F16, D_, D_, false>(p, s);
+  VMO_MB_U(32) VMO_MB_U(64) VMO_MB_U(128)
+  VMO_MB(32, 32) VMO_MB(32, 64) VMO_MB(32, 128)
+  VMO_MB(64, 32) VMO_MB(64, 64) VMO_MB(64, 128)
+  VMO_MB(128, 32) VMO_MB(128, 64) VMO_MB(128, 128)
+#undef VMO_MB
+#undef VMO_MB_U
+  return set_error(VMO_ERR_UNSUPPORTED, "lstep_mb: no kernel for d=%d dv=%d last=%d", d, dv, (int)last);
+}
+
+int mb_lstep_fwd(const LParams& p, bool f16, int d, int dv, bool last, hipStream_t s) {
+  return f16 ? dispatch_mb<true>(p, d, dv, last, s) : dispatch_mb<false>(p, d, dv, last, s);
+}
+
+}  // namespace vmo

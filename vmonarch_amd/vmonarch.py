@@ -118,10 +118,35 @@ def _lstep_general_lds(m, d, dv, last, bwd):
     return total
 
 
+_MB_MAX_FRAMES = 128
+_MB_BWD = False   # the multi-block backward kernels
+
+
+def _lstep_mb_lds(m, d, dv, last, bwd):
+    """LDS bytes per grid column of the multi-block L-step kernels (csrc/lstep_mb.hip mb_layout): q and kr tiles (and
+    y, and the upstream gradient) of M = 32 ceil(m / 32) 16-bit rows, M-float vectors, at least the four row-store
+    patches."""
+    M = 32 * ((m + 31) // 32)
+    r = lambda b: (b + 255) // 256 * 256   # noqa: E731
+    total = 2 * r(M * d * 2) + (r(M * dv * 2) if last else 0) + 2 * r(M * 4)
+    if bwd:
+        total += r(M * (dv if last else d) * 2) + 2 * r(M * 4)
+    return max(total, 4 * 4096)
+
+
+def _lstep_mb(m, d, dv, bwd):
+    """Whether the multi-block MFMA L-step kernels take this grid: up to 128 frames, head dims 32 / 64 / 128."""
+    return ((_MB_BWD or not bwd) and 1 <= m <= _MB_MAX_FRAMES and d in (32, 64, 128) and dv in (32, 64, 128)
+            and all(_lstep_mb_lds(m, d, dv, last, bwd) <= _LDS_BYTES for last in (False, True)))
+
+
 def _lstep_supported(m, d, dv, bwd):
-    """Whether the HIP L-steps run this grid: the one-tile MFMA kernels (m <= 32, d and dv in {64, 128}) or the
-    general kernels (any m whose per-column tiles fit the LDS)."""
+    """Whether the HIP L-steps run this grid: the one-tile MFMA kernels (m <= 32, d and dv in {64, 128}), the
+    multi-block MFMA kernels (m <= 128, head dims 32 / 64 / 128), or the general kernels (any m whose per-column
+    tiles fit the LDS)."""
     if m <= 32 and d in (64, 128) and dv in (64, 128):
+        return True
+    if _lstep_mb(m, d, dv, bwd):
         return True
     return all(_lstep_general_lds(m, d, dv, last, bwd) <= _LDS_BYTES for last in (False, True))
 
