@@ -106,10 +106,11 @@ typedef struct vmo_fea_fwd_args {
  *   last == 1:  z[i,j]  = sum_k attn[i,k] out[k,j,d:d+dv]                (vmonarch.py:57-59)
  * ent is the R-step entropy (the reference subtracts neg_ent = -ent).  `res` receives u
  * (d features) or z (dv features).  With last == 1, tokens n < skip_tokens are not written
- * (the recompute of vmonarch.py:66-68 owns them).  One MFMA tile per grid column for m <= 32 with d and
- * dv in {64, 128}; otherwise a general kernel that takes any m whose per-column tiles fit the LDS
- * (m <= 64 for head dims up to 128) and d, dv multiples of 8 up to 256.  Larger grids are rejected
- * with VMO_ERR_UNSUPPORTED before any launch.
+ * (the recompute of vmonarch.py:66-68 owns them).  Kernels by grid: one MFMA tile per grid column for
+ * m <= 32 with d and dv in {64, 128}; multi-block MFMA kernels (one workgroup per column, 32 x 32 blocks)
+ * for m <= 128 with d and dv in {32, 64, 128}; otherwise a general kernel that takes any m whose
+ * per-column tiles fit the LDS and d, dv multiples of 8 up to 256.  Larger grids are rejected with
+ * VMO_ERR_UNSUPPORTED before any launch.
  */
 typedef struct vmo_lstep_args {
   int32_t dtype;
@@ -224,8 +225,9 @@ typedef struct vmo_fea_bwd_args {
  *               grad_out[k,j,:d] = scale sum_i dlogit[i,k] q[i,j]
  * grad_q is float32 and accumulated into (+=); grad_out (the dtype of q) is written.  Replaces
  * the autograd graph of the reference's L-step (batched einsum/softmax/clamp backward); there is
- * no launch site of its own in the reference.  Supported grids and head dims: as vmo_lstep_args (the
- * general kernel keeps one more m x m matrix and the gradient rows in LDS: m <= 64 up to head dim 128).
+ * no launch site of its own in the reference.  Supported grids and head dims: as vmo_lstep_args (one-tile
+ * kernels for m <= 32 at d, dv in {64, 128}; multi-block MFMA kernels for m <= 128 at d, dv in {32, 64, 128};
+ * the general kernel, which keeps one more m x m matrix and the gradient rows in LDS, beyond).
  */
 typedef struct vmo_lstep_bwd_args {
   int32_t dtype;

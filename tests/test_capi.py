@@ -110,8 +110,9 @@ def test_fea_fwd_empty_problem_is_a_no_op(L):
 
 
 def test_lstep_rejects_too_many_blocks(L):
-    """m = 200 frames: the one-tile kernels stop at 32 and the general ones need more LDS per grid
-    column than a CU has, so the call is refused on the host (the addresses are never dereferenced)."""
+    """m = 200 frames: the one-tile kernels stop at 32, the multi-block ones at 128, and the general ones need
+    more LDS per grid column than a CU has, so the call is refused on the host (the addresses are never
+    dereferenced)."""
     from vmonarch_amd import _lib
     a = _lib.LstepArgs()
     a.dtype, a.batch, a.heads, a.num_blocks, a.block_size, a.d, a.dv = 0, 1, 1, 200, 4, 128, 128
@@ -127,11 +128,11 @@ def test_lstep_rejects_too_many_blocks(L):
 def test_lstep_bwd_rejects_too_many_blocks_and_null_args(L):
     from vmonarch_amd import _lib
     a = _lib.LstepBwdArgs()
-    a.dtype, a.batch, a.heads, a.num_blocks, a.block_size, a.d, a.dv = 0, 1, 1, 100, 4, 128, 128
+    a.dtype, a.batch, a.heads, a.num_blocks, a.block_size, a.d, a.dv = 0, 1, 1, 200, 4, 128, 128
     v = _lib.View(_addr(), 128, 128, 128)
     a.q = a.out = a.grad_res = a.grad_q = a.grad_out = v
     a.ent = _addr()
-    assert L.vmo_lstep_bwd(ctypes.byref(a), None) == 2   # 100 frames: beyond the LDS of a CU
+    assert L.vmo_lstep_bwd(ctypes.byref(a), None) == 2   # 200 frames: beyond the multi-block kernels and the LDS
     assert b"LDS" in L.vmo_last_error()
     assert L.vmo_lstep_bwd(None, None) != 0
     a.num_blocks, a.delta = 40, _addr()                  # delta from a general (m > 32) kernel: not built

@@ -1064,7 +1064,8 @@ extern "C" int vmo_lstep_bwd(const vmo_lstep_bwd_args* a, void* stream) {
   if ((int64_t)a->batch * a->heads == 0) return VMO_OK;
   if (a->d <= 0 || (a->d % 8) != 0) return set_error(VMO_ERR_INVALID, "lstep_bwd: d");
   const bool one_tile = a->num_blocks <= 32 && one_tile_built(a->d, a->dv, a->last != 0);
-  if (!one_tile) {
+  const bool multi_block = !one_tile && mb_lstep_check(a->num_blocks, a->d, a->dv, a->last != 0, true);
+  if (!one_tile && !multi_block) {
     const int rc = lw_check(a->num_blocks, a->d, a->dv, a->last != 0, true, "lstep_bwd");
     if (rc != VMO_OK) return rc;
   }
@@ -1099,6 +1100,7 @@ extern "C" int vmo_lstep_bwd(const vmo_lstep_bwd_args* a, void* stream) {
   p.scale = a->scale;
   p.min_col_mass = a->min_col_mass;
   hipStream_t s = (hipStream_t)stream;
+  if (multi_block) return mb_lstep_bwd(p, a->dtype == VMO_DTYPE_F16, a->d, a->dv, a->last != 0, s);
   if (!one_tile) {
     const int lds = lw_layout(p.m, p.d, p.dv, a->last != 0, true).total;
     if (a->dtype == VMO_DTYPE_F16)

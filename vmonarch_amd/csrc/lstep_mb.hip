@@ -34,10 +34,13 @@ constexpr int kMbWaves = 4;
 constexpr int kMbMaxBlocks = 4;                  // one 32-row block per wave
 constexpr int kMbMaxFrames = 32 * kMbMaxBlocks;  // m <= 128
 
-// Byte offsets of a column's LDS arrays.  The row-store patches (kEpiPatchBytes per wave) reuse the start
-// of the allocation once every wave has passed the barrier that ends the compute.
+// Byte offsets of a column's LDS arrays: 16-bit row tiles (q, kr, and y for the last step; the backward's
+// upstream gradient), M-float vectors (entropy bias, row LSE; the backward's row sums rs_i, column factors f_k
+// and dc_k).  The forward's row-store patches (kEpiPatchBytes per wave) reuse the start of the allocation
+// once every wave has passed the barrier that ends the compute; the backward, which stores between its
+// passes, has patches of its own.
 struct MbLayout {
-  int q, k, y, g, e, lse, vec2, vec3, total;
+  int q, k, y, g, e, lse, rs, f, dc, patch, total;
 };
 __host__ __device__ inline MbLayout mb_layout(int M, int d, int dv, bool last, bool bwd) {
   MbLayout L;
@@ -49,8 +52,10 @@ __host__ __device__ inline MbLayout mb_layout(int M, int d, int dv, bool last, b
   L.g = bwd ? take(M * (last ? dv : d) * 2) : 0;
   L.e = take(M * 4);
   L.lse = take(M * 4);
-  L.vec2 = bwd ? take(M * 4) : 0;
-  L.vec3 = bwd ? take(M * 4) : 0;
+  L.rs = bwd ? take(M * 4) : 0;
+  L.f = bwd ? take(M * 4) : 0;
+  L.dc = bwd ? take(M * 4) : 0;
+  L.patch = bwd ? take(kMbWaves * kEpiPatchBytes) : 0;
   L.total = off > kMbWaves * kEpiPatchBytes ? off : kMbWaves * kEpiPatchBytes;
   return L;
 }
@@ -261,6 +266,373 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_kernel(LParams p) {
   }
 }
 
+
+// Backward of the multi-block L-step (the gradient autograd takes through vmonarch.py:51-63 with the entropy
+// bias detached, vmonarch.py:26), one 4-wave workgroup per grid column as the forward, with g the upstream
+// gradient rows (dz rows i when last, du rows k otherwise) staged beside q, kr (and y):
+//   last:  da[i,k] = g_i . y_k,  rs_i = sum_k a da,  dl = scale a (da - rs_i)
+//          pass A (wave = query block, one query row per lane): S^T and DA^T blocks -> lse_i, rs_i, then
+//          dq^T += Kr^T dl^T;  pass B (wave = key block, one key per lane): L and DA blocks ->
+//          dy^T += G^T a, dkr^T += Q^T dl
+//   else:  c_k = sum_i a, gv_k = sum_i a (g_k . q_i), f_k = scale / max(c_k, mcm),
+//          dc_k = -[c_k >= mcm] gv_k f_k / max(c_k, mcm),  da[i,k] = f_k (g_k . q_i) + dc_k
+//          pass 0 (query blocks): lse_i;  pass 1 (key blocks): c_k, gv_k -> f_k, dc_k;
+//          pass 2 (query blocks): rs_i, dq^T += Kr^T dl^T + G^T (a f)^T;  pass 3 (key blocks): dkr^T += Q^T dl
+// Every m x m block is recomputed where an orientation needs it (the MFMAs are cheap next to the column's
+// HBM traffic); the attention is exp2(logit - lse_i), exactly normalised.  MFMA operands a, dl and a f are
+// rounded to the 16-bit type, the sums rs, c, gv kept in fp32 from the fp32 attention.  dq (fp32) is added
+// to or overwritten, d out (the 16-bit type) written; rows past m carry zero attention and are not stored.
+template <bool F16, int D, int DV, bool LAST>
+__global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams p) {
+  using E = Elem<F16>;
+  using T = typename E::T;
+  using V8 = typename E::V8;
+  constexpr int NDS = D / 16, NDSV = DV / 16;
+  constexpr int ND = D / 32, NV = DV / 32;
+  constexpr int GW = LAST ? DV : D;
+  constexpr int RBD = D * 2, RBY = DV * 2, RBG = GW * 2;
+  extern __shared__ __attribute__((aligned(1024))) char smem_raw[];
+  VMO_LDS char* sm = (VMO_LDS char*)smem_raw;
+
+  const int m = p.m, MB = (m + 31) / 32, M = 32 * MB;
+  const MbLayout Lo = mb_layout(M, D, DV, LAST, true);
+  VMO_LDS char* q_t = sm + Lo.q;
+  VMO_LDS char* k_t = sm + Lo.k;
+  VMO_LDS char* y_t = sm + Lo.y;
+  VMO_LDS char* g_t = sm + Lo.g;
+  VMO_LDS float* e_t = (VMO_LDS float*)(sm + Lo.e);
+  VMO_LDS float* lse_t = (VMO_LDS float*)(sm + Lo.lse);
+  VMO_LDS float* rs_t = (VMO_LDS float*)(sm + Lo.rs);
+  VMO_LDS float* f_t = (VMO_LDS float*)(sm + Lo.f);
+  VMO_LDS float* dc_t = (VMO_LDS float*)(sm + Lo.dc);
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int hl = lane >> 5, l32 = lane & 31;
+  VMO_LDS float* patch = (VMO_LDS float*)(sm + Lo.patch + wave * kEpiPatchBytes);
+
+  const int col = blockIdx.x, bh = col / p.bs, j = col % p.bs, hh = bh % p.heads, bb = bh / p.heads;
+  const int64_t q_rs = (int64_t)p.bs * p.q_sn, o_rs = (int64_t)p.bs * p.out_sn, g_rs = (int64_t)p.bs * p.g_sn;
+  const int64_t dq_rs = (int64_t)p.bs * p.dq_sn, do_rs = (int64_t)p.bs * p.do_sn;
+  const T* qcol = (const T*)p.q + bb * p.q_sb + hh * p.q_sh + (int64_t)j * p.q_sn;
+  const T* ocol = (const T*)p.out + bb * p.out_sb + hh * p.out_sh + (int64_t)j * p.out_sn;
+  const T* gcol = (const T*)p.g + bb * p.g_sb + hh * p.g_sh + (int64_t)j * p.g_sn;
+  float* dqcol = p.dq + bb * p.dq_sb + hh * p.dq_sh + (int64_t)j * p.dq_sn;
+  T* dcol = (T*)p.dout + bb * p.do_sb + hh * p.do_sh + (int64_t)j * p.do_sn;
+
+  mb_stage<T, D>(qcol, q_rs, m, M, q_t, wave, lane);
+  mb_stage<T, D>(ocol, o_rs, m, M, k_t, wave, lane);
+  if constexpr (LAST) mb_stage<T, DV>(ocol + D, o_rs, m, M, y_t, wave, lane);
+  mb_stage<T, GW>(gcol, g_rs, m, M, g_t, wave, lane);
+  const float* ep = p.ent + bb * p.ent_sb + hh * p.ent_sh + j;
+  for (int k = tid; k < M; k += 64 * kMbWaves) e_t[k] = k < m ? ep[(int64_t)k * p.bs] * kLog2e : -1.0e30f;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if constexpr (LAST) {   // z rows of tokens < skip are the recompute's: no gradient reaches the L-path
+    constexpr int CH = RBG / 16;
+    for (int idx = tid; idx < M * CH; idx += 64 * kMbWaves) {
+      const int r = idx / CH;
+      if ((int64_t)r * p.bs + j < p.skip) *(VMO_LDS i32x4*)(g_t + r * RBG + (idx % CH) * 16) = i32x4{0, 0, 0, 0};
+    }
+    __syncthreads();
+  }
+
+  const float c = p.logit_scale_log2;
+  const int blk = wave;
+  const bool busy = blk < MB;
+  const int dq_mode = p.dq_overwrite ? kGradStoreF32 : kGradAddF32;
+
+  // S^T block (keys kb x queries of qb, one query row per lane), biased, log2 units
+  auto s_block = [&](int kb, const V8 (&qb)[NDS]) __attribute__((always_inline)) {
+    f32x16 x = f32x16{};
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds) x = E::mfma(mb_row8<V8, RBD>(k_t + 32 * kb * RBD, l32, hl, ds), qb[ds], x);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 ev = *(const VMO_LDS f32x4*)(e_t + 32 * kb + 8 * g + 4 * hl);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[4 * g + e] = fmaf(x[4 * g + e], c, ev[e]);
+    }
+    return x;
+  };
+  // L block (queries ib x keys of key block kb, one key per lane): attn = exp2(c q.kr + e_k - lse_i); the kr
+  // operand rows are read at each use (the passes that call this hold two accumulator sets)
+  auto attn_block = [&](int ib, int kb, float ek) __attribute__((always_inline)) {
+    f32x16 x = f32x16{};
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds)
+      x = E::mfma(mb_row8<V8, RBD>(q_t + 32 * ib * RBD, l32, hl, ds), mb_row8<V8, RBD>(k_t + 32 * kb * RBD, l32, hl, ds), x);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 lv = *(const VMO_LDS f32x4*)(lse_t + 32 * ib + 8 * g + 4 * hl);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[4 * g + e] = fast_exp2(fmaf(x[4 * g + e], c, ek - lv[e]));
+    }
+    return x;
+  };
+  // query block's row LSE from its S^T blocks (kept in x for the caller)
+  auto row_lse = [&](const V8 (&qb)[NDS], f32x16 (&x)[kMbMaxBlocks]) __attribute__((always_inline)) {
+    float mx = -3.0e38f;
+#pragma unroll
+    for (int kb = 0; kb < kMbMaxBlocks; ++kb) {
+      if (kb >= MB) break;
+      x[kb] = s_block(kb, qb);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, x[kb][r]);
+    }
+    mx = wave_max32(mx);
+    float sum = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < kMbMaxBlocks; ++kb) {
+      if (kb >= MB) break;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sum += fast_exp2(x[kb][r] - mx);
+    }
+    return mx + fast_log2(wave_sum32(sum));
+  };
+  auto load_rows = [&](V8 (&op)[NDS], const VMO_LDS char* tile, int b) __attribute__((always_inline)) {
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds) op[ds] = mb_row8<V8, RBD>(tile + 32 * b * RBD, l32, hl, ds);
+  };
+  const bool row_ok = 32 * blk + l32 < m;   // this lane's query row (query-block passes) or key (key-block passes)
+  const int nrows = busy ? min(32, m - 32 * blk) : 0;
+
+  if constexpr (LAST) {
+    // ---- pass A: one query row per lane
+    if (busy) {
+      V8 qb[NDS];
+      load_rows(qb, q_t, blk);
+      f32x16 x[kMbMaxBlocks];
+      const float lse = row_lse(qb, x);
+      auto da_block = [&](int kb) __attribute__((always_inline)) {   // DA^T[k][i] = y_k . g_i (g rows read at each use)
+        f32x16 d = f32x16{};
+#pragma unroll
+        for (int ds = 0; ds < NDSV; ++ds)
+          d = E::mfma(mb_row8<V8, RBY>(y_t + 32 * kb * RBY, l32, hl, ds), mb_row8<V8, RBY>(g_t + 32 * blk * RBY, l32, hl, ds),
+                      d);
+        return d;
+      };
+      float rs = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < kMbMaxBlocks; ++kb) {
+        if (kb >= MB) break;
+        const f32x16 d = da_block(kb);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) rs = fmaf(fast_exp2(x[kb][r] - lse), d[r], rs);
+      }
+      rs = wave_sum32(rs);
+      if (hl == 0) {
+        lse_t[32 * blk + l32] = row_ok ? lse : 1.0e30f;
+        rs_t[32 * blk + l32] = row_ok ? rs : 0.f;
+      }
+      f32x16 accq[ND];
+#pragma unroll
+      for (int a = 0; a < ND; ++a) accq[a] = f32x16{};
+#pragma unroll
+      for (int kb = 0; kb < kMbMaxBlocks; ++kb) {
+        if (kb >= MB) break;
+        f32x16 dl = da_block(kb);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dl[r] = p.scale * fast_exp2(x[kb][r] - lse) * (dl[r] - rs);
+        const V8 P0 = mb_pack<T, V8>(dl, 0, 1.f), P1 = mb_pack<T, V8>(dl, 1, 1.f);
+#pragma unroll
+        for (int a = 0; a < ND; ++a) {
+          accq[a] = E::mfma(mb_tr8<V8, RBD>(k_t + 32 * kb * RBD, lane, a, 0), P0, accq[a]);
+          accq[a] = E::mfma(mb_tr8<V8, RBD>(k_t + 32 * kb * RBD, lane, a, 1), P1, accq[a]);
+        }
+      }
+      store_acc_rows<F16>(patch, accq, ND, 1.f, dq_mode, (char*)(dqcol + 32 * blk * dq_rs), dq_rs * 4, nrows, lane);
+    }
+    __syncthreads();
+    // ---- pass B: one key per lane, as two sweeps over the query blocks (dy, then dkr: holding both accumulator
+    // sets at once spills at 128 / 128, and recomputing the attention block is cheap next to the HBM traffic)
+    if (busy) {
+      const float ek = e_t[32 * blk + l32];
+      f32x16 accy[NV];
+#pragma unroll
+      for (int a = 0; a < NV; ++a) accy[a] = f32x16{};
+#pragma unroll
+      for (int ib = 0; ib < kMbMaxBlocks; ++ib) {
+        if (ib >= MB) break;
+        const f32x16 at = attn_block(ib, blk, ek);
+        // dy^T[dv][k] += sum_i g^T[dv][i] a[i][k]
+        const V8 A0 = mb_pack<T, V8>(at, 0, 1.f), A1 = mb_pack<T, V8>(at, 1, 1.f);
+#pragma unroll
+        for (int a = 0; a < NV; ++a) {
+          accy[a] = E::mfma(mb_tr8<V8, RBY>(g_t + 32 * ib * RBY, lane, a, 0), A0, accy[a]);
+          accy[a] = E::mfma(mb_tr8<V8, RBY>(g_t + 32 * ib * RBY, lane, a, 1), A1, accy[a]);
+        }
+      }
+      store_acc_rows<F16>(patch, accy, NV, 1.f, kGradStore, (char*)(dcol + 32 * blk * do_rs + D), do_rs * 2, nrows,
+                          lane);
+      f32x16 acck[ND];
+#pragma unroll
+      for (int a = 0; a < ND; ++a) acck[a] = f32x16{};
+#pragma unroll
+      for (int ib = 0; ib < kMbMaxBlocks; ++ib) {
+        if (ib >= MB) break;
+        const f32x16 at = attn_block(ib, blk, ek);
+        // DA[i][k] = g_i . y_k, dl = scale a (da - rs_i)
+        f32x16 dl = f32x16{};
+#pragma unroll
+        for (int ds = 0; ds < NDSV; ++ds)
+          dl = E::mfma(mb_row8<V8, RBY>(g_t + 32 * ib * RBY, l32, hl, ds), mb_row8<V8, RBY>(y_t + 32 * blk * RBY, l32, hl, ds),
+                       dl);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 rv = *(const VMO_LDS f32x4*)(rs_t + 32 * ib + 8 * g + 4 * hl);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) dl[4 * g + e] = p.scale * at[4 * g + e] * (dl[4 * g + e] - rv[e]);
+        }
+        const V8 P0 = mb_pack<T, V8>(dl, 0, 1.f), P1 = mb_pack<T, V8>(dl, 1, 1.f);
+#pragma unroll
+        for (int a = 0; a < ND; ++a) {
+          acck[a] = E::mfma(mb_tr8<V8, RBD>(q_t + 32 * ib * RBD, lane, a, 0), P0, acck[a]);
+          acck[a] = E::mfma(mb_tr8<V8, RBD>(q_t + 32 * ib * RBD, lane, a, 1), P1, acck[a]);
+        }
+      }
+      store_acc_rows<F16>(patch, acck, ND, 1.f, kGradStore, (char*)(dcol + 32 * blk * do_rs), do_rs * 2, nrows, lane);
+    }
+  } else {
+    // ---- pass 0: row LSE (query blocks)
+    if (busy) {
+      V8 qb[NDS];
+      load_rows(qb, q_t, blk);
+      f32x16 x[kMbMaxBlocks];
+      const float lse = row_lse(qb, x);
+      if (hl == 0) lse_t[32 * blk + l32] = row_ok ? lse : 1.0e30f;
+    }
+    __syncthreads();
+    // ---- pass 1: column mass c_k and gv_k = sum_i a (g_k . q_i) (key blocks) -> f_k, dc_k
+    if (busy) {
+      V8 gop[NDS];
+      load_rows(gop, g_t, blk);
+      const float ek = e_t[32 * blk + l32];
+      float cs = 0.f, gv = 0.f;
+#pragma unroll
+      for (int ib = 0; ib < kMbMaxBlocks; ++ib) {
+        if (ib >= MB) break;
+        const f32x16 at = attn_block(ib, blk, ek);
+        f32x16 gq = f32x16{};   // GQ[i][k] = q_i . g_k
+#pragma unroll
+        for (int ds = 0; ds < NDS; ++ds) gq = E::mfma(mb_row8<V8, RBD>(q_t + 32 * ib * RBD, l32, hl, ds), gop[ds], gq);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          cs += at[r];
+          gv = fmaf(at[r], gq[r], gv);
+        }
+      }
+      cs = wave_sum32(cs);
+      gv = wave_sum32(gv);
+      const float cm = fmaxf(cs, p.min_col_mass), f = p.scale / cm;
+      if (hl == 0) {
+        f_t[32 * blk + l32] = f;
+        dc_t[32 * blk + l32] = (row_ok && cs >= p.min_col_mass) ? -gv * f / cm : 0.f;
+      }
+    }
+    __syncthreads();
+    // ---- pass 2: rs_i and dq (query blocks)
+    if (busy) {
+      V8 qb[NDS];
+      load_rows(qb, q_t, blk);
+      f32x16 x[kMbMaxBlocks];
+      const float lse = lse_t[32 * blk + l32];
+#pragma unroll
+      for (int kb = 0; kb < kMbMaxBlocks; ++kb) {
+        if (kb >= MB) break;
+        x[kb] = s_block(kb, qb);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) x[kb][r] = fast_exp2(x[kb][r] - lse);   // attn^T[k][i]
+      }
+      // da^T[k][i] = f_k (g_k . q_i) + dc_k
+      auto da_block = [&](int kb) __attribute__((always_inline)) {
+        f32x16 d = f32x16{};
+#pragma unroll
+        for (int ds = 0; ds < NDS; ++ds) d = E::mfma(mb_row8<V8, RBD>(g_t + 32 * kb * RBD, l32, hl, ds), qb[ds], d);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 fv = *(const VMO_LDS f32x4*)(f_t + 32 * kb + 8 * g + 4 * hl);
+          const f32x4 cv = *(const VMO_LDS f32x4*)(dc_t + 32 * kb + 8 * g + 4 * hl);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) d[4 * g + e] = fmaf(fv[e], d[4 * g + e], cv[e]);
+        }
+        return d;
+      };
+      float rs = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < kMbMaxBlocks; ++kb) {
+        if (kb >= MB) break;
+        const f32x16 d = da_block(kb);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) rs = fmaf(x[kb][r], d[r], rs);
+      }
+      rs = wave_sum32(rs);
+      if (hl == 0) rs_t[32 * blk + l32] = row_ok ? rs : 0.f;
+      f32x16 accq[ND];
+#pragma unroll
+      for (int a = 0; a < ND; ++a) accq[a] = f32x16{};
+#pragma unroll
+      for (int kb = 0; kb < kMbMaxBlocks; ++kb) {
+        if (kb >= MB) break;
+        f32x16 dl = da_block(kb), af;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 fv = *(const VMO_LDS f32x4*)(f_t + 32 * kb + 8 * g + 4 * hl);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * g + e;
+            af[r] = x[kb][r] * fv[e];
+            dl[r] = p.scale * x[kb][r] * (dl[r] - rs);
+          }
+        }
+        const V8 P0 = mb_pack<T, V8>(dl, 0, 1.f), P1 = mb_pack<T, V8>(dl, 1, 1.f);
+        const V8 F0 = mb_pack<T, V8>(af, 0, 1.f), F1 = mb_pack<T, V8>(af, 1, 1.f);
+#pragma unroll
+        for (int a = 0; a < ND; ++a) {
+          accq[a] = E::mfma(mb_tr8<V8, RBD>(k_t + 32 * kb * RBD, lane, a, 0), P0, accq[a]);
+          accq[a] = E::mfma(mb_tr8<V8, RBD>(k_t + 32 * kb * RBD, lane, a, 1), P1, accq[a]);
+          accq[a] = E::mfma(mb_tr8<V8, RBD>(g_t + 32 * kb * RBD, lane, a, 0), F0, accq[a]);
+          accq[a] = E::mfma(mb_tr8<V8, RBD>(g_t + 32 * kb * RBD, lane, a, 1), F1, accq[a]);
+        }
+      }
+      store_acc_rows<F16>(patch, accq, ND, 1.f, dq_mode, (char*)(dqcol + 32 * blk * dq_rs), dq_rs * 4, nrows, lane);
+    }
+    __syncthreads();
+    // ---- pass 3: dkr (key blocks)
+    if (busy) {
+      V8 gop[NDS];
+      load_rows(gop, g_t, blk);
+      const float ek = e_t[32 * blk + l32];
+      const float fk = f_t[32 * blk + l32], dck = dc_t[32 * blk + l32];
+      f32x16 acck[ND];
+#pragma unroll
+      for (int a = 0; a < ND; ++a) acck[a] = f32x16{};
+#pragma unroll
+      for (int ib = 0; ib < kMbMaxBlocks; ++ib) {
+        if (ib >= MB) break;
+        const f32x16 at = attn_block(ib, blk, ek);
+        f32x16 dl = f32x16{};
+#pragma unroll
+        for (int ds = 0; ds < NDS; ++ds) dl = E::mfma(mb_row8<V8, RBD>(q_t + 32 * ib * RBD, l32, hl, ds), gop[ds], dl);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 rv = *(const VMO_LDS f32x4*)(rs_t + 32 * ib + 8 * g + 4 * hl);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * g + e;
+            dl[r] = p.scale * at[r] * (fmaf(fk, dl[r], dck) - rv[e]);
+          }
+        }
+        const V8 P0 = mb_pack<T, V8>(dl, 0, 1.f), P1 = mb_pack<T, V8>(dl, 1, 1.f);
+#pragma unroll
+        for (int a = 0; a < ND; ++a) {
+          acck[a] = E::mfma(mb_tr8<V8, RBD>(q_t + 32 * ib * RBD, lane, a, 0), P0, acck[a]);
+          acck[a] = E::mfma(mb_tr8<V8, RBD>(q_t + 32 * ib * RBD, lane, a, 1), P1, acck[a]);
+        }
+      }
+      store_acc_rows<F16>(patch, acck, ND, 1.f, kGradStore, (char*)(dcol + 32 * blk * do_rs), do_rs * 2, nrows, lane);
+    }
+  }
+}
+
 // Head-dim pairs the multi-block kernels are built for.
 static bool mb_dims(int d, int dv, bool last) {
   const auto ok = [](int x) { return x == 32 || x == 64 || x == 128; };
@@ -300,6 +672,36 @@ static int dispatch_mb(const LParams& p, int d, int dv, bool last, hipStream_t s
 
 int mb_lstep_fwd(const LParams& p, bool f16, int d, int dv, bool last, hipStream_t s) {
   return f16 ? dispatch_mb<true>(p, d, dv, last, s) : dispatch_mb<false>(p, d, dv, last, s);
+}
+
+template <bool F16, int D, int DV, bool LAST>
+static int launch_mb_bwd(const LBParams& p, hipStream_t s) {
+  const int M = 32 * ((p.m + 31) / 32);
+  const int lds = mb_layout(M, D, DV, LAST, true).total;
+  auto kern = lstep_mb_bwd_kernel<F16, D, DV, LAST>;
+  if (lds > 65536 && hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
+    return set_error(VMO_ERR_LAUNCH, "lstep_mb_bwd: cannot raise the LDS limit to %d bytes", lds);
+  hipLaunchKernelGGL(kern, dim3(p.cols_total), dim3(64 * kMbWaves), lds, s, p);
+  return launch_status("lstep_mb_bwd");
+}
+
+template <bool F16>
+static int dispatch_mb_bwd(const LBParams& p, int d, int dv, bool last, hipStream_t s) {
+#define VMO_MB(D_, DV_)                                                                   \
+  if (d == D_ && dv == DV_ && last) return launch_mb_bwd<F16, D_, DV_, true>(p, s);
+#define VMO_MB_U(D_) \
+  if (d == D_ && !last) return launch_mb_bwd<F16, D_, D_, false>(p, s);
+  VMO_MB_U(32) VMO_MB_U(64) VMO_MB_U(128)
+  VMO_MB(32, 32) VMO_MB(32, 64) VMO_MB(32, 128)
+  VMO_MB(64, 32) VMO_MB(64, 64) VMO_MB(64, 128)
+  VMO_MB(128, 32) VMO_MB(128, 64) VMO_MB(128, 128)
+#undef VMO_MB
+#undef VMO_MB_U
+  return set_error(VMO_ERR_UNSUPPORTED, "lstep_mb_bwd: no kernel for d=%d dv=%d last=%d", d, dv, (int)last);
+}
+
+int mb_lstep_bwd(const LBParams& p, bool f16, int d, int dv, bool last, hipStream_t s) {
+  return f16 ? dispatch_mb_bwd<true>(p, d, dv, last, s) : dispatch_mb_bwd<false>(p, d, dv, last, s);
 }
 
 }  // namespace vmo

@@ -52,5 +52,6 @@ struct LBParams {
 // mb_lstep_check: whether they take (m, d, dv) (forward or backward); mb_lstep_fwd / mb_lstep_bwd launch.
 int mb_lstep_check(int m, int d, int dv, bool last, bool bwd);
 int mb_lstep_fwd(const LParams& p, bool f16, int d, int dv, bool last, hipStream_t s);
+int mb_lstep_bwd(const LBParams& p, bool f16, int d, int dv, bool last, hipStream_t s);
 
 }  // namespace vmo

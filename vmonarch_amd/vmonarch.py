@@ -119,7 +119,7 @@ def _lstep_general_lds(m, d, dv, last, bwd):
 
 
 _MB_MAX_FRAMES = 128
-_MB_BWD = False   # the multi-block backward kernels
+_MB_BWD = True    # the multi-block backward kernels
 
 
 def _lstep_mb_lds(m, d, dv, last, bwd):
@@ -129,8 +129,8 @@ def _lstep_mb_lds(m, d, dv, last, bwd):
     M = 32 * ((m + 31) // 32)
     r = lambda b: (b + 255) // 256 * 256   # noqa: E731
     total = 2 * r(M * d * 2) + (r(M * dv * 2) if last else 0) + 2 * r(M * 4)
-    if bwd:
-        total += r(M * (dv if last else d) * 2) + 2 * r(M * 4)
+    if bwd:   # the upstream gradient rows, three more vectors, the backward's own row-store patches
+        total += r(M * (dv if last else d) * 2) + 3 * r(M * 4) + 4 * 4096
     return max(total, 4 * 4096)
 
 
