@@ -60,19 +60,24 @@ __host__ __device__ inline MbLayout mb_layout(int M, int d, int dv, bool last, b
   return L;
 }
 
-// Stage M rows of W 16-bit values (row r < m: src + r rs; rows past m repeat row m - 1) into a tile whose
-// chunk c of row r sits at chunk c ^ swz_rows(r): wave instruction inst covers rows inst RPI .. + RPI - 1,
-// lane l lands at byte 16 l of its 1 KB and so loads global chunk (l % CH) ^ swz_rows(row).
+// Stage M rows of W 16-bit values (row r < m: src + r rs) into a tile whose chunk c of row r sits at chunk
+// c ^ swz_rows(r): wave instruction inst covers rows inst RPI .. + RPI - 1, lane l lands at byte 16 l of its
+// 1 KB and so loads global chunk (l % CH) ^ swz_rows(row).  Only instructions that hold a row below m copy
+// (their rows past m repeat row m - 1); the rows after them are zeroed -- finite data whose weights are exact
+// zeros, without copying the last row over and over.
 template <class T, int W>
 __device__ __forceinline__ void mb_stage(const T* src, int64_t rs, int m, int M, VMO_LDS char* dst, int wave,
                                          int lane) {
   constexpr int RB = W * 2, CH = RB / 16, RPI = 64 / CH;
   const int c = lane % CH;
-  for (int inst = wave; inst * RPI < M; inst += kMbWaves) {
+  const int ninst = (m + RPI - 1) / RPI;
+  for (int inst = wave; inst < ninst; inst += kMbWaves) {
     const int r = inst * RPI + lane / CH;
     const int rr = r < m ? r : m - 1;
     g2l_16(src + (int64_t)rr * rs + (c ^ swz_rows<RB>(r)) * 8, dst + inst * 1024);
   }
+  for (int o = ninst * 1024 + (64 * wave + lane) * 16; o < M * RB; o += 64 * kMbWaves * 16)
+    *(VMO_LDS i32x4*)(dst + o) = i32x4{0, 0, 0, 0};
 }
 
 // Row-read MFMA operand: lane (row l32 of a 32-row block at `rows`, half hl) gets elements 16 ds + 8 hl .. + 7.
@@ -256,13 +261,13 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_kernel(LParams p) {
   if (!busy) return;
   VMO_LDS float* patch = (VMO_LDS float*)(sm + wave * kEpiPatchBytes);
   const int nrows = min(32, m - 32 * blk);
+  T* const rows = rcol + 32 * blk * r_rs;
   if constexpr (LAST) {
     // z rows i from the first one the recompute does not overwrite (token i b + j >= skip)
     const int ibeg = p.skip > j ? (p.skip - j + p.bs - 1) / p.bs : 0;
-    store_acc_rows<F16>(patch, acc, NACC, 1.f, kGradStore, (char*)(rcol + 32 * blk * r_rs), r_rs * 2, nrows, lane,
-                        max(0, ibeg - 32 * blk));
+    store_acc_rows<F16>(patch, acc, NACC, 1.f, kGradStore, (char*)rows, r_rs * 2, nrows, lane, max(0, ibeg - 32 * blk));
   } else {
-    store_acc_rows<F16>(patch, acc, NACC, fscale, kGradStore, (char*)(rcol + 32 * blk * r_rs), r_rs * 2, nrows, lane);
+    store_acc_rows<F16>(patch, acc, NACC, fscale, kGradStore, (char*)rows, r_rs * 2, nrows, lane);
   }
 }
 
