@@ -146,8 +146,8 @@ def test_vmonarch_head_dim_32_native(m, b, rt):
 
 @pytest.mark.parametrize("D, Dv", [(32, 64), (32, 128), (64, 32), (128, 32), (16, 64), (16, 256), (32, 256)])
 def test_narrow_and_wide_head_mixes(D, Dv):
-    """A 32-wide (or 16-wide) dim with a wider one: the 32 / 64, 32 / 128, 64 / 32 and 128 / 32 kernels, and
-    32 / 256 through q, k zero-padded to 64; o, e and the gradients against the oracle."""
+    """A 32-wide (or 16-wide) dim with a wider one: the 32 / 64, 32 / 128, 32 / 256, 64 / 32 and 128 / 32 kernels
+    (16-wide dims zero-padded to 32); o, e and the gradients against the oracle."""
     from vmonarch_amd import flash_entropy_attention
     g = torch.Generator().manual_seed(4000 + D + 3 * Dv)
     N = 333
@@ -204,3 +204,31 @@ def test_vmonarch_head_dim_32_fp16():
     refs = vmonarch_attention_grad(qn, kn, vn, do.numpy(), m, b, 2, rt)
     for gd, gr, name in zip(grads, refs, ("dq", "dk", "dv")):
         assert_grad_close(gd.float().cpu().numpy(), gr, 5e-2, name)
+
+
+@pytest.mark.parametrize("D, Dv", [(32, 256), (32, 64), (128, 32), (64, 256)])
+def test_head_mixes_make_no_padded_copies(D, Dv, monkeypatch):
+    """Pairs with a native kernel run on the caller's tensors: forward and backward never zero-pad a feature dim
+    (torch.nn.functional.pad is made to raise for the duration of the call), with o and the gradients checked
+    against the oracle."""
+    from vmonarch_amd import flash_entropy_attention
+
+    def no_pad(*args, **kwargs):
+        raise AssertionError("a zero-padded copy was made")
+
+    g = torch.Generator().manual_seed(4100 + D + Dv)
+    N = 200
+    q, k, v = randn_lp(g, 1, 2, N, D), randn_lp(g, 1, 2, N, D), randn_lp(g, 1, 2, N, Dv)
+    do, de = torch.randn(1, 2, N, Dv, generator=g), torch.randn(1, 2, N, generator=g)
+    leaves = [t.to(DEV).requires_grad_() for t in (q, k, v)]
+    print(f"head mix without padding D={D} Dv={Dv}", flush=True)
+    monkeypatch.setattr(torch.nn.functional, "pad", no_pad)
+    o, e = flash_entropy_attention(*leaves)
+    grads = torch.autograd.grad((o.float() * do.to(DEV)).sum() + (e * de.to(DEV)).sum(), leaves)
+    monkeypatch.undo()
+    qn, kn, vn = (t.float().numpy() for t in (q, k, v))
+    o_ref, e_ref = entropy_attention(qn, kn, vn, D ** -0.5)
+    _check(o.detach(), e.detach(), o_ref, e_ref)
+    refs = entropy_attention_grad(qn, kn, vn, do.bfloat16().float().numpy(), de.numpy(), D ** -0.5)
+    for gd, gr, name in zip(grads, refs, ("dq", "dk", "dv")):
+        assert_grad_close(gd.float().cpu().numpy(), gr, 3e-2, name)

@@ -1051,6 +1051,7 @@ static int dispatch_bwd(const BwdParams& p, int d, int dv, hipStream_t s) {
   if (d == 64 && dv == 128) return launch_bwd<F16, 64, 128>(p, s);
   if (d == 128 && dv == 64) return launch_bwd<F16, 128, 64>(p, s);
   if (d == 128 && dv == 128) return launch_bwd<F16, 128, 128>(p, s);
+  if (d == 32 && dv == 256) return launch_bwd<F16, 32, 256>(p, s);
   if (d == 64 && dv == 256) return launch_bwd<F16, 64, 256>(p, s);
   if (d == 128 && dv == 256) return launch_bwd<F16, 128, 256>(p, s);
   if (d == 256 && dv == 256) return launch_bwd<F16, 256, 256>(p, s);

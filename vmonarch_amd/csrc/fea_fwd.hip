@@ -907,6 +907,7 @@ static int dispatch_fwd(const FwdParams& p, int d, int dw0, int dw1, bool w0k, b
   VMO_FWD(32, 32, 0, false, kEntNone, false)
   VMO_FWD(64, 64, 0, false, kEntOnline, false)
   VMO_FWD(64, 128, 0, false, kEntOnline, false)
+  VMO_FWD(32, 256, 0, false, kEntOnline, false)
   VMO_FWD(64, 256, 0, false, kEntOnline, false)
   VMO_FWD(128, 64, 0, false, kEntOnline, false)
   VMO_FWD(128, 128, 0, false, kEntOnline, false)

@@ -24,13 +24,9 @@ def _pad_features(t, width):
 
 def _kernel_widths(d, dv):
     """Head dims of the flash-entropy kernels (forward and backward) that serve (d, dv): each dim of at most 32
-    runs 32 wide (16 zero-padded to 32), wider ones as they are (64, 128, 256); the 32 / 256 pair, which has
-    no kernel, takes q and k zero-padded to 64."""
+    runs 32 wide (16 zero-padded to 32), wider ones as they are (64, 128, 256)."""
     w = lambda x: 32 if x <= 32 else x   # noqa: E731
-    dk, dvk = w(d), w(dv)
-    if dk == 32 and dvk == 256:
-        dk = 64
-    return dk, dvk
+    return w(d), w(dv)
 
 
 def fea_forward(q, k, w0, w1, sm_scale, frames=1, o=None, lse=None, ent=None, want_ent=True, want_lse=True,
