@@ -66,10 +66,11 @@ typedef struct vmo_view {
  * ranges (split-KV, for problems with few query tiles such as the recompute of
  * vmonarch.py:66-68); it needs ent == NULL and a workspace of
  * vmo_fea_fwd_workspace_size() bytes.  Supported (d, dw0): with entropy output and one split, d in {64, 128}
- * with dw0 in {64, 128, 256}, (256, 256), and the 32-wide (32, 32), (32, 64), (32, 128), (64, 32), (128, 32);
- * without entropy, one split or several, (32, 32), (64, 64), (64, 128), (128, 64), (128, 128).  Values that
- * start with k (w0 aliasing k, entropy, one split): d = dw0 in {32, 64, 128} with dw1 in {0, d}, and
- * dw1 = 128 at d = 64, dw1 = 64 at d = 128.  sm_scale >= 0.
+ * with dw0 in {64, 128, 256}, (256, 256), d = 16 or 32 with dw0 in {d, 32, 64, 128, 256}, (64, 32), (128, 32);
+ * without entropy, one split or several, (16, 16), (32, 32), (64, 64), (64, 128), (128, 64), (128, 128).  Values
+ * that start with k (w0 aliasing k, entropy, one split): d = dw0 in {16, 32, 64, 128} with dw1 in {0, d}, and
+ * dw1 = 128 at d = 64, dw1 = 64 at d = 128.  16-wide q / k or values are read as they are (no padded copy is
+ * expected from the caller).  sm_scale >= 0.
  */
 typedef struct vmo_fea_fwd_args {
   int32_t dtype;
@@ -108,7 +109,7 @@ typedef struct vmo_fea_fwd_args {
  * (d features) or z (dv features).  With last == 1, tokens n < skip_tokens are not written
  * (the recompute of vmonarch.py:66-68 owns them).  Kernels by grid: one MFMA tile per grid column for
  * m <= 32 with d and dv in {64, 128}; multi-block MFMA kernels (one workgroup per column, 32 x 32 blocks)
- * for m <= 128 with d and dv in {32, 64, 128}; otherwise a general kernel that takes any m whose
+ * for m <= 128 with d and dv in {32, 64, 128} or d = dv = 16; otherwise a general kernel that takes any m whose
  * per-column tiles fit the LDS and d, dv multiples of 8 up to 256.  Larger grids are rejected with
  * VMO_ERR_UNSUPPORTED before any launch.
  */
@@ -138,8 +139,8 @@ typedef struct vmo_lstep_args {
  *   grad_q = sm_scale dS k,  grad_k = sm_scale dS^T q,  grad_v = P^T grad_o
  * with P rebuilt from `lse` (log2 units, as written by vmo_fea_fwd).  nq queries attend to nk
  * keys per (batch, head) (nq != nk allowed).  Supported: d in {64, 128} with dv in {64, 128, 256},
- * d = dv = 256, and the 32-wide (32, 32), (32, 64), (32, 128), (64, 32), (128, 32).  Needs
- * vmo_fea_bwd_workspace_size() bytes of workspace.
+ * d = dv = 256, d = 16 or 32 with dv in {d, 32, 64, 128, 256}, (64, 32) and (128, 32) (16-wide rows read as
+ * they are).  Needs vmo_fea_bwd_workspace_size() bytes of workspace.
  */
 /* vmo_fea_bwd_args.flags: the marked gradient is float32 and the kernels add into it (+=, ACCUM) or
  * overwrite it (=, F32); without either bit it has the inputs' dtype.  ACCUM and F32 of the same
@@ -147,9 +148,9 @@ typedef struct vmo_lstep_args {
  * VMO_BWD_FOLD_K: the values are k, or [k | v1] (v is k: same address and strides), as in the
  * VMonarch R-steps (vmonarch.py:50, where autograd sums k's two gradients).  grad_k then receives
  * k's whole gradient, key role plus value role, and grad_v only v1's (dv1 columns; with values k
- * alone grad_v is not written and may be null).  Built for (d, dv) = (32, 32), (64, 64), (128, 128) and,
- * with v1, (32, 64), (64, 128), (128, 256); other shapes, or values that do not start with k, are
- * rejected. */
+ * alone grad_v is not written and may be null).  Built for (d, dv) = (16, 16), (32, 32), (64, 64), (128, 128)
+ * and, with v1, (16, 32), (32, 64), (64, 128), (128, 256); other shapes, or values that do not start with k,
+ * are rejected. */
 enum {
   VMO_BWD_ACCUM_Q = 1, VMO_BWD_ACCUM_K = 2, VMO_BWD_ACCUM_V = 4,
   VMO_BWD_F32_Q = 8, VMO_BWD_F32_K = 16, VMO_BWD_F32_V = 32,
@@ -194,7 +195,7 @@ typedef struct vmo_fea_bwd_args {
   /* Values given in two parts: with dv1 > 0 the value tensor is [v | v1], v holding columns
    * [0, dv - dv1) and v1 (same strides as v) the last dv1 (VMonarch's last R-step, values [k | v],
    * vmonarch.py:50, without the concatenated copy).  Built for dv1 = dv / 2 with (d, dv) = (64, 128)
-   * and (128, 256).  grad_v stays one (.., dv) tensor. */
+   * and (128, 256), and when v is k also (16, 32) and (32, 64).  grad_v stays one (.., dv) tensor. */
   vmo_view v1;
   int32_t dv1;
   vmo_view grad_k_base, grad_v_base;   /* fp32, read with VMO_BWD_SUM_K / VMO_BWD_SUM_V */
@@ -226,7 +227,8 @@ typedef struct vmo_fea_bwd_args {
  * grad_q is float32 and accumulated into (+=); grad_out (the dtype of q) is written.  Replaces
  * the autograd graph of the reference's L-step (batched einsum/softmax/clamp backward); there is
  * no launch site of its own in the reference.  Supported grids and head dims: as vmo_lstep_args (one-tile
- * kernels for m <= 32 at d, dv in {64, 128}; multi-block MFMA kernels for m <= 128 at d, dv in {32, 64, 128};
+ * kernels for m <= 32 at d, dv in {64, 128}; multi-block MFMA kernels for m <= 128 at d, dv in {32, 64, 128} or
+ * d = dv = 16;
  * the general kernel, which keeps one more m x m matrix and the gradient rows in LDS, beyond).
  */
 typedef struct vmo_lstep_bwd_args {

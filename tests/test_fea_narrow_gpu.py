@@ -1,4 +1,4 @@
-"""The 32-wide flash-entropy kernels (heads of at most 32; 16-wide heads zero-padded to 32 by the caller)
+"""The narrow flash-entropy kernels (heads of 32, and of 16 held as 32-wide LDS tiles with each row twice)
 against the CPU oracle: the reference's narrow head dims (kernel.py:324), ragged N, fp16, frames, the
 no-entropy variant called through the C ABI, the exact two-pass path of the fixed reference point, and the
 gradients (dq with key splits at N = 4096).  Tolerances as tests/test_fea_gpu.py: the reference metric
@@ -146,8 +146,8 @@ def test_vmonarch_head_dim_32_native(m, b, rt):
 
 @pytest.mark.parametrize("D, Dv", [(32, 64), (32, 128), (64, 32), (128, 32), (16, 64), (16, 256), (32, 256)])
 def test_narrow_and_wide_head_mixes(D, Dv):
-    """A 32-wide (or 16-wide) dim with a wider one: the 32 / 64, 32 / 128, 32 / 256, 64 / 32 and 128 / 32 kernels
-    (16-wide dims zero-padded to 32); o, e and the gradients against the oracle."""
+    """A 32-wide (or 16-wide) dim with a wider one: the 32 / 64, 32 / 128, 32 / 256, 64 / 32, 128 / 32, 16 / 64 and
+    16 / 256 kernels; o, e and the gradients against the oracle."""
     from vmonarch_amd import flash_entropy_attention
     g = torch.Generator().manual_seed(4000 + D + 3 * Dv)
     N = 333
@@ -206,7 +206,7 @@ def test_vmonarch_head_dim_32_fp16():
         assert_grad_close(gd.float().cpu().numpy(), gr, 5e-2, name)
 
 
-@pytest.mark.parametrize("D, Dv", [(32, 256), (32, 64), (128, 32), (64, 256)])
+@pytest.mark.parametrize("D, Dv", [(32, 256), (32, 64), (128, 32), (64, 256), (16, 16), (16, 32), (16, 64), (16, 256)])
 def test_head_mixes_make_no_padded_copies(D, Dv, monkeypatch):
     """Pairs with a native kernel run on the caller's tensors: forward and backward never zero-pad a feature dim
     (torch.nn.functional.pad is made to raise for the duration of the call), with o and the gradients checked
@@ -232,3 +232,43 @@ def test_head_mixes_make_no_padded_copies(D, Dv, monkeypatch):
     refs = entropy_attention_grad(qn, kn, vn, do.bfloat16().float().numpy(), de.numpy(), D ** -0.5)
     for gd, gr, name in zip(grads, refs, ("dq", "dk", "dv")):
         assert_grad_close(gd.float().cpu().numpy(), gr, 3e-2, name)
+
+
+@pytest.mark.parametrize("m, b, rt, dtype", [(21, 100, 100, torch.bfloat16), (8, 77, 30, torch.bfloat16),
+                                             (40, 24, 24, torch.bfloat16), (8, 100, 100, torch.float16)])
+def test_vmonarch_head_dim_16_native(m, b, rt, dtype, monkeypatch):
+    """VMonarch at D = Dv = 16 (the reference runs it: kernel.py:324 takes 16-wide heads) on the 16-wide kernels --
+    R-steps with values k and [k | v], the split-KV recompute, the multi-block L-steps, and their backward --
+    with no zero-padded copy (torch.nn.functional.pad raises for the duration of the calls): z and the gradients
+    against the oracle (reference metric 3e-2 / 5e-2 as tests/test_vmonarch.py:64-66, and z elementwise)."""
+    import vmonarch_amd.vmonarch as vm
+    from vmonarch_amd import vmonarch_attention
+
+    def no_pad(*args, **kwargs):
+        raise AssertionError("a zero-padded copy was made")
+
+    g = torch.Generator().manual_seed(3100 + m + b)
+    q, k, v = (randn_lp(g, 1, 2, m * b, 16, dtype=dtype) for _ in range(3))
+    do = torch.randn(1, 2, m * b, 16, generator=g)
+    assert vm._fused_supported(q.to(DEV), k.to(DEV), v.to(DEV), m)
+    print(f"vmonarch D=16 m={m} b={b} rt={rt} {dtype}", flush=True)
+    leaves = [t.to(DEV).requires_grad_() for t in (q, k, v)]
+    monkeypatch.setattr(torch.nn.functional, "pad", no_pad)
+    with torch.no_grad():
+        z = vmonarch_attention(*(t.detach() for t in leaves), m, b, 2, recompute_tokens=rt)
+    zg = vmonarch_attention(*leaves, m, b, 2, recompute_tokens=rt)
+    grads = torch.autograd.grad((zg.float() * do.to(DEV)).sum(), leaves)
+    monkeypatch.undo()
+    assert type(zg.grad_fn).__name__ == "_VMonarchFunctionBackward"
+    assert z.shape == (1, 2, m * b, 16) and z.dtype == dtype and torch.equal(zg.detach(), z)
+    qn, kn, vn = (t.float().numpy() for t in (q, k, v))
+    z_ref = vmonarch_oracle(qn, kn, vn, m, b, 2, rt)
+    zz = z.float().cpu().numpy()
+    assert np.isfinite(zz).all()
+    assert_close_ref(zz, z_ref, 3e-2)
+    assert_close_elementwise(zz, z_ref)
+    refs = vmonarch_attention_grad(qn, kn, vn, do.numpy(), m, b, 2, rt)
+    for gd, gr, t, name in zip(grads, refs, leaves, ("dq", "dk", "dv")):
+        assert gd.shape == t.shape and gd.dtype == dtype
+        assert_grad_close(gd.float().cpu().numpy(), gr, 5e-2, name)
+    assert hip_library_loaded()

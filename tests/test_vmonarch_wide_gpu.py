@@ -1,6 +1,7 @@
 """GPU parity of the VMonarch shapes outside the one-tile L-step kernels (m <= 32 frames, head dims 64 /
 128): the general L-step kernels (csrc/lstep.hip, lstep_wide_kernel / lstep_wide_bwd_kernel) for more
-frames and other head dims, head dims 16 / 32 (16 zero-padded to 32) and the zero-padded route for D != Dv with autograd,
+frames and other head dims, head dims 16 / 32 (16-wide rows held in 32-wide LDS tiles) and the zero-padded route for
+D != Dv with autograd,
 and the flash-entropy backward at narrow head dims -- all against the CPU oracle, with the same
 tolerances as the rest of the suite: elementwise 2e-2 + 1e-2 |ref| beside the reference's metric (3e-2 for
 z, 5e-2 for VMonarch gradients as tests/test_vmonarch.py:64-66, 2e-2 for one L-step's gradients, 3e-2 for
@@ -27,7 +28,7 @@ def _r5(t, m, b):
 
 
 @pytest.mark.parametrize("m", [7, 33, 48, 64, 65, 96, 128])
-@pytest.mark.parametrize("d, dv", [(64, 64), (128, 128), (32, 32), (128, 64), (32, 128), (256, 256)])
+@pytest.mark.parametrize("d, dv", [(64, 64), (128, 128), (32, 32), (128, 64), (32, 128), (256, 256), (16, 16)])
 @pytest.mark.parametrize("last", [False, True])
 def test_general_lstep_forward_matches_oracle(m, d, dv, last):
     from vmonarch_amd.vmonarch import _lstep_launch, _lstep_supported
@@ -55,7 +56,7 @@ def test_general_lstep_forward_matches_oracle(m, d, dv, last):
 
 
 @pytest.mark.parametrize("m", [7, 33, 64, 65, 96, 128])
-@pytest.mark.parametrize("d, dv", [(64, 64), (128, 128), (32, 32), (64, 128), (128, 32)])
+@pytest.mark.parametrize("d, dv", [(64, 64), (128, 128), (32, 32), (64, 128), (128, 32), (16, 16)])
 @pytest.mark.parametrize("last, mcm", [(False, 0.01), (False, 0.6), (True, 0.01)])
 def test_general_lstep_backward_matches_oracle(m, d, dv, last, mcm):
     from vmonarch_amd.vmonarch import _lstep_bwd_launch, _lstep_supported
@@ -127,11 +128,11 @@ def test_vmonarch_many_frames_forward_and_grad(m, b, D):
         assert_grad_close(gd.float().cpu().numpy(), gr, 5e-2, name)
 
 
-@pytest.mark.parametrize("D, Dv", [(64, 128), (128, 64), (32, 32), (16, 16), (32, 64)])
+@pytest.mark.parametrize("D, Dv", [(64, 128), (128, 64), (32, 32), (16, 16), (32, 64), (16, 32)])
 def test_vmonarch_other_head_dims_forward_and_grad(D, Dv):
     """Head dims the kernels do not take as they are run on q, k, v zero-padded to one kernel width (32, 64 or
-    128) with the softmax scale of the true D (32 / 32 itself runs unpadded); z and the gradients against the
-    oracle."""
+    128) with the softmax scale of the true D (32 / 32 and 16 / 16 themselves run unpadded); z and the gradients
+    against the oracle."""
     from vmonarch_amd import vmonarch_attention
     g = torch.Generator().manual_seed(D + 3 * Dv)
     m, b = 4, 64

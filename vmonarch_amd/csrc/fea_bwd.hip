@@ -125,8 +125,9 @@ __device__ __forceinline__ void stage_rows_n2(const T* __restrict__ a, const T* 
 // The same copy for the tiles staged inside the key / query loops: per-lane byte offsets computed
 // once, a scalar row base per tile (a full tile costs scalar adds only; the clamped per-lane path is
 // taken by a tile that runs past the end).  Row strides must stay below 2^27 elements (32-bit lane
-// offsets over up to 7 rows).
-template <class T, int W, int ROWS>
+// offsets over up to 7 rows).  SW < W (a 16-wide tensor in a 32-wide tile, tile_w): logical chunk c of a row
+// holds the source row's chunk c % (SW / 8).
+template <class T, int W, int ROWS, int SW = W>
 struct BwdTileCopy {
   static constexpr int CH = W / 8;
   static constexpr int RPI = 64 / CH;
@@ -145,7 +146,7 @@ struct BwdTileCopy {
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       const int r = (v * kBwdWaves + w) * RPI + l / CH;
-      voff[v] = (uint32_t)((int64_t)(l / CH) * sn * 2) + (uint32_t)(((l % CH) ^ swz_rows<W * 2>(r)) * 16);
+      voff[v] = (uint32_t)((int64_t)(l / CH) * sn * 2) + (uint32_t)((((l % CH) ^ swz_rows<W * 2>(r)) & (SW / 8 - 1)) * 16);
     }
   }
   __device__ __forceinline__ void issue(int row0, int nrows, uint32_t dst) const {
@@ -163,7 +164,8 @@ struct BwdTileCopy {
         const int inst = i * kBwdWaves + wave;
         const int r = inst * RPI + lane / CH;
         const int gr = min(row0 + r, nrows - 1);
-        dma16_async((const void*)(uintptr_t)(ub + (uint64_t)gr * rbytes + ((lane % CH) ^ swz_rows<W * 2>(r)) * 16),
+        dma16_async((const void*)(uintptr_t)(ub + (uint64_t)gr * rbytes +
+                                             (((lane % CH) ^ swz_rows<W * 2>(r)) & (SW / 8 - 1)) * 16),
                     dst + inst * 1024);
       }
     }
@@ -266,7 +268,7 @@ constexpr int dkdv_v_width() { return W0K ? DV - D : DV; }
 template <int D, int DV, int PART, bool W0K>
 constexpr int dkdv_lds_bytes() {
   // (at least the four waves' epilogue patches: the narrow heads' stages are smaller)
-  constexpr int ring = 2 * (kKvBM * (D + dkdv_do_width<DV, PART>()) * 2 + 512) +
+  constexpr int ring = 2 * (kKvBM * (tile_w(D) + tile_w(dkdv_do_width<DV, PART>())) * 2 + 512) +
                        (dkdv_v_in_lds<D, DV, PART>() ? kKvBN * dkdv_v_width<D, DV, W0K>() * 2 : 0) +
                        (dkdv_k_in_lds<D, DV, PART>() ? kKvBN * D * 2 : 0);
   return ring > kBwdWaves * kEpiPatchBytes ? ring : kBwdWaves * kEpiPatchBytes;
@@ -282,13 +284,14 @@ constexpr int dq_staged_dv() { return W0K ? DV - D : DV; }
 // The dq kernels' epilogue: a wave's 32 rows of dQ (accumulated unscaled, times sm_scale here) as the fp32
 // partial of its key split (summed by fea_bwd_dq_reduce), or into grad_q in the mode the flags ask for.
 template <bool F16, int D>
-__device__ __forceinline__ void store_dq(const BwdParams& p, const f32x16 (&acc)[D / 32], VMO_LDS float* patch,
+__device__ __forceinline__ void store_dq(const BwdParams& p, const f32x16 (&acc)[tile_w(D) / 32], VMO_LDS float* patch,
                                          int prob, int split, int bb, int hh, int64_t qoff, int q0, int lane,
                                          float scale) {
+  constexpr int NA = tile_w(D) / 32, CW = D < 32 ? 16 : 32;
   const int nrows = min(32, p.nq - q0);
   if (p.dq_splits > 1) {
     float* pr = p.dq_part + (((int64_t)split * p.problems + prob) * p.nq + q0) * D;
-    store_acc_rows<F16>(patch, acc, D / 32, scale, kGradStoreF32, (char*)pr, (int64_t)D * 4, nrows, lane);
+    store_acc_rows<F16, CW>(patch, acc, NA, scale, kGradStoreF32, (char*)pr, (int64_t)D * 4, nrows, lane);
   } else {
     const int mode = grad_mode(p.accum, VMO_BWD_ACCUM_Q, VMO_BWD_F32_Q, VMO_BWD_SUM_Q);
     const int64_t es = mode == kGradStore || mode == kGradSumStore ? 2 : 4;
@@ -296,7 +299,7 @@ __device__ __forceinline__ void store_dq(const BwdParams& p, const f32x16 (&acc)
     const char* src0 = mode == kGradSumStore
                            ? (const char*)p.dq_base + (bb * p.dqb_sb + hh * p.dqb_sh + (qoff + q0) * p.dqb_sn) * 4
                            : nullptr;
-    store_acc_rows<F16>(patch, acc, D / 32, scale, mode, row0, p.dq_sn * es, nrows, lane, 0, src0, p.dqb_sn * 4);
+    store_acc_rows<F16, CW>(patch, acc, NA, scale, mode, row0, p.dq_sn * es, nrows, lane, 0, src0, p.dqb_sn * 4);
   }
 }
 
@@ -308,9 +311,10 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
   using V4 = typename E::V4;
   static_assert(!W0K || (V2 ? DV == 2 * D : DV == D), "values k or [k | v1]");
   constexpr int DVL = dq_staged_dv<D, DV, W0K>();
-  constexpr int K_BYTES = kDqBN * D * 2;
-  constexpr int STAGE = kDqBN * (D + DVL) * 2;
-  constexpr int NA = D / 32;
+  constexpr int DK = tile_w(D), DVLK = DVL ? tile_w(DVL) : 0;   // widths in LDS
+  constexpr int K_BYTES = kDqBN * DK * 2;
+  constexpr int STAGE = kDqBN * (DK + DVLK) * 2;
+  constexpr int NA = DK / 32;
   extern __shared__ __attribute__((aligned(1024))) char smem_raw[];
   VMO_LDS char* smem = (VMO_LDS char*)smem_raw;
 
@@ -378,16 +382,16 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
 
   const int n_tiles = (kend - kbeg + kDqBN - 1) / kDqBN;
   const uint32_t smem_u32 = (uint32_t)(uintptr_t)smem;
-  const BwdTileCopy<T, D, kDqBN> kcopy(kb, p.k_sn, wave, lane);
+  const BwdTileCopy<T, DK, kDqBN, D> kcopy(kb, p.k_sn, wave, lane);
   const auto vcopy = [&]() __attribute__((always_inline)) {
     if constexpr (W0K && DVL == 0)
       return 0;   // values k: nothing beyond the K tile
     else if constexpr (W0K)
-      return BwdTileCopy<T, DVL, kDqBN>(v1b, p.v_sn, wave, lane);
+      return BwdTileCopy<T, DVLK, kDqBN, DVL>(v1b, p.v_sn, wave, lane);
     else if constexpr (V2)
       return BwdTileCopy2<T, DV, kDqBN>(vb, v1b, p.v_sn, wave, lane);
     else
-      return BwdTileCopy<T, DV, kDqBN>(vb, p.v_sn, wave, lane);
+      return BwdTileCopy<T, DVLK, kDqBN, DV>(vb, p.v_sn, wave, lane);
   }();
   auto issue = [&](int t) {
     const uint32_t st = smem_u32 + (uint32_t)((t & 1) * STAGE);
@@ -399,7 +403,7 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
 #pragma unroll
   for (int a = 0; a < NA; ++a) acc[a] = f32x16{};
   const float c = p.c;
-  const int ksw = swz_rows<D * 2>(l32), vsw = swz_rows<(DVL > 0 ? DVL : D) * 2>(l32);
+  const int ksw = swz_rows<DK * 2>(l32), vsw = swz_rows<(DVL > 0 ? DVLK : DK) * 2>(l32);
   const int trow = 4 * hl + ((lane & 15) >> 2);
   const int tchunk = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
   const int tbyte = (lane & 1) * 8;
@@ -419,8 +423,8 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
     prefetched_chain<2 * NSD, dq_prefetch<D, DV>()>(
         [&](int i) __attribute__((always_inline)) {
           const int kb2 = i / NSD, j = i % NSD;
-          return j < NSQ ? lds_read8<V8>(Ks + (32 * kb2 + l32) * (D * 2) + ((2 * j + hl) ^ ksw) * 16)
-                         : lds_read8<V8>(Vs + (32 * kb2 + l32) * (DVL * 2) + ((2 * (j - NSQ) + hl) ^ vsw) * 16);
+          return j < NSQ ? lds_read8<V8>(Ks + (32 * kb2 + l32) * (DK * 2) + ((2 * j + hl) ^ ksw) * 16)
+                         : lds_read8<V8>(Vs + (32 * kb2 + l32) * (DVLK * 2) + ((2 * (j - NSQ) + hl) ^ vsw) * 16);
         },
         [&](int i, const V8& x) __attribute__((always_inline)) {
           const int kb2 = i / NSD, j = i % NSD;
@@ -445,7 +449,7 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
     // dQ^T[d][q] += K^T dS^T (transposed reads of the staged K tile)
     prefetched_chain<4 * NA, dq_prefetch<D, DV>()>(
         [&](int i) __attribute__((always_inline)) {
-          return tr_pair<V8, D * 2>(Ks + 16 * (i % 4) * (D * 2), tr_offset<D * 2>(trow, tchunk, tbyte, i / 4));
+          return tr_pair<V8, DK * 2>(Ks + 16 * (i % 4) * (DK * 2), tr_offset<DK * 2>(trow, tchunk, tbyte, i / 4));
         },
         [&](int i, const V8& x) __attribute__((always_inline)) { acc[i / 4] = E::mfma(x, G[i % 4], acc[i / 4]); });
   };
@@ -660,11 +664,13 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
   constexpr int DOW = dkdv_do_width<DV, PART>();
   constexpr int VOFF = PART == 2 ? DV / 2 : 0;  // first dV (and staged dO) column of this launch
   constexpr bool WANT_DK = PART != 2;           // dK, and with it dP and dS
-  constexpr int Q_BYTES = kKvBM * D * 2;
-  constexpr int DO_BYTES = kKvBM * DOW * 2;
+  constexpr int DK = tile_w(D), DOWK = tile_w(DOW);   // widths in LDS
+  constexpr int Q_BYTES = kKvBM * DK * 2;
+  constexpr int DO_BYTES = kKvBM * DOWK * 2;
   constexpr int ST_BYTES = 512;                 // lse[32] | alpha[32] | beta[32] | spare
   constexpr int STAGE = Q_BYTES + DO_BYTES + ST_BYTES;
-  constexpr int NK = D / 32, NV = dkdv_dv_width<DV, PART>() / 32;
+  constexpr int NK = DK / 32, NV = (dkdv_dv_width<DV, PART>() + 31) / 32;
+  constexpr int CWK = D < 32 ? 16 : 32, CWV = DV < 32 ? 16 : 32;   // stored columns per dK / dV block
   constexpr bool V_LDS = dkdv_v_in_lds<D, DV, PART>();
   constexpr bool K_LDS = dkdv_k_in_lds<D, DV, PART>();
   constexpr int VW = dkdv_v_width<D, DV, W0K>();   // V columns held (LDS tile or registers)
@@ -727,8 +733,8 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
   // dS route: the wave's row of 32 x 32 dS^T blocks (keys k0 .. k0 + 31, one block per query stage)
   const uint64_t ds_base =
       DS ? uniform64((uint64_t)(uintptr_t)p.ds + (((uint64_t)prob * p.ds_kblocks + (k0 >> 5)) * p.ds_qblocks) * 2048) : 0;
-  const BwdTileCopy<T, D, kKvBM> qcopy(qb, p.q_sn, wave, lane);
-  const BwdTileCopy<T, DOW, kKvBM> docopy(dob + VOFF, p.do_sn, wave, lane);
+  const BwdTileCopy<T, DK, kKvBM, D> qcopy(qb, p.q_sn, wave, lane);
+  const BwdTileCopy<T, DOWK, kKvBM, DOW> docopy(dob + VOFF, p.do_sn, wave, lane);
   auto issue = [&](int t) {
     const uint32_t st = smem_u32 + (uint32_t)((t & 1) * STAGE);
     const int row0 = t * kKvBM;
@@ -750,7 +756,7 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
   for (int a = 0; a < NV; ++a) dv[a] = f32x16{};
   const float gs = FOLD ? p.sm_scale : 1.f;   // dS enters the dK MFMAs times this
   const float c = p.c;
-  const int qsw = swz_rows<D * 2>(l32), dsw = swz_rows<DOW * 2>(l32), vsw = swz_rows<(VW > 0 ? VW : D) * 2>(l32);
+  const int qsw = swz_rows<DK * 2>(l32), dsw = swz_rows<DOWK * 2>(l32), vsw = swz_rows<tile_w(VW > 0 ? VW : D) * 2>(l32);
   const int trow = 4 * hl + ((lane & 15) >> 2);
   const int tchunk = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
   const int tbyte = (lane & 1) * 8;
@@ -785,8 +791,8 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
     // S[q][key] = Q K^T and dP[q][key] = dO V^T: lane = key l32, queries 8(r/4) + 4 hl + r%4
     f32x16 s = f32x16{}, dp = f32x16{};
     {
-      const VMO_LDS char* qrow = Qs + l32 * (D * 2);
-      const VMO_LDS char* drow = dOs + l32 * (DOW * 2);
+      const VMO_LDS char* qrow = Qs + l32 * (DK * 2);
+      const VMO_LDS char* drow = dOs + l32 * (DOWK * 2);
       // with W0K the K operand of S also multiplies dO's first D columns (dP's k half), in the
       // same column order as a concatenated [k | v1] would
       constexpr bool KDP = W0K && WANT_DK;
@@ -862,9 +868,9 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
     prefetched_chain<NT, kBwdPrefetch>(
         [&](int i) __attribute__((always_inline)) {
           if (i < 2 * NPV)
-            return tr_pair<V8, DOW * 2>(dOs + 16 * (i % 2) * (DOW * 2), tr_offset<DOW * 2>(trow, tchunk, tbyte, i / 2));
+            return tr_pair<V8, DOWK * 2>(dOs + 16 * (i % 2) * (DOWK * 2), tr_offset<DOWK * 2>(trow, tchunk, tbyte, i / 2));
           const int j = i - 2 * NPV;
-          return tr_pair<V8, D * 2>(Qs + 16 * (j % 2) * (D * 2), tr_offset<D * 2>(trow, tchunk, tbyte, j / 2));
+          return tr_pair<V8, DK * 2>(Qs + 16 * (j % 2) * (DK * 2), tr_offset<DK * 2>(trow, tchunk, tbyte, j / 2));
         },
         [&](int i, const V8& x) __attribute__((always_inline)) {
           if (i < 2 * NPV) {
@@ -886,18 +892,20 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
   const int nrows = min(32, p.nk - k0);
   // write NACC accumulator blocks times f: stored in T, added to / stored into an fp32 gradient, or
   // stored in T as the sum with an fp32 base (src, same column offset)
-  auto put = [&](void* base, int64_t sb, int64_t sh, int64_t sn, int col0, const f32x16* acc, int nacc, float f,
-                 int mode, const void* src = nullptr, int64_t ssb = 0, int64_t ssh = 0, int64_t ssn = 0)
+  auto put = [&](auto cw_tag, void* base, int64_t sb, int64_t sh, int64_t sn, int col0, const f32x16* acc, int nacc,
+                 float f, int mode, const void* src = nullptr, int64_t ssb = 0, int64_t ssh = 0, int64_t ssn = 0)
       __attribute__((always_inline)) {
     const int64_t es = mode == kGradStore || mode == kGradSumStore ? 2 : 4;
     char* row0 = (char*)base + (bb * sb + hh * sh + (koff + k0) * sn + col0) * es;
     const char* src0 = src ? (const char*)src + (bb * ssb + hh * ssh + (koff + k0) * ssn + col0) * 4 : nullptr;
-    store_acc_rows<F16>(patch, acc, nacc, f, mode, row0, sn * es, nrows, lane, 0, src0, ssn * 4);
+    store_acc_rows<F16, decltype(cw_tag)::value>(patch, acc, nacc, f, mode, row0, sn * es, nrows, lane, 0, src0, ssn * 4);
   };
+  const std::integral_constant<int, CWK> cwk{};
+  const std::integral_constant<int, CWV> cwv{};
   const int mode_k = grad_mode(p.accum, VMO_BWD_ACCUM_K, VMO_BWD_F32_K, VMO_BWD_SUM_K);
   const int mode_v = grad_mode(p.accum, VMO_BWD_ACCUM_V, VMO_BWD_F32_V, VMO_BWD_SUM_V);
   if constexpr (FOLD) {   // dK in natural units already (dS times sm_scale); v1's gradient is PART 2's
-    put(p.dk, p.dk_sb, p.dk_sh, p.dk_sn, 0, dk, NK, 1.0f, mode_k, p.dk_base, p.dkb_sb, p.dkb_sh, p.dkb_sn);
+    put(cwk, p.dk, p.dk_sb, p.dk_sh, p.dk_sn, 0, dk, NK, 1.0f, mode_k, p.dk_base, p.dkb_sb, p.dkb_sh, p.dkb_sn);
     return;
   }
   if constexpr (W0K && PART == 0) {
@@ -913,18 +921,26 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
       for (int b = 0; b < NK; ++b)
 #pragma unroll
         for (int r = 0; r < 16; ++r) dk[b][r] = fold(dk[b][r], p.sm_scale, dv[b][r]);
-      put(p.dk, p.dk_sb, p.dk_sh, p.dk_sn, 0, dk, NK, 1.0f, mode_k, p.dk_base, p.dkb_sb, p.dkb_sh, p.dkb_sn);
-      if constexpr (NV > NK)
-        put(p.dv, p.dv_sb, p.dv_sh, p.dv_sn, 0, dv + NK, NV - NK, 1.0f, mode_v, p.dv_base, p.dvb_sb, p.dvb_sh,
+      put(cwk, p.dk, p.dk_sb, p.dk_sh, p.dk_sn, 0, dk, NK, 1.0f, mode_k, p.dk_base, p.dkb_sb, p.dkb_sh, p.dkb_sn);
+      if constexpr (D < 32 && DV == 2 * D) {
+        // 16-wide k: v1's gradient is rows 16-31 of the one dV block (its registers 8-15)
+        f32x16 v1g = f32x16{};
+#pragma unroll
+        for (int r = 0; r < 8; ++r) v1g[r] = dv[0][8 + r];
+        put(std::integral_constant<int, 16>{}, p.dv, p.dv_sb, p.dv_sh, p.dv_sn, 0, &v1g, 1, 1.0f, mode_v, p.dv_base,
+            p.dvb_sb, p.dvb_sh, p.dvb_sn);
+      } else if constexpr (NV > NK) {
+        put(cwv, p.dv, p.dv_sb, p.dv_sh, p.dv_sn, 0, dv + NK, NV - NK, 1.0f, mode_v, p.dv_base, p.dvb_sb, p.dvb_sh,
             p.dvb_sn);
+      }
       return;
     }
   }
   if constexpr (WANT_DK)
-    put(p.dk, p.dk_sb, p.dk_sh, p.dk_sn, 0, dk, NK, p.sm_scale, mode_k, p.dk_base, p.dkb_sb, p.dkb_sh, p.dkb_sn);
+    put(cwk, p.dk, p.dk_sb, p.dk_sh, p.dk_sn, 0, dk, NK, p.sm_scale, mode_k, p.dk_base, p.dkb_sb, p.dkb_sh, p.dkb_sn);
   // (PART 2 after the folded PART 3: dv holds v1's gradient alone, from its column 0)
   const int vcol = PART == 2 && p.fold_k ? 0 : VOFF;
-  put(p.dv, p.dv_sb, p.dv_sh, p.dv_sn, vcol, dv, NV, 1.0f, mode_v, p.dv_base, p.dvb_sb, p.dvb_sh, p.dvb_sn);
+  put(cwv, p.dv, p.dv_sb, p.dv_sh, p.dv_sn, vcol, dv, NV, 1.0f, mode_v, p.dv_base, p.dvb_sb, p.dvb_sh, p.dvb_sn);
 }
 
 template <bool F16, int D, int DV, int PART, bool W0K, bool DS = false>
@@ -984,7 +1000,8 @@ static int launch_bwd(const BwdParams& p, hipStream_t s) {
     if constexpr (bwd_ds_built<D>()) return launch_bwd_ds<F16, D, DV, W0K>(p, s);
     return set_error(VMO_ERR_UNSUPPORTED, "fea_bwd: no dS route for d=%d", D);
   }
-  constexpr int RING_DQ = 2 * kDqBN * (D + dq_staged_dv<D, DV, W0K>()) * 2;
+  constexpr int DVL = dq_staged_dv<D, DV, W0K>();
+  constexpr int RING_DQ = 2 * kDqBN * (tile_w(D) + (DVL ? tile_w(DVL) : 0)) * 2;
   constexpr int LDS_DQ = RING_DQ > kBwdWaves * kEpiPatchBytes ? RING_DQ : kBwdWaves * kEpiPatchBytes;   // + patches
   static_assert(LDS_DQ <= 160 * 1024 && LDS_DQ >= kBwdWaves * kEpiPatchBytes, "bwd LDS");
   if (LDS_DQ > 65536) {
@@ -1024,17 +1041,20 @@ static int launch_bwd(const BwdParams& p, hipStream_t s) {
 template <bool F16>
 static int dispatch_bwd(const BwdParams& p, int d, int dv, hipStream_t s) {
   if (p.v1 && p.v0_is_k) {   // values [k | v1]
+    if (d == 16 && dv == 32) return launch_bwd<F16, 16, 32, true, true>(p, s);
     if (d == 32 && dv == 64) return launch_bwd<F16, 32, 64, true, true>(p, s);
     if (d == 64 && dv == 128) return launch_bwd<F16, 64, 128, true, true>(p, s);
     if (d == 128 && dv == 256) return launch_bwd<F16, 128, 256, true, true>(p, s);
   } else if (p.v0_is_k) {   // values k (VMonarch's R-steps before the last, vmonarch.py:50)
+    if (d == 16 && dv == 16) return launch_bwd<F16, 16, 16, false, true>(p, s);
     if (d == 32 && dv == 32) return launch_bwd<F16, 32, 32, false, true>(p, s);
     if (d == 64 && dv == 64) return launch_bwd<F16, 64, 64, false, true>(p, s);
     if (d == 128 && dv == 128) return launch_bwd<F16, 128, 128, false, true>(p, s);
   }
   if (p.fold_k)
-    return set_error(VMO_ERR_UNSUPPORTED, "fea_bwd: VMO_BWD_FOLD_K is built for values k with (d, dv) = (32, 32), (64, 64), "
-                     "(128, 128) and values [k | v1] with (32, 64), (64, 128), (128, 256); got d=%d dv=%d", d, dv);
+    return set_error(VMO_ERR_UNSUPPORTED, "fea_bwd: VMO_BWD_FOLD_K is built for values k with (d, dv) = (16, 16), (32, 32), "
+                     "(64, 64), (128, 128) and values [k | v1] with (16, 32), (32, 64), (64, 128), (128, 256); got d=%d "
+                     "dv=%d", d, dv);
   if (p.v1 && p.v0_is_k) {
     return set_error(VMO_ERR_UNSUPPORTED, "fea_bwd: no kernel for d=%d with values [k | v1] of %d", d, dv);
   } else if (p.v1) {   // values in two halves (the caller checked dv1 = dv / 2)
@@ -1042,7 +1062,12 @@ static int dispatch_bwd(const BwdParams& p, int d, int dv, hipStream_t s) {
     if (d == 128 && dv == 256) return launch_bwd<F16, 128, 256, true>(p, s);
     return set_error(VMO_ERR_UNSUPPORTED, "fea_bwd: no kernel for d=%d with values in two parts of %d", d, dv / 2);
   }
-  if (d == 32 && dv == 32) return launch_bwd<F16, 32, 32>(p, s);   // 32-wide dims (16: zero-padded to 32)
+  if (d == 16 && dv == 16) return launch_bwd<F16, 16, 16>(p, s);   // 16-wide heads: 32-wide tiles, rows twice
+  if (d == 16 && dv == 32) return launch_bwd<F16, 16, 32>(p, s);
+  if (d == 16 && dv == 64) return launch_bwd<F16, 16, 64>(p, s);
+  if (d == 16 && dv == 128) return launch_bwd<F16, 16, 128>(p, s);
+  if (d == 16 && dv == 256) return launch_bwd<F16, 16, 256>(p, s);
+  if (d == 32 && dv == 32) return launch_bwd<F16, 32, 32>(p, s);
   if (d == 32 && dv == 64) return launch_bwd<F16, 32, 64>(p, s);
   if (d == 32 && dv == 128) return launch_bwd<F16, 32, 128>(p, s);
   if (d == 64 && dv == 32) return launch_bwd<F16, 64, 32>(p, s);
@@ -1149,11 +1174,11 @@ extern "C" int vmo_fea_bwd(const vmo_fea_bwd_args* a, void* stream) {
     return set_error(VMO_ERR_INVALID, "fea_bwd: VMO_BWD_FOLD_K needs values that start with k (v is k: same address "
                      "and strides, dv - dv1 = d)");
   // shapes with a fold kernel (dispatch_bwd): rejected here, before any pointer is looked at further
-  if (fold_k && !(a->dv1 == 0 ? ((a->d == 32 || a->d == 64 || a->d == 128) && a->dv == a->d)
-                              : ((a->d == 32 || a->d == 64 || a->d == 128) && a->dv == 2 * a->d)))
-    return set_error(VMO_ERR_UNSUPPORTED, "fea_bwd: VMO_BWD_FOLD_K is built for values k with (d, dv) = (32, 32), "
-                     "(64, 64), (128, 128) and values [k | v1] with (32, 64), (64, 128), (128, 256); got d=%d dv=%d",
-                     a->d, a->dv);
+  const bool fold_dims = a->d == 16 || a->d == 32 || a->d == 64 || a->d == 128;
+  if (fold_k && !(fold_dims && a->dv == (a->dv1 == 0 ? a->d : 2 * a->d)))
+    return set_error(VMO_ERR_UNSUPPORTED, "fea_bwd: VMO_BWD_FOLD_K is built for values k with (d, dv) = (16, 16), "
+                     "(32, 32), (64, 64), (128, 128) and values [k | v1] with (16, 32), (32, 64), (64, 128), (128, 256); "
+                     "got d=%d dv=%d", a->d, a->dv);
   if (!(a->sm_scale >= 0.f)) return set_error(VMO_ERR_INVALID, "fea_bwd: sm_scale");
   // the tile copies address up to 7 rows from a lane with a 32-bit byte offset
   const int64_t kMaxRowStride = 1ll << 27;

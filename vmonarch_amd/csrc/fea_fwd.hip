@@ -70,7 +70,9 @@ struct FwdParams {
 // Bytes of one pipeline stage: the K tile, the value tiles the K tile does not double as, and with fp8 S
 // the fp8 K tile (one byte per element).
 template <int D, int DW0, int DW1, bool W0K, bool QK8>
-constexpr int fwd_stage_bytes() { return kFwdBN * (D + (W0K ? 0 : DW0) + DW1) * 2 + (QK8 ? kFwdBN * D : 0); }
+constexpr int fwd_stage_bytes() {
+  return kFwdBN * (tile_w(D) + (W0K ? 0 : tile_w(DW0)) + (DW1 ? tile_w(DW1) : 0)) * 2 + (QK8 ? kFwdBN * D : 0);
+}
 
 // fp8 (e4m3) operand layout of the fp8 S product: a 128-wide row as two 64-dim products; lane half hl of
 // product m takes dims 16 ds + 8 hl + e (ds = 4 m .. 4 m + 3, e = 0 .. 7), which are those the lane holds
@@ -91,8 +93,9 @@ constexpr int fwd_slots(int stage_bytes, int waves) {
 // multiple of 16 (and alternates with i otherwise), so the lane's byte offset from its instruction's
 // first row takes one or two values: a full tile costs scalar address arithmetic only.  A tile that runs
 // past the end of the tensor (row >= nrows) re-reads the last row instead: finite data, masked out
-// later.  Each wave issues NI copies per tile (vmcnt units).
-template <class T, int W, int WAVES>
+// later.  Each wave issues NI copies per tile (vmcnt units).  SW < W (a 16-wide tensor in a 32-wide tile):
+// logical chunk c of a row holds the source row's chunk c % (SW / 8).
+template <class T, int W, int WAVES, int SW = W>
 struct TileCopy {
   static constexpr int CH = W / 8;       // 16-byte chunks per row
   static constexpr int RPI = 64 / CH;    // rows per wave instruction
@@ -110,7 +113,7 @@ struct TileCopy {
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       const int r = (v * WAVES + w) * RPI + l / CH;   // the lane's row in instruction i = v
-      voff[v] = (uint32_t)((int64_t)(l / CH) * s * 2) + (uint32_t)(((l % CH) ^ swz_rows<W * 2>(r)) * 16);
+      voff[v] = (uint32_t)((int64_t)(l / CH) * s * 2) + (uint32_t)((((l % CH) ^ swz_rows<W * 2>(r)) & (SW / 8 - 1)) * 16);
     }
   }
   __device__ __forceinline__ void issue(int row0, int nrows, uint32_t dst) const {
@@ -135,7 +138,8 @@ struct TileCopy {
         const int inst = i * WAVES + wave;
         const int r = inst * RPI + lane / CH;
         const int gr = min(row0 + r, nrows - 1);
-        dma16_async((const void*)(uintptr_t)(ub + (uint64_t)gr * rbytes + ((lane % CH) ^ swz_rows<W * 2>(r)) * 16),
+        dma16_async((const void*)(uintptr_t)(ub + (uint64_t)gr * rbytes +
+                                             (((lane % CH) ^ swz_rows<W * 2>(r)) & (SW / 8 - 1)) * 16),
                     dst + inst * 1024);
       }
     }
@@ -158,7 +162,7 @@ enum { kEntNone = 0, kEntOnline = 1, kEntFromPK = 2 };
 // than k) run one 4-wave workgroup per CU.
 template <int D, int DW0, int DW1, int ENT, int WAVES>
 constexpr int fwd_min_blocks() {
-  return (D >= 256 || DW0 >= 256 || (ENT == kEntOnline && D < DW0) || (DW1 > 0 && DW1 < D)) ? 1 : 8 / WAVES;
+  return (D >= 256 || DW0 >= 256 || (ENT == kEntOnline && tile_w(D) < DW0) || (DW1 > 0 && DW1 < D)) ? 1 : 8 / WAVES;
 }
 
 template <bool F16, int D, int DW0, int DW1, bool W0K, int ENT, bool SPLIT, int WAVES, bool QK8>
@@ -168,18 +172,21 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
   using V8 = typename E::V8;
   using V4 = typename E::V4;
   using V2 = typename E::V2;
-  constexpr int K_BYTES = kFwdBN * D * 2;
-  constexpr int W0_BYTES = W0K ? 0 : kFwdBN * DW0 * 2;
-  constexpr int W1_BYTES = kFwdBN * DW1 * 2;
+  constexpr int DK = tile_w(D), DW0K = tile_w(DW0), DW1K = DW1 ? tile_w(DW1) : 0;   // widths in LDS
+  constexpr int K_BYTES = kFwdBN * DK * 2;
+  constexpr int W0_BYTES = W0K ? 0 : kFwdBN * DW0K * 2;
+  constexpr int W1_BYTES = kFwdBN * DW1K * 2;
   constexpr int K8_OFF = K_BYTES + W0_BYTES + W1_BYTES;   // the fp8 K tile (QK8)
   constexpr int STAGE = fwd_stage_bytes<D, DW0, DW1, W0K, QK8>();
   constexpr int NSLOT = fwd_slots(STAGE, WAVES);
   static_assert(!QK8 || D == 128, "fp8 S is built for 128-wide q / k");
   constexpr int kBM = 32 * kFwdQB * WAVES;   // queries per workgroup
-  constexpr int NA0 = DW0 / 32;
-  constexpr int NA1 = DW1 / 32;
+  constexpr int NA0 = DW0K / 32;
+  constexpr int NA1 = DW1K / 32;
   constexpr int NA = NA0 + NA1;
-  constexpr int NDS = D / 16;
+  constexpr int NDS = D / 16;   // 16-dim MFMA steps of S (one for a 16-wide head)
+  constexpr int CW = DW0 < 32 ? 16 : 32;   // stored columns per accumulator block
+  static_assert(DW1 == 0 || (DW1 < 32) == (DW0 < 32), "value parts of one width class");
   constexpr int QB = kFwdQB;
   // global_load_lds instructions one tile costs each wave (vmcnt units)
   constexpr int DMA_PER_TILE = STAGE / 1024 / WAVES;
@@ -258,9 +265,9 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
     }
   }
 
-  const TileCopy<T, D, WAVES> kcopy(kb, p.k_sn, wave, lane);
-  const TileCopy<T, W0K ? 64 : DW0, WAVES> w0copy(w0b, p.w0_sn, wave, lane);
-  const TileCopy<T, DW1 ? DW1 : 64, WAVES> w1copy(w1b, p.w1_sn, wave, lane);
+  const TileCopy<T, DK, WAVES, D> kcopy(kb, p.k_sn, wave, lane);
+  const TileCopy<T, W0K ? 64 : DW0K, WAVES, W0K ? 64 : DW0> w0copy(w0b, p.w0_sn, wave, lane);
+  const TileCopy<T, DW1 ? DW1K : 64, WAVES, DW1 ? DW1 : 64> w1copy(w1b, p.w1_sn, wave, lane);
   // fp8 K rows: 128 bytes, copied as 64 16-bit elements
   const TileCopy<T, 64, WAVES> k8copy(QK8 ? (const T*)((const char*)p.k8 + (int64_t)loc.prob * p.nk * D) : kb, 64,
                                       wave, lane);
@@ -327,7 +334,7 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
   bool overflow = false;
 
   // per-lane LDS offsets
-  const int srow_sw = swz_rows<D * 2>(l32);                       // S operand rows 32 kb + l32
+  const int srow_sw = swz_rows<DK * 2>(l32);                      // S operand rows 32 kb + l32
   const int trow = 4 * hl + ((lane & 15) >> 2);                   // W^T rows 16 ks + trow (+8)
   const int tchunk = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);   // logical chunk within 32 cols
   const int tbyte = (lane & 1) * 8;
@@ -359,7 +366,7 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
       }
       return;
     }
-    const VMO_LDS char* arow = Ks + (32 * kb2 + l32) * (D * 2);
+    const VMO_LDS char* arow = Ks + (32 * kb2 + l32) * (DK * 2);
     V8 a[NDS];
 #pragma unroll
     for (int ds = 0; ds < NDS; ++ds) a[ds] = lds_read8<V8>(arow + ((2 * ds + hl) ^ srow_sw) * 16);
@@ -369,7 +376,7 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
     for (int ds = 0; ds < NDS; ++ds)
 #pragma unroll
       for (int j = 0; j < QB; ++j) x[j] = E::mfma(a[ds], qf[j][ds], x[j]);
-    if constexpr (decltype(sched_tag)::value) {
+    if constexpr (decltype(sched_tag)::value && NDS >= kPre) {
       constexpr int NV = int(decltype(sched_tag)::value) - 1;
       __builtin_amdgcn_sched_group_barrier(0x100, kPre, 0);
 #pragma unroll
@@ -485,10 +492,10 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
   };
   auto pv_block = [&](const VMO_LDS char* Ks, int kb2, const V8 (&P)[QB][2], auto sched_tag)
       __attribute__((always_inline)) {
-    pv_part(W0K ? Ks : Ks + K_BYTES, std::integral_constant<int, DW0 * 2>{}, std::integral_constant<int, NA0>{}, 0,
+    pv_part(W0K ? Ks : Ks + K_BYTES, std::integral_constant<int, DW0K * 2>{}, std::integral_constant<int, NA0>{}, 0,
             kb2, P, sched_tag);
     if constexpr (DW1 > 0)
-      pv_part(Ks + K_BYTES + W0_BYTES, std::integral_constant<int, DW1 * 2>{}, std::integral_constant<int, NA1>{}, NA0,
+      pv_part(Ks + K_BYTES + W0_BYTES, std::integral_constant<int, DW1K * 2>{}, std::integral_constant<int, NA1>{}, NA0,
               kb2, P, sched_tag);
   };
 
@@ -743,7 +750,7 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
     const int qr = qb0 + l32;
     const bool qv = qr < p.nq;
     if constexpr (SPLIT) {
-      store_acc_rows<F16>(patch, acc[j], NA, inv_l, kGradStoreF32, (char*)(p.part_o + (part0 + qb0) * (int64_t)(DW0 + DW1)),
+      store_acc_rows<F16, CW>(patch, acc[j], NA, inv_l, kGradStoreF32, (char*)(p.part_o + (part0 + qb0) * (int64_t)(DW0 + DW1)),
                           (int64_t)(DW0 + DW1) * 4, nrows, lane);
       if (qv && hl == 0) p.part_lse[part0 + qr] = lse;
     } else {
@@ -755,7 +762,7 @@ __global__ __launch_bounds__(64 * WAVES, (fwd_min_blocks<D, DW0, DW1, ENT, WAVES
         // sum_j P~_j s_j = q . (sum_j p~_j k_j) / l~
         ent = lse * kLn2 - (c * kLn2) * pkdot[j] * inv_l;
       }
-      store_acc_rows<F16>(patch, acc[j], NA, inv_l, kGradStore, (char*)(ob + (int64_t)qb0 * o_sn), o_sn * 2, nrows, lane);
+      store_acc_rows<F16, CW>(patch, acc[j], NA, inv_l, kGradStore, (char*)(ob + (int64_t)qb0 * o_sn), o_sn * 2, nrows, lane);
       if (qv) {
         const int64_t si = st0 + qr;
         if (ENT != kEntNone && hl == 0 && p.ent) p.ent[si] = ent;
@@ -897,8 +904,12 @@ static int dispatch_fwd(const FwdParams& p, int d, int dw0, int dw1, bool w0k, b
 #define VMO_FWD(D_, DW0_, DW1_, W0K_, ENT_, SPLIT_)                                                  \
   if (d == D_ && dw0 == DW0_ && dw1 == DW1_ && w0k == W0K_ && ent == (ENT_ != kEntNone) && split == SPLIT_) \
     return launch_fwd<F16, D_, DW0_, DW1_, W0K_, ENT_, SPLIT_, kFwdWavesFor(D_, DW0_, DW1_, SPLIT_)>(p, s);
-  // standalone flash_entropy_attention (kernel.py:384-402): online entropy (32 / 32 also takes 16-wide heads,
-  // zero-padded by the caller)
+  // standalone flash_entropy_attention (kernel.py:384-402): online entropy
+  VMO_FWD(16, 16, 0, false, kEntOnline, false)
+  VMO_FWD(16, 32, 0, false, kEntOnline, false)
+  VMO_FWD(16, 64, 0, false, kEntOnline, false)
+  VMO_FWD(16, 128, 0, false, kEntOnline, false)
+  VMO_FWD(16, 256, 0, false, kEntOnline, false)
   VMO_FWD(32, 32, 0, false, kEntOnline, false)
   VMO_FWD(32, 64, 0, false, kEntOnline, false)
   VMO_FWD(32, 128, 0, false, kEntOnline, false)
@@ -914,6 +925,8 @@ static int dispatch_fwd(const FwdParams& p, int d, int dw0, int dw1, bool w0k, b
   VMO_FWD(128, 256, 0, false, kEntOnline, false)
   VMO_FWD(256, 256, 0, false, kEntOnline, false)
   // VMonarch R-step (vmonarch.py:50): values k, or [k | v]; entropy from the P.K accumulator
+  VMO_FWD(16, 16, 0, true, kEntFromPK, false)
+  VMO_FWD(16, 16, 16, true, kEntFromPK, false)
   VMO_FWD(32, 32, 0, true, kEntFromPK, false)
   VMO_FWD(32, 32, 32, true, kEntFromPK, false)
   VMO_FWD(64, 64, 0, true, kEntFromPK, false)
@@ -923,10 +936,12 @@ static int dispatch_fwd(const FwdParams& p, int d, int dw0, int dw1, bool w0k, b
   VMO_FWD(128, 128, 64, true, kEntFromPK, false)
   VMO_FWD(128, 128, 128, true, kEntFromPK, false)
   // exact recompute (vmonarch.py:66-68): no entropy, optionally split-KV
+  VMO_FWD(16, 16, 0, false, kEntNone, false)
   VMO_FWD(64, 64, 0, false, kEntNone, false)
   VMO_FWD(64, 128, 0, false, kEntNone, false)
   VMO_FWD(128, 64, 0, false, kEntNone, false)
   VMO_FWD(128, 128, 0, false, kEntNone, false)
+  VMO_FWD(16, 16, 0, false, kEntNone, true)
   VMO_FWD(32, 32, 0, false, kEntNone, true)
   VMO_FWD(64, 64, 0, false, kEntNone, true)
   VMO_FWD(64, 128, 0, false, kEntNone, true)

@@ -64,8 +64,9 @@ __host__ __device__ inline MbLayout mb_layout(int M, int d, int dv, bool last, b
 // c ^ swz_rows(r): wave instruction inst covers rows inst RPI .. + RPI - 1, lane l lands at byte 16 l of its
 // 1 KB and so loads global chunk (l % CH) ^ swz_rows(row).  Only instructions that hold a row below m copy
 // (their rows past m repeat row m - 1); the rows after them are zeroed -- finite data whose weights are exact
-// zeros, without copying the last row over and over.
-template <class T, int W>
+// zeros, without copying the last row over and over.  SW < W: a 16-wide tensor in a 32-wide tile (tile_w),
+// each row's two chunks stored twice.
+template <class T, int W, int SW = W>
 __device__ __forceinline__ void mb_stage(const T* src, int64_t rs, int m, int M, VMO_LDS char* dst, int wave,
                                          int lane) {
   constexpr int RB = W * 2, CH = RB / 16, RPI = 64 / CH;
@@ -74,7 +75,7 @@ __device__ __forceinline__ void mb_stage(const T* src, int64_t rs, int m, int M,
   for (int inst = wave; inst < ninst; inst += kMbWaves) {
     const int r = inst * RPI + lane / CH;
     const int rr = r < m ? r : m - 1;
-    g2l_16(src + (int64_t)rr * rs + (c ^ swz_rows<RB>(r)) * 8, dst + inst * 1024);
+    g2l_16(src + (int64_t)rr * rs + ((c ^ swz_rows<RB>(r)) & (SW / 8 - 1)) * 8, dst + inst * 1024);
   }
   for (int o = ninst * 1024 + (64 * wave + lane) * 16; o < M * RB; o += 64 * kMbWaves * 16)
     *(VMO_LDS i32x4*)(dst + o) = i32x4{0, 0, 0, 0};
@@ -114,14 +115,16 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_kernel(LParams p) {
   using E = Elem<F16>;
   using T = typename E::T;
   using V8 = typename E::V8;
+  constexpr int DK = tile_w(D), DVK = tile_w(DV);   // widths in LDS
   constexpr int NDS = D / 16;
-  constexpr int NACC = (LAST ? DV : D) / 32;
-  constexpr int RBD = D * 2, RBY = DV * 2;
+  constexpr int NACC = (LAST ? DVK : DK) / 32;
+  constexpr int CW = (LAST ? DV : D) < 32 ? 16 : 32;   // stored columns per accumulator block
+  constexpr int RBD = DK * 2, RBY = DVK * 2;
   extern __shared__ __attribute__((aligned(1024))) char smem_raw[];
   VMO_LDS char* sm = (VMO_LDS char*)smem_raw;
 
   const int m = p.m, MB = (m + 31) / 32, M = 32 * MB;
-  const MbLayout Lo = mb_layout(M, D, DV, LAST, false);
+  const MbLayout Lo = mb_layout(M, DK, DVK, LAST, false);
   VMO_LDS char* q_t = sm + Lo.q;
   VMO_LDS char* k_t = sm + Lo.k;
   VMO_LDS char* y_t = sm + Lo.y;
@@ -136,9 +139,9 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_kernel(LParams p) {
   const T* ocol = (const T*)p.out + bb * p.out_sb + hh * p.out_sh + (int64_t)j * p.out_sn;
   T* rcol = (T*)p.res + bb * p.res_sb + hh * p.res_sh + (int64_t)j * p.res_sn;
 
-  mb_stage<T, D>(qcol, q_rs, m, M, q_t, wave, lane);
-  mb_stage<T, D>(ocol, o_rs, m, M, k_t, wave, lane);
-  if constexpr (LAST) mb_stage<T, DV>(ocol + D, o_rs, m, M, y_t, wave, lane);
+  mb_stage<T, DK, D>(qcol, q_rs, m, M, q_t, wave, lane);
+  mb_stage<T, DK, D>(ocol, o_rs, m, M, k_t, wave, lane);
+  if constexpr (LAST) mb_stage<T, DVK, DV>(ocol + D, o_rs, m, M, y_t, wave, lane);
   const float* ep = p.ent + bb * p.ent_sb + hh * p.ent_sh + j;
   for (int k = tid; k < M; k += 64 * kMbWaves) e_t[k] = k < m ? ep[(int64_t)k * p.bs] * kLog2e : -1.0e30f;
   __builtin_amdgcn_s_waitcnt(0);
@@ -265,9 +268,9 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_kernel(LParams p) {
   if constexpr (LAST) {
     // z rows i from the first one the recompute does not overwrite (token i b + j >= skip)
     const int ibeg = p.skip > j ? (p.skip - j + p.bs - 1) / p.bs : 0;
-    store_acc_rows<F16>(patch, acc, NACC, 1.f, kGradStore, (char*)rows, r_rs * 2, nrows, lane, max(0, ibeg - 32 * blk));
+    store_acc_rows<F16, CW>(patch, acc, NACC, 1.f, kGradStore, (char*)rows, r_rs * 2, nrows, lane, max(0, ibeg - 32 * blk));
   } else {
-    store_acc_rows<F16>(patch, acc, NACC, fscale, kGradStore, (char*)rows, r_rs * 2, nrows, lane);
+    store_acc_rows<F16, CW>(patch, acc, NACC, fscale, kGradStore, (char*)rows, r_rs * 2, nrows, lane);
   }
 }
 
@@ -292,15 +295,17 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
   using E = Elem<F16>;
   using T = typename E::T;
   using V8 = typename E::V8;
+  constexpr int DK = tile_w(D), DVK = tile_w(DV);   // widths in LDS
   constexpr int NDS = D / 16, NDSV = DV / 16;
-  constexpr int ND = D / 32, NV = DV / 32;
-  constexpr int GW = LAST ? DV : D;
-  constexpr int RBD = D * 2, RBY = DV * 2, RBG = GW * 2;
+  constexpr int ND = DK / 32, NV = DVK / 32;
+  constexpr int CWD = D < 32 ? 16 : 32, CWV = DV < 32 ? 16 : 32;   // stored columns per accumulator block
+  constexpr int GW = LAST ? DV : D, GWK = tile_w(GW);
+  constexpr int RBD = DK * 2, RBY = DVK * 2, RBG = GWK * 2;
   extern __shared__ __attribute__((aligned(1024))) char smem_raw[];
   VMO_LDS char* sm = (VMO_LDS char*)smem_raw;
 
   const int m = p.m, MB = (m + 31) / 32, M = 32 * MB;
-  const MbLayout Lo = mb_layout(M, D, DV, LAST, true);
+  const MbLayout Lo = mb_layout(M, DK, DVK, LAST, true);
   VMO_LDS char* q_t = sm + Lo.q;
   VMO_LDS char* k_t = sm + Lo.k;
   VMO_LDS char* y_t = sm + Lo.y;
@@ -323,10 +328,10 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
   float* dqcol = p.dq + bb * p.dq_sb + hh * p.dq_sh + (int64_t)j * p.dq_sn;
   T* dcol = (T*)p.dout + bb * p.do_sb + hh * p.do_sh + (int64_t)j * p.do_sn;
 
-  mb_stage<T, D>(qcol, q_rs, m, M, q_t, wave, lane);
-  mb_stage<T, D>(ocol, o_rs, m, M, k_t, wave, lane);
-  if constexpr (LAST) mb_stage<T, DV>(ocol + D, o_rs, m, M, y_t, wave, lane);
-  mb_stage<T, GW>(gcol, g_rs, m, M, g_t, wave, lane);
+  mb_stage<T, DK, D>(qcol, q_rs, m, M, q_t, wave, lane);
+  mb_stage<T, DK, D>(ocol, o_rs, m, M, k_t, wave, lane);
+  if constexpr (LAST) mb_stage<T, DVK, DV>(ocol + D, o_rs, m, M, y_t, wave, lane);
+  mb_stage<T, GWK, GW>(gcol, g_rs, m, M, g_t, wave, lane);
   const float* ep = p.ent + bb * p.ent_sb + hh * p.ent_sh + j;
   for (int k = tid; k < M; k += 64 * kMbWaves) e_t[k] = k < m ? ep[(int64_t)k * p.bs] * kLog2e : -1.0e30f;
   __builtin_amdgcn_s_waitcnt(0);
@@ -444,7 +449,7 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
           accq[a] = E::mfma(mb_tr8<V8, RBD>(k_t + 32 * kb * RBD, lane, a, 1), P1, accq[a]);
         }
       }
-      store_acc_rows<F16>(patch, accq, ND, 1.f, dq_mode, (char*)(dqcol + 32 * blk * dq_rs), dq_rs * 4, nrows, lane);
+      store_acc_rows<F16, CWD>(patch, accq, ND, 1.f, dq_mode, (char*)(dqcol + 32 * blk * dq_rs), dq_rs * 4, nrows, lane);
     }
     __syncthreads();
     // ---- pass B: one key per lane, as two sweeps over the query blocks (dy, then dkr: holding both accumulator
@@ -466,8 +471,8 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
           accy[a] = E::mfma(mb_tr8<V8, RBY>(g_t + 32 * ib * RBY, lane, a, 1), A1, accy[a]);
         }
       }
-      store_acc_rows<F16>(patch, accy, NV, 1.f, kGradStore, (char*)(dcol + 32 * blk * do_rs + D), do_rs * 2, nrows,
-                          lane);
+      store_acc_rows<F16, CWV>(patch, accy, NV, 1.f, kGradStore, (char*)(dcol + 32 * blk * do_rs + D), do_rs * 2, nrows,
+                               lane);
       f32x16 acck[ND];
 #pragma unroll
       for (int a = 0; a < ND; ++a) acck[a] = f32x16{};
@@ -494,7 +499,7 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
           acck[a] = E::mfma(mb_tr8<V8, RBD>(q_t + 32 * ib * RBD, lane, a, 1), P1, acck[a]);
         }
       }
-      store_acc_rows<F16>(patch, acck, ND, 1.f, kGradStore, (char*)(dcol + 32 * blk * do_rs), do_rs * 2, nrows, lane);
+      store_acc_rows<F16, CWD>(patch, acck, ND, 1.f, kGradStore, (char*)(dcol + 32 * blk * do_rs), do_rs * 2, nrows, lane);
     }
   } else {
     // ---- pass 0: row LSE (query blocks)
@@ -598,7 +603,7 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
           accq[a] = E::mfma(mb_tr8<V8, RBD>(g_t + 32 * kb * RBD, lane, a, 1), F1, accq[a]);
         }
       }
-      store_acc_rows<F16>(patch, accq, ND, 1.f, dq_mode, (char*)(dqcol + 32 * blk * dq_rs), dq_rs * 4, nrows, lane);
+      store_acc_rows<F16, CWD>(patch, accq, ND, 1.f, dq_mode, (char*)(dqcol + 32 * blk * dq_rs), dq_rs * 4, nrows, lane);
     }
     __syncthreads();
     // ---- pass 3: dkr (key blocks)
@@ -633,26 +638,28 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
           acck[a] = E::mfma(mb_tr8<V8, RBD>(q_t + 32 * ib * RBD, lane, a, 1), P1, acck[a]);
         }
       }
-      store_acc_rows<F16>(patch, acck, ND, 1.f, kGradStore, (char*)(dcol + 32 * blk * do_rs), do_rs * 2, nrows, lane);
+      store_acc_rows<F16, CWD>(patch, acck, ND, 1.f, kGradStore, (char*)(dcol + 32 * blk * do_rs), do_rs * 2, nrows, lane);
     }
   }
 }
 
-// Head-dim pairs the multi-block kernels are built for.
+// Head-dim pairs the multi-block kernels are built for: 32 / 64 / 128 in any pair, and 16 with 16 (the
+// reference's VMonarch runs d = dv).
 static bool mb_dims(int d, int dv, bool last) {
   const auto ok = [](int x) { return x == 32 || x == 64 || x == 128; };
+  if (d == 16) return !last || dv == 16;
   return ok(d) && (!last || ok(dv));
 }
 
 int mb_lstep_check(int m, int d, int dv, bool last, bool bwd) {
   if (!mb_dims(d, dv, last) || m < 1 || m > kMbMaxFrames) return 0;
-  return mb_layout(32 * ((m + 31) / 32), d, last ? dv : 0, last, bwd).total <= 160 * 1024;
+  return mb_layout(32 * ((m + 31) / 32), tile_w(d), last ? tile_w(dv) : 0, last, bwd).total <= 160 * 1024;
 }
 
 template <bool F16, int D, int DV, bool LAST>
 static int launch_mb(const LParams& p, hipStream_t s) {
   const int M = 32 * ((p.m + 31) / 32);
-  const int lds = mb_layout(M, D, DV, LAST, false).total;
+  const int lds = mb_layout(M, tile_w(D), tile_w(DV), LAST, false).total;
   auto kern = lstep_mb_kernel<F16, D, DV, LAST>;
   if (lds > 65536 && hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
     return set_error(VMO_ERR_LAUNCH, "lstep_mb: cannot raise the LDS limit to %d bytes", lds);
@@ -666,8 +673,8 @@ static int dispatch_mb(const LParams& p, int d, int dv, bool last, hipStream_t s
   if (d == D_ && dv == DV_ && last) return launch_mb<F16, D_, DV_, true>(p, s);
 #define VMO_MB_U(D_) \
   if (d == D_ && !last) return launch_mb<F16, D_, D_, false>(p, s);
-  VMO_MB_U(32) VMO_MB_U(64) VMO_MB_U(128)
-  VMO_MB(32, 32) VMO_MB(32, 64) VMO_MB(32, 128)
+  VMO_MB_U(16) VMO_MB_U(32) VMO_MB_U(64) VMO_MB_U(128)
+  VMO_MB(16, 16) VMO_MB(32, 32) VMO_MB(32, 64) VMO_MB(32, 128)
   VMO_MB(64, 32) VMO_MB(64, 64) VMO_MB(64, 128)
   VMO_MB(128, 32) VMO_MB(128, 64) VMO_MB(128, 128)
 #undef VMO_MB
@@ -682,7 +689,7 @@ int mb_lstep_fwd(const LParams& p, bool f16, int d, int dv, bool last, hipStream
 template <bool F16, int D, int DV, bool LAST>
 static int launch_mb_bwd(const LBParams& p, hipStream_t s) {
   const int M = 32 * ((p.m + 31) / 32);
-  const int lds = mb_layout(M, D, DV, LAST, true).total;
+  const int lds = mb_layout(M, tile_w(D), tile_w(DV), LAST, true).total;
   auto kern = lstep_mb_bwd_kernel<F16, D, DV, LAST>;
   if (lds > 65536 && hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
     return set_error(VMO_ERR_LAUNCH, "lstep_mb_bwd: cannot raise the LDS limit to %d bytes", lds);
@@ -696,8 +703,8 @@ static int dispatch_mb_bwd(const LBParams& p, int d, int dv, bool last, hipStrea
   if (d == D_ && dv == DV_ && last) return launch_mb_bwd<F16, D_, DV_, true>(p, s);
 #define VMO_MB_U(D_) \
   if (d == D_ && !last) return launch_mb_bwd<F16, D_, D_, false>(p, s);
-  VMO_MB_U(32) VMO_MB_U(64) VMO_MB_U(128)
-  VMO_MB(32, 32) VMO_MB(32, 64) VMO_MB(32, 128)
+  VMO_MB_U(16) VMO_MB_U(32) VMO_MB_U(64) VMO_MB_U(128)
+  VMO_MB(16, 16) VMO_MB(32, 32) VMO_MB(32, 64) VMO_MB(32, 128)
   VMO_MB(64, 32) VMO_MB(64, 64) VMO_MB(64, 128)
   VMO_MB(128, 32) VMO_MB(128, 64) VMO_MB(128, 128)
 #undef VMO_MB

@@ -189,8 +189,16 @@ __device__ __forceinline__ int grad_mode(int flags, int accum_bit, int f32_bit, 
 // per lane (it scales the lane's own row l32).  One wave writes and reads its own patch (LDS accesses
 // of a wave complete in order); the caller makes sure no other wave still uses that LDS.  Used by the
 // flash-entropy forward (o) and backward (gradients) and both L-step kernels (u / z, gradients).
+// Width of a 16-bit tile row in LDS for a head dim w: a 16-wide head (q / k, a value tensor, dO) is laid out 32
+// wide with each row's two 16-byte chunks stored twice, so that the 32-wide operand reads apply unchanged:
+// products over the head dim take one 16-dim MFMA step, and products that output it (P.V, dQ, dK, dV, u, z)
+// fill accumulator rows 16-31 with a copy of rows 0-15, which are not stored (CW = 16 below).
+constexpr int tile_w(int w) { return w < 32 ? 32 : w; }
+
+// CW = 16: each accumulator block holds 16 valid columns (rows 0-15 of the transposed accumulator; the 16-wide
+// heads, whose LDS tiles hold every row twice), stored as columns 16 a .. 16 a + 15.
 constexpr int kEpiPatchBytes = 32 * 32 * 4;
-template <bool F16>
+template <bool F16, int CW = 32>
 __device__ __forceinline__ void store_acc_rows(VMO_LDS float* patch, const f32x16* acc, int nacc, float f, int mode,
                                                char* row0, int64_t row_stride_bytes, int nrows, int lane,
                                                int rbegin = 0, const char* src0 = nullptr,
@@ -199,7 +207,8 @@ __device__ __forceinline__ void store_acc_rows(VMO_LDS float* patch, const f32x1
   using V4 = typename Elem<F16>::V4;
   using V8 = typename Elem<F16>::V8;
   const int hl = lane >> 5, l32 = lane & 31, rr0 = lane >> 3, c = lane & 7;
-  if (mode == kGradStore && nacc % 2 == 0) {
+  static_assert(CW == 16 || CW == 32, "block width");
+  if (CW == 32 && mode == kGradStore && nacc % 2 == 0) {
     // 16-bit rows: two blocks (64 columns) per pass, so that 8 lanes write a whole 128-byte segment
     VMO_LDS char* pb = (VMO_LDS char*)patch;   // [32 rows][8 chunks of 16 bytes], chunk ^ (row & 7)
     for (int a = 0; a < nacc; a += 2) {
@@ -234,13 +243,13 @@ __device__ __forceinline__ void store_acc_rows(VMO_LDS float* patch, const f32x1
     for (int i = 0; i < 4; ++i) {   // rows rr0 + 8 i, chunk c: 8 lanes per row
       const int rr = rr0 + 8 * i;
       const f32x4 v = *(const VMO_LDS f32x4*)(patch + rr * 32 + (c ^ (rr & 7)) * 4);
-      if (rr >= rbegin && rr < nrows) {
-        char* dst = row0 + rr * row_stride_bytes + (int64_t)(32 * a + 4 * c) * esize;
+      if (rr >= rbegin && rr < nrows && 4 * c < CW) {
+        char* dst = row0 + rr * row_stride_bytes + (int64_t)(CW * a + 4 * c) * esize;
         if (mode == kGradStore || mode == kGradSumStore) {
           // (sum: the base row src0 is fp32, same columns; the product came through LDS, so the
           // sum is its own rounding, as adding the fp32 store of this result would be)
           const f32x4 b = mode == kGradSumStore
-                              ? *(const f32x4*)(src0 + rr * src_stride_bytes + (int64_t)(32 * a + 4 * c) * 4)
+                              ? *(const f32x4*)(src0 + rr * src_stride_bytes + (int64_t)(CW * a + 4 * c) * 4)
                               : f32x4{0.f, 0.f, 0.f, 0.f};
           V4 x;
 #pragma unroll

@@ -23,10 +23,10 @@ def _pad_features(t, width):
 
 
 def _kernel_widths(d, dv):
-    """Head dims of the flash-entropy kernels (forward and backward) that serve (d, dv): each dim of at most 32
-    runs 32 wide (16 zero-padded to 32), wider ones as they are (64, 128, 256)."""
-    w = lambda x: 32 if x <= 32 else x   # noqa: E731
-    return w(d), w(dv)
+    """Head dims of the flash-entropy kernels (forward and backward) that serve (d, dv): every pair the reference
+    accepts (dv a multiple of d) as it is, 16-wide heads included (their kernels hold 16-wide rows in 32-wide LDS
+    tiles); a 16-wide value head under wider q / k (beyond the reference) runs 32 wide, zero-padded."""
+    return d, (32 if dv < 32 <= d else dv)
 
 
 def fea_forward(q, k, w0, w1, sm_scale, frames=1, o=None, lse=None, ent=None, want_ent=True, want_lse=True,

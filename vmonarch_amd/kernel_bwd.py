@@ -102,7 +102,8 @@ def fea_backward(q, k, v, o, lse, ent, do, de, sm_scale, n_valid):
     n = int(n_valid)
     from .kernel import _kernel_widths
     Dk, Dvk = _kernel_widths(D, Dv)
-    if not ((Dk in (32, 64, 128) and Dvk in (32, 64, 128, 256)) or (Dk == 256 and Dvk == 256)):
+    if not ((Dk in (32, 64, 128) and Dvk in (32, 64, 128, 256)) or (Dk == 16 and Dvk in (16, 32, 64, 128, 256))
+            or (Dk == 256 and Dvk == 256)):
         raise NotImplementedError(f"vmonarch_amd: backward for head dims ({D}, {Dv}) is not built")
     if de is None:
         de = torch.zeros((B, H, N), device=q.device, dtype=torch.float32)

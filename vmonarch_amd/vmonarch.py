@@ -15,8 +15,9 @@ Execution paths, with identical results within bf16 tolerance:
     m <= 32, a general kernel beyond), and the recompute of the first tokens is a split-KV flash
     kernel writing straight into z;
   * _VMonarchFunction (autograd): the same forward keeping its activations, and a HIP backward;
-  * head dims the kernels do not take as they are (16, 32; D != Dv with autograd) run either of
-    the above on q, k, v zero-padded to one kernel width;
+  * head-dim mixes the kernels do not take as they are (16 with 32; D != Dv with autograd; neither
+    is a shape the reference's VMonarch runs) run either of the above on q, k, v zero-padded to one
+    kernel width;
   * composed: the reference's structure step by step (R-step through the `_row_block_attention`
     seam, L-step as torch tensor ops), used when a caller replaced `_row_block_attention`
     (tests/test_vmonarch.py:59 does), and -- with a RuntimeWarning -- for shapes no HIP path takes.
@@ -128,6 +129,7 @@ def _lstep_mb_lds(m, d, dv, last, bwd):
     patches."""
     M = 32 * ((m + 31) // 32)
     r = lambda b: (b + 255) // 256 * 256   # noqa: E731
+    d, dv = max(d, 32), max(dv, 32)   # 16-wide heads sit in 32-wide tiles
     total = 2 * r(M * d * 2) + (r(M * dv * 2) if last else 0) + 2 * r(M * 4)
     if bwd:   # the upstream gradient rows, three more vectors, the backward's own row-store patches
         total += r(M * (dv if last else d) * 2) + 3 * r(M * 4) + 4 * 4096
@@ -135,15 +137,17 @@ def _lstep_mb_lds(m, d, dv, last, bwd):
 
 
 def _lstep_mb(m, d, dv, bwd):
-    """Whether the multi-block MFMA L-step kernels take this grid: up to 128 frames, head dims 32 / 64 / 128."""
-    return ((_MB_BWD or not bwd) and 1 <= m <= _MB_MAX_FRAMES and d in (32, 64, 128) and dv in (32, 64, 128)
+    """Whether the multi-block MFMA L-step kernels take this grid: up to 128 frames, head dims 32 / 64 / 128 in
+    any pair, or 16 / 16."""
+    dims = (d in (32, 64, 128) and dv in (32, 64, 128)) or d == dv == 16
+    return ((_MB_BWD or not bwd) and 1 <= m <= _MB_MAX_FRAMES and dims
             and all(_lstep_mb_lds(m, d, dv, last, bwd) <= _LDS_BYTES for last in (False, True)))
 
 
 def _lstep_supported(m, d, dv, bwd):
     """Whether the HIP L-steps run this grid: the one-tile MFMA kernels (m <= 32, d and dv in {64, 128}), the
-    multi-block MFMA kernels (m <= 128, head dims 32 / 64 / 128), or the general kernels (any m whose per-column
-    tiles fit the LDS)."""
+    multi-block MFMA kernels (m <= 128, head dims 32 / 64 / 128, or 16 / 16), or the general kernels (any m whose
+    per-column tiles fit the LDS)."""
     if m <= 32 and d in (64, 128) and dv in (64, 128):
         return True
     if _lstep_mb(m, d, dv, bwd):
@@ -153,9 +157,9 @@ def _lstep_supported(m, d, dv, bwd):
 
 def _fused_supported(q, k, v, num_blocks):
     D, Dv = q.shape[-1], v.shape[-1]
-    # flash-entropy kernels at 64 / 128 (either dim) or 32 / 32; 32-wide L-steps on the general kernels
+    # flash-entropy kernels at 64 / 128 (either dim), 32 / 32 or 16 / 16
     return (q.is_cuda and q.dtype in _lib.DTYPES and k.dtype == q.dtype and v.dtype == q.dtype
-            and ((D in (64, 128) and Dv in (64, 128)) or D == Dv == 32)
+            and ((D in (64, 128) and Dv in (64, 128)) or D == Dv == 32 or D == Dv == 16)
             and _lstep_supported(num_blocks, D, Dv, False)
             and k.shape == q.shape and v.shape[:-1] == q.shape[:-1])
 
@@ -434,7 +438,7 @@ def vmonarch_attention(q, k, v, num_blocks, block_size, num_iters=2, recompute_t
             return _vmonarch_fused(q, k, v, *args)
         if needs_graph and _hip_backward_supported(q, k, v, num_blocks):
             return _VMonarchFunction.apply(q, k, v, *args)
-        # Head dims the kernels do not take as they are (16, mixes with 16 / 32, or D != Dv with autograd): zero columns
+        # Head dims the kernels do not take as they are (mixes of 16 and 32, or D != Dv with autograd): zero columns
         # change neither q.k nor P.v, so q, k and v padded to one kernel width give z with zero columns
         # past Dv, with the softmax scale of the true D; autograd slices the padded gradients back.
         w = _padded_width(D, Dv)
