@@ -19,6 +19,7 @@ the CPU oracle (numpy restatement of the reference) on a bounded sample of the s
     python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--cpu-heads 6 | --no-cpu-baseline]
     python bench.py --copy-calibration     # a plain 1 GiB device copy, x5 (for HBM counter scaling)
     python bench.py --serial-only ...      # only the serial-order region (what kernel traces use)
+    python bench.py --lstep-grids          # the fused L-step alone at 21-128 frames (JSON lines)
 
 `roofline.traffic` is the HBM traffic of the dominant launch measured with rocprofv3 counters
 (FETCH_SIZE and WRITE_SIZE, each scaled by what the same counter reads for the 1 GiB copy of
@@ -178,6 +179,56 @@ def backward_timings(steps):
     }
 
 
+def lstep_grids(reps=20):
+    """The fused L-step alone (vmo_lstep_fwd / vmo_lstep_bwd) at grids of m frames of b ~ 32760 / m tokens (H = 12,
+    D = Dv = 128, bf16; inputs resident in HBM): m <= 32 on the one-tile kernels, m up to 128 on the multi-block
+    kernels.  Per grid and step kind, the launch time (HIP events around `reps` back-to-back launches on the
+    launch stream, after a warm-up) and the rate of its algorithmic bytes: forward reads q, the R-step output
+    (kr, or [kr | y] when last) and the entropy and writes u / z; backward also reads the upstream gradient and
+    the fp32 dq (accumulated into) and writes dq and d out."""
+    import torch
+    from vmonarch_amd.vmonarch import _lstep_bwd_launch, _lstep_launch
+    dev = torch.device("cuda:0")
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        ev[0].record()
+        for _ in range(reps):
+            fn()
+        ev[1].record()
+        torch.cuda.synchronize()
+        return ev[0].elapsed_time(ev[1]) / reps
+
+    g = torch.Generator().manual_seed(0)
+    rows = []
+    for m in (21, 32, 33, 48, 64, 96, 128):
+        b = 32760 // m
+        n = m * b
+        tok = B * H * n
+        q = (torch.randn(B, H, n, D, generator=g) * 0.5).bfloat16().to(dev)
+        out = (torch.randn(B, H, n, 2 * D, generator=g) * 0.5).bfloat16().to(dev)
+        ent = (torch.rand(B, H, n, generator=g) * 3).to(dev)
+        res = torch.empty(B, H, n, D, device=dev, dtype=torch.bfloat16)
+        grad = torch.randn(B, H, n, D, generator=g).bfloat16().to(dev)
+        dq = torch.zeros(B, H, n, D, device=dev)
+        for last in (False, True):
+            o = out if last else out[..., :D].contiguous()
+            dout = torch.empty_like(o)
+            ms_f = timed(lambda: _lstep_launch(q, o, ent, res, m, b, D ** -0.5, last, 0, 0.01))
+            ms_b = timed(lambda: _lstep_bwd_launch(q, o, ent, grad, dq, dout, m, b, D ** -0.5, last, 0, 0.01))
+            bytes_f = tok * (D * 2 + o.shape[-1] * 2 + 4 + D * 2)
+            bytes_b = tok * (D * 2 + o.shape[-1] * 2 + 4 + D * 2 + D * 4 * 2 + o.shape[-1] * 2)
+            rows.append({"m": m, "b": b, "last": last,
+                         "fwd_us": round(ms_f * 1e3, 1), "fwd_hbm_frac": round(bytes_f / ms_f / 1e6 / PEAK_HBM_GBS, 3),
+                         "bwd_us": round(ms_b * 1e3, 1), "bwd_hbm_frac": round(bytes_b / ms_b / 1e6 / PEAK_HBM_GBS, 3)})
+            print(json.dumps(rows[-1]), flush=True)
+        del q, out, ent, res, grad, dq
+    print(json.dumps({"lstep_grids": rows, "heads": H, "head_dim": D, "dtype": "bf16", "reps": reps}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -192,9 +243,14 @@ def main():
                     help="also time the opt-in fp8 q k^T mode of the R-steps (reported beside `value`, never as it)")
     ap.add_argument("--serial-only", action="store_true",
                     help="time only the serial order (every launch alone; for kernel traces)")
+    ap.add_argument("--lstep-grids", action="store_true",
+                    help="instead of the step: the fused L-step forward and backward alone at 21-128 frames")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.lstep_grids:
+        lstep_grids()
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); the multi-GPU design "

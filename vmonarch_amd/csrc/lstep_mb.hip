@@ -38,7 +38,10 @@ constexpr int kMbMaxFrames = 32 * kMbMaxBlocks;  // m <= 128
 // upstream gradient), M-float vectors (entropy bias, row LSE; the backward's row sums rs_i, column factors f_k
 // and dc_k).  The forward's row-store patches (kEpiPatchBytes per wave) reuse the start of the allocation
 // once every wave has passed the barrier that ends the compute; the backward, which stores between its
-// passes, has patches of its own.
+// passes, has patches of its own -- half-size ones (16 rows at a time) for the last step up to 64 frames, whose
+// four tiles at head dim 128 then leave room for two workgroups per CU (73.3 instead of 81.3 KB); beyond that one
+// workgroup fits either way, and the whole patches store faster.
+__host__ __device__ constexpr int mb_bwd_patch_rows(bool last, int M) { return last && M <= 64 ? 16 : 32; }
 struct MbLayout {
   int q, k, y, g, e, lse, rs, f, dc, patch, total;
 };
@@ -55,7 +58,7 @@ __host__ __device__ inline MbLayout mb_layout(int M, int d, int dv, bool last, b
   L.rs = bwd ? take(M * 4) : 0;
   L.f = bwd ? take(M * 4) : 0;
   L.dc = bwd ? take(M * 4) : 0;
-  L.patch = bwd ? take(kMbWaves * kEpiPatchBytes) : 0;
+  L.patch = bwd ? take(kMbWaves * mb_bwd_patch_rows(last, M) * 32 * 4) : 0;
   L.total = off > kMbWaves * kEpiPatchBytes ? off : kMbWaves * kEpiPatchBytes;
   return L;
 }
@@ -317,7 +320,8 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
   VMO_LDS float* dc_t = (VMO_LDS float*)(sm + Lo.dc);
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int hl = lane >> 5, l32 = lane & 31;
-  VMO_LDS float* patch = (VMO_LDS float*)(sm + Lo.patch + wave * kEpiPatchBytes);
+  const bool half_patch = mb_bwd_patch_rows(LAST, M) == 16;
+  VMO_LDS float* patch = (VMO_LDS float*)(sm + Lo.patch + wave * mb_bwd_patch_rows(LAST, M) * 32 * 4);
 
   const int col = blockIdx.x, bh = col / p.bs, j = col % p.bs, hh = bh % p.heads, bb = bh / p.heads;
   const int64_t q_rs = (int64_t)p.bs * p.q_sn, o_rs = (int64_t)p.bs * p.out_sn, g_rs = (int64_t)p.bs * p.g_sn;
@@ -404,6 +408,13 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
   };
   const bool row_ok = 32 * blk + l32 < m;   // this lane's query row (query-block passes) or key (key-block passes)
   const int nrows = busy ? min(32, m - 32 * blk) : 0;
+  // row stores through the patch: whole (32 rows) or half (16 rows at a time)
+  auto store_rows = [&](auto cw_tag, const f32x16* acc, int nacc, int mode, char* row0, int64_t stride)
+      __attribute__((always_inline)) {
+    constexpr int CWS = decltype(cw_tag)::value;
+    if (half_patch) store_acc_rows<F16, CWS, 16>(patch, acc, nacc, 1.f, mode, row0, stride, nrows, lane);
+    else store_acc_rows<F16, CWS, 32>(patch, acc, nacc, 1.f, mode, row0, stride, nrows, lane);
+  };
 
   if constexpr (LAST) {
     // ---- pass A: one query row per lane
@@ -449,7 +460,7 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
           accq[a] = E::mfma(mb_tr8<V8, RBD>(k_t + 32 * kb * RBD, lane, a, 1), P1, accq[a]);
         }
       }
-      store_acc_rows<F16, CWD>(patch, accq, ND, 1.f, dq_mode, (char*)(dqcol + 32 * blk * dq_rs), dq_rs * 4, nrows, lane);
+      store_rows(std::integral_constant<int, CWD>{}, accq, ND, dq_mode, (char*)(dqcol + 32 * blk * dq_rs), dq_rs * 4);
     }
     __syncthreads();
     // ---- pass B: one key per lane, as two sweeps over the query blocks (dy, then dkr: holding both accumulator
@@ -471,8 +482,8 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
           accy[a] = E::mfma(mb_tr8<V8, RBY>(g_t + 32 * ib * RBY, lane, a, 1), A1, accy[a]);
         }
       }
-      store_acc_rows<F16, CWV>(patch, accy, NV, 1.f, kGradStore, (char*)(dcol + 32 * blk * do_rs + D), do_rs * 2, nrows,
-                               lane);
+      store_rows(std::integral_constant<int, CWV>{}, accy, NV, kGradStore, (char*)(dcol + 32 * blk * do_rs + D),
+                 do_rs * 2);
       f32x16 acck[ND];
 #pragma unroll
       for (int a = 0; a < ND; ++a) acck[a] = f32x16{};
@@ -499,7 +510,7 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
           acck[a] = E::mfma(mb_tr8<V8, RBD>(q_t + 32 * ib * RBD, lane, a, 1), P1, acck[a]);
         }
       }
-      store_acc_rows<F16, CWD>(patch, acck, ND, 1.f, kGradStore, (char*)(dcol + 32 * blk * do_rs), do_rs * 2, nrows, lane);
+      store_rows(std::integral_constant<int, CWD>{}, acck, ND, kGradStore, (char*)(dcol + 32 * blk * do_rs), do_rs * 2);
     }
   } else {
     // ---- pass 0: row LSE (query blocks)

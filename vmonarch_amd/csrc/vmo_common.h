@@ -196,9 +196,10 @@ __device__ __forceinline__ int grad_mode(int flags, int accum_bit, int f32_bit, 
 constexpr int tile_w(int w) { return w < 32 ? 32 : w; }
 
 // CW = 16: each accumulator block holds 16 valid columns (rows 0-15 of the transposed accumulator; the 16-wide
-// heads, whose LDS tiles hold every row twice), stored as columns 16 a .. 16 a + 15.
+// heads, whose LDS tiles hold every row twice), stored as columns 16 a .. 16 a + 15.  PROWS = 16: a 2 KB patch
+// that takes the 32 rows in two halves (for kernels whose LDS budget is that tight).
 constexpr int kEpiPatchBytes = 32 * 32 * 4;
-template <bool F16, int CW = 32>
+template <bool F16, int CW = 32, int PROWS = 32>
 __device__ __forceinline__ void store_acc_rows(VMO_LDS float* patch, const f32x16* acc, int nacc, float f, int mode,
                                                char* row0, int64_t row_stride_bytes, int nrows, int lane,
                                                int rbegin = 0, const char* src0 = nullptr,
@@ -208,7 +209,8 @@ __device__ __forceinline__ void store_acc_rows(VMO_LDS float* patch, const f32x1
   using V8 = typename Elem<F16>::V8;
   const int hl = lane >> 5, l32 = lane & 31, rr0 = lane >> 3, c = lane & 7;
   static_assert(CW == 16 || CW == 32, "block width");
-  if (CW == 32 && mode == kGradStore && nacc % 2 == 0) {
+  static_assert(PROWS == 16 || PROWS == 32, "patch rows");
+  if (CW == 32 && PROWS == 32 && mode == kGradStore && nacc % 2 == 0) {
     // 16-bit rows: two blocks (64 columns) per pass, so that 8 lanes write a whole 128-byte segment
     VMO_LDS char* pb = (VMO_LDS char*)patch;   // [32 rows][8 chunks of 16 bytes], chunk ^ (row & 7)
     for (int a = 0; a < nacc; a += 2) {
@@ -231,18 +233,26 @@ __device__ __forceinline__ void store_acc_rows(VMO_LDS float* patch, const f32x1
     return;
   }
   const int esize = mode == kGradStore || mode == kGradSumStore ? 2 : 4;
-  for (int a = 0; a < nacc; ++a) {
+  for (int a = 0; a < nacc; ++a)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {   // row l32, 16-byte chunk 2 j + hl, swizzled by row against bank conflicts
-      f32x4 v;
+  for (int h = 0; h < 32 / PROWS; ++h) {   // rows h PROWS .. h PROWS + PROWS - 1 through the patch
+    if (PROWS == 32 || (l32 / PROWS) == h) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = acc[a][4 * j + e] * f;
-      *(VMO_LDS f32x4*)(patch + l32 * 32 + ((2 * j + hl) ^ (l32 & 7)) * 4) = v;
+      for (int j = 0; j < 4; ++j) {   // row l32, 16-byte chunk 2 j + hl, swizzled by row against bank conflicts
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = acc[a][4 * j + e] * f;
+        *(VMO_LDS f32x4*)(patch + (l32 % PROWS) * 32 + ((2 * j + hl) ^ (l32 & 7)) * 4) = v;
+      }
     }
+    // The lanes read rows other lanes wrote: to the compiler's one-thread view, a lane that wrote nothing in this
+    // half re-reads the address it read in the last one, and it forwarded that old value (the reads of a wave
+    // follow its writes in order in the hardware; this keeps the compiler from caching across the exchange).
+    asm volatile("" ::: "memory");
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {   // rows rr0 + 8 i, chunk c: 8 lanes per row
-      const int rr = rr0 + 8 * i;
-      const f32x4 v = *(const VMO_LDS f32x4*)(patch + rr * 32 + (c ^ (rr & 7)) * 4);
+    for (int i = 0; i < PROWS / 8; ++i) {   // rows rr0 + 8 i of the patch, chunk c: 8 lanes per row
+      const int pr = rr0 + 8 * i, rr = h * PROWS + pr;
+      const f32x4 v = *(const VMO_LDS f32x4*)(patch + pr * 32 + (c ^ (pr & 7)) * 4);
       if (rr >= rbegin && rr < nrows && 4 * c < CW) {
         char* dst = row0 + rr * row_stride_bytes + (int64_t)(CW * a + 4 * c) * esize;
         if (mode == kGradStore || mode == kGradSumStore) {
@@ -261,6 +271,7 @@ __device__ __forceinline__ void store_acc_rows(VMO_LDS float* patch, const f32x1
         }
       }
     }
+    asm volatile("" ::: "memory");   // this half's reads before the next half's (or block's) writes
   }
 }
 
