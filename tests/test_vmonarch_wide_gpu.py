@@ -27,7 +27,7 @@ def _r5(t, m, b):
     return t.float().cpu().numpy().reshape(B, H, m, b, F)
 
 
-@pytest.mark.parametrize("m", [7, 33, 48, 64, 65, 96, 128])
+@pytest.mark.parametrize("m", [7, 33, 48, 64, 65, 96, 128, 140])   # 140: past the multi-block kernels
 @pytest.mark.parametrize("d, dv", [(64, 64), (128, 128), (32, 32), (128, 64), (32, 128), (256, 256), (16, 16)])
 @pytest.mark.parametrize("last", [False, True])
 def test_general_lstep_forward_matches_oracle(m, d, dv, last):
@@ -55,7 +55,7 @@ def test_general_lstep_forward_matches_oracle(m, d, dv, last):
     assert hip_library_loaded()
 
 
-@pytest.mark.parametrize("m", [7, 33, 64, 65, 96, 128])
+@pytest.mark.parametrize("m", [7, 33, 64, 65, 96, 128, 129])   # 129: the general kernel (fits at 16 / 16)
 @pytest.mark.parametrize("d, dv", [(64, 64), (128, 128), (32, 32), (64, 128), (128, 32), (16, 16)])
 @pytest.mark.parametrize("last, mcm", [(False, 0.01), (False, 0.6), (True, 0.01)])
 def test_general_lstep_backward_matches_oracle(m, d, dv, last, mcm):
