@@ -13,7 +13,7 @@ from oracle import entropy_attention, entropy_attention_grad
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 PAIRS = [(16, 16), (32, 32), (32, 64), (64, 32), (32, 128), (128, 32), (64, 64), (64, 128), (128, 64),
-         (128, 128), (64, 256), (128, 256), (256, 256)]
+         (128, 128), (64, 256), (128, 256), (256, 256), (16, 32), (16, 64), (16, 128), (16, 256), (32, 256)]
 
 
 def _case(seed):
@@ -32,7 +32,7 @@ def _tensor(g, B, H, N, D, dtype, dit):
     return t.transpose(1, 2) if dit else t
 
 
-@pytest.mark.parametrize("seed", range(16))
+@pytest.mark.parametrize("seed", range(24))
 def test_fuzz_forward_frames(seed):
     """fea_forward over `frames` problems of nq queries and nk keys (C ABI), against the oracle per frame."""
     from vmonarch_amd.kernel import fea_forward, _kernel_widths
