@@ -27,13 +27,20 @@ def _r5(t, m, b):
     return t.float().cpu().numpy().reshape(B, H, m, b, F)
 
 
-@pytest.mark.parametrize("m", [7, 33, 48, 64, 65, 96, 128, 140])   # 140: past the multi-block kernels
-@pytest.mark.parametrize("d, dv", [(64, 64), (128, 128), (32, 32), (128, 64), (32, 128), (256, 256), (16, 16)])
-@pytest.mark.parametrize("last", [False, True])
+def _grids(ms, dims, lasts, bwd):
+    """(m, d, dv, last) for the grids some HIP L-step kernel takes (the others are refused on the host: the LDS of a
+    CU bounds a column's tiles; a non-last step has no value width of its own)."""
+    from vmonarch_amd.vmonarch import _lstep_supported
+    return [(m, d, dv, last) for m in ms for d, dv in dims for last in lasts
+            if _lstep_supported(m, d, dv, bwd) and (last or not bwd or d == dv)]
+
+
+# m = 140: past the multi-block kernels (the general ones)
+@pytest.mark.parametrize("m, d, dv, last", _grids([7, 33, 48, 64, 65, 96, 128, 140],
+                                                  [(64, 64), (128, 128), (32, 32), (128, 64), (32, 128), (256, 256),
+                                                   (16, 16)], [False, True], False))
 def test_general_lstep_forward_matches_oracle(m, d, dv, last):
-    from vmonarch_amd.vmonarch import _lstep_launch, _lstep_supported
-    if not _lstep_supported(m, d, dv, False):
-        pytest.skip("tiles beyond the LDS of a CU")
+    from vmonarch_amd.vmonarch import _lstep_launch
     g = torch.Generator().manual_seed(7 * m + d + dv + last)
     B, H, b = 1, 2, 24
     N = m * b
@@ -55,13 +62,14 @@ def test_general_lstep_forward_matches_oracle(m, d, dv, last):
     assert hip_library_loaded()
 
 
-@pytest.mark.parametrize("m", [7, 33, 64, 65, 96, 128, 129])   # 129: the general kernel (fits at 16 / 16)
-@pytest.mark.parametrize("d, dv", [(64, 64), (128, 128), (32, 32), (64, 128), (128, 32), (16, 16)])
-@pytest.mark.parametrize("last, mcm", [(False, 0.01), (False, 0.6), (True, 0.01)])
+# m = 129: the general kernel (fits at 16 / 16); mcm 0.6 keeps the column-mass clamp active
+@pytest.mark.parametrize("m, d, dv, last, mcm",
+                         [(m, d, dv, last, mcm) for m, d, dv, last in
+                          _grids([7, 33, 64, 65, 96, 128, 129], [(64, 64), (128, 128), (32, 32), (64, 128), (128, 32),
+                                                                  (16, 16)], [False, True], True)
+                          for mcm in ((0.01,) if last else (0.01, 0.6))])
 def test_general_lstep_backward_matches_oracle(m, d, dv, last, mcm):
-    from vmonarch_amd.vmonarch import _lstep_bwd_launch, _lstep_supported
-    if (not last and d != dv) or not _lstep_supported(m, d, dv, True):
-        pytest.skip("non-last steps have no value width; or tiles beyond the LDS of a CU")
+    from vmonarch_amd.vmonarch import _lstep_bwd_launch
     g = torch.Generator().manual_seed(11 * m + d + dv + last + int(10 * mcm))
     B, H, b = 1, 2, 20
     N = m * b

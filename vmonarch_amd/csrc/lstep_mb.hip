@@ -24,6 +24,8 @@
 // Rounding points as the one-tile kernels: logits in fp32 from the 16-bit q and kr, attn rounded to the
 // 16-bit type where it multiplies q or y, the column mass from the fp32 attn, u / z rounded once when stored.
 // Results leave through per-wave LDS patches as whole row segments (store_acc_rows).
+#include <atomic>
+
 #include "vmo_common.h"
 #include "vmo_host.h"
 #include "lstep_params.h"
@@ -672,8 +674,12 @@ static int launch_mb(const LParams& p, hipStream_t s) {
   const int M = 32 * ((p.m + 31) / 32);
   const int lds = mb_layout(M, tile_w(D), tile_w(DV), LAST, false).total;
   auto kern = lstep_mb_kernel<F16, D, DV, LAST>;
-  if (lds > 65536 && hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
-    return set_error(VMO_ERR_LAUNCH, "lstep_mb: cannot raise the LDS limit to %d bytes", lds);
+  static std::atomic<int> lds_limit{65536};   // this kernel's dynamic-LDS limit as raised so far
+  if (lds > lds_limit.load(std::memory_order_relaxed)) {   // (idempotent: a race only repeats the call)
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
+      return set_error(VMO_ERR_LAUNCH, "lstep_mb: cannot raise the LDS limit to %d bytes", lds);
+    lds_limit.store(lds, std::memory_order_relaxed);
+  }
   hipLaunchKernelGGL(kern, dim3(p.cols_total), dim3(64 * kMbWaves), lds, s, p);
   return launch_status("lstep_mb");
 }
@@ -702,8 +708,12 @@ static int launch_mb_bwd(const LBParams& p, hipStream_t s) {
   const int M = 32 * ((p.m + 31) / 32);
   const int lds = mb_layout(M, tile_w(D), tile_w(DV), LAST, true).total;
   auto kern = lstep_mb_bwd_kernel<F16, D, DV, LAST>;
-  if (lds > 65536 && hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
-    return set_error(VMO_ERR_LAUNCH, "lstep_mb_bwd: cannot raise the LDS limit to %d bytes", lds);
+  static std::atomic<int> lds_limit{65536};   // as in launch_mb
+  if (lds > lds_limit.load(std::memory_order_relaxed)) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
+      return set_error(VMO_ERR_LAUNCH, "lstep_mb_bwd: cannot raise the LDS limit to %d bytes", lds);
+    lds_limit.store(lds, std::memory_order_relaxed);
+  }
   hipLaunchKernelGGL(kern, dim3(p.cols_total), dim3(64 * kMbWaves), lds, s, p);
   return launch_status("lstep_mb_bwd");
 }
