@@ -45,7 +45,7 @@ constexpr int kMbMaxFrames = 32 * kMbMaxBlocks;  // m <= 128
 // workgroup fits either way, and the whole patches store faster.
 __host__ __device__ constexpr int mb_bwd_patch_rows(bool last, int M) { return last && M <= 64 ? 16 : 32; }
 struct MbLayout {
-  int q, k, y, g, e, lse, rs, f, dc, patch, total;
+  int q, k, y, g, e, lse, part, rs, f, dc, patch, total;
 };
 __host__ __device__ inline MbLayout mb_layout(int M, int d, int dv, bool last, bool bwd) {
   MbLayout L;
@@ -57,6 +57,7 @@ __host__ __device__ inline MbLayout mb_layout(int M, int d, int dv, bool last, b
   L.g = bwd ? take(M * (last ? dv : d) * 2) : 0;
   L.e = take(M * 4);
   L.lse = take(M * 4);
+  L.part = bwd ? 0 : take(4 * M * 4);   // the forward's partial row max / sum (two key blocks)
   L.rs = bwd ? take(M * 4) : 0;
   L.f = bwd ? take(M * 4) : 0;
   L.dc = bwd ? take(M * 4) : 0;
@@ -178,6 +179,117 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_kernel(LParams p) {
     }
     return wave_max32(mx);
   };
+
+  // Two 32-frame blocks (33-64 frames) with an even number of output blocks: all four waves compute (with one
+  // wave per block, waves 2 and 3 -- and so two of the CU's four SIMDs -- would idle through the passes, which
+  // then took half of the launch at 33 frames).  The LSE pass splits the keys (wave w: query block w & 1 against
+  // key block w >> 1; partial row max and sum through LDS), the product pass the output columns (wave w: row
+  // block w & 1, column half w >> 1; both halves recompute the block's attention, the products' MFMAs are split).
+  constexpr int NH = NACC / 2;
+  if (NACC % 2 == 0 && MB == 2) {
+    const int rb = wave & 1, half = wave >> 1;
+    f32x16 acch[NH > 0 ? NH : 1];
+#pragma unroll
+    for (int a = 0; a < NH; ++a) acch[a] = f32x16{};
+    float fsc = 1.f;
+    if constexpr (LAST) {
+      f32x16 x[kMbMaxBlocks];
+      const float mx = s_blocks(rb, x);
+      float sum = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          x[kb][r] = fast_exp2(x[kb][r] - mx);
+          sum += x[kb][r];
+        }
+      const float inv = 1.0f / wave_sum32(sum);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const V8 P0 = mb_pack<T, V8>(x[kb], 0, inv), P1 = mb_pack<T, V8>(x[kb], 1, inv);
+#pragma unroll
+        for (int a = 0; a < NH; ++a) {
+          acch[a] = E::mfma(mb_tr8<V8, RBY>(y_t + 32 * kb * RBY, lane, half * NH + a, 0), P0, acch[a]);
+          acch[a] = E::mfma(mb_tr8<V8, RBY>(y_t + 32 * kb * RBY, lane, half * NH + a, 1), P1, acch[a]);
+        }
+      }
+    } else {
+      VMO_LDS float* pmax = (VMO_LDS float*)(sm + Lo.part);   // [key block][M]
+      VMO_LDS float* psum = pmax + 2 * M;
+      {   // S^T block (keys of block half, queries of block rb): partial max and sum per query row
+        f32x16 x = f32x16{};
+#pragma unroll
+        for (int ds = 0; ds < NDS; ++ds)
+          x = E::mfma(mb_row8<V8, RBD>(k_t + 32 * half * RBD, l32, hl, ds), mb_row8<V8, RBD>(q_t + 32 * rb * RBD, l32, hl, ds), x);
+        float mx = -3.0e38f;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 ev = *(const VMO_LDS f32x4*)(e_t + 32 * half + 8 * g + 4 * hl);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            x[4 * g + e] = fmaf(x[4 * g + e], c, ev[e]);
+            mx = fmaxf(mx, x[4 * g + e]);
+          }
+        }
+        mx = wave_max32(mx);
+        float sum = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sum += fast_exp2(x[r] - mx);
+        sum = wave_sum32(sum);
+        if (hl == 0) {
+          pmax[half * M + 32 * rb + l32] = mx;
+          psum[half * M + 32 * rb + l32] = sum;
+        }
+      }
+      __syncthreads();
+      if (tid < M) {   // LSE of query row tid from the two key blocks' partials; rows past m get +1e30
+        const float m0 = pmax[tid], m1 = pmax[M + tid], mm = fmaxf(m0, m1);
+        const float l = psum[tid] * fast_exp2(m0 - mm) + psum[M + tid] * fast_exp2(m1 - mm);
+        lse_t[tid] = tid < m ? mm + fast_log2(l) : 1.0e30f;
+      }
+      __syncthreads();
+      // u^T columns of half `half` for key block rb: one key per lane
+      V8 kb_op[NDS];
+#pragma unroll
+      for (int ds = 0; ds < NDS; ++ds) kb_op[ds] = mb_row8<V8, RBD>(k_t + 32 * rb * RBD, l32, hl, ds);
+      const float ek = e_t[32 * rb + l32];
+      float cm = 0.f;
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib) {
+        f32x16 x = f32x16{};
+#pragma unroll
+        for (int ds = 0; ds < NDS; ++ds) x = E::mfma(mb_row8<V8, RBD>(q_t + 32 * ib * RBD, l32, hl, ds), kb_op[ds], x);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 lv = *(const VMO_LDS f32x4*)(lse_t + 32 * ib + 8 * g + 4 * hl);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float a = fast_exp2(fmaf(x[4 * g + e], c, ek - lv[e]));
+            x[4 * g + e] = a;
+            cm += a;
+          }
+        }
+        const V8 P0 = mb_pack<T, V8>(x, 0, 1.f), P1 = mb_pack<T, V8>(x, 1, 1.f);
+#pragma unroll
+        for (int a = 0; a < NH; ++a) {
+          acch[a] = E::mfma(mb_tr8<V8, RBD>(q_t + 32 * ib * RBD, lane, half * NH + a, 0), P0, acch[a]);
+          acch[a] = E::mfma(mb_tr8<V8, RBD>(q_t + 32 * ib * RBD, lane, half * NH + a, 1), P1, acch[a]);
+        }
+      }
+      fsc = p.scale / fmaxf(wave_sum32(cm), p.min_col_mass);
+    }
+    __syncthreads();   // every wave is done with the tiles: the patches reuse them
+    VMO_LDS float* patch = (VMO_LDS float*)(sm + wave * kEpiPatchBytes);
+    const int nrows = min(32, m - 32 * rb);
+    T* const rows = rcol + 32 * rb * r_rs + half * NH * 32;
+    if constexpr (LAST) {
+      const int ibeg = p.skip > j ? (p.skip - j + p.bs - 1) / p.bs : 0;
+      store_acc_rows<F16, CW>(patch, acch, NH, 1.f, kGradStore, (char*)rows, r_rs * 2, nrows, lane, max(0, ibeg - 32 * rb));
+    } else {
+      store_acc_rows<F16, CW>(patch, acch, NH, fsc, kGradStore, (char*)rows, r_rs * 2, nrows, lane);
+    }
+    return;
+  }
 
   f32x16 acc[NACC];
 #pragma unroll
