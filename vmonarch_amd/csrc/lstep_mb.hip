@@ -1,5 +1,5 @@
-// Multi-block fused L-step for gfx950: grids of more than 32 frames (and head dims 32 / 64 / 128 at any
-// frame count up to kMbMaxFrames), on MFMA.
+// Multi-block fused L-step for gfx950: grids of more than 32 frames (and head dims 16 / 32 / 64 / 128 at
+// any frame count up to kMbMaxFrames), on MFMA.
 //
 // Reference: video_monarch_attention/vmonarch.py:51-63 -- per grid column j (the same spatial position in
 // all m frames) an m x m attention over the frames:
@@ -9,9 +9,9 @@
 // (the one-tile kernels in lstep.hip take m <= 32 in a single 32 x 32 MFMA tile per column).
 //
 // Here one 4-wave workgroup owns a column: its q, kr (and y) rows -- tokens i b + j, i < m -- are staged
-// whole into swizzled LDS tiles of M = 32 * MB rows (MB = ceil(m / 32) <= kMbMaxBlocks; rows past m repeat
-// the last row, finite data whose weights are exact zeros), and the m x m products run on
-// v_mfma_f32_32x32x16 in 32 x 32 blocks:
+// whole into swizzled LDS tiles of M = 32 * MB rows (MB = ceil(m / 32) <= kMbMaxBlocks; rows past m are
+// finite data whose weights are exact zeros), and the m x m products run on v_mfma_f32_32x32x16 in 32 x 32
+// blocks (with MB = 2 split over all four waves, see lstep_mb_kernel):
 //   * last: wave w owns query block w.  S^T blocks (keys x queries: one query row per lane) for every key
 //     block, softmax over all of them in registers (max, sum, normalise: the attention is rounded to the
 //     16-bit type only once normalised, as the reference's attn.to(y.dtype)), then z^T += Y^T P^T with the
