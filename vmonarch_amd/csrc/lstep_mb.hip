@@ -216,15 +216,23 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_kernel(LParams p) {
     } else {
       VMO_LDS float* pmax = (VMO_LDS float*)(sm + Lo.part);   // [key block][M]
       VMO_LDS float* psum = pmax + 2 * M;
-      {   // S^T block (keys of block half, queries of block rb): partial max and sum per query row
+      // The LSE pass takes key block rb against query block half: the kr rows it reads are the product pass's
+      // B operand (same lanes and dims), and its q rows that pass's A operand for query block half, so both stay
+      // in registers and the product pass reads one query block's rows from LDS instead of both and kr.
+      V8 kr_op[NDS], q_op[NDS];
+#pragma unroll
+      for (int ds = 0; ds < NDS; ++ds) {
+        kr_op[ds] = mb_row8<V8, RBD>(k_t + 32 * rb * RBD, l32, hl, ds);
+        q_op[ds] = mb_row8<V8, RBD>(q_t + 32 * half * RBD, l32, hl, ds);
+      }
+      {   // S^T block (keys of block rb, queries of block half): partial max and sum per query row
         f32x16 x = f32x16{};
 #pragma unroll
-        for (int ds = 0; ds < NDS; ++ds)
-          x = E::mfma(mb_row8<V8, RBD>(k_t + 32 * half * RBD, l32, hl, ds), mb_row8<V8, RBD>(q_t + 32 * rb * RBD, l32, hl, ds), x);
+        for (int ds = 0; ds < NDS; ++ds) x = E::mfma(kr_op[ds], q_op[ds], x);
         float mx = -3.0e38f;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const f32x4 ev = *(const VMO_LDS f32x4*)(e_t + 32 * half + 8 * g + 4 * hl);
+          const f32x4 ev = *(const VMO_LDS f32x4*)(e_t + 32 * rb + 8 * g + 4 * hl);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             x[4 * g + e] = fmaf(x[4 * g + e], c, ev[e]);
@@ -237,8 +245,8 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_kernel(LParams p) {
         for (int r = 0; r < 16; ++r) sum += fast_exp2(x[r] - mx);
         sum = wave_sum32(sum);
         if (hl == 0) {
-          pmax[half * M + 32 * rb + l32] = mx;
-          psum[half * M + 32 * rb + l32] = sum;
+          pmax[rb * M + 32 * half + l32] = mx;
+          psum[rb * M + 32 * half + l32] = sum;
         }
       }
       __syncthreads();
@@ -248,17 +256,16 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_kernel(LParams p) {
         lse_t[tid] = tid < m ? mm + fast_log2(l) : 1.0e30f;
       }
       __syncthreads();
-      // u^T columns of half `half` for key block rb: one key per lane
-      V8 kb_op[NDS];
-#pragma unroll
-      for (int ds = 0; ds < NDS; ++ds) kb_op[ds] = mb_row8<V8, RBD>(k_t + 32 * rb * RBD, l32, hl, ds);
+      // u^T columns of half `half` for key block rb: one key per lane; query block half first (rows in registers)
       const float ek = e_t[32 * rb + l32];
       float cm = 0.f;
 #pragma unroll
-      for (int ib = 0; ib < 2; ++ib) {
+      for (int t = 0; t < 2; ++t) {
+        const int ib = t == 0 ? half : 1 - half;
         f32x16 x = f32x16{};
 #pragma unroll
-        for (int ds = 0; ds < NDS; ++ds) x = E::mfma(mb_row8<V8, RBD>(q_t + 32 * ib * RBD, l32, hl, ds), kb_op[ds], x);
+        for (int ds = 0; ds < NDS; ++ds)
+          x = E::mfma(t == 0 ? q_op[ds] : mb_row8<V8, RBD>(q_t + 32 * ib * RBD, l32, hl, ds), kr_op[ds], x);
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const f32x4 lv = *(const VMO_LDS f32x4*)(lse_t + 32 * ib + 8 * g + 4 * hl);
