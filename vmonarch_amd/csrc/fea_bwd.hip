@@ -435,6 +435,14 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
             dp[kb2] = E::mfma(x, dof[DO0 + j - NSQ], dp[kb2]);
           }
         });
+    if constexpr (dq_prefetch<D, DV>() > 0) {   // reads two steps ahead of their MFMAs, as in dkdv
+      struct Chain {
+        static constexpr int reads(int) { return 1; }
+        static constexpr int mfmas(int i) { return W0K && i % NSD < NSQ ? 2 : 1; }
+        static constexpr int ahead(int) { return 2; }
+      };
+      pin_chain<Chain, 2 * NSD>();
+    }
     V8 G[4];
 #pragma unroll
     for (int kb2 = 0; kb2 < 2; ++kb2) {
@@ -821,6 +829,14 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
               dp = E::mfma(o.a, o.b, dp);
             }
           });
+      // the operand reads run two steps ahead of their MFMAs (at the register limit the scheduler would
+      // otherwise move each read next to its MFMA and wait for it there)
+      struct Chain {
+        static constexpr int reads(int i) { return i < NS ? 1 + (K_LDS ? 1 : 0) + (KDP ? 1 : 0) : 1 + (V_LDS ? 1 : 0); }
+        static constexpr int mfmas(int i) { return i < NS && KDP ? 2 : 1; }
+        static constexpr int ahead(int) { return 2; }
+      };
+      pin_chain<Chain, NOP>();
     }
     V8 P[2], G[2];
 #pragma unroll

@@ -13,6 +13,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace vmo {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -299,6 +301,37 @@ __device__ __forceinline__ void prefetched_chain(Operand operand, Step step) {
       step(i, cur);
     }
   }
+}
+
+// Compile-time loop: f(std::integral_constant<int, I>{}) for I = B .. E - 1.
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+// Pins the order of an unrolled operand chain (prefetched_chain) for the scheduler: step i has
+// Chain::reads(i) LDS reads and Chain::mfmas(i) MFMAs, and its reads are issued Chain::ahead(i) steps
+// before its MFMAs, i.e. after the MFMAs of step i - ahead(i).  Without it the scheduler moves each read
+// next to its MFMA under register pressure and waits for it there.  Place it after the chain's code.
+template <class Chain, int N>
+__device__ __forceinline__ void pin_chain() {
+  constexpr auto reads_after = [](int i) {   // LDS reads issued after the MFMAs of step i (i = -1: first)
+    int n = 0;
+    for (int j = 0; j < N; ++j) {
+      const int at = j - Chain::ahead(j);
+      if (at == i || (i == -1 && at < 0)) n += Chain::reads(j);
+    }
+    return n;
+  };
+  if constexpr (reads_after(-1) > 0) __builtin_amdgcn_sched_group_barrier(0x100, reads_after(-1), 0);
+  static_for<0, N>([&](auto ic) __attribute__((always_inline)) {
+    constexpr int i = decltype(ic)::value;
+    __builtin_amdgcn_sched_group_barrier(0x008, Chain::mfmas(i), 0);
+    if constexpr (reads_after(i) > 0) __builtin_amdgcn_sched_group_barrier(0x100, reads_after(i), 0);
+  });
 }
 
 }  // namespace vmo
