@@ -440,6 +440,7 @@ __global__ __launch_bounds__(256, (bwd_waves_per_simd<D, DV>())) void fea_bwd_dq
         static constexpr int reads(int) { return 1; }
         static constexpr int mfmas(int i) { return W0K && i % NSD < NSQ ? 2 : 1; }
         static constexpr int ahead(int) { return 2; }
+        static constexpr int lead() { return 0; }
       };
       pin_chain<Chain, 2 * NSD>();
     }
@@ -798,6 +799,14 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
 
     // S[q][key] = Q K^T and dP[q][key] = dO V^T: lane = key l32, queries 8(r/4) + 4 hl + r%4
     f32x16 s = f32x16{}, dp = f32x16{};
+    if constexpr (WANT_DK) {   // dP starts from alpha: G = P (dP + alpha + beta x) then costs one fma less
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 av = *(const VMO_LDS f32x4*)(sts + 32 + 8 * g + 4 * hl);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dp[4 * g + e] = av[e];
+      }
+    }
     {
       const VMO_LDS char* qrow = Qs + l32 * (DK * 2);
       const VMO_LDS char* drow = dOs + l32 * (DOWK * 2);
@@ -835,6 +844,7 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
         static constexpr int reads(int i) { return i < NS ? 1 + (K_LDS ? 1 : 0) + (KDP ? 1 : 0) : 1 + (V_LDS ? 1 : 0); }
         static constexpr int mfmas(int i) { return i < NS && KDP ? 2 : 1; }
         static constexpr int ahead(int) { return 2; }
+        static constexpr int lead() { return WANT_DK ? 4 : 0; }   // the alpha rows that dP starts from
       };
       pin_chain<Chain, NOP>();
     }
@@ -842,14 +852,13 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, DV, PART>())) void fea
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const f32x4 lv = *(const VMO_LDS f32x4*)(sts + 8 * g + 4 * hl);
-      const f32x4 av = *(const VMO_LDS f32x4*)(sts + 32 + 8 * g + 4 * hl);
       const f32x4 bv = *(const VMO_LDS f32x4*)(sts + 64 + 8 * g + 4 * hl);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int r = 4 * g + e;
         const float x = fmaf(s[r], c, -lv[e]);
         float pv = fast_exp2(x);
-        float gv = WANT_DK ? pv * (dp[r] + fmaf(bv[e], x, av[e])) : 0.f;
+        float gv = WANT_DK ? pv * fmaf(bv[e], x, dp[r]) : 0.f;   // dp holds dP + alpha
         if constexpr (FOLD) gv *= gs;
         if (MASKED && 8 * g + 4 * hl + e >= nvalid) { pv = 0.f; gv = 0.f; }
         P[r >> 3][r & 7] = to_elem<T>(pv);

@@ -314,12 +314,13 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 // Pins the order of an unrolled operand chain (prefetched_chain) for the scheduler: step i has
 // Chain::reads(i) LDS reads and Chain::mfmas(i) MFMAs, and its reads are issued Chain::ahead(i) steps
-// before its MFMAs, i.e. after the MFMAs of step i - ahead(i).  Without it the scheduler moves each read
-// next to its MFMA under register pressure and waits for it there.  Place it after the chain's code.
+// before its MFMAs, i.e. after the MFMAs of step i - ahead(i); Chain::lead() more LDS reads (issued before
+// the chain in the same region) go first.  Without it the scheduler moves each read next to its MFMA
+// under register pressure and waits for it there.  Place it after the chain's code.
 template <class Chain, int N>
 __device__ __forceinline__ void pin_chain() {
   constexpr auto reads_after = [](int i) {   // LDS reads issued after the MFMAs of step i (i = -1: first)
-    int n = 0;
+    int n = i == -1 ? Chain::lead() : 0;
     for (int j = 0; j < N; ++j) {
       const int at = j - Chain::ahead(j);
       if (at == i || (i == -1 && at < 0)) n += Chain::reads(j);
