@@ -66,7 +66,10 @@ __global__ __launch_bounds__(256) void lstep_kernel(LParams p) {
   constexpr int NACC = (LAST ? DV : D) / 32;
 
   extern __shared__ __attribute__((aligned(1024))) char smem_raw[];
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  // the wave's column and its decoded indices are wave-uniform: held in scalar registers, so that the integer
+  // divisions and the 64-bit address arithmetic run on the scalar unit instead of once per lane
+  auto uni = [](int x) __attribute__((always_inline)) { return __builtin_amdgcn_readfirstlane(x); };
+  const int tid = threadIdx.x, wave = uni(tid >> 6), lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const bool live = blockIdx.x * kLWaves + wave < p.cols_total;   // tail waves compute, never store
   const int col = live ? blockIdx.x * kLWaves + wave : p.cols_total - 1;
   VMO_LDS char* wl = (VMO_LDS char*)smem_raw + wave * LL::PER_WAVE;
@@ -75,8 +78,8 @@ __global__ __launch_bounds__(256) void lstep_kernel(LParams p) {
   VMO_LDS float* att = (VMO_LDS float*)(wl + LL::QT + LL::YT);
   VMO_LDS float* e_t = (VMO_LDS float*)(wl + LL::QT + LL::YT + LL::AT);
 
-  const int bh = col / p.bs, j = col % p.bs;
-  const int hh = bh % p.heads, bb = bh / p.heads;
+  const int bh = uni(col / p.bs), j = uni(col % p.bs);
+  const int hh = uni(bh % p.heads), bb = uni(bh / p.heads);
   const int m = p.m;
   const int64_t q_rs = (int64_t)p.bs * p.q_sn;       // stride between grid rows i, i+1 of column j
   const int64_t o_rs = (int64_t)p.bs * p.out_sn;
@@ -302,9 +305,10 @@ __global__ __launch_bounds__(64 * kLBWaves, 2) void lstep_bwd_kernel(LBParams p)
   constexpr int NV = DV / 32;
 
   extern __shared__ __attribute__((aligned(1024))) char smem_raw[];
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  auto uni = [](int x) __attribute__((always_inline)) { return __builtin_amdgcn_readfirstlane(x); };
+  const int tid = threadIdx.x, wave = uni(tid >> 6), lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const bool live = blockIdx.x * kLBWaves + wave < p.cols_total;   // tail waves compute, never store
-  const int col = live ? blockIdx.x * kLBWaves + wave : p.cols_total - 1;
+  const int col = live ? blockIdx.x * kLBWaves + wave : p.cols_total - 1;   // (wave-uniform, as lstep_kernel)
   VMO_LDS char* q_t = (VMO_LDS char*)smem_raw + wave * LL::PER_WAVE;
   VMO_LDS char* k_t = q_t + LL::QT;
   VMO_LDS char* g_t = k_t + LL::KT;
@@ -314,8 +318,8 @@ __global__ __launch_bounds__(64 * kLBWaves, 2) void lstep_bwd_kernel(LBParams p)
   VMO_LDS float* e_t = att + 32 * kAttStride;
   VMO_LDS float* c_t = e_t + 32;
 
-  const int bh = col / p.bs, j = col % p.bs;
-  const int hh = bh % p.heads, bb = bh / p.heads;
+  const int bh = uni(col / p.bs), j = uni(col % p.bs);
+  const int hh = uni(bh % p.heads), bb = uni(bh / p.heads);
   const int m = p.m;
   const int64_t q_rs = (int64_t)p.bs * p.q_sn;
   const int64_t o_rs = (int64_t)p.bs * p.out_sn;

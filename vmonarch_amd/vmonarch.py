@@ -168,8 +168,9 @@ def _fused_supported(q, k, v, num_blocks):
 # Where the exact recompute of the first rt queries starts on its own stream: it reads q, k, v only
 # and writes rows [0, rt) of z, which the L-steps never write, so it can run beside the R/L chain
 # ("start": with R-step 0, "after_r0": beside L-step 0 onwards, "after_r1": beside the last L-step,
-# "off": after the chain on the caller's stream).
-_RECOMPUTE_OVERLAP = "after_r0"
+# "off": after the chain on the caller's stream).  Measured at cfg4 (four interleaved rounds of 100
+# steps on one box): start 1.126-1.128 ms, after_r0 1.131-1.137 ms with the same 3 key splits.
+_RECOMPUTE_OVERLAP = "start"
 _side_streams = {}
 
 
