@@ -57,7 +57,7 @@ __host__ __device__ inline MbLayout mb_layout(int M, int d, int dv, bool last, b
   L.g = bwd ? take(M * (last ? dv : d) * 2) : 0;
   L.e = take(M * 4);
   L.lse = take(M * 4);
-  L.part = bwd ? 0 : take(4 * M * 4);   // the forward's partial row max / sum (two key blocks)
+  L.part = take(4 * M * 4);   // two blocks' partial row / column vectors (the two-block passes)
   L.rs = bwd ? take(M * 4) : 0;
   L.f = bwd ? take(M * 4) : 0;
   L.dc = bwd ? take(M * 4) : 0;
@@ -414,7 +414,7 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_kernel(LParams p) {
 // HBM traffic); the attention is exp2(logit - lse_i), exactly normalised.  MFMA operands a, dl and a f are
 // rounded to the 16-bit type, the sums rs, c, gv kept in fp32 from the fp32 attention.  dq (fp32) is added
 // to or overwritten, d out (the 16-bit type) written; rows past m carry zero attention and are not stored.
-template <bool F16, int D, int DV, bool LAST>
+template <bool F16, int D, int DV, bool LAST, bool TWO>
 __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams p) {
   using E = Elem<F16>;
   using T = typename E::T;
@@ -538,6 +538,142 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
   };
 
   if constexpr (LAST) {
+    if constexpr (TWO) {
+      // Two blocks on four waves, as the non-last step's passes below: (query block, key block) pairs, the row
+      // sums combined through `part`, the products split by output columns over operands exchanged in `xch`
+      // (the row-store patches: 16-row ones up to 64 frames, room for two operands per wave and lane).
+      constexpr int NH = ND / 2, NVH = NV / 2;
+      VMO_LDS float* part = (VMO_LDS float*)(sm + Lo.part);
+      VMO_LDS V8* xch = (VMO_LDS V8*)(sm + Lo.patch);
+      const int ib = wave >> 1, kb = wave & 1;   // pass A: query block ib against key block kb
+      const int kq = wave >> 1, iq = wave & 1;   // pass B: key block kq against query block iq
+      auto store_n = [&](auto cw_tag, const f32x16* acc, int nacc, int mode, char* row0, int64_t stride, int nr)
+          __attribute__((always_inline)) {
+        constexpr int CWS = decltype(cw_tag)::value;
+        if (half_patch) store_acc_rows<F16, CWS, 16>(patch, acc, nacc, 1.f, mode, row0, stride, nr, lane);
+        else store_acc_rows<F16, CWS, 32>(patch, acc, nacc, 1.f, mode, row0, stride, nr, lane);
+      };
+      // ---- pass A: row LSE from two partials, rs_i from two partials, then dq (query block ib, column half kb)
+      {
+        V8 qb[NDS];
+        load_rows(qb, q_t, ib);
+        f32x16 x = s_block(kb, qb);
+        {
+          float mx = -3.0e38f;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, x[r]);
+          mx = wave_max32(mx);
+          float sum = 0.f;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) sum += fast_exp2(x[r] - mx);
+          sum = wave_sum32(sum);
+          if (hl == 0) {
+            part[kb * M + 32 * ib + l32] = mx;
+            part[2 * M + kb * M + 32 * ib + l32] = sum;
+          }
+        }
+        __syncthreads();
+        if (tid < M) {
+          const float m0 = part[tid], m1 = part[M + tid], mm = fmaxf(m0, m1);
+          const float l = part[2 * M + tid] * fast_exp2(m0 - mm) + part[3 * M + tid] * fast_exp2(m1 - mm);
+          lse_t[tid] = tid < m ? mm + fast_log2(l) : 1.0e30f;
+        }
+        __syncthreads();
+        const float lse = lse_t[32 * ib + l32];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) x[r] = fast_exp2(x[r] - lse);   // attn^T[k][i]
+        f32x16 d = f32x16{};   // DA^T[k][i] = y_k . g_i
+#pragma unroll
+        for (int ds = 0; ds < NDSV; ++ds)
+          d = E::mfma(mb_row8<V8, RBY>(y_t + 32 * kb * RBY, l32, hl, ds), mb_row8<V8, RBY>(g_t + 32 * ib * RBY, l32, hl, ds), d);
+        float rs = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) rs = fmaf(x[r], d[r], rs);
+        rs = wave_sum32(rs);
+        if (hl == 0) part[kb * M + 32 * ib + l32] = rs;
+        __syncthreads();
+        rs = part[32 * ib + l32] + part[M + 32 * ib + l32];
+        if (kb == 0 && hl == 0) rs_t[32 * ib + l32] = 32 * ib + l32 < m ? rs : 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) d[r] = p.scale * x[r] * (d[r] - rs);   // dl^T
+        VMO_LDS V8* mine = xch + wave * 2 * 64 + lane;
+        mine[0] = mb_pack<T, V8>(d, 0, 1.f);
+        mine[64] = mb_pack<T, V8>(d, 1, 1.f);
+        __syncthreads();
+        f32x16 accq[NH];
+#pragma unroll
+        for (int a = 0; a < NH; ++a) accq[a] = f32x16{};
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2) {
+          const VMO_LDS V8* src = xch + (2 * ib + k2) * 2 * 64 + lane;
+          const V8 P0 = src[0], P1 = src[64];
+#pragma unroll
+          for (int a = 0; a < NH; ++a) {
+            accq[a] = E::mfma(mb_tr8<V8, RBD>(k_t + 32 * k2 * RBD, lane, kb * NH + a, 0), P0, accq[a]);
+            accq[a] = E::mfma(mb_tr8<V8, RBD>(k_t + 32 * k2 * RBD, lane, kb * NH + a, 1), P1, accq[a]);
+          }
+        }
+        __syncthreads();   // every wave is done with xch: the patches may reuse it
+        store_n(std::integral_constant<int, CWD>{}, accq, NH, dq_mode, (char*)(dqcol + 32 * ib * dq_rs + 32 * kb * NH),
+                dq_rs * 4, min(32, m - 32 * ib));
+      }
+      __syncthreads();   // the patches are free again for xch, and rs_t is complete
+      // ---- pass B: dy and dkr (key block kq, column half iq) over the two query blocks
+      {
+        const f32x16 at = attn_block(iq, kq, e_t[32 * kq + l32]);
+        f32x16 dl = f32x16{};   // DA[i][k] = g_i . y_k
+#pragma unroll
+        for (int ds = 0; ds < NDSV; ++ds)
+          dl = E::mfma(mb_row8<V8, RBY>(g_t + 32 * iq * RBY, l32, hl, ds), mb_row8<V8, RBY>(y_t + 32 * kq * RBY, l32, hl, ds), dl);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 rv = *(const VMO_LDS f32x4*)(rs_t + 32 * iq + 8 * g + 4 * hl);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) dl[4 * g + e] = p.scale * at[4 * g + e] * (dl[4 * g + e] - rv[e]);
+        }
+        VMO_LDS V8* mine = xch + wave * 2 * 64 + lane;
+        mine[0] = mb_pack<T, V8>(at, 0, 1.f);   // the attention block first: dy^T += G^T a
+        mine[64] = mb_pack<T, V8>(at, 1, 1.f);
+        __syncthreads();
+        f32x16 accy[NVH];
+#pragma unroll
+        for (int a = 0; a < NVH; ++a) accy[a] = f32x16{};
+#pragma unroll
+        for (int i2 = 0; i2 < 2; ++i2) {
+          const VMO_LDS V8* src = xch + (2 * kq + i2) * 2 * 64 + lane;
+          const V8 A0 = src[0], A1 = src[64];
+#pragma unroll
+          for (int a = 0; a < NVH; ++a) {
+            accy[a] = E::mfma(mb_tr8<V8, RBY>(g_t + 32 * i2 * RBY, lane, iq * NVH + a, 0), A0, accy[a]);
+            accy[a] = E::mfma(mb_tr8<V8, RBY>(g_t + 32 * i2 * RBY, lane, iq * NVH + a, 1), A1, accy[a]);
+          }
+        }
+        __syncthreads();
+        mine[0] = mb_pack<T, V8>(dl, 0, 1.f);   // then dl: dkr^T += Q^T dl
+        mine[64] = mb_pack<T, V8>(dl, 1, 1.f);
+        __syncthreads();
+        f32x16 acck[NH];
+#pragma unroll
+        for (int a = 0; a < NH; ++a) acck[a] = f32x16{};
+#pragma unroll
+        for (int i2 = 0; i2 < 2; ++i2) {
+          const VMO_LDS V8* src = xch + (2 * kq + i2) * 2 * 64 + lane;
+          const V8 P0 = src[0], P1 = src[64];
+#pragma unroll
+          for (int a = 0; a < NH; ++a) {
+            acck[a] = E::mfma(mb_tr8<V8, RBD>(q_t + 32 * i2 * RBD, lane, iq * NH + a, 0), P0, acck[a]);
+            acck[a] = E::mfma(mb_tr8<V8, RBD>(q_t + 32 * i2 * RBD, lane, iq * NH + a, 1), P1, acck[a]);
+          }
+        }
+        __syncthreads();
+        const int nr = min(32, m - 32 * kq);
+        store_n(std::integral_constant<int, CWV>{}, accy, NVH, kGradStore,
+                (char*)(dcol + 32 * kq * do_rs + D + 32 * iq * NVH), do_rs * 2, nr);
+        store_n(std::integral_constant<int, CWD>{}, acck, NH, kGradStore, (char*)(dcol + 32 * kq * do_rs + 32 * iq * NH),
+                do_rs * 2, nr);
+      }
+      return;
+    }
     // ---- pass A: one query row per lane
     if (busy) {
       V8 qb[NDS];
@@ -634,6 +770,176 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
       store_rows(std::integral_constant<int, CWD>{}, acck, ND, kGradStore, (char*)(dcol + 32 * blk * do_rs), do_rs * 2);
     }
   } else {
+    if constexpr (TWO) {
+      // Two blocks on four waves: each pass takes one (query block, key block) pair per wave instead of one block
+      // per wave (which left two waves idle).  The per-row / per-column sums over the pair's two blocks are
+      // combined through `part`; the dq and dkr products are split by output columns (half NH of the ND
+      // blocks per wave), each wave reading the 16-bit B operands that its block pair's waves wrote to `xch`
+      // (the row-store patch region, free until the stores).  Each accumulator takes its products in the same
+      // order as the one-block-per-wave passes.
+      constexpr int NH = ND / 2;
+      VMO_LDS float* part = (VMO_LDS float*)(sm + Lo.part);   // [block][M] x two vectors
+      VMO_LDS V8* xch = (VMO_LDS V8*)(sm + Lo.patch);         // [wave][operand][lane]
+      const int ib = wave >> 1, kb = wave & 1;   // passes 0 and 2: query block ib against key block kb
+      const int kq = wave >> 1, iq = wave & 1;   // passes 1 and 3: key block kq against query block iq
+      const bool ib_ok = 32 * ib + l32 < m;
+      V8 qb[NDS];
+      load_rows(qb, q_t, ib);
+      // ---- pass 0: row LSE from the two key blocks' partial max / sum
+      {
+        const f32x16 x = s_block(kb, qb);
+        float mx = -3.0e38f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, x[r]);
+        mx = wave_max32(mx);
+        float sum = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sum += fast_exp2(x[r] - mx);
+        sum = wave_sum32(sum);
+        if (hl == 0) {
+          part[kb * M + 32 * ib + l32] = mx;
+          part[2 * M + kb * M + 32 * ib + l32] = sum;
+        }
+      }
+      __syncthreads();
+      if (tid < M) {   // rows past m get +1e30: their attention is exactly zero
+        const float m0 = part[tid], m1 = part[M + tid], mm = fmaxf(m0, m1);
+        const float l = part[2 * M + tid] * fast_exp2(m0 - mm) + part[3 * M + tid] * fast_exp2(m1 - mm);
+        lse_t[tid] = tid < m ? mm + fast_log2(l) : 1.0e30f;
+      }
+      __syncthreads();
+      // ---- pass 1: column mass c_k and gv_k from the two query blocks' partials -> f_k, dc_k
+      {
+        V8 gop[NDS];
+        load_rows(gop, g_t, kq);
+        const f32x16 at = attn_block(iq, kq, e_t[32 * kq + l32]);
+        f32x16 gq = f32x16{};   // GQ[i][k] = q_i . g_k
+#pragma unroll
+        for (int ds = 0; ds < NDS; ++ds) gq = E::mfma(mb_row8<V8, RBD>(q_t + 32 * iq * RBD, l32, hl, ds), gop[ds], gq);
+        float cs = 0.f, gv = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          cs += at[r];
+          gv = fmaf(at[r], gq[r], gv);
+        }
+        cs = wave_sum32(cs);
+        gv = wave_sum32(gv);
+        if (hl == 0) {
+          part[iq * M + 32 * kq + l32] = cs;
+          part[2 * M + iq * M + 32 * kq + l32] = gv;
+        }
+      }
+      __syncthreads();
+      if (tid < M) {
+        const float cs = part[tid] + part[M + tid], gv = part[2 * M + tid] + part[3 * M + tid];
+        const float cm = fmaxf(cs, p.min_col_mass), f = p.scale / cm;
+        f_t[tid] = f;
+        dc_t[tid] = (tid < m && cs >= p.min_col_mass) ? -gv * f / cm : 0.f;
+      }
+      __syncthreads();
+      // ---- pass 2: rs_i from the two key blocks' partials, then dq (query block ib, column half kb)
+      {
+        f32x16 x = s_block(kb, qb);
+        const float lse = lse_t[32 * ib + l32];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) x[r] = fast_exp2(x[r] - lse);   // attn^T[k][i]
+        f32x16 d = f32x16{};   // da^T[k][i] = f_k (g_k . q_i) + dc_k
+#pragma unroll
+        for (int ds = 0; ds < NDS; ++ds) d = E::mfma(mb_row8<V8, RBD>(g_t + 32 * kb * RBD, l32, hl, ds), qb[ds], d);
+        f32x4 fv[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          fv[g] = *(const VMO_LDS f32x4*)(f_t + 32 * kb + 8 * g + 4 * hl);
+          const f32x4 cv = *(const VMO_LDS f32x4*)(dc_t + 32 * kb + 8 * g + 4 * hl);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) d[4 * g + e] = fmaf(fv[g][e], d[4 * g + e], cv[e]);
+        }
+        float rs = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) rs = fmaf(x[r], d[r], rs);
+        rs = wave_sum32(rs);
+        if (hl == 0) part[kb * M + 32 * ib + l32] = rs;
+        __syncthreads();
+        rs = part[32 * ib + l32] + part[M + 32 * ib + l32];
+        if (kb == 0 && hl == 0) rs_t[32 * ib + l32] = ib_ok ? rs : 0.f;
+        f32x16 dl, af;
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * g + e;
+            af[r] = x[r] * fv[g][e];
+            dl[r] = p.scale * x[r] * (d[r] - rs);
+          }
+        VMO_LDS V8* mine = xch + wave * 4 * 64 + lane;
+        mine[0] = mb_pack<T, V8>(dl, 0, 1.f);
+        mine[64] = mb_pack<T, V8>(dl, 1, 1.f);
+        mine[128] = mb_pack<T, V8>(af, 0, 1.f);
+        mine[192] = mb_pack<T, V8>(af, 1, 1.f);
+        __syncthreads();
+        f32x16 accq[NH];
+#pragma unroll
+        for (int a = 0; a < NH; ++a) accq[a] = f32x16{};
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2) {
+          const VMO_LDS V8* src = xch + (2 * ib + k2) * 4 * 64 + lane;
+          const V8 P0 = src[0], P1 = src[64], F0 = src[128], F1 = src[192];
+#pragma unroll
+          for (int a = 0; a < NH; ++a) {
+            const int ca = kb * NH + a;   // this wave's column half
+            accq[a] = E::mfma(mb_tr8<V8, RBD>(k_t + 32 * k2 * RBD, lane, ca, 0), P0, accq[a]);
+            accq[a] = E::mfma(mb_tr8<V8, RBD>(k_t + 32 * k2 * RBD, lane, ca, 1), P1, accq[a]);
+            accq[a] = E::mfma(mb_tr8<V8, RBD>(g_t + 32 * k2 * RBD, lane, ca, 0), F0, accq[a]);
+            accq[a] = E::mfma(mb_tr8<V8, RBD>(g_t + 32 * k2 * RBD, lane, ca, 1), F1, accq[a]);
+          }
+        }
+        __syncthreads();   // every wave is done with xch: the patches may reuse it
+        store_acc_rows<F16, CWD>(patch, accq, NH, 1.f, dq_mode, (char*)(dqcol + 32 * ib * dq_rs + 32 * kb * NH),
+                                 dq_rs * 4, min(32, m - 32 * ib), lane);
+      }
+      __syncthreads();   // the patches are free again for xch, and rs_t is complete
+      // ---- pass 3: dkr (key block kq, column half iq) over the two query blocks
+      {
+        V8 gop[NDS];
+        load_rows(gop, g_t, kq);
+        const float fk = f_t[32 * kq + l32], dck = dc_t[32 * kq + l32];
+        const f32x16 at = attn_block(iq, kq, e_t[32 * kq + l32]);
+        f32x16 dl = f32x16{};
+#pragma unroll
+        for (int ds = 0; ds < NDS; ++ds) dl = E::mfma(mb_row8<V8, RBD>(q_t + 32 * iq * RBD, l32, hl, ds), gop[ds], dl);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 rv = *(const VMO_LDS f32x4*)(rs_t + 32 * iq + 8 * g + 4 * hl);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * g + e;
+            dl[r] = p.scale * at[r] * (fmaf(fk, dl[r], dck) - rv[e]);
+          }
+        }
+        VMO_LDS V8* mine = xch + wave * 2 * 64 + lane;
+        mine[0] = mb_pack<T, V8>(dl, 0, 1.f);
+        mine[64] = mb_pack<T, V8>(dl, 1, 1.f);
+        __syncthreads();
+        f32x16 acck[NH];
+#pragma unroll
+        for (int a = 0; a < NH; ++a) acck[a] = f32x16{};
+#pragma unroll
+        for (int i2 = 0; i2 < 2; ++i2) {
+          const VMO_LDS V8* src = xch + (2 * kq + i2) * 2 * 64 + lane;
+          const V8 P0 = src[0], P1 = src[64];
+#pragma unroll
+          for (int a = 0; a < NH; ++a) {
+            const int ca = iq * NH + a;
+            acck[a] = E::mfma(mb_tr8<V8, RBD>(q_t + 32 * i2 * RBD, lane, ca, 0), P0, acck[a]);
+            acck[a] = E::mfma(mb_tr8<V8, RBD>(q_t + 32 * i2 * RBD, lane, ca, 1), P1, acck[a]);
+          }
+        }
+        __syncthreads();
+        store_acc_rows<F16, CWD>(patch, acck, NH, 1.f, kGradStore, (char*)(dcol + 32 * kq * do_rs + 32 * iq * NH),
+                                 do_rs * 2, min(32, m - 32 * kq), lane);
+      }
+      return;
+    }
     // ---- pass 0: row LSE (query blocks)
     if (busy) {
       V8 qb[NDS];
@@ -822,12 +1128,12 @@ int mb_lstep_fwd(const LParams& p, bool f16, int d, int dv, bool last, hipStream
   return f16 ? dispatch_mb<true>(p, d, dv, last, s) : dispatch_mb<false>(p, d, dv, last, s);
 }
 
-template <bool F16, int D, int DV, bool LAST>
-static int launch_mb_bwd(const LBParams& p, hipStream_t s) {
+template <bool F16, int D, int DV, bool LAST, bool TWO>
+static int launch_mb_bwd_k(const LBParams& p, hipStream_t s) {
   const int M = 32 * ((p.m + 31) / 32);
   const int lds = mb_layout(M, tile_w(D), tile_w(DV), LAST, true).total;
-  auto kern = lstep_mb_bwd_kernel<F16, D, DV, LAST>;
-  static std::atomic<int> lds_limit{65536};   // as in launch_mb
+  auto kern = lstep_mb_bwd_kernel<F16, D, DV, LAST, TWO>;
+  static std::atomic<int> lds_limit{65536};   // as in launch_mb, per kernel
   if (lds > lds_limit.load(std::memory_order_relaxed)) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
       return set_error(VMO_ERR_LAUNCH, "lstep_mb_bwd: cannot raise the LDS limit to %d bytes", lds);
@@ -835,6 +1141,17 @@ static int launch_mb_bwd(const LBParams& p, hipStream_t s) {
   }
   hipLaunchKernelGGL(kern, dim3(p.cols_total), dim3(64 * kMbWaves), lds, s, p);
   return launch_status("lstep_mb_bwd");
+}
+
+// Grids of two row blocks (33-64 frames) take the kernel whose passes split the block pairs over all four waves,
+// where the accumulator blocks split evenly (32-wide heads and 16-wide tiles have one block); larger grids keep
+// one block per wave.
+template <bool F16, int D, int DV, bool LAST>
+static int launch_mb_bwd(const LBParams& p, hipStream_t s) {
+  constexpr bool TWO_OK = (tile_w(D) / 32) % 2 == 0 && (!LAST || (tile_w(DV) / 32) % 2 == 0);
+  if constexpr (TWO_OK)
+    if ((p.m + 31) / 32 == 2) return launch_mb_bwd_k<F16, D, DV, LAST, true>(p, s);
+  return launch_mb_bwd_k<F16, D, DV, LAST, false>(p, s);
 }
 
 template <bool F16>

@@ -130,7 +130,7 @@ def _lstep_mb_lds(m, d, dv, last, bwd):
     M = 32 * ((m + 31) // 32)
     r = lambda b: (b + 255) // 256 * 256   # noqa: E731
     d, dv = max(d, 32), max(dv, 32)   # 16-wide heads sit in 32-wide tiles
-    total = 2 * r(M * d * 2) + (r(M * dv * 2) if last else 0) + 2 * r(M * 4) + (0 if bwd else r(4 * M * 4))
+    total = 2 * r(M * d * 2) + (r(M * dv * 2) if last else 0) + 2 * r(M * 4) + r(4 * M * 4)
     if bwd:   # the upstream gradient rows, three more vectors, the backward's own row-store patches (half-size
         # ones for the last step up to 64 frames)
         total += r(M * (dv if last else d) * 2) + 3 * r(M * 4) + 4 * (2048 if last and M <= 64 else 4096)
