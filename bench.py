@@ -422,8 +422,9 @@ def main():
     if ms_graph is not None:
         result["graph_replay"] = {
             "note": "capture compatibility, not a speed path: the production-order step captured once in a HIP graph "
-                    "and replayed (checked bit for bit against the eager step); on this ROCm the replay runs slower "
-                    "than the eager launches, whose host side already runs ahead of the kernels; never `value`",
+                    "and replayed (checked bit for bit against the eager step); after `warmup` replays it runs within "
+                    "a few percent of the eager step, whose host side already runs ahead of the kernels (runs with "
+                    "few warm-up replays also time the first replays' one-time cost); never `value`",
             "ms_per_step": round(ms_graph, 4), "vs_eager": round(ms_graph / ms, 4)}
     if args.qk_fp8:
         result["qk_fp8"] = {
