@@ -65,3 +65,33 @@ def test_fuzz_vmonarch(seed):
         assert gd.shape == t.shape and gd.dtype == t.dtype
         assert_grad_close(gd.float().cpu().numpy(), gr, 5e-2, name)
     assert hip_library_loaded()
+
+
+@pytest.mark.parametrize("m, b, rt, D", [(4, 48, 100, 64), (8, 40, 320, 128), (21, 24, 61, 128), (40, 16, 47, 64),
+                                         (6, 32, 192, 32)])
+def test_vmonarch_recompute_spans_frames(m, b, rt, D):
+    """recompute_tokens past one frame's block (rt > b, up to all N tokens): vmonarch.py:66-68 recomputes rows
+    [0, rt) exactly whatever frames they cover, and the last L-step leaves exactly those rows to it."""
+    from vmonarch_amd import vmonarch_attention
+    g = torch.Generator().manual_seed(m * 1000 + rt)
+    B, H, N = 1, 2, m * b
+    q, k, v = (randn_lp(g, B, H, N, D).to(DEV) for _ in range(3))
+    do = torch.randn(B, H, N, D, generator=g)
+    print(f"vmonarch recompute spanning frames m={m} b={b} rt={rt} D={D}", flush=True)
+    qn, kn, vn = (t.float().cpu().numpy() for t in (q, k, v))
+    z_ref = vmonarch_oracle(qn, kn, vn, m, b, 2, rt)
+    with warnings.catch_warnings():
+        warnings.simplefilter("error", RuntimeWarning)
+        with torch.no_grad():
+            z = vmonarch_attention(q, k, v, m, b, 2, recompute_tokens=rt)
+        leaves = [t.detach().requires_grad_() for t in (q, k, v)]
+        zg = vmonarch_attention(*leaves, m, b, 2, recompute_tokens=rt)
+    zz = z.float().cpu().numpy()
+    assert_close_ref(zz, z_ref, 3e-2)
+    assert_close_elementwise(zz, z_ref)
+    assert torch.equal(zg.detach(), z)
+    grads = torch.autograd.grad((zg.float() * do.to(DEV)).sum(), leaves)
+    refs = vmonarch_attention_grad(qn, kn, vn, do.numpy(), m, b, 2, rt)
+    for gd, gr, name in zip(grads, refs, ("dq", "dk", "dv")):
+        assert_grad_close(gd.float().cpu().numpy(), gr, 5e-2, name)
+    assert hip_library_loaded()
