@@ -95,3 +95,36 @@ def test_vmonarch_recompute_spans_frames(m, b, rt, D):
     for gd, gr, name in zip(grads, refs, ("dq", "dk", "dv")):
         assert_grad_close(gd.float().cpu().numpy(), gr, 5e-2, name)
     assert hip_library_loaded()
+
+
+@pytest.mark.parametrize("m, b, D, dit", [(4, 48, 64, False), (21, 24, 128, True), (40, 16, 128, False),
+                                          (40, 16, 64, True), (97, 8, 32, False)])
+def test_vmonarch_batch_of_two(m, b, D, dit):
+    """B = 2 through every kernel (one-tile and multi-block L-steps, forward and backward; (B, H, N, D) and
+    (B, N, H, D) inputs): each batch entry must match the oracle run on its own."""
+    from vmonarch_amd import vmonarch_attention
+    g = torch.Generator().manual_seed(m * 100 + D + dit)
+    B, H, N, rt = 2, 2, m * b, b
+
+    def tensor():
+        t = randn_lp(g, B, N, H, D) if dit else randn_lp(g, B, H, N, D)
+        t = t.to(DEV)
+        return t.transpose(1, 2) if dit else t
+
+    q, k, v = tensor(), tensor(), tensor()
+    do = torch.randn(B, H, N, D, generator=g)
+    print(f"vmonarch batch 2 m={m} b={b} D={D} dit={dit}", flush=True)
+    with warnings.catch_warnings():
+        warnings.simplefilter("error", RuntimeWarning)
+        leaves = [t.detach().requires_grad_() for t in (q, k, v)]
+        zg = vmonarch_attention(*leaves, m, b, 2, recompute_tokens=rt)
+    grads = torch.autograd.grad((zg.float() * do.to(DEV)).sum(), leaves)
+    qn, kn, vn = (t.float().cpu().numpy() for t in (q, k, v))
+    for bi in range(B):
+        sl = slice(bi, bi + 1)
+        z_ref = vmonarch_oracle(qn[sl], kn[sl], vn[sl], m, b, 2, rt)
+        assert_close_ref(zg[sl].detach().float().cpu().numpy(), z_ref, 3e-2)
+        refs = vmonarch_attention_grad(qn[sl], kn[sl], vn[sl], do[sl].numpy(), m, b, 2, rt)
+        for gd, gr, name in zip(grads, refs, ("dq", "dk", "dv")):
+            assert_grad_close(gd[sl].float().cpu().numpy(), gr, 5e-2, f"{name} batch {bi}")
+    assert hip_library_loaded()
