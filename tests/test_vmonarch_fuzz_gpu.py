@@ -128,3 +128,34 @@ def test_vmonarch_batch_of_two(m, b, D, dit):
         for gd, gr, name in zip(grads, refs, ("dq", "dk", "dv")):
             assert_grad_close(gd[sl].float().cpu().numpy(), gr, 5e-2, f"{name} batch {bi}")
     assert hip_library_loaded()
+
+
+@pytest.mark.parametrize("m, b, rt", [(1, 64, 0), (1, 64, 64), (16, 1, 0), (16, 1, 1), (48, 1, 5), (1, 1, 0)])
+def test_vmonarch_degenerate_grids(m, b, rt):
+    """One frame (m = 1: the L-step attends over a single row) and one token per frame (b = 1: the R-steps attend
+    over a single key), forward and gradients against the oracle."""
+    from vmonarch_amd import vmonarch_attention
+    g = torch.Generator().manual_seed(m * 10 + b + rt)
+    B, H, N, D = 1, 2, m * b, 64
+    q, k, v = (randn_lp(g, B, H, N, D).to(DEV) for _ in range(3))
+    do = torch.randn(B, H, N, D, generator=g)
+    print(f"vmonarch degenerate m={m} b={b} rt={rt}", flush=True)
+    with warnings.catch_warnings():
+        warnings.simplefilter("error", RuntimeWarning)
+        leaves = [t.detach().requires_grad_() for t in (q, k, v)]
+        zg = vmonarch_attention(*leaves, m, b, 2, recompute_tokens=rt)
+    grads = torch.autograd.grad((zg.float() * do.to(DEV)).sum(), leaves)
+    qn, kn, vn = (t.float().cpu().numpy() for t in (q, k, v))
+    z_ref = vmonarch_oracle(qn, kn, vn, m, b, 2, rt)
+    zz = zg.detach().float().cpu().numpy()
+    assert np.isfinite(zz).all()
+    assert_close_ref(zz, z_ref, 3e-2)
+    refs = vmonarch_attention_grad(qn, kn, vn, do.numpy(), m, b, 2, rt)
+    for gd, gr, name in zip(grads, refs, ("dq", "dk", "dv")):
+        gn = gd.float().cpu().numpy()
+        assert np.isfinite(gn).all()
+        if not np.abs(gr).max() > 0:   # a softmax over one element passes no gradient: zero up to fp32 rounding
+            assert np.abs(gn).max() < 1e-5, name
+            continue
+        assert_grad_close(gn, gr, 5e-2, name)
+    assert hip_library_loaded()
