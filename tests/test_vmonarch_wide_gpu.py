@@ -65,8 +65,8 @@ def test_general_lstep_forward_matches_oracle(m, d, dv, last):
 # m = 129: the general kernel (fits at 16 / 16); mcm 0.6 keeps the column-mass clamp active
 @pytest.mark.parametrize("m, d, dv, last, mcm",
                          [(m, d, dv, last, mcm) for m, d, dv, last in
-                          _grids([7, 33, 64, 65, 96, 128, 129], [(64, 64), (128, 128), (32, 32), (64, 128), (128, 32),
-                                                                  (16, 16)], [False, True], True)
+                          _grids([7, 33, 48, 64, 65, 96, 128, 129], [(64, 64), (128, 128), (32, 32), (64, 128), (128, 32),
+                                                                      (128, 64), (16, 16)], [False, True], True)
                           for mcm in ((0.01,) if last else (0.01, 0.6))])
 def test_general_lstep_backward_matches_oracle(m, d, dv, last, mcm):
     from vmonarch_amd.vmonarch import _lstep_bwd_launch
