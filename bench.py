@@ -130,28 +130,30 @@ def backward_timings(steps):
     """Training-side timings (not `value`): the cfg4 VMonarch step with autograd (HIP forward that
     keeps its activations, then the HIP backward: fused L-step backward + flash-entropy backward)
     and the cfg5 flash-entropy forward + backward, (1, 24, 16384, 128) bf16.  Events on the
-    current stream around each half, the median of `steps` timed steps after one warm-up."""
+    current stream around each half, the median of `steps` timed steps after one warm-up.  The steps run
+    back to back (one synchronisation after the last), as a training loop issues them: the host queues
+    ahead of the GPU and the events time the GPU's work, not the Python autograd overhead before each
+    step's first launch (with a synchronisation per step that overhead lands inside the forward's time)."""
     import torch
     from vmonarch_amd import flash_entropy_attention, vmonarch_attention
 
     dev = torch.device("cuda:0")
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
 
     def timed(fwd, grads_of):
         out = fwd()
         torch.autograd.grad(*grads_of(out))
         torch.cuda.synchronize()
-        tf, tb = [], []
-        for _ in range(steps):
-            ev[0].record()
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+        for e in ev:
+            e[0].record()
             out = fwd()
-            ev[1].record()
+            e[1].record()
             torch.autograd.grad(*grads_of(out))
-            ev[2].record()
-            torch.cuda.synchronize()
-            tf.append(ev[0].elapsed_time(ev[1]))
-            tb.append(ev[1].elapsed_time(ev[2]))
-        return sorted(tf)[len(tf) // 2], sorted(tb)[len(tb) // 2]
+            e[2].record()
+        torch.cuda.synchronize()
+        tf = sorted(e[0].elapsed_time(e[1]) for e in ev)
+        tb = sorted(e[1].elapsed_time(e[2]) for e in ev)
+        return tf[len(tf) // 2], tb[len(tb) // 2]
 
     g = torch.Generator().manual_seed(0)
     q = (torch.randn(B, H, N, D, generator=g) * 0.5).bfloat16().to(dev).requires_grad_()

@@ -278,6 +278,20 @@ class _VMonarchFunction(torch.autograd.Function):
         dev, dt = q.device, q.dtype
         rt = min(int(recompute_tokens), N)
         saved = []
+        lse_rt = None
+        main, side = torch.cuda.current_stream(dev), None
+
+        def recompute():
+            return fea_forward(q[:, :, :rt], k, v, None, scale, o=z[:, :, :rt], want_ent=False,
+                               num_splits=_recompute_splits(B * H, rt, N))[1]
+
+        if rt > 0 and _RECOMPUTE_OVERLAP != "off":
+            # the exact recompute of rows [0, rt) beside the R/L chain, as in _vmonarch_fused (it reads q, k, v
+            # only and writes rows of z that the last L-step leaves alone)
+            side = _side_stream(dev)
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                lse_rt = recompute()
         u = None
         for it in range(num_iters):
             last = it == num_iters - 1
@@ -289,10 +303,11 @@ class _VMonarchFunction(torch.autograd.Function):
                 u = torch.empty((B, H, N, D), device=dev, dtype=dt)
                 _lstep_launch(q, out, ent, u, m, b, scale, False, 0, min_col_mass)
             saved += [x, out, lse, ent]
-        lse_rt = None
-        if rt > 0:
-            _, lse_rt, _ = fea_forward(q[:, :, :rt], k, v, None, scale, o=z[:, :, :rt], want_ent=False,
-                                       num_splits=_recompute_splits(B * H, rt, N))
+        if side is not None:
+            main.wait_stream(side)       # z and lse_rt are complete on the caller's stream
+            lse_rt.record_stream(main)   # allocated on the side stream, read by the backward on this one
+        elif rt > 0:
+            lse_rt = recompute()
         ctx.dims = (m, b, num_iters, rt, float(min_col_mass), float(scale))
         ctx.save_for_backward(q, k, v, z, lse_rt if lse_rt is not None else z.new_empty(0), *saved)
         return z
