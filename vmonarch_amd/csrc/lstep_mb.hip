@@ -530,11 +530,42 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
   const bool row_ok = 32 * blk + l32 < m;   // this lane's query row (query-block passes) or key (key-block passes)
   const int nrows = busy ? min(32, m - 32 * blk) : 0;
   // row stores through the patch: whole (32 rows) or half (16 rows at a time)
-  auto store_rows = [&](auto cw_tag, const f32x16* acc, int nacc, int mode, char* row0, int64_t stride)
+  auto store_rows = [&](auto cw_tag, const f32x16* acc, int nacc, int mode, char* row0, int64_t stride, int nr)
       __attribute__((always_inline)) {
     constexpr int CWS = decltype(cw_tag)::value;
-    if (half_patch) store_acc_rows<F16, CWS, 16>(patch, acc, nacc, 1.f, mode, row0, stride, nrows, lane);
-    else store_acc_rows<F16, CWS, 32>(patch, acc, nacc, 1.f, mode, row0, stride, nrows, lane);
+    if (half_patch) store_acc_rows<F16, CWS, 16>(patch, acc, nacc, 1.f, mode, row0, stride, nr, lane);
+    else store_acc_rows<F16, CWS, 32>(patch, acc, nacc, 1.f, mode, row0, stride, nr, lane);
+  };
+  // The two-block kernels (TWO) give each wave a (query block ib, key block kb) pair.  pair_lse: the row LSE of
+  // the query rows from the S^T blocks of the pairs (each wave's x), as the partial max and sum of each key
+  // block combined through `part` (rows past m get +1e30: their attention is exactly zero).  pair_row_sum: a
+  // per-query-row sum over the two key blocks, each wave's partial v for its pair (every lane gets the total).
+  VMO_LDS float* part = (VMO_LDS float*)(sm + Lo.part);   // [block][M] x two vectors
+  auto pair_lse = [&](const f32x16& x, int ib, int kb) __attribute__((always_inline)) {
+    float mx = -3.0e38f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, x[r]);
+    mx = wave_max32(mx);
+    float sum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sum += fast_exp2(x[r] - mx);
+    sum = wave_sum32(sum);
+    if (hl == 0) {
+      part[kb * M + 32 * ib + l32] = mx;
+      part[2 * M + kb * M + 32 * ib + l32] = sum;
+    }
+    __syncthreads();
+    if (tid < M) {
+      const float m0 = part[tid], m1 = part[M + tid], mm = fmaxf(m0, m1);
+      const float l = part[2 * M + tid] * fast_exp2(m0 - mm) + part[3 * M + tid] * fast_exp2(m1 - mm);
+      lse_t[tid] = tid < m ? mm + fast_log2(l) : 1.0e30f;
+    }
+    __syncthreads();
+  };
+  auto pair_row_sum = [&](float v, int ib, int kb) __attribute__((always_inline)) {
+    if (hl == 0) part[kb * M + 32 * ib + l32] = v;
+    __syncthreads();
+    return part[32 * ib + l32] + part[M + 32 * ib + l32];
   };
 
   if constexpr (LAST) {
@@ -543,42 +574,15 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
       // sums combined through `part`, the products split by output columns over operands exchanged in `xch`
       // (the row-store patches: 16-row ones up to 64 frames, room for two operands per wave and lane).
       constexpr int NH = ND / 2, NVH = NV / 2;
-      VMO_LDS float* part = (VMO_LDS float*)(sm + Lo.part);
       VMO_LDS V8* xch = (VMO_LDS V8*)(sm + Lo.patch);
       const int ib = wave >> 1, kb = wave & 1;   // pass A: query block ib against key block kb
       const int kq = wave >> 1, iq = wave & 1;   // pass B: key block kq against query block iq
-      auto store_n = [&](auto cw_tag, const f32x16* acc, int nacc, int mode, char* row0, int64_t stride, int nr)
-          __attribute__((always_inline)) {
-        constexpr int CWS = decltype(cw_tag)::value;
-        if (half_patch) store_acc_rows<F16, CWS, 16>(patch, acc, nacc, 1.f, mode, row0, stride, nr, lane);
-        else store_acc_rows<F16, CWS, 32>(patch, acc, nacc, 1.f, mode, row0, stride, nr, lane);
-      };
       // ---- pass A: row LSE from two partials, rs_i from two partials, then dq (query block ib, column half kb)
       {
         V8 qb[NDS];
         load_rows(qb, q_t, ib);
         f32x16 x = s_block(kb, qb);
-        {
-          float mx = -3.0e38f;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, x[r]);
-          mx = wave_max32(mx);
-          float sum = 0.f;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) sum += fast_exp2(x[r] - mx);
-          sum = wave_sum32(sum);
-          if (hl == 0) {
-            part[kb * M + 32 * ib + l32] = mx;
-            part[2 * M + kb * M + 32 * ib + l32] = sum;
-          }
-        }
-        __syncthreads();
-        if (tid < M) {
-          const float m0 = part[tid], m1 = part[M + tid], mm = fmaxf(m0, m1);
-          const float l = part[2 * M + tid] * fast_exp2(m0 - mm) + part[3 * M + tid] * fast_exp2(m1 - mm);
-          lse_t[tid] = tid < m ? mm + fast_log2(l) : 1.0e30f;
-        }
-        __syncthreads();
+        pair_lse(x, ib, kb);
         const float lse = lse_t[32 * ib + l32];
 #pragma unroll
         for (int r = 0; r < 16; ++r) x[r] = fast_exp2(x[r] - lse);   // attn^T[k][i]
@@ -589,10 +593,7 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
         float rs = 0.f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) rs = fmaf(x[r], d[r], rs);
-        rs = wave_sum32(rs);
-        if (hl == 0) part[kb * M + 32 * ib + l32] = rs;
-        __syncthreads();
-        rs = part[32 * ib + l32] + part[M + 32 * ib + l32];
+        rs = pair_row_sum(wave_sum32(rs), ib, kb);
         if (kb == 0 && hl == 0) rs_t[32 * ib + l32] = 32 * ib + l32 < m ? rs : 0.f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) d[r] = p.scale * x[r] * (d[r] - rs);   // dl^T
@@ -614,8 +615,8 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
           }
         }
         __syncthreads();   // every wave is done with xch: the patches may reuse it
-        store_n(std::integral_constant<int, CWD>{}, accq, NH, dq_mode, (char*)(dqcol + 32 * ib * dq_rs + 32 * kb * NH),
-                dq_rs * 4, min(32, m - 32 * ib));
+        store_rows(std::integral_constant<int, CWD>{}, accq, NH, dq_mode, (char*)(dqcol + 32 * ib * dq_rs + 32 * kb * NH),
+                   dq_rs * 4, min(32, m - 32 * ib));
       }
       __syncthreads();   // the patches are free again for xch, and rs_t is complete
       // ---- pass B: dy and dkr (key block kq, column half iq) over the two query blocks
@@ -667,10 +668,10 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
         }
         __syncthreads();
         const int nr = min(32, m - 32 * kq);
-        store_n(std::integral_constant<int, CWV>{}, accy, NVH, kGradStore,
-                (char*)(dcol + 32 * kq * do_rs + D + 32 * iq * NVH), do_rs * 2, nr);
-        store_n(std::integral_constant<int, CWD>{}, acck, NH, kGradStore, (char*)(dcol + 32 * kq * do_rs + 32 * iq * NH),
-                do_rs * 2, nr);
+        store_rows(std::integral_constant<int, CWV>{}, accy, NVH, kGradStore,
+                   (char*)(dcol + 32 * kq * do_rs + D + 32 * iq * NVH), do_rs * 2, nr);
+        store_rows(std::integral_constant<int, CWD>{}, acck, NH, kGradStore, (char*)(dcol + 32 * kq * do_rs + 32 * iq * NH),
+                   do_rs * 2, nr);
       }
       return;
     }
@@ -717,7 +718,7 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
           accq[a] = E::mfma(mb_tr8<V8, RBD>(k_t + 32 * kb * RBD, lane, a, 1), P1, accq[a]);
         }
       }
-      store_rows(std::integral_constant<int, CWD>{}, accq, ND, dq_mode, (char*)(dqcol + 32 * blk * dq_rs), dq_rs * 4);
+      store_rows(std::integral_constant<int, CWD>{}, accq, ND, dq_mode, (char*)(dqcol + 32 * blk * dq_rs), dq_rs * 4, nrows);
     }
     __syncthreads();
     // ---- pass B: one key per lane, as two sweeps over the query blocks (dy, then dkr: holding both accumulator
@@ -740,7 +741,7 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
         }
       }
       store_rows(std::integral_constant<int, CWV>{}, accy, NV, kGradStore, (char*)(dcol + 32 * blk * do_rs + D),
-                 do_rs * 2);
+                 do_rs * 2, nrows);
       f32x16 acck[ND];
 #pragma unroll
       for (int a = 0; a < ND; ++a) acck[a] = f32x16{};
@@ -767,7 +768,8 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
           acck[a] = E::mfma(mb_tr8<V8, RBD>(q_t + 32 * ib * RBD, lane, a, 1), P1, acck[a]);
         }
       }
-      store_rows(std::integral_constant<int, CWD>{}, acck, ND, kGradStore, (char*)(dcol + 32 * blk * do_rs), do_rs * 2);
+      store_rows(std::integral_constant<int, CWD>{}, acck, ND, kGradStore, (char*)(dcol + 32 * blk * do_rs), do_rs * 2,
+                 nrows);
     }
   } else {
     if constexpr (TWO) {
@@ -778,7 +780,6 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
       // (the row-store patch region, free until the stores).  Each accumulator takes its products in the same
       // order as the one-block-per-wave passes.
       constexpr int NH = ND / 2;
-      VMO_LDS float* part = (VMO_LDS float*)(sm + Lo.part);   // [block][M] x two vectors
       VMO_LDS V8* xch = (VMO_LDS V8*)(sm + Lo.patch);         // [wave][operand][lane]
       const int ib = wave >> 1, kb = wave & 1;   // passes 0 and 2: query block ib against key block kb
       const int kq = wave >> 1, iq = wave & 1;   // passes 1 and 3: key block kq against query block iq
@@ -786,28 +787,7 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
       V8 qb[NDS];
       load_rows(qb, q_t, ib);
       // ---- pass 0: row LSE from the two key blocks' partial max / sum
-      {
-        const f32x16 x = s_block(kb, qb);
-        float mx = -3.0e38f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, x[r]);
-        mx = wave_max32(mx);
-        float sum = 0.f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sum += fast_exp2(x[r] - mx);
-        sum = wave_sum32(sum);
-        if (hl == 0) {
-          part[kb * M + 32 * ib + l32] = mx;
-          part[2 * M + kb * M + 32 * ib + l32] = sum;
-        }
-      }
-      __syncthreads();
-      if (tid < M) {   // rows past m get +1e30: their attention is exactly zero
-        const float m0 = part[tid], m1 = part[M + tid], mm = fmaxf(m0, m1);
-        const float l = part[2 * M + tid] * fast_exp2(m0 - mm) + part[3 * M + tid] * fast_exp2(m1 - mm);
-        lse_t[tid] = tid < m ? mm + fast_log2(l) : 1.0e30f;
-      }
-      __syncthreads();
+      pair_lse(s_block(kb, qb), ib, kb);
       // ---- pass 1: column mass c_k and gv_k from the two query blocks' partials -> f_k, dc_k
       {
         V8 gop[NDS];
@@ -857,10 +837,7 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
         float rs = 0.f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) rs = fmaf(x[r], d[r], rs);
-        rs = wave_sum32(rs);
-        if (hl == 0) part[kb * M + 32 * ib + l32] = rs;
-        __syncthreads();
-        rs = part[32 * ib + l32] + part[M + 32 * ib + l32];
+        rs = pair_row_sum(wave_sum32(rs), ib, kb);
         if (kb == 0 && hl == 0) rs_t[32 * ib + l32] = ib_ok ? rs : 0.f;
         f32x16 dl, af;
 #pragma unroll
@@ -894,8 +871,8 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
           }
         }
         __syncthreads();   // every wave is done with xch: the patches may reuse it
-        store_acc_rows<F16, CWD>(patch, accq, NH, 1.f, dq_mode, (char*)(dqcol + 32 * ib * dq_rs + 32 * kb * NH),
-                                 dq_rs * 4, min(32, m - 32 * ib), lane);
+        store_rows(std::integral_constant<int, CWD>{}, accq, NH, dq_mode, (char*)(dqcol + 32 * ib * dq_rs + 32 * kb * NH),
+                   dq_rs * 4, min(32, m - 32 * ib));
       }
       __syncthreads();   // the patches are free again for xch, and rs_t is complete
       // ---- pass 3: dkr (key block kq, column half iq) over the two query blocks
@@ -935,8 +912,8 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
           }
         }
         __syncthreads();
-        store_acc_rows<F16, CWD>(patch, acck, NH, 1.f, kGradStore, (char*)(dcol + 32 * kq * do_rs + 32 * iq * NH),
-                                 do_rs * 2, min(32, m - 32 * kq), lane);
+        store_rows(std::integral_constant<int, CWD>{}, acck, NH, kGradStore, (char*)(dcol + 32 * kq * do_rs + 32 * iq * NH),
+                   do_rs * 2, min(32, m - 32 * kq));
       }
       return;
     }
