@@ -116,8 +116,8 @@ __device__ __forceinline__ V8 mb_pack(const f32x16& x, int h2, float f) {
   return v;
 }
 
-template <bool F16, int D, int DV, bool LAST>
-__global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_kernel(LParams p) {
+template <bool F16, int D, int DV, bool LAST, bool TWO>
+__global__ __launch_bounds__(64 * kMbWaves, TWO && !LAST ? 4 : 2) void lstep_mb_kernel(LParams p) {
   using E = Elem<F16>;
   using T = typename E::T;
   using V8 = typename E::V8;
@@ -186,7 +186,7 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_kernel(LParams p) {
   // key block w >> 1; partial row max and sum through LDS), the product pass the output columns (wave w: row
   // block w & 1, column half w >> 1; both halves recompute the block's attention, the products' MFMAs are split).
   constexpr int NH = NACC / 2;
-  if (NACC % 2 == 0 && MB == 2) {
+  if constexpr (TWO) {
     const int rb = wave & 1, half = wave >> 1;
     f32x16 acch[NH > 0 ? NH : 1];
 #pragma unroll
@@ -296,8 +296,7 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_kernel(LParams p) {
       store_acc_rows<F16, CW>(patch, acch, NH, fsc, kGradStore, (char*)rows, r_rs * 2, nrows, lane);
     }
     return;
-  }
-
+  } else {
   f32x16 acc[NACC];
 #pragma unroll
   for (int a = 0; a < NACC; ++a) acc[a] = f32x16{};
@@ -395,6 +394,7 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_kernel(LParams p) {
     store_acc_rows<F16, CW>(patch, acc, NACC, 1.f, kGradStore, (char*)rows, r_rs * 2, nrows, lane, max(0, ibeg - 32 * blk));
   } else {
     store_acc_rows<F16, CW>(patch, acc, NACC, fscale, kGradStore, (char*)rows, r_rs * 2, nrows, lane);
+  }
   }
 }
 
@@ -1071,11 +1071,16 @@ int mb_lstep_check(int m, int d, int dv, bool last, bool bwd) {
   return mb_layout(32 * ((m + 31) / 32), tile_w(d), last ? tile_w(dv) : 0, last, bwd).total <= 160 * 1024;
 }
 
-template <bool F16, int D, int DV, bool LAST>
-static int launch_mb(const LParams& p, hipStream_t s) {
+template <bool F16, int D, int DV, bool LAST, bool TWO>
+static int launch_mb_k(const LParams& p, hipStream_t s) {
   const int M = 32 * ((p.m + 31) / 32);
-  const int lds = mb_layout(M, tile_w(D), tile_w(DV), LAST, false).total;
-  auto kern = lstep_mb_kernel<F16, D, DV, LAST>;
+  int lds = mb_layout(M, tile_w(D), tile_w(DV), LAST, false).total;
+  // The two-block non-last kernel is built for four columns per CU (33-48 frames: their chain of passes is
+  // the bound, and a fourth column in flight hides more of it); past 48 frames the column's bytes dominate,
+  // and its LDS request is raised to hold the CU at three (measured faster there).
+  if constexpr (TWO && !LAST)
+    if (p.m > 48) lds = lds > 160 * 1024 / 4 + 256 ? lds : 160 * 1024 / 4 + 256;
+  auto kern = lstep_mb_kernel<F16, D, DV, LAST, TWO>;
   static std::atomic<int> lds_limit{65536};   // this kernel's dynamic-LDS limit as raised so far
   if (lds > lds_limit.load(std::memory_order_relaxed)) {   // (idempotent: a race only repeats the call)
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
@@ -1084,6 +1089,15 @@ static int launch_mb(const LParams& p, hipStream_t s) {
   }
   hipLaunchKernelGGL(kern, dim3(p.cols_total), dim3(64 * kMbWaves), lds, s, p);
   return launch_status("lstep_mb");
+}
+// Two 32-frame blocks with an even number of output blocks run the instantiation whose passes split over all
+// four waves (TWO).
+template <bool F16, int D, int DV, bool LAST>
+static int launch_mb(const LParams& p, hipStream_t s) {
+  constexpr bool TWO_OK = (tile_w(LAST ? DV : D) / 32) % 2 == 0;
+  if constexpr (TWO_OK)
+    if ((p.m + 31) / 32 == 2) return launch_mb_k<F16, D, DV, LAST, true>(p, s);
+  return launch_mb_k<F16, D, DV, LAST, false>(p, s);
 }
 
 template <bool F16>
