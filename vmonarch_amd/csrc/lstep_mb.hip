@@ -11,7 +11,7 @@
 // Here one 4-wave workgroup owns a column: its q, kr (and y) rows -- tokens i b + j, i < m -- are staged
 // whole into swizzled LDS tiles of M = 32 * MB rows (MB = ceil(m / 32) <= kMbMaxBlocks; rows past m are
 // finite data whose weights are exact zeros), and the m x m products run on v_mfma_f32_32x32x16 in 32 x 32
-// blocks (with MB = 2 split over all four waves, see lstep_mb_kernel):
+// blocks (two-block grids run kernel instantiations, TWO, whose passes split over all four waves):
 //   * last: wave w owns query block w.  S^T blocks (keys x queries: one query row per lane) for every key
 //     block, softmax over all of them in registers (max, sum, normalise: the attention is rounded to the
 //     16-bit type only once normalised, as the reference's attn.to(y.dtype)), then z^T += Y^T P^T with the
