@@ -36,7 +36,7 @@ def _grids(ms, dims, lasts, bwd):
 
 
 # m = 140: past the multi-block kernels (the general ones)
-@pytest.mark.parametrize("m, d, dv, last", _grids([7, 33, 48, 64, 65, 96, 128, 140],
+@pytest.mark.parametrize("m, d, dv, last", _grids([7, 33, 40, 41, 48, 64, 65, 96, 128, 140],
                                                   [(64, 64), (128, 128), (32, 32), (128, 64), (32, 128), (256, 256),
                                                    (16, 16)], [False, True], False))
 def test_general_lstep_forward_matches_oracle(m, d, dv, last):
@@ -65,7 +65,7 @@ def test_general_lstep_forward_matches_oracle(m, d, dv, last):
 # m = 129: the general kernel (fits at 16 / 16); mcm 0.6 keeps the column-mass clamp active
 @pytest.mark.parametrize("m, d, dv, last, mcm",
                          [(m, d, dv, last, mcm) for m, d, dv, last in
-                          _grids([7, 33, 48, 64, 65, 96, 128, 129], [(64, 64), (128, 128), (32, 32), (64, 128), (128, 32),
+                          _grids([7, 33, 40, 41, 48, 64, 65, 96, 128, 129], [(64, 64), (128, 128), (32, 32), (64, 128), (128, 32),
                                                                       (128, 64), (16, 16)], [False, True], True)
                           for mcm in ((0.01,) if last else (0.01, 0.6))])
 def test_general_lstep_backward_matches_oracle(m, d, dv, last, mcm):

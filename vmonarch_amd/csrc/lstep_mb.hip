@@ -47,14 +47,37 @@ __host__ __device__ constexpr int mb_bwd_patch_rows(bool last, int M) { return l
 struct MbLayout {
   int q, k, y, g, e, lse, part, rs, f, dc, patch, total;
 };
-__host__ __device__ inline MbLayout mb_layout(int M, int d, int dv, bool last, bool bwd) {
+// A staged tile holds M = 32 ceil(m / 32) rows, those past m zeros (finite data whose weights are exact zeros).
+// A compact tile (CT: the two-block last-step kernels up to kMbCompactMaxFrames, where it lets one more column
+// share the CU) holds the m rows, the rows by which the last copy instruction overhangs them (copies of row
+// m - 1; one instruction covers 1024 / rb rows of rb bytes) and one zero row, at which every operand read of a
+// row past m is pointed.  The other kernels keep whole blocks: their reads take each block's rows at immediate
+// offsets from one per-lane address, where the compact tile needs a clamped address per block (a build with
+// compact tiles everywhere ran up to 14% slower on the grids it gave no extra column).
+__host__ __device__ constexpr int mb_zero_row(int m, int rb) { return (m + 1024 / rb - 1) / (1024 / rb) * (1024 / rb); }
+__host__ __device__ constexpr int mb_tile_bytes(int m, int rb, bool compact) {
+  return compact ? (mb_zero_row(m, rb) + 1) * rb : (m + 31) / 32 * 32 * rb;
+}
+// Compact tiles are built for the two-block last step at head dims 128 / 128 and taken up to 40 frames: there its
+// four tiles (three in the forward) shrink enough for one more column per CU (the backward 3 instead of 2, the
+// forward 4 instead of 3); beyond that, or with narrower tiles, the per-row clamp costs without a column to gain.
+constexpr int kMbCompactMaxFrames = 40;
+constexpr bool mb_compact_built(int d, int dv, bool last) { return last && d == 128 && dv == 128; }
+template <int RB, bool CT>
+__device__ __forceinline__ int mb_phys_row(int r, int m) {
+  if constexpr (CT) return r < m ? r : mb_zero_row(m, RB);
+  else return r;
+}
+
+__host__ __device__ inline MbLayout mb_layout(int m, int d, int dv, bool last, bool bwd, bool compact) {
   MbLayout L;
+  const int M = 32 * ((m + 31) / 32);
   int off = 0;
   auto take = [&](int bytes) { const int o = off; off += (bytes + 255) / 256 * 256; return o; };
-  L.q = take(M * d * 2);
-  L.k = take(M * d * 2);
-  L.y = last ? take(M * dv * 2) : 0;
-  L.g = bwd ? take(M * (last ? dv : d) * 2) : 0;
+  L.q = take(mb_tile_bytes(m, d * 2, compact));
+  L.k = take(mb_tile_bytes(m, d * 2, compact));
+  L.y = last ? take(mb_tile_bytes(m, dv * 2, compact)) : 0;
+  L.g = bwd ? take(mb_tile_bytes(m, (last ? dv : d) * 2, compact)) : 0;
   L.e = take(M * 4);
   L.lse = take(M * 4);
   L.part = take(4 * M * 4);   // two blocks' partial row / column vectors (the two-block passes)
@@ -66,15 +89,13 @@ __host__ __device__ inline MbLayout mb_layout(int M, int d, int dv, bool last, b
   return L;
 }
 
-// Stage M rows of W 16-bit values (row r < m: src + r rs) into a tile whose chunk c of row r sits at chunk
+// Stage the m rows of W 16-bit values (row r: src + r rs) into a tile whose chunk c of row r sits at chunk
 // c ^ swz_rows(r): wave instruction inst covers rows inst RPI .. + RPI - 1, lane l lands at byte 16 l of its
 // 1 KB and so loads global chunk (l % CH) ^ swz_rows(row).  Only instructions that hold a row below m copy
-// (their rows past m repeat row m - 1); the rows after them are zeroed -- finite data whose weights are exact
-// zeros, without copying the last row over and over.  SW < W: a 16-wide tensor in a 32-wide tile (tile_w),
-// each row's two chunks stored twice.
-template <class T, int W, int SW = W>
-__device__ __forceinline__ void mb_stage(const T* src, int64_t rs, int m, int M, VMO_LDS char* dst, int wave,
-                                         int lane) {
+// (their rows past m repeat row m - 1); the rows after them are zeroed up to M (a compact tile: the one zero
+// row, mb_zero_row).  SW < W: a 16-wide tensor in a 32-wide tile (tile_w), each row's two chunks stored twice.
+template <class T, int W, int SW = W, bool CT = false>
+__device__ __forceinline__ void mb_stage(const T* src, int64_t rs, int m, VMO_LDS char* dst, int wave, int lane) {
   constexpr int RB = W * 2, CH = RB / 16, RPI = 64 / CH;
   const int c = lane % CH;
   const int ninst = (m + RPI - 1) / RPI;
@@ -83,28 +104,43 @@ __device__ __forceinline__ void mb_stage(const T* src, int64_t rs, int m, int M,
     const int rr = r < m ? r : m - 1;
     g2l_16(src + (int64_t)rr * rs + ((c ^ swz_rows<RB>(r)) & (SW / 8 - 1)) * 8, dst + inst * 1024);
   }
-  for (int o = ninst * 1024 + (64 * wave + lane) * 16; o < M * RB; o += 64 * kMbWaves * 16)
+  const int end = CT ? ninst * 1024 + RB : (m + 31) / 32 * 32 * RB;
+  for (int o = ninst * 1024 + (64 * wave + lane) * 16; o < end; o += 64 * kMbWaves * 16)
     *(VMO_LDS i32x4*)(dst + o) = i32x4{0, 0, 0, 0};
 }
 
-// Row-read MFMA operand: lane (row l32 of a 32-row block at `rows`, half hl) gets elements 16 ds + 8 hl .. + 7.
-template <class V8, int RB>
-__device__ __forceinline__ V8 mb_row8(const VMO_LDS char* rows, int l32, int hl, int ds) {
-  return lds_read8<V8>(rows + l32 * RB + ((2 * ds + hl) ^ swz_rows<RB>(l32)) * 16);
+// Row-read MFMA operand: lane (row l32 of 32-row block blk of the tile, half hl) gets elements 16 ds + 8 hl .. + 7
+// (zeros for a row past m).
+template <class V8, int RB, bool CT = false>
+__device__ __forceinline__ V8 mb_row8(const VMO_LDS char* tile, int blk, int m, int l32, int hl, int ds) {
+  if constexpr (CT) {
+    const int r = mb_phys_row<RB, CT>(32 * blk + l32, m);
+    return lds_read8<V8>(tile + r * RB + ((2 * ds + hl) ^ swz_rows<RB>(r)) * 16);
+  } else {   // (swz_rows depends on the row mod 16 alone)
+    return lds_read8<V8>(tile + 32 * blk * RB + l32 * RB + ((2 * ds + hl) ^ swz_rows<RB>(l32)) * 16);
+  }
 }
 
 // Transposed MFMA A operand for the 32 columns 32 a .. 32 a + 31 of a row-major tile, K step h2 (16 rows) of
-// the 32-row block at `rows`: the rows are taken in the S^T / L accumulator's order (rows 4 hl + 0..3 and
-// 8 + 4 hl + 0..3 of the step), so that accumulator rows 8 h2 .. 8 h2 + 7, rounded, are the B operand.
-template <class V8, int RB>
-__device__ __forceinline__ V8 mb_tr8(const VMO_LDS char* rows, int lane, int a, int h2) {
+// its 32-row block blk: the rows are taken in the S^T / L accumulator's order (rows 4 hl + 0..3 and
+// 8 + 4 hl + 0..3 of the step), so that accumulator rows 8 h2 .. 8 h2 + 7, rounded, are the B operand.  Each
+// lane reads 8 bytes of one row; a row past m is read from the zero row.
+template <class V8, int RB, bool CT = false>
+__device__ __forceinline__ V8 mb_tr8(const VMO_LDS char* tile, int blk, int m, int lane, int a, int h2) {
   const int hl = lane >> 5;
   const int trow = 4 * hl + ((lane & 15) >> 2);
   const int tchunk = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
   const int tbyte = (lane & 1) * 8;
-  const int c0 = trow * RB + (((4 * a + tchunk) ^ swz_rows<RB>(trow)) * 16 + tbyte);
-  const VMO_LDS char* rp = rows + 16 * h2 * RB;
-  return lds_read_tr8<V8>(rp + c0, rp + 8 * RB + (c0 ^ 32));
+  if constexpr (CT) {
+    const int r0 = mb_phys_row<RB, CT>(32 * blk + 16 * h2 + trow, m);
+    const int r1 = mb_phys_row<RB, CT>(32 * blk + 16 * h2 + trow + 8, m);
+    return lds_read_tr8<V8>(tile + r0 * RB + ((4 * a + tchunk) ^ swz_rows<RB>(r0)) * 16 + tbyte,
+                            tile + r1 * RB + ((4 * a + tchunk) ^ swz_rows<RB>(r1)) * 16 + tbyte);
+  } else {   // row 8 further on: the swizzle's chunk bit 1 flips
+    const int c0 = trow * RB + (((4 * a + tchunk) ^ swz_rows<RB>(trow)) * 16 + tbyte);
+    const VMO_LDS char* rp = tile + (32 * blk + 16 * h2) * RB;
+    return lds_read_tr8<V8>(rp + c0, rp + 8 * RB + (c0 ^ 32));
+  }
 }
 
 // Accumulator rows 8 h2 .. 8 h2 + 7 of x, times f, rounded to the 16-bit type: a B operand.
@@ -116,12 +152,13 @@ __device__ __forceinline__ V8 mb_pack(const f32x16& x, int h2, float f) {
   return v;
 }
 
-template <bool F16, int D, int DV, bool LAST, bool TWO>
+template <bool F16, int D, int DV, bool LAST, bool TWO, bool CT>
 __global__ __launch_bounds__(64 * kMbWaves, TWO && !LAST ? 4 : 2) void lstep_mb_kernel(LParams p) {
   using E = Elem<F16>;
   using T = typename E::T;
   using V8 = typename E::V8;
   constexpr int DK = tile_w(D), DVK = tile_w(DV);   // widths in LDS
+  static_assert(!CT || (LAST && TWO), "compact tiles: the two-block last-step kernels");
   constexpr int NDS = D / 16;
   constexpr int NACC = (LAST ? DVK : DK) / 32;
   constexpr int CW = (LAST ? DV : D) < 32 ? 16 : 32;   // stored columns per accumulator block
@@ -130,7 +167,7 @@ __global__ __launch_bounds__(64 * kMbWaves, TWO && !LAST ? 4 : 2) void lstep_mb_
   VMO_LDS char* sm = (VMO_LDS char*)smem_raw;
 
   const int m = p.m, MB = (m + 31) / 32, M = 32 * MB;
-  const MbLayout Lo = mb_layout(M, DK, DVK, LAST, false);
+  const MbLayout Lo = mb_layout(m, DK, DVK, LAST, false, CT);
   VMO_LDS char* q_t = sm + Lo.q;
   VMO_LDS char* k_t = sm + Lo.k;
   VMO_LDS char* y_t = sm + Lo.y;
@@ -145,9 +182,9 @@ __global__ __launch_bounds__(64 * kMbWaves, TWO && !LAST ? 4 : 2) void lstep_mb_
   const T* ocol = (const T*)p.out + bb * p.out_sb + hh * p.out_sh + (int64_t)j * p.out_sn;
   T* rcol = (T*)p.res + bb * p.res_sb + hh * p.res_sh + (int64_t)j * p.res_sn;
 
-  mb_stage<T, DK, D>(qcol, q_rs, m, M, q_t, wave, lane);
-  mb_stage<T, DK, D>(ocol, o_rs, m, M, k_t, wave, lane);
-  if constexpr (LAST) mb_stage<T, DVK, DV>(ocol + D, o_rs, m, M, y_t, wave, lane);
+  mb_stage<T, DK, D, CT>(qcol, q_rs, m, q_t, wave, lane);
+  mb_stage<T, DK, D, CT>(ocol, o_rs, m, k_t, wave, lane);
+  if constexpr (LAST) mb_stage<T, DVK, DV, CT>(ocol + D, o_rs, m, y_t, wave, lane);
   const float* ep = p.ent + bb * p.ent_sb + hh * p.ent_sh + j;
   for (int k = tid; k < M; k += 64 * kMbWaves) e_t[k] = k < m ? ep[(int64_t)k * p.bs] * kLog2e : -1.0e30f;
   __builtin_amdgcn_s_waitcnt(0);
@@ -159,14 +196,14 @@ __global__ __launch_bounds__(64 * kMbWaves, TWO && !LAST ? 4 : 2) void lstep_mb_
   auto s_blocks = [&](int ib, f32x16 (&x)[kMbMaxBlocks]) __attribute__((always_inline)) {
     V8 qb[NDS];
 #pragma unroll
-    for (int ds = 0; ds < NDS; ++ds) qb[ds] = mb_row8<V8, RBD>(q_t + 32 * ib * RBD, l32, hl, ds);
+    for (int ds = 0; ds < NDS; ++ds) qb[ds] = mb_row8<V8, RBD, CT>(q_t, ib, m, l32, hl, ds);
     float mx = -3.0e38f;
 #pragma unroll
     for (int kb = 0; kb < kMbMaxBlocks; ++kb) {
       if (kb >= MB) break;
       x[kb] = f32x16{};
 #pragma unroll
-      for (int ds = 0; ds < NDS; ++ds) x[kb] = E::mfma(mb_row8<V8, RBD>(k_t + 32 * kb * RBD, l32, hl, ds), qb[ds], x[kb]);
+      for (int ds = 0; ds < NDS; ++ds) x[kb] = E::mfma(mb_row8<V8, RBD, CT>(k_t, kb, m, l32, hl, ds), qb[ds], x[kb]);
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const f32x4 ev = *(const VMO_LDS f32x4*)(e_t + 32 * kb + 8 * g + 4 * hl);
@@ -209,8 +246,8 @@ __global__ __launch_bounds__(64 * kMbWaves, TWO && !LAST ? 4 : 2) void lstep_mb_
         const V8 P0 = mb_pack<T, V8>(x[kb], 0, inv), P1 = mb_pack<T, V8>(x[kb], 1, inv);
 #pragma unroll
         for (int a = 0; a < NH; ++a) {
-          acch[a] = E::mfma(mb_tr8<V8, RBY>(y_t + 32 * kb * RBY, lane, half * NH + a, 0), P0, acch[a]);
-          acch[a] = E::mfma(mb_tr8<V8, RBY>(y_t + 32 * kb * RBY, lane, half * NH + a, 1), P1, acch[a]);
+          acch[a] = E::mfma(mb_tr8<V8, RBY, CT>(y_t, kb, m, lane, half * NH + a, 0), P0, acch[a]);
+          acch[a] = E::mfma(mb_tr8<V8, RBY, CT>(y_t, kb, m, lane, half * NH + a, 1), P1, acch[a]);
         }
       }
     } else {
@@ -222,8 +259,8 @@ __global__ __launch_bounds__(64 * kMbWaves, TWO && !LAST ? 4 : 2) void lstep_mb_
       V8 kr_op[NDS], q_op[NDS];
 #pragma unroll
       for (int ds = 0; ds < NDS; ++ds) {
-        kr_op[ds] = mb_row8<V8, RBD>(k_t + 32 * rb * RBD, l32, hl, ds);
-        q_op[ds] = mb_row8<V8, RBD>(q_t + 32 * half * RBD, l32, hl, ds);
+        kr_op[ds] = mb_row8<V8, RBD, CT>(k_t, rb, m, l32, hl, ds);
+        q_op[ds] = mb_row8<V8, RBD, CT>(q_t, half, m, l32, hl, ds);
       }
       {   // S^T block (keys of block rb, queries of block half): partial max and sum per query row
         f32x16 x = f32x16{};
@@ -265,7 +302,7 @@ __global__ __launch_bounds__(64 * kMbWaves, TWO && !LAST ? 4 : 2) void lstep_mb_
         f32x16 x = f32x16{};
 #pragma unroll
         for (int ds = 0; ds < NDS; ++ds)
-          x = E::mfma(t == 0 ? q_op[ds] : mb_row8<V8, RBD>(q_t + 32 * ib * RBD, l32, hl, ds), kr_op[ds], x);
+          x = E::mfma(t == 0 ? q_op[ds] : mb_row8<V8, RBD, CT>(q_t, ib, m, l32, hl, ds), kr_op[ds], x);
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const f32x4 lv = *(const VMO_LDS f32x4*)(lse_t + 32 * ib + 8 * g + 4 * hl);
@@ -279,8 +316,8 @@ __global__ __launch_bounds__(64 * kMbWaves, TWO && !LAST ? 4 : 2) void lstep_mb_
         const V8 P0 = mb_pack<T, V8>(x, 0, 1.f), P1 = mb_pack<T, V8>(x, 1, 1.f);
 #pragma unroll
         for (int a = 0; a < NH; ++a) {
-          acch[a] = E::mfma(mb_tr8<V8, RBD>(q_t + 32 * ib * RBD, lane, half * NH + a, 0), P0, acch[a]);
-          acch[a] = E::mfma(mb_tr8<V8, RBD>(q_t + 32 * ib * RBD, lane, half * NH + a, 1), P1, acch[a]);
+          acch[a] = E::mfma(mb_tr8<V8, RBD, CT>(q_t, ib, m, lane, half * NH + a, 0), P0, acch[a]);
+          acch[a] = E::mfma(mb_tr8<V8, RBD, CT>(q_t, ib, m, lane, half * NH + a, 1), P1, acch[a]);
         }
       }
       fsc = p.scale / fmaxf(wave_sum32(cm), p.min_col_mass);
@@ -326,8 +363,8 @@ __global__ __launch_bounds__(64 * kMbWaves, TWO && !LAST ? 4 : 2) void lstep_mb_
         const V8 P0 = mb_pack<T, V8>(x[kb], 0, inv), P1 = mb_pack<T, V8>(x[kb], 1, inv);
 #pragma unroll
         for (int a = 0; a < NACC; ++a) {
-          acc[a] = E::mfma(mb_tr8<V8, RBY>(y_t + 32 * kb * RBY, lane, a, 0), P0, acc[a]);
-          acc[a] = E::mfma(mb_tr8<V8, RBY>(y_t + 32 * kb * RBY, lane, a, 1), P1, acc[a]);
+          acc[a] = E::mfma(mb_tr8<V8, RBY, CT>(y_t, kb, m, lane, a, 0), P0, acc[a]);
+          acc[a] = E::mfma(mb_tr8<V8, RBY, CT>(y_t, kb, m, lane, a, 1), P1, acc[a]);
         }
       }
     }
@@ -351,7 +388,7 @@ __global__ __launch_bounds__(64 * kMbWaves, TWO && !LAST ? 4 : 2) void lstep_mb_
     if (busy) {
       V8 kb_op[NDS];
 #pragma unroll
-      for (int ds = 0; ds < NDS; ++ds) kb_op[ds] = mb_row8<V8, RBD>(k_t + 32 * blk * RBD, l32, hl, ds);
+      for (int ds = 0; ds < NDS; ++ds) kb_op[ds] = mb_row8<V8, RBD, CT>(k_t, blk, m, l32, hl, ds);
       const float ek = e_t[32 * blk + l32];
       float cm = 0.f;
 #pragma unroll
@@ -360,7 +397,7 @@ __global__ __launch_bounds__(64 * kMbWaves, TWO && !LAST ? 4 : 2) void lstep_mb_
         // L[i][k] = q_i . kr_k: A = q rows (lane = query row), B = kr rows (lane = key)
         f32x16 x = f32x16{};
 #pragma unroll
-        for (int ds = 0; ds < NDS; ++ds) x = E::mfma(mb_row8<V8, RBD>(q_t + 32 * ib * RBD, l32, hl, ds), kb_op[ds], x);
+        for (int ds = 0; ds < NDS; ++ds) x = E::mfma(mb_row8<V8, RBD, CT>(q_t, ib, m, l32, hl, ds), kb_op[ds], x);
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const f32x4 lv = *(const VMO_LDS f32x4*)(lse_t + 32 * ib + 8 * g + 4 * hl);
@@ -375,8 +412,8 @@ __global__ __launch_bounds__(64 * kMbWaves, TWO && !LAST ? 4 : 2) void lstep_mb_
         const V8 P0 = mb_pack<T, V8>(x, 0, 1.f), P1 = mb_pack<T, V8>(x, 1, 1.f);
 #pragma unroll
         for (int a = 0; a < NACC; ++a) {
-          acc[a] = E::mfma(mb_tr8<V8, RBD>(q_t + 32 * ib * RBD, lane, a, 0), P0, acc[a]);
-          acc[a] = E::mfma(mb_tr8<V8, RBD>(q_t + 32 * ib * RBD, lane, a, 1), P1, acc[a]);
+          acc[a] = E::mfma(mb_tr8<V8, RBD, CT>(q_t, ib, m, lane, a, 0), P0, acc[a]);
+          acc[a] = E::mfma(mb_tr8<V8, RBD, CT>(q_t, ib, m, lane, a, 1), P1, acc[a]);
         }
       }
       fscale = p.scale / fmaxf(wave_sum32(cm), p.min_col_mass);
@@ -414,12 +451,13 @@ __global__ __launch_bounds__(64 * kMbWaves, TWO && !LAST ? 4 : 2) void lstep_mb_
 // HBM traffic); the attention is exp2(logit - lse_i), exactly normalised.  MFMA operands a, dl and a f are
 // rounded to the 16-bit type, the sums rs, c, gv kept in fp32 from the fp32 attention.  dq (fp32) is added
 // to or overwritten, d out (the 16-bit type) written; rows past m carry zero attention and are not stored.
-template <bool F16, int D, int DV, bool LAST, bool TWO>
+template <bool F16, int D, int DV, bool LAST, bool TWO, bool CT>
 __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams p) {
   using E = Elem<F16>;
   using T = typename E::T;
   using V8 = typename E::V8;
   constexpr int DK = tile_w(D), DVK = tile_w(DV);   // widths in LDS
+  static_assert(!CT || (LAST && TWO), "compact tiles: the two-block last-step kernels");
   constexpr int NDS = D / 16, NDSV = DV / 16;
   constexpr int ND = DK / 32, NV = DVK / 32;
   constexpr int CWD = D < 32 ? 16 : 32, CWV = DV < 32 ? 16 : 32;   // stored columns per accumulator block
@@ -429,7 +467,7 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
   VMO_LDS char* sm = (VMO_LDS char*)smem_raw;
 
   const int m = p.m, MB = (m + 31) / 32, M = 32 * MB;
-  const MbLayout Lo = mb_layout(M, DK, DVK, LAST, true);
+  const MbLayout Lo = mb_layout(m, DK, DVK, LAST, true, CT);
   VMO_LDS char* q_t = sm + Lo.q;
   VMO_LDS char* k_t = sm + Lo.k;
   VMO_LDS char* y_t = sm + Lo.y;
@@ -453,17 +491,17 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
   float* dqcol = p.dq + bb * p.dq_sb + hh * p.dq_sh + (int64_t)j * p.dq_sn;
   T* dcol = (T*)p.dout + bb * p.do_sb + hh * p.do_sh + (int64_t)j * p.do_sn;
 
-  mb_stage<T, DK, D>(qcol, q_rs, m, M, q_t, wave, lane);
-  mb_stage<T, DK, D>(ocol, o_rs, m, M, k_t, wave, lane);
-  if constexpr (LAST) mb_stage<T, DVK, DV>(ocol + D, o_rs, m, M, y_t, wave, lane);
-  mb_stage<T, GWK, GW>(gcol, g_rs, m, M, g_t, wave, lane);
+  mb_stage<T, DK, D, CT>(qcol, q_rs, m, q_t, wave, lane);
+  mb_stage<T, DK, D, CT>(ocol, o_rs, m, k_t, wave, lane);
+  if constexpr (LAST) mb_stage<T, DVK, DV, CT>(ocol + D, o_rs, m, y_t, wave, lane);
+  mb_stage<T, GWK, GW, CT>(gcol, g_rs, m, g_t, wave, lane);
   const float* ep = p.ent + bb * p.ent_sb + hh * p.ent_sh + j;
   for (int k = tid; k < M; k += 64 * kMbWaves) e_t[k] = k < m ? ep[(int64_t)k * p.bs] * kLog2e : -1.0e30f;
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if constexpr (LAST) {   // z rows of tokens < skip are the recompute's: no gradient reaches the L-path
     constexpr int CH = RBG / 16;
-    for (int idx = tid; idx < M * CH; idx += 64 * kMbWaves) {
+    for (int idx = tid; idx < m * CH; idx += 64 * kMbWaves) {
       const int r = idx / CH;
       if ((int64_t)r * p.bs + j < p.skip) *(VMO_LDS i32x4*)(g_t + r * RBG + (idx % CH) * 16) = i32x4{0, 0, 0, 0};
     }
@@ -479,7 +517,7 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
   auto s_block = [&](int kb, const V8 (&qb)[NDS]) __attribute__((always_inline)) {
     f32x16 x = f32x16{};
 #pragma unroll
-    for (int ds = 0; ds < NDS; ++ds) x = E::mfma(mb_row8<V8, RBD>(k_t + 32 * kb * RBD, l32, hl, ds), qb[ds], x);
+    for (int ds = 0; ds < NDS; ++ds) x = E::mfma(mb_row8<V8, RBD, CT>(k_t, kb, m, l32, hl, ds), qb[ds], x);
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const f32x4 ev = *(const VMO_LDS f32x4*)(e_t + 32 * kb + 8 * g + 4 * hl);
@@ -494,7 +532,7 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
     f32x16 x = f32x16{};
 #pragma unroll
     for (int ds = 0; ds < NDS; ++ds)
-      x = E::mfma(mb_row8<V8, RBD>(q_t + 32 * ib * RBD, l32, hl, ds), mb_row8<V8, RBD>(k_t + 32 * kb * RBD, l32, hl, ds), x);
+      x = E::mfma(mb_row8<V8, RBD, CT>(q_t, ib, m, l32, hl, ds), mb_row8<V8, RBD, CT>(k_t, kb, m, l32, hl, ds), x);
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const f32x4 lv = *(const VMO_LDS f32x4*)(lse_t + 32 * ib + 8 * g + 4 * hl);
@@ -525,7 +563,7 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
   };
   auto load_rows = [&](V8 (&op)[NDS], const VMO_LDS char* tile, int b) __attribute__((always_inline)) {
 #pragma unroll
-    for (int ds = 0; ds < NDS; ++ds) op[ds] = mb_row8<V8, RBD>(tile + 32 * b * RBD, l32, hl, ds);
+    for (int ds = 0; ds < NDS; ++ds) op[ds] = mb_row8<V8, RBD, CT>(tile, b, m, l32, hl, ds);
   };
   const bool row_ok = 32 * blk + l32 < m;   // this lane's query row (query-block passes) or key (key-block passes)
   const int nrows = busy ? min(32, m - 32 * blk) : 0;
@@ -589,7 +627,7 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
         f32x16 d = f32x16{};   // DA^T[k][i] = y_k . g_i
 #pragma unroll
         for (int ds = 0; ds < NDSV; ++ds)
-          d = E::mfma(mb_row8<V8, RBY>(y_t + 32 * kb * RBY, l32, hl, ds), mb_row8<V8, RBY>(g_t + 32 * ib * RBY, l32, hl, ds), d);
+          d = E::mfma(mb_row8<V8, RBY, CT>(y_t, kb, m, l32, hl, ds), mb_row8<V8, RBY, CT>(g_t, ib, m, l32, hl, ds), d);
         float rs = 0.f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) rs = fmaf(x[r], d[r], rs);
@@ -610,8 +648,8 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
           const V8 P0 = src[0], P1 = src[64];
 #pragma unroll
           for (int a = 0; a < NH; ++a) {
-            accq[a] = E::mfma(mb_tr8<V8, RBD>(k_t + 32 * k2 * RBD, lane, kb * NH + a, 0), P0, accq[a]);
-            accq[a] = E::mfma(mb_tr8<V8, RBD>(k_t + 32 * k2 * RBD, lane, kb * NH + a, 1), P1, accq[a]);
+            accq[a] = E::mfma(mb_tr8<V8, RBD, CT>(k_t, k2, m, lane, kb * NH + a, 0), P0, accq[a]);
+            accq[a] = E::mfma(mb_tr8<V8, RBD, CT>(k_t, k2, m, lane, kb * NH + a, 1), P1, accq[a]);
           }
         }
         __syncthreads();   // every wave is done with xch: the patches may reuse it
@@ -625,7 +663,7 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
         f32x16 dl = f32x16{};   // DA[i][k] = g_i . y_k
 #pragma unroll
         for (int ds = 0; ds < NDSV; ++ds)
-          dl = E::mfma(mb_row8<V8, RBY>(g_t + 32 * iq * RBY, l32, hl, ds), mb_row8<V8, RBY>(y_t + 32 * kq * RBY, l32, hl, ds), dl);
+          dl = E::mfma(mb_row8<V8, RBY, CT>(g_t, iq, m, l32, hl, ds), mb_row8<V8, RBY, CT>(y_t, kq, m, l32, hl, ds), dl);
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const f32x4 rv = *(const VMO_LDS f32x4*)(rs_t + 32 * iq + 8 * g + 4 * hl);
@@ -645,8 +683,8 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
           const V8 A0 = src[0], A1 = src[64];
 #pragma unroll
           for (int a = 0; a < NVH; ++a) {
-            accy[a] = E::mfma(mb_tr8<V8, RBY>(g_t + 32 * i2 * RBY, lane, iq * NVH + a, 0), A0, accy[a]);
-            accy[a] = E::mfma(mb_tr8<V8, RBY>(g_t + 32 * i2 * RBY, lane, iq * NVH + a, 1), A1, accy[a]);
+            accy[a] = E::mfma(mb_tr8<V8, RBY, CT>(g_t, i2, m, lane, iq * NVH + a, 0), A0, accy[a]);
+            accy[a] = E::mfma(mb_tr8<V8, RBY, CT>(g_t, i2, m, lane, iq * NVH + a, 1), A1, accy[a]);
           }
         }
         __syncthreads();
@@ -662,8 +700,8 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
           const V8 P0 = src[0], P1 = src[64];
 #pragma unroll
           for (int a = 0; a < NH; ++a) {
-            acck[a] = E::mfma(mb_tr8<V8, RBD>(q_t + 32 * i2 * RBD, lane, iq * NH + a, 0), P0, acck[a]);
-            acck[a] = E::mfma(mb_tr8<V8, RBD>(q_t + 32 * i2 * RBD, lane, iq * NH + a, 1), P1, acck[a]);
+            acck[a] = E::mfma(mb_tr8<V8, RBD, CT>(q_t, i2, m, lane, iq * NH + a, 0), P0, acck[a]);
+            acck[a] = E::mfma(mb_tr8<V8, RBD, CT>(q_t, i2, m, lane, iq * NH + a, 1), P1, acck[a]);
           }
         }
         __syncthreads();
@@ -685,7 +723,7 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
         f32x16 d = f32x16{};
 #pragma unroll
         for (int ds = 0; ds < NDSV; ++ds)
-          d = E::mfma(mb_row8<V8, RBY>(y_t + 32 * kb * RBY, l32, hl, ds), mb_row8<V8, RBY>(g_t + 32 * blk * RBY, l32, hl, ds),
+          d = E::mfma(mb_row8<V8, RBY, CT>(y_t, kb, m, l32, hl, ds), mb_row8<V8, RBY, CT>(g_t, blk, m, l32, hl, ds),
                       d);
         return d;
       };
@@ -714,8 +752,8 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
         const V8 P0 = mb_pack<T, V8>(dl, 0, 1.f), P1 = mb_pack<T, V8>(dl, 1, 1.f);
 #pragma unroll
         for (int a = 0; a < ND; ++a) {
-          accq[a] = E::mfma(mb_tr8<V8, RBD>(k_t + 32 * kb * RBD, lane, a, 0), P0, accq[a]);
-          accq[a] = E::mfma(mb_tr8<V8, RBD>(k_t + 32 * kb * RBD, lane, a, 1), P1, accq[a]);
+          accq[a] = E::mfma(mb_tr8<V8, RBD, CT>(k_t, kb, m, lane, a, 0), P0, accq[a]);
+          accq[a] = E::mfma(mb_tr8<V8, RBD, CT>(k_t, kb, m, lane, a, 1), P1, accq[a]);
         }
       }
       store_rows(std::integral_constant<int, CWD>{}, accq, ND, dq_mode, (char*)(dqcol + 32 * blk * dq_rs), dq_rs * 4, nrows);
@@ -736,8 +774,8 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
         const V8 A0 = mb_pack<T, V8>(at, 0, 1.f), A1 = mb_pack<T, V8>(at, 1, 1.f);
 #pragma unroll
         for (int a = 0; a < NV; ++a) {
-          accy[a] = E::mfma(mb_tr8<V8, RBY>(g_t + 32 * ib * RBY, lane, a, 0), A0, accy[a]);
-          accy[a] = E::mfma(mb_tr8<V8, RBY>(g_t + 32 * ib * RBY, lane, a, 1), A1, accy[a]);
+          accy[a] = E::mfma(mb_tr8<V8, RBY, CT>(g_t, ib, m, lane, a, 0), A0, accy[a]);
+          accy[a] = E::mfma(mb_tr8<V8, RBY, CT>(g_t, ib, m, lane, a, 1), A1, accy[a]);
         }
       }
       store_rows(std::integral_constant<int, CWV>{}, accy, NV, kGradStore, (char*)(dcol + 32 * blk * do_rs + D),
@@ -753,7 +791,7 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
         f32x16 dl = f32x16{};
 #pragma unroll
         for (int ds = 0; ds < NDSV; ++ds)
-          dl = E::mfma(mb_row8<V8, RBY>(g_t + 32 * ib * RBY, l32, hl, ds), mb_row8<V8, RBY>(y_t + 32 * blk * RBY, l32, hl, ds),
+          dl = E::mfma(mb_row8<V8, RBY, CT>(g_t, ib, m, l32, hl, ds), mb_row8<V8, RBY, CT>(y_t, blk, m, l32, hl, ds),
                        dl);
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
@@ -764,8 +802,8 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
         const V8 P0 = mb_pack<T, V8>(dl, 0, 1.f), P1 = mb_pack<T, V8>(dl, 1, 1.f);
 #pragma unroll
         for (int a = 0; a < ND; ++a) {
-          acck[a] = E::mfma(mb_tr8<V8, RBD>(q_t + 32 * ib * RBD, lane, a, 0), P0, acck[a]);
-          acck[a] = E::mfma(mb_tr8<V8, RBD>(q_t + 32 * ib * RBD, lane, a, 1), P1, acck[a]);
+          acck[a] = E::mfma(mb_tr8<V8, RBD, CT>(q_t, ib, m, lane, a, 0), P0, acck[a]);
+          acck[a] = E::mfma(mb_tr8<V8, RBD, CT>(q_t, ib, m, lane, a, 1), P1, acck[a]);
         }
       }
       store_rows(std::integral_constant<int, CWD>{}, acck, ND, kGradStore, (char*)(dcol + 32 * blk * do_rs), do_rs * 2,
@@ -795,7 +833,7 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
         const f32x16 at = attn_block(iq, kq, e_t[32 * kq + l32]);
         f32x16 gq = f32x16{};   // GQ[i][k] = q_i . g_k
 #pragma unroll
-        for (int ds = 0; ds < NDS; ++ds) gq = E::mfma(mb_row8<V8, RBD>(q_t + 32 * iq * RBD, l32, hl, ds), gop[ds], gq);
+        for (int ds = 0; ds < NDS; ++ds) gq = E::mfma(mb_row8<V8, RBD, CT>(q_t, iq, m, l32, hl, ds), gop[ds], gq);
         float cs = 0.f, gv = 0.f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -825,7 +863,7 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
         for (int r = 0; r < 16; ++r) x[r] = fast_exp2(x[r] - lse);   // attn^T[k][i]
         f32x16 d = f32x16{};   // da^T[k][i] = f_k (g_k . q_i) + dc_k
 #pragma unroll
-        for (int ds = 0; ds < NDS; ++ds) d = E::mfma(mb_row8<V8, RBD>(g_t + 32 * kb * RBD, l32, hl, ds), qb[ds], d);
+        for (int ds = 0; ds < NDS; ++ds) d = E::mfma(mb_row8<V8, RBD, CT>(g_t, kb, m, l32, hl, ds), qb[ds], d);
         f32x4 fv[4];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
@@ -864,10 +902,10 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
 #pragma unroll
           for (int a = 0; a < NH; ++a) {
             const int ca = kb * NH + a;   // this wave's column half
-            accq[a] = E::mfma(mb_tr8<V8, RBD>(k_t + 32 * k2 * RBD, lane, ca, 0), P0, accq[a]);
-            accq[a] = E::mfma(mb_tr8<V8, RBD>(k_t + 32 * k2 * RBD, lane, ca, 1), P1, accq[a]);
-            accq[a] = E::mfma(mb_tr8<V8, RBD>(g_t + 32 * k2 * RBD, lane, ca, 0), F0, accq[a]);
-            accq[a] = E::mfma(mb_tr8<V8, RBD>(g_t + 32 * k2 * RBD, lane, ca, 1), F1, accq[a]);
+            accq[a] = E::mfma(mb_tr8<V8, RBD, CT>(k_t, k2, m, lane, ca, 0), P0, accq[a]);
+            accq[a] = E::mfma(mb_tr8<V8, RBD, CT>(k_t, k2, m, lane, ca, 1), P1, accq[a]);
+            accq[a] = E::mfma(mb_tr8<V8, RBD, CT>(g_t, k2, m, lane, ca, 0), F0, accq[a]);
+            accq[a] = E::mfma(mb_tr8<V8, RBD, CT>(g_t, k2, m, lane, ca, 1), F1, accq[a]);
           }
         }
         __syncthreads();   // every wave is done with xch: the patches may reuse it
@@ -883,7 +921,7 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
         const f32x16 at = attn_block(iq, kq, e_t[32 * kq + l32]);
         f32x16 dl = f32x16{};
 #pragma unroll
-        for (int ds = 0; ds < NDS; ++ds) dl = E::mfma(mb_row8<V8, RBD>(q_t + 32 * iq * RBD, l32, hl, ds), gop[ds], dl);
+        for (int ds = 0; ds < NDS; ++ds) dl = E::mfma(mb_row8<V8, RBD, CT>(q_t, iq, m, l32, hl, ds), gop[ds], dl);
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const f32x4 rv = *(const VMO_LDS f32x4*)(rs_t + 32 * iq + 8 * g + 4 * hl);
@@ -907,8 +945,8 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
 #pragma unroll
           for (int a = 0; a < NH; ++a) {
             const int ca = iq * NH + a;
-            acck[a] = E::mfma(mb_tr8<V8, RBD>(q_t + 32 * i2 * RBD, lane, ca, 0), P0, acck[a]);
-            acck[a] = E::mfma(mb_tr8<V8, RBD>(q_t + 32 * i2 * RBD, lane, ca, 1), P1, acck[a]);
+            acck[a] = E::mfma(mb_tr8<V8, RBD, CT>(q_t, i2, m, lane, ca, 0), P0, acck[a]);
+            acck[a] = E::mfma(mb_tr8<V8, RBD, CT>(q_t, i2, m, lane, ca, 1), P1, acck[a]);
           }
         }
         __syncthreads();
@@ -938,7 +976,7 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
         const f32x16 at = attn_block(ib, blk, ek);
         f32x16 gq = f32x16{};   // GQ[i][k] = q_i . g_k
 #pragma unroll
-        for (int ds = 0; ds < NDS; ++ds) gq = E::mfma(mb_row8<V8, RBD>(q_t + 32 * ib * RBD, l32, hl, ds), gop[ds], gq);
+        for (int ds = 0; ds < NDS; ++ds) gq = E::mfma(mb_row8<V8, RBD, CT>(q_t, ib, m, l32, hl, ds), gop[ds], gq);
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           cs += at[r];
@@ -971,7 +1009,7 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
       auto da_block = [&](int kb) __attribute__((always_inline)) {
         f32x16 d = f32x16{};
 #pragma unroll
-        for (int ds = 0; ds < NDS; ++ds) d = E::mfma(mb_row8<V8, RBD>(g_t + 32 * kb * RBD, l32, hl, ds), qb[ds], d);
+        for (int ds = 0; ds < NDS; ++ds) d = E::mfma(mb_row8<V8, RBD, CT>(g_t, kb, m, l32, hl, ds), qb[ds], d);
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const f32x4 fv = *(const VMO_LDS f32x4*)(f_t + 32 * kb + 8 * g + 4 * hl);
@@ -1012,10 +1050,10 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
         const V8 F0 = mb_pack<T, V8>(af, 0, 1.f), F1 = mb_pack<T, V8>(af, 1, 1.f);
 #pragma unroll
         for (int a = 0; a < ND; ++a) {
-          accq[a] = E::mfma(mb_tr8<V8, RBD>(k_t + 32 * kb * RBD, lane, a, 0), P0, accq[a]);
-          accq[a] = E::mfma(mb_tr8<V8, RBD>(k_t + 32 * kb * RBD, lane, a, 1), P1, accq[a]);
-          accq[a] = E::mfma(mb_tr8<V8, RBD>(g_t + 32 * kb * RBD, lane, a, 0), F0, accq[a]);
-          accq[a] = E::mfma(mb_tr8<V8, RBD>(g_t + 32 * kb * RBD, lane, a, 1), F1, accq[a]);
+          accq[a] = E::mfma(mb_tr8<V8, RBD, CT>(k_t, kb, m, lane, a, 0), P0, accq[a]);
+          accq[a] = E::mfma(mb_tr8<V8, RBD, CT>(k_t, kb, m, lane, a, 1), P1, accq[a]);
+          accq[a] = E::mfma(mb_tr8<V8, RBD, CT>(g_t, kb, m, lane, a, 0), F0, accq[a]);
+          accq[a] = E::mfma(mb_tr8<V8, RBD, CT>(g_t, kb, m, lane, a, 1), F1, accq[a]);
         }
       }
       store_acc_rows<F16, CWD>(patch, accq, ND, 1.f, dq_mode, (char*)(dqcol + 32 * blk * dq_rs), dq_rs * 4, nrows, lane);
@@ -1036,7 +1074,7 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
         const f32x16 at = attn_block(ib, blk, ek);
         f32x16 dl = f32x16{};
 #pragma unroll
-        for (int ds = 0; ds < NDS; ++ds) dl = E::mfma(mb_row8<V8, RBD>(q_t + 32 * ib * RBD, l32, hl, ds), gop[ds], dl);
+        for (int ds = 0; ds < NDS; ++ds) dl = E::mfma(mb_row8<V8, RBD, CT>(q_t, ib, m, l32, hl, ds), gop[ds], dl);
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const f32x4 rv = *(const VMO_LDS f32x4*)(rs_t + 32 * ib + 8 * g + 4 * hl);
@@ -1049,8 +1087,8 @@ __global__ __launch_bounds__(64 * kMbWaves, 2) void lstep_mb_bwd_kernel(LBParams
         const V8 P0 = mb_pack<T, V8>(dl, 0, 1.f), P1 = mb_pack<T, V8>(dl, 1, 1.f);
 #pragma unroll
         for (int a = 0; a < ND; ++a) {
-          acck[a] = E::mfma(mb_tr8<V8, RBD>(q_t + 32 * ib * RBD, lane, a, 0), P0, acck[a]);
-          acck[a] = E::mfma(mb_tr8<V8, RBD>(q_t + 32 * ib * RBD, lane, a, 1), P1, acck[a]);
+          acck[a] = E::mfma(mb_tr8<V8, RBD, CT>(q_t, ib, m, lane, a, 0), P0, acck[a]);
+          acck[a] = E::mfma(mb_tr8<V8, RBD, CT>(q_t, ib, m, lane, a, 1), P1, acck[a]);
         }
       }
       store_acc_rows<F16, CWD>(patch, acck, ND, 1.f, kGradStore, (char*)(dcol + 32 * blk * do_rs), do_rs * 2, nrows, lane);
@@ -1068,19 +1106,18 @@ static bool mb_dims(int d, int dv, bool last) {
 
 int mb_lstep_check(int m, int d, int dv, bool last, bool bwd) {
   if (!mb_dims(d, dv, last) || m < 1 || m > kMbMaxFrames) return 0;
-  return mb_layout(32 * ((m + 31) / 32), tile_w(d), last ? tile_w(dv) : 0, last, bwd).total <= 160 * 1024;
+  return mb_layout(m, tile_w(d), last ? tile_w(dv) : 0, last, bwd, false).total <= 160 * 1024;
 }
 
-template <bool F16, int D, int DV, bool LAST, bool TWO>
+template <bool F16, int D, int DV, bool LAST, bool TWO, bool CT>
 static int launch_mb_k(const LParams& p, hipStream_t s) {
-  const int M = 32 * ((p.m + 31) / 32);
-  int lds = mb_layout(M, tile_w(D), tile_w(DV), LAST, false).total;
+  int lds = mb_layout(p.m, tile_w(D), tile_w(DV), LAST, false, CT).total;
   // The two-block non-last kernel is built for four columns per CU (33-48 frames: their chain of passes is
   // the bound, and a fourth column in flight hides more of it); past 48 frames the column's bytes dominate,
   // and its LDS request is raised to hold the CU at three (measured faster there).
   if constexpr (TWO && !LAST)
     if (p.m > 48) lds = lds > 160 * 1024 / 4 + 256 ? lds : 160 * 1024 / 4 + 256;
-  auto kern = lstep_mb_kernel<F16, D, DV, LAST, TWO>;
+  auto kern = lstep_mb_kernel<F16, D, DV, LAST, TWO, CT>;
   static std::atomic<int> lds_limit{65536};   // this kernel's dynamic-LDS limit as raised so far
   if (lds > lds_limit.load(std::memory_order_relaxed)) {   // (idempotent: a race only repeats the call)
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
@@ -1095,9 +1132,14 @@ static int launch_mb_k(const LParams& p, hipStream_t s) {
 template <bool F16, int D, int DV, bool LAST>
 static int launch_mb(const LParams& p, hipStream_t s) {
   constexpr bool TWO_OK = (tile_w(LAST ? DV : D) / 32) % 2 == 0;
-  if constexpr (TWO_OK)
-    if ((p.m + 31) / 32 == 2) return launch_mb_k<F16, D, DV, LAST, true>(p, s);
-  return launch_mb_k<F16, D, DV, LAST, false>(p, s);
+  if constexpr (TWO_OK) {
+    if ((p.m + 31) / 32 == 2) {
+      if constexpr (mb_compact_built(D, DV, LAST))
+        if (p.m <= kMbCompactMaxFrames) return launch_mb_k<F16, D, DV, LAST, true, true>(p, s);
+      return launch_mb_k<F16, D, DV, LAST, true, false>(p, s);
+    }
+  }
+  return launch_mb_k<F16, D, DV, LAST, false, false>(p, s);
 }
 
 template <bool F16>
@@ -1119,11 +1161,10 @@ int mb_lstep_fwd(const LParams& p, bool f16, int d, int dv, bool last, hipStream
   return f16 ? dispatch_mb<true>(p, d, dv, last, s) : dispatch_mb<false>(p, d, dv, last, s);
 }
 
-template <bool F16, int D, int DV, bool LAST, bool TWO>
+template <bool F16, int D, int DV, bool LAST, bool TWO, bool CT>
 static int launch_mb_bwd_k(const LBParams& p, hipStream_t s) {
-  const int M = 32 * ((p.m + 31) / 32);
-  const int lds = mb_layout(M, tile_w(D), tile_w(DV), LAST, true).total;
-  auto kern = lstep_mb_bwd_kernel<F16, D, DV, LAST, TWO>;
+  const int lds = mb_layout(p.m, tile_w(D), tile_w(DV), LAST, true, CT).total;
+  auto kern = lstep_mb_bwd_kernel<F16, D, DV, LAST, TWO, CT>;
   static std::atomic<int> lds_limit{65536};   // as in launch_mb, per kernel
   if (lds > lds_limit.load(std::memory_order_relaxed)) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
@@ -1140,9 +1181,14 @@ static int launch_mb_bwd_k(const LBParams& p, hipStream_t s) {
 template <bool F16, int D, int DV, bool LAST>
 static int launch_mb_bwd(const LBParams& p, hipStream_t s) {
   constexpr bool TWO_OK = (tile_w(D) / 32) % 2 == 0 && (!LAST || (tile_w(DV) / 32) % 2 == 0);
-  if constexpr (TWO_OK)
-    if ((p.m + 31) / 32 == 2) return launch_mb_bwd_k<F16, D, DV, LAST, true>(p, s);
-  return launch_mb_bwd_k<F16, D, DV, LAST, false>(p, s);
+  if constexpr (TWO_OK) {
+    if ((p.m + 31) / 32 == 2) {
+      if constexpr (mb_compact_built(D, DV, LAST))
+        if (p.m <= kMbCompactMaxFrames) return launch_mb_bwd_k<F16, D, DV, LAST, true, true>(p, s);
+      return launch_mb_bwd_k<F16, D, DV, LAST, true, false>(p, s);
+    }
+  }
+  return launch_mb_bwd_k<F16, D, DV, LAST, false, false>(p, s);
 }
 
 template <bool F16>
