@@ -334,104 +334,104 @@ __global__ __launch_bounds__(64 * kMbWaves, TWO && !LAST ? 4 : 2) void lstep_mb_
     }
     return;
   } else {
-  f32x16 acc[NACC];
+    f32x16 acc[NACC];
 #pragma unroll
-  for (int a = 0; a < NACC; ++a) acc[a] = f32x16{};
-  const int blk = wave;            // this wave's query block (last) or key block (otherwise)
-  const bool busy = blk < MB;
-  float fscale = 1.f;
+    for (int a = 0; a < NACC; ++a) acc[a] = f32x16{};
+    const int blk = wave;            // this wave's query block (last) or key block (otherwise)
+    const bool busy = blk < MB;
+    float fscale = 1.f;
 
-  if constexpr (LAST) {
-    if (busy) {
-      f32x16 x[kMbMaxBlocks];
-      const float mx = s_blocks(blk, x);
-      float sum = 0.f;
+    if constexpr (LAST) {
+      if (busy) {
+        f32x16 x[kMbMaxBlocks];
+        const float mx = s_blocks(blk, x);
+        float sum = 0.f;
 #pragma unroll
-      for (int kb = 0; kb < kMbMaxBlocks; ++kb) {
-        if (kb >= MB) break;
+        for (int kb = 0; kb < kMbMaxBlocks; ++kb) {
+          if (kb >= MB) break;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          x[kb][r] = fast_exp2(x[kb][r] - mx);
-          sum += x[kb][r];
-        }
-      }
-      const float inv = 1.0f / wave_sum32(sum);
-      // z^T[dv][i] = sum_k y^T[dv][k] attn^T[k][i]
-#pragma unroll
-      for (int kb = 0; kb < kMbMaxBlocks; ++kb) {
-        if (kb >= MB) break;
-        const V8 P0 = mb_pack<T, V8>(x[kb], 0, inv), P1 = mb_pack<T, V8>(x[kb], 1, inv);
-#pragma unroll
-        for (int a = 0; a < NACC; ++a) {
-          acc[a] = E::mfma(mb_tr8<V8, RBY, CT>(y_t, kb, m, lane, a, 0), P0, acc[a]);
-          acc[a] = E::mfma(mb_tr8<V8, RBY, CT>(y_t, kb, m, lane, a, 1), P1, acc[a]);
-        }
-      }
-    }
-  } else {
-    // pass 1: row log-sum-exp (log2 units) of every query row; rows past m get +1e30 (zero attention)
-    if (busy) {
-      f32x16 x[kMbMaxBlocks];
-      const float mx = s_blocks(blk, x);
-      float sum = 0.f;
-#pragma unroll
-      for (int kb = 0; kb < kMbMaxBlocks; ++kb) {
-        if (kb >= MB) break;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sum += fast_exp2(x[kb][r] - mx);
-      }
-      const float lse = mx + fast_log2(wave_sum32(sum));
-      if (hl == 0) lse_t[32 * blk + l32] = 32 * blk + l32 < m ? lse : 1.0e30f;
-    }
-    __syncthreads();
-    // pass 2: key block blk; one key per lane
-    if (busy) {
-      V8 kb_op[NDS];
-#pragma unroll
-      for (int ds = 0; ds < NDS; ++ds) kb_op[ds] = mb_row8<V8, RBD, CT>(k_t, blk, m, l32, hl, ds);
-      const float ek = e_t[32 * blk + l32];
-      float cm = 0.f;
-#pragma unroll
-      for (int ib = 0; ib < kMbMaxBlocks; ++ib) {
-        if (ib >= MB) break;
-        // L[i][k] = q_i . kr_k: A = q rows (lane = query row), B = kr rows (lane = key)
-        f32x16 x = f32x16{};
-#pragma unroll
-        for (int ds = 0; ds < NDS; ++ds) x = E::mfma(mb_row8<V8, RBD, CT>(q_t, ib, m, l32, hl, ds), kb_op[ds], x);
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const f32x4 lv = *(const VMO_LDS f32x4*)(lse_t + 32 * ib + 8 * g + 4 * hl);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float a = fast_exp2(fmaf(x[4 * g + e], c, ek - lv[e]));
-            x[4 * g + e] = a;
-            cm += a;
+          for (int r = 0; r < 16; ++r) {
+            x[kb][r] = fast_exp2(x[kb][r] - mx);
+            sum += x[kb][r];
           }
         }
-        // u^T[d][k] += sum_i q^T[d][i] attn[i][k]
-        const V8 P0 = mb_pack<T, V8>(x, 0, 1.f), P1 = mb_pack<T, V8>(x, 1, 1.f);
+        const float inv = 1.0f / wave_sum32(sum);
+        // z^T[dv][i] = sum_k y^T[dv][k] attn^T[k][i]
 #pragma unroll
-        for (int a = 0; a < NACC; ++a) {
-          acc[a] = E::mfma(mb_tr8<V8, RBD, CT>(q_t, ib, m, lane, a, 0), P0, acc[a]);
-          acc[a] = E::mfma(mb_tr8<V8, RBD, CT>(q_t, ib, m, lane, a, 1), P1, acc[a]);
+        for (int kb = 0; kb < kMbMaxBlocks; ++kb) {
+          if (kb >= MB) break;
+          const V8 P0 = mb_pack<T, V8>(x[kb], 0, inv), P1 = mb_pack<T, V8>(x[kb], 1, inv);
+#pragma unroll
+          for (int a = 0; a < NACC; ++a) {
+            acc[a] = E::mfma(mb_tr8<V8, RBY, CT>(y_t, kb, m, lane, a, 0), P0, acc[a]);
+            acc[a] = E::mfma(mb_tr8<V8, RBY, CT>(y_t, kb, m, lane, a, 1), P1, acc[a]);
+          }
         }
       }
-      fscale = p.scale / fmaxf(wave_sum32(cm), p.min_col_mass);
+    } else {
+      // pass 1: row log-sum-exp (log2 units) of every query row; rows past m get +1e30 (zero attention)
+      if (busy) {
+        f32x16 x[kMbMaxBlocks];
+        const float mx = s_blocks(blk, x);
+        float sum = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < kMbMaxBlocks; ++kb) {
+          if (kb >= MB) break;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) sum += fast_exp2(x[kb][r] - mx);
+        }
+        const float lse = mx + fast_log2(wave_sum32(sum));
+        if (hl == 0) lse_t[32 * blk + l32] = 32 * blk + l32 < m ? lse : 1.0e30f;
+      }
+      __syncthreads();
+      // pass 2: key block blk; one key per lane
+      if (busy) {
+        V8 kb_op[NDS];
+#pragma unroll
+        for (int ds = 0; ds < NDS; ++ds) kb_op[ds] = mb_row8<V8, RBD, CT>(k_t, blk, m, l32, hl, ds);
+        const float ek = e_t[32 * blk + l32];
+        float cm = 0.f;
+#pragma unroll
+        for (int ib = 0; ib < kMbMaxBlocks; ++ib) {
+          if (ib >= MB) break;
+          // L[i][k] = q_i . kr_k: A = q rows (lane = query row), B = kr rows (lane = key)
+          f32x16 x = f32x16{};
+#pragma unroll
+          for (int ds = 0; ds < NDS; ++ds) x = E::mfma(mb_row8<V8, RBD, CT>(q_t, ib, m, l32, hl, ds), kb_op[ds], x);
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const f32x4 lv = *(const VMO_LDS f32x4*)(lse_t + 32 * ib + 8 * g + 4 * hl);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float a = fast_exp2(fmaf(x[4 * g + e], c, ek - lv[e]));
+              x[4 * g + e] = a;
+              cm += a;
+            }
+          }
+          // u^T[d][k] += sum_i q^T[d][i] attn[i][k]
+          const V8 P0 = mb_pack<T, V8>(x, 0, 1.f), P1 = mb_pack<T, V8>(x, 1, 1.f);
+#pragma unroll
+          for (int a = 0; a < NACC; ++a) {
+            acc[a] = E::mfma(mb_tr8<V8, RBD, CT>(q_t, ib, m, lane, a, 0), P0, acc[a]);
+            acc[a] = E::mfma(mb_tr8<V8, RBD, CT>(q_t, ib, m, lane, a, 1), P1, acc[a]);
+          }
+        }
+        fscale = p.scale / fmaxf(wave_sum32(cm), p.min_col_mass);
+      }
     }
-  }
 
-  __syncthreads();   // every wave is done with the tiles: the patches reuse them
-  if (!busy) return;
-  VMO_LDS float* patch = (VMO_LDS float*)(sm + wave * kEpiPatchBytes);
-  const int nrows = min(32, m - 32 * blk);
-  T* const rows = rcol + 32 * blk * r_rs;
-  if constexpr (LAST) {
-    // z rows i from the first one the recompute does not overwrite (token i b + j >= skip)
-    const int ibeg = p.skip > j ? (p.skip - j + p.bs - 1) / p.bs : 0;
-    store_acc_rows<F16, CW>(patch, acc, NACC, 1.f, kGradStore, (char*)rows, r_rs * 2, nrows, lane, max(0, ibeg - 32 * blk));
-  } else {
-    store_acc_rows<F16, CW>(patch, acc, NACC, fscale, kGradStore, (char*)rows, r_rs * 2, nrows, lane);
-  }
+    __syncthreads();   // every wave is done with the tiles: the patches reuse them
+    if (!busy) return;
+    VMO_LDS float* patch = (VMO_LDS float*)(sm + wave * kEpiPatchBytes);
+    const int nrows = min(32, m - 32 * blk);
+    T* const rows = rcol + 32 * blk * r_rs;
+    if constexpr (LAST) {
+      // z rows i from the first one the recompute does not overwrite (token i b + j >= skip)
+      const int ibeg = p.skip > j ? (p.skip - j + p.bs - 1) / p.bs : 0;
+      store_acc_rows<F16, CW>(patch, acc, NACC, 1.f, kGradStore, (char*)rows, r_rs * 2, nrows, lane, max(0, ibeg - 32 * blk));
+    } else {
+      store_acc_rows<F16, CW>(patch, acc, NACC, fscale, kGradStore, (char*)rows, r_rs * 2, nrows, lane);
+    }
   }
 }
 
