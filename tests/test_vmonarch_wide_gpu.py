@@ -20,6 +20,7 @@ from oracle import vmonarch_attention_grad
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
+BF16, FP16 = torch.bfloat16, torch.float16
 
 
 def _r5(t, m, b):
@@ -108,15 +109,19 @@ def _no_composed_warning(fn):
         return fn()
 
 
-@pytest.mark.parametrize("m, b, D", [(33, 24, 64), (48, 16, 64), (64, 12, 64), (65, 8, 64), (96, 6, 64), (128, 4, 64),
-                                     (33, 20, 128), (65, 6, 128), (96, 4, 128), (128, 3, 128)])
-def test_vmonarch_many_frames_forward_and_grad(m, b, D):
+@pytest.mark.parametrize("m, b, D, dt", [(33, 24, 64, BF16), (48, 16, 64, BF16), (64, 12, 64, BF16), (65, 8, 64, BF16),
+                                         (96, 6, 64, BF16), (128, 4, 64, BF16), (33, 20, 128, BF16), (65, 6, 128, BF16),
+                                         (96, 4, 128, BF16), (128, 3, 128, BF16),
+                                         # the two-block kernels on compact tiles (up to 40 frames) and past them
+                                         (33, 20, 128, FP16), (40, 16, 128, FP16), (41, 16, 128, FP16), (40, 16, 128, BF16)],
+                         ids=lambda x: str(x).replace("torch.", "") if isinstance(x, torch.dtype) else None)
+def test_vmonarch_many_frames_forward_and_grad(m, b, D, dt):
     """More than 32 frames (HunyuanVideo's 129 frames are 33 latent frames; 128 latent frames are ~512 video
     frames) through the HIP path -- no composed-path warning -- forward without autograd and forward + backward
     with it, against the oracle."""
     from vmonarch_amd import vmonarch_attention
     g = torch.Generator().manual_seed(m + b + D)
-    q, k, v = (randn_lp(g, 1, 2, m * b, D) for _ in range(3))
+    q, k, v = (randn_lp(g, 1, 2, m * b, D, dtype=dt) for _ in range(3))
     do = torch.randn(1, 2, m * b, D, generator=g)
     print(f"vmonarch many frames m={m} b={b}", flush=True)
     with torch.no_grad():
