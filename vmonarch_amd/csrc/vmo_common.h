@@ -183,6 +183,12 @@ __device__ __forceinline__ int grad_mode(int flags, int accum_bit, int f32_bit, 
          : (flags & accum_bit) ? kGradAddF32 : (flags & f32_bit) ? kGradStoreF32 : kGradStore;
 }
 
+// Width of a 16-bit tile row in LDS for a head dim w: a 16-wide head (q / k, a value tensor, dO) is laid out 32
+// wide with each row's two 16-byte chunks stored twice, so that the 32-wide operand reads apply unchanged:
+// products over the head dim take one 16-dim MFMA step, and products that output it (P.V, dQ, dK, dV, u, z)
+// fill accumulator rows 16-31 with a copy of rows 0-15, which are not stored (CW = 16 below).
+constexpr int tile_w(int w) { return w < 32 ? 32 : w; }
+
 // Write a wave's 32-row result tile -- acc[a][r] is the value at (row l32, column 32 a + 8 (r / 4) +
 // 4 hl + r % 4), the transposed accumulator layout every kernel here ends with -- through a 4 KB LDS
 // patch, so that 8 consecutive lanes write one row's 128-byte segment (32 fp32 or 64 16-bit columns)
@@ -191,13 +197,7 @@ __device__ __forceinline__ int grad_mode(int flags, int accum_bit, int f32_bit, 
 // per lane (it scales the lane's own row l32).  One wave writes and reads its own patch (LDS accesses
 // of a wave complete in order); the caller makes sure no other wave still uses that LDS.  Used by the
 // flash-entropy forward (o) and backward (gradients) and both L-step kernels (u / z, gradients).
-// Width of a 16-bit tile row in LDS for a head dim w: a 16-wide head (q / k, a value tensor, dO) is laid out 32
-// wide with each row's two 16-byte chunks stored twice, so that the 32-wide operand reads apply unchanged:
-// products over the head dim take one 16-dim MFMA step, and products that output it (P.V, dQ, dK, dV, u, z)
-// fill accumulator rows 16-31 with a copy of rows 0-15, which are not stored (CW = 16 below).
-constexpr int tile_w(int w) { return w < 32 ? 32 : w; }
-
-// CW = 16: each accumulator block holds 16 valid columns (rows 0-15 of the transposed accumulator; the 16-wide
+// kEpiPatchBytes is the 32-row patch.  CW = 16: each accumulator block holds 16 valid columns (rows 0-15 of the transposed accumulator; the 16-wide
 // heads, whose LDS tiles hold every row twice), stored as columns 16 a .. 16 a + 15.  PROWS = 16: a 2 KB patch
 // that takes the 32 rows in two halves (for kernels whose LDS budget is that tight).
 constexpr int kEpiPatchBytes = 32 * 32 * 4;
