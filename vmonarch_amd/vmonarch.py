@@ -124,9 +124,10 @@ _MB_BWD = True    # the multi-block backward kernels
 
 
 def _lstep_mb_lds(m, d, dv, last, bwd):
-    """LDS bytes per grid column of the multi-block L-step kernels (csrc/lstep_mb.hip mb_layout): q and kr tiles (and
-    y, and the upstream gradient) of M = 32 ceil(m / 32) 16-bit rows, M-float vectors, at least the four row-store
-    patches."""
+    """LDS bytes per grid column of the multi-block L-step kernels (csrc/lstep_mb.hip mb_layout with whole tiles):
+    q and kr tiles (and y, and the upstream gradient) of M = 32 ceil(m / 32) 16-bit rows, M-float vectors, at least
+    the four row-store patches.  (The two-block last step up to 40 frames stages compact tiles, which take less:
+    this is the bound the host checks.)"""
     M = 32 * ((m + 31) // 32)
     r = lambda b: (b + 255) // 256 * 256   # noqa: E731
     d, dv = max(d, 32), max(dv, 32)   # 16-wide heads sit in 32-wide tiles
